@@ -1,0 +1,411 @@
+"""accel_amd -- Python binding of libaccel_hip.so, the gfx950 backend for
+golang-design/accel's int4 weight-only linear path.
+
+The product is the C ABI in ``include/accel_hip.h``; this module binds it
+with ctypes for the tests and the benchmark.  Device memory, streams and
+events are the library's own (``accel_hip_alloc`` etc.); numpy arrays are
+only the host side.  Importing fails loudly when the library has not been
+built: there is no other implementation to fall back to.
+
+Names follow the reference: ``Int4MatVec`` / ``Int4MatMul``
+(tensor/int4.go:99,168), ``GroupedMatVec`` / ``GroupedMatMul``
+(tensor/grouped.go:48,138), ``SegmentOffsets`` (tensor/segment.go:31),
+``int4_quantize`` (quant/int4.go:71).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libaccel_hip.so")
+
+if not os.path.exists(LIB_PATH):
+    raise ImportError(
+        f"{LIB_PATH} is not built; run `python accel_amd/build.py` (hipcc, gfx950). "
+        "accel_amd has no other implementation to fall back to.")
+
+_lib = ctypes.CDLL(LIB_PATH)
+
+OK = 0
+E_INVALID = -1
+E_NO_DEVICE = -2
+E_DEVICE_LOST = -3
+E_OOM = -4
+E_UNSUPPORTED = -5
+E_HIP = -6
+
+F32, F16, BF16, U32 = 1, 2, 3, 4
+_NP_DTYPE = {F32: np.float32, F16: np.uint16, BF16: np.uint16, U32: np.uint32}
+
+
+class AccelError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(message)
+        self.code = code
+
+
+class DeviceLost(AccelError):
+    """The sticky loss of internal/driver/plan.go:385-391."""
+
+
+class Refused(AccelError):
+    """A refusal by the operator layer's validation (the tensor builder's b.fail)."""
+
+
+class HipInfo(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 128), ("arch", ctypes.c_char * 64),
+                ("compute_units", ctypes.c_int32), ("wavefront", ctypes.c_int32),
+                ("lds_per_block", ctypes.c_int32), ("clock_khz", ctypes.c_int32),
+                ("mem_clock_khz", ctypes.c_int32), ("mem_bus_bits", ctypes.c_int32),
+                ("hbm_bytes", ctypes.c_uint64), ("l2_bytes", ctypes.c_int32),
+                ("pci_bus", ctypes.c_int32)]
+
+
+class Tensor(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_void_p), ("dtype", ctypes.c_int32),
+                ("rank", ctypes.c_int32), ("shape", ctypes.c_int64 * 4)]
+
+
+class Int4Desc(ctypes.Structure):
+    _fields_ = [("codes", ctypes.c_void_p), ("codes_len", ctypes.c_int64),
+                ("scales", ctypes.c_void_p), ("scales_len", ctypes.c_int64),
+                ("zeros", ctypes.c_void_p), ("zeros_len", ctypes.c_int64),
+                ("weights", ctypes.c_int64)]
+
+
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_sz = ctypes.c_size_t
+_P = ctypes.POINTER
+
+# Every symbol include/accel_hip.h declares, with its argument types.
+SIGNATURES = {
+    "accel_hip_last_error": ([], ctypes.c_char_p),
+    "accel_hip_abi_version": ([], _i),
+    "accel_hip_probe": ([_P(_i)], _i),
+    "accel_hip_info": ([_i, _P(HipInfo)], _i),
+    "accel_hip_open": ([_i], _i),
+    "accel_hip_close": ([_i], _i),
+    "accel_hip_lost": ([_i], _i),
+    "accel_hip_inject_loss": ([_i, ctypes.c_int64], _i),
+    "accel_hip_alloc": ([_i, _sz, _P(_vp)], _i),
+    "accel_hip_free": ([_i, _vp], _i),
+    "accel_hip_write": ([_i, _vp, _sz, _vp, _sz], _i),
+    "accel_hip_read": ([_i, _vp, _sz, _vp, _sz], _i),
+    "accel_hip_copy": ([_i, _vp, _vp, _vp, _sz], _i),
+    "accel_hip_stream_create": ([_i, _P(_vp)], _i),
+    "accel_hip_stream_destroy": ([_i, _vp], _i),
+    "accel_hip_stream_sync": ([_i, _vp], _i),
+    "accel_hip_event_create": ([_i, _P(_vp)], _i),
+    "accel_hip_event_destroy": ([_i, _vp], _i),
+    "accel_hip_event_record": ([_i, _vp, _vp], _i),
+    "accel_hip_event_query": ([_i, _vp], _i),
+    "accel_hip_event_sync": ([_i, _vp], _i),
+    "accel_hip_event_elapsed": ([_i, _vp, _vp, _P(ctypes.c_float)], _i),
+    "accel_hip_capture_begin": ([_i, _vp], _i),
+    "accel_hip_capture_end": ([_i, _vp, _P(_vp)], _i),
+    "accel_hip_exec_launch": ([_i, _vp, _vp], _i),
+    "accel_hip_exec_destroy": ([_i, _vp], _i),
+    "accel_hip_supports_kernel": ([ctypes.c_char_p], _i),
+    "accel_hip_dispatch": ([_i, _vp, ctypes.c_char_p, _P(_vp), _P(ctypes.c_uint64),
+                            ctypes.c_int32, _vp, _sz, _P(ctypes.c_uint32)], _i),
+    "accel_int4_matvec": ([_i, _vp, _P(Tensor), _P(Int4Desc), _P(Tensor)], _i),
+    "accel_int4_matmul": ([_i, _vp, _P(Tensor), _P(Int4Desc), _P(Tensor)], _i),
+    "accel_segment_offsets": ([_i, _vp, _P(Tensor), _P(Tensor)], _i),
+    "accel_grouped_matvec": ([_i, _vp, _P(Tensor), _P(Tensor), _P(Tensor), _P(Tensor)], _i),
+    "accel_grouped_matmul": ([_i, _vp, _P(Tensor), _P(Tensor), _P(Tensor), _P(Tensor)], _i),
+    "accel_int4_grouped_matvec": ([_i, _vp, _P(Tensor), _P(Int4Desc), ctypes.c_int64,
+                                   _P(Tensor), _P(Tensor)], _i),
+    "accel_int4_grouped_matmul": ([_i, _vp, _P(Tensor), _P(Int4Desc), ctypes.c_int64,
+                                   _P(Tensor), _P(Tensor)], _i),
+    "accel_int4_quantize": ([_vp, ctypes.c_int64, _vp, _vp, _vp], _i),
+    "accel_int4_dequantize": ([_vp, _vp, _vp, ctypes.c_int64, _vp], _i),
+    "accel_int4_quantize_device": ([_i, _vp, _vp, ctypes.c_int64, _vp, _vp, _vp], _i),
+}
+
+for _name, (_args, _ret) in SIGNATURES.items():
+    _fn = getattr(_lib, _name)  # AttributeError here means the ABI is incomplete
+    _fn.argtypes = _args
+    _fn.restype = _ret
+
+
+def lib():
+    return _lib
+
+
+def last_error() -> str:
+    return (_lib.accel_hip_last_error() or b"").decode()
+
+
+def _check(rc: int) -> int:
+    if rc >= 0:
+        return rc
+    msg = last_error()
+    if rc == E_DEVICE_LOST:
+        raise DeviceLost(rc, msg)
+    if rc == E_INVALID:
+        raise Refused(rc, msg)
+    raise AccelError(rc, msg)
+
+
+def device_count() -> int:
+    n = ctypes.c_int(0)
+    _check(_lib.accel_hip_probe(ctypes.byref(n)))
+    return n.value
+
+
+# ---- host-side quantisation (quant/int4.go) --------------------------------
+
+def _ptr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+def int4_quantize(w: np.ndarray):
+    """quant.Int4Quantize on host memory: (packed u32, scales f16 bits, zeros f16 bits)."""
+    w = np.ascontiguousarray(w, np.float32).ravel()
+    n = w.size
+    packed = np.zeros((n + 7) // 8, np.uint32)
+    scales = np.zeros((n + 127) // 128, np.uint16)
+    zeros = np.zeros((n + 127) // 128, np.uint16)
+    if n:
+        _check(_lib.accel_int4_quantize(_ptr(w), n, _ptr(packed), _ptr(scales), _ptr(zeros)))
+    return packed, scales, zeros
+
+
+def int4_dequantize(packed, scales, zeros, n: int) -> np.ndarray:
+    packed = np.ascontiguousarray(packed, np.uint32)
+    scales = np.ascontiguousarray(scales, np.uint16)
+    zeros = np.ascontiguousarray(zeros, np.uint16)
+    out = np.zeros(n, np.float32)
+    if n:
+        _check(_lib.accel_int4_dequantize(_ptr(packed), _ptr(scales), _ptr(zeros), n,
+                                          _ptr(out)))
+    return out
+
+
+# ---- device objects ---------------------------------------------------------
+
+@dataclass
+class Buffer:
+    """One device allocation with a dtype code and a shape (row-major)."""
+    device: "Device"
+    ptr: int
+    nbytes: int
+    dtype: int
+    shape: tuple
+
+    def tensor(self, shape=None, dtype=None) -> Tensor:
+        shape = tuple(self.shape if shape is None else shape)
+        t = Tensor()
+        t.data = self.ptr
+        t.dtype = self.dtype if dtype is None else dtype
+        t.rank = len(shape)
+        for i, s in enumerate(shape):
+            t.shape[i] = int(s)
+        return t
+
+    def numpy(self) -> np.ndarray:
+        host = np.empty(self.shape, _NP_DTYPE[self.dtype])
+        if self.nbytes:
+            _check(_lib.accel_hip_read(self.device.index, self.ptr, 0, _ptr(host),
+                                       host.nbytes))
+        return host
+
+    def write(self, host: np.ndarray) -> None:
+        host = np.ascontiguousarray(host)
+        if host.nbytes > self.nbytes:
+            raise ValueError("host array is larger than the buffer")
+        if host.nbytes:
+            _check(_lib.accel_hip_write(self.device.index, self.ptr, 0, _ptr(host),
+                                        host.nbytes))
+
+    def free(self) -> None:
+        if self.ptr:
+            _lib.accel_hip_free(self.device.index, self.ptr)
+            self.ptr = 0
+
+
+@dataclass
+class Int4Weights:
+    """tensor.Int4 on the device: codes, scales, zeros and the weight count."""
+    codes: Buffer
+    scales: Buffer
+    zeros: Buffer
+    weights: int
+
+    def desc(self) -> Int4Desc:
+        d = Int4Desc()
+        d.codes = self.codes.ptr if self.codes else None
+        d.codes_len = self.codes.shape[0] if self.codes else 0
+        d.scales = self.scales.ptr if self.scales else None
+        d.scales_len = self.scales.shape[0] if self.scales else 0
+        d.zeros = self.zeros.ptr if self.zeros else None
+        d.zeros_len = self.zeros.shape[0] if self.zeros else 0
+        d.weights = self.weights
+        return d
+
+    def free(self) -> None:
+        for b in (self.codes, self.scales, self.zeros):
+            if b:
+                b.free()
+
+
+class Device:
+    """An opened HIP device (accel_hip_open)."""
+
+    def __init__(self, index: int = 0):
+        self.index = index
+        _check(_lib.accel_hip_open(index))
+
+    def info(self) -> HipInfo:
+        info = HipInfo()
+        _check(_lib.accel_hip_info(self.index, ctypes.byref(info)))
+        return info
+
+    def close(self) -> None:
+        _check(_lib.accel_hip_close(self.index))
+
+    @property
+    def lost(self) -> bool:
+        return bool(_lib.accel_hip_lost(self.index))
+
+    def inject_loss(self, at_submission: int) -> None:
+        _check(_lib.accel_hip_inject_loss(self.index, at_submission))
+
+    # memory
+    def alloc(self, shape, dtype: int) -> Buffer:
+        shape = tuple(int(s) for s in np.atleast_1d(shape)) if not isinstance(shape, tuple) \
+            else tuple(int(s) for s in shape)
+        nbytes = int(np.prod(shape, dtype=np.int64)) * np.dtype(_NP_DTYPE[dtype]).itemsize
+        p = ctypes.c_void_p()
+        _check(_lib.accel_hip_alloc(self.index, max(nbytes, 1), ctypes.byref(p)))
+        return Buffer(self, p.value, nbytes, dtype, shape)
+
+    def upload(self, host: np.ndarray, dtype: int = None) -> Buffer:
+        host = np.ascontiguousarray(host)
+        if dtype is None:
+            dtype = {np.dtype(np.float32): F32, np.dtype(np.uint32): U32,
+                     np.dtype(np.uint16): F16}[host.dtype]
+        buf = self.alloc(host.shape if host.shape else (1,), dtype)
+        buf.write(host)
+        return buf
+
+    def upload_int4(self, packed, scales, zeros, weights: int) -> Int4Weights:
+        return Int4Weights(self.upload(np.asarray(packed, np.uint32), U32),
+                           self.upload(np.asarray(scales, np.uint16), F16),
+                           self.upload(np.asarray(zeros, np.uint16), F16), int(weights))
+
+    # streams and events
+    def stream(self) -> int:
+        s = ctypes.c_void_p()
+        _check(_lib.accel_hip_stream_create(self.index, ctypes.byref(s)))
+        return s.value
+
+    def destroy_stream(self, s) -> None:
+        _check(_lib.accel_hip_stream_destroy(self.index, s))
+
+    def sync(self, stream=None) -> None:
+        _check(_lib.accel_hip_stream_sync(self.index, stream))
+
+    def event(self) -> int:
+        e = ctypes.c_void_p()
+        _check(_lib.accel_hip_event_create(self.index, ctypes.byref(e)))
+        return e.value
+
+    def record(self, event, stream=None) -> None:
+        _check(_lib.accel_hip_event_record(self.index, event, stream))
+
+    def event_done(self, event) -> bool:
+        return _check(_lib.accel_hip_event_query(self.index, event)) == 1
+
+    def wait(self, event) -> None:
+        _check(_lib.accel_hip_event_sync(self.index, event))
+
+    def elapsed_ms(self, start, end) -> float:
+        ms = ctypes.c_float()
+        _check(_lib.accel_hip_event_elapsed(self.index, start, end, ctypes.byref(ms)))
+        return ms.value
+
+    def destroy_event(self, e) -> None:
+        _check(_lib.accel_hip_event_destroy(self.index, e))
+
+    # graphs: the resubmittable executable
+    def capture_begin(self, stream) -> None:
+        _check(_lib.accel_hip_capture_begin(self.index, stream))
+
+    def capture_end(self, stream) -> int:
+        e = ctypes.c_void_p()
+        _check(_lib.accel_hip_capture_end(self.index, stream, ctypes.byref(e)))
+        return e.value
+
+    def launch(self, exec_, stream=None) -> None:
+        _check(_lib.accel_hip_exec_launch(self.index, exec_, stream))
+
+    def destroy_exec(self, exec_) -> None:
+        _check(_lib.accel_hip_exec_destroy(self.index, exec_))
+
+    # ---- operators ----------------------------------------------------------
+    def Int4MatVec(self, a: Buffer, w: Int4Weights, out: Buffer, stream=None) -> None:
+        ta, tw, to = a.tensor(), w.desc(), out.tensor()
+        _check(_lib.accel_int4_matvec(self.index, stream, ctypes.byref(ta), ctypes.byref(tw),
+                                      ctypes.byref(to)))
+
+    def Int4MatMul(self, a: Buffer, w: Int4Weights, out: Buffer, stream=None) -> None:
+        ta, tw, to = a.tensor(), w.desc(), out.tensor()
+        _check(_lib.accel_int4_matmul(self.index, stream, ctypes.byref(ta), ctypes.byref(tw),
+                                      ctypes.byref(to)))
+
+    def SegmentOffsets(self, counts: Buffer, offsets: Buffer, stream=None) -> None:
+        tc, to = counts.tensor(), offsets.tensor()
+        _check(_lib.accel_segment_offsets(self.index, stream, ctypes.byref(tc),
+                                          ctypes.byref(to)))
+
+    def GroupedMatVec(self, x: Buffer, w: Buffer, counts: Buffer, out: Buffer,
+                      stream=None) -> None:
+        tx, tw, tc, to = x.tensor(), w.tensor(), counts.tensor(), out.tensor()
+        _check(_lib.accel_grouped_matvec(self.index, stream, ctypes.byref(tx), ctypes.byref(tw),
+                                         ctypes.byref(tc), ctypes.byref(to)))
+
+    def GroupedMatMul(self, x: Buffer, w: Buffer, counts: Buffer, out: Buffer,
+                      stream=None) -> None:
+        tx, tw, tc, to = x.tensor(), w.tensor(), counts.tensor(), out.tensor()
+        _check(_lib.accel_grouped_matmul(self.index, stream, ctypes.byref(tx), ctypes.byref(tw),
+                                         ctypes.byref(tc), ctypes.byref(to)))
+
+    def Int4GroupedMatVec(self, x: Buffer, w: Int4Weights, experts: int, counts: Buffer,
+                          out: Buffer, stream=None) -> None:
+        tx, tw, tc, to = x.tensor(), w.desc(), counts.tensor(), out.tensor()
+        _check(_lib.accel_int4_grouped_matvec(self.index, stream, ctypes.byref(tx),
+                                              ctypes.byref(tw), experts, ctypes.byref(tc),
+                                              ctypes.byref(to)))
+
+    def Int4GroupedMatMul(self, x: Buffer, w: Int4Weights, experts: int, counts: Buffer,
+                          out: Buffer, stream=None) -> None:
+        tx, tw, tc, to = x.tensor(), w.desc(), counts.tensor(), out.tensor()
+        _check(_lib.accel_int4_grouped_matmul(self.index, stream, ctypes.byref(tx),
+                                              ctypes.byref(tw), experts, ctypes.byref(tc),
+                                              ctypes.byref(to)))
+
+    def int4_quantize(self, w: Buffer, n: int, packed: Buffer, scales: Buffer, zeros: Buffer,
+                      stream=None) -> None:
+        _check(_lib.accel_int4_quantize_device(self.index, stream, w.ptr, n, packed.ptr,
+                                               scales.ptr, zeros.ptr))
+
+    def dispatch(self, kernel: str, bindings, lens, uniform: bytes, count=(1, 1, 1),
+                 stream=None) -> None:
+        """One kernel-record dispatch through the backend seam."""
+        n = len(bindings)
+        b = (ctypes.c_void_p * n)(*[x.ptr if isinstance(x, Buffer) else x for x in bindings])
+        ln = (ctypes.c_uint64 * n)(*lens)
+        u = ctypes.create_string_buffer(uniform, len(uniform))
+        c = (ctypes.c_uint32 * 3)(*count)
+        _check(_lib.accel_hip_dispatch(self.index, stream, kernel.encode(), b, ln, n,
+                                       ctypes.cast(u, ctypes.c_void_p), len(uniform), c))
+
+
+def supports_kernel(name: str) -> bool:
+    return bool(_lib.accel_hip_supports_kernel(name.encode()))

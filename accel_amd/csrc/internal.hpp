@@ -1,0 +1,104 @@
+// Internal declarations shared by the translation units of libaccel_hip.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdarg>
+#include <cstddef>
+#include <cstdint>
+#include <mutex>
+
+#include "../../include/accel_hip.h"
+
+namespace accel {
+
+// Records a message for accel_hip_last_error() on this thread and returns code.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+
+// Per-device state: the open flag, sticky loss, fault injection and the
+// library-owned workspace.
+struct Device {
+    int ordinal = -1;
+    bool open = false;
+    std::atomic<int> lost{0};
+    std::mutex mu;
+    int64_t submissions = 0;
+    int64_t lose_at = 0;
+    void* ws = nullptr;        // workspace (device memory)
+    size_t ws_bytes = 0;
+    int cu_count = 256;
+    size_t lds_per_block = 65536;
+};
+
+// The open device `dev`, made current on this thread, or nullptr with the
+// error recorded.
+Device* device(int dev);
+
+// Counts an accepted submission and applies fault injection; returns
+// ACCEL_OK or ACCEL_E_DEVICE_LOST (cpu.go:179-191's beginSubmission).
+int begin_submission(Device* d);
+
+// Classifies a HIP status after a launch or a wait.  Errors that leave the
+// device's memory undefined mark it lost for good; an allocation failure
+// does not.  Returns the ACCEL_* code.
+int classify(Device* d, hipError_t e, const char* what);
+
+// The workspace, at least `bytes` long.  The first kWorkspaceCounterBytes are
+// kept zero between launches by the kernels that use them (a counter is reset
+// by the workgroup that consumes it).
+constexpr size_t kWorkspaceCounterBytes = 1 << 16;
+void* workspace(Device* d, size_t bytes, int* status);
+
+// ---- kernel launchers (defined in the .hip files) ------------------------
+
+struct Int4Planes {
+    const uint32_t* codes;
+    const uint16_t* scales;
+    const uint16_t* zeros;
+};
+
+// Decode product, M <= 16 rows of f32 activations -> f32 out.
+hipError_t launch_int4_decode_f32(Device* d, hipStream_t st, const float* a,
+                                  Int4Planes w, float* out, int M, int K, int N,
+                                  int* status);
+// Any shape, f32: one thread per output element (small or ragged shapes).
+hipError_t launch_int4_generic_f32(hipStream_t st, const float* a, Int4Planes w,
+                                   float* out, int M, int K, int N);
+// Any shape, bf16 activations and output.
+hipError_t launch_int4_generic_bf16(hipStream_t st, const uint16_t* a, Int4Planes w,
+                                    uint16_t* out, int M, int K, int N);
+// Prefill product on MFMA: bf16 activations [M,K] -> bf16 out [M,N].
+hipError_t launch_int4_gemm_bf16(Device* d, hipStream_t st, const uint16_t* a,
+                                 Int4Planes w, uint16_t* out, int M, int K, int N);
+bool int4_gemm_bf16_supported(int M, int K, int N);
+// f32 activations with M > 16, fp32 arithmetic.
+hipError_t launch_int4_gemm_f32(Device* d, hipStream_t st, const float* a,
+                                Int4Planes w, float* out, int M, int K, int N);
+bool int4_decode_f32_supported(int M, int K, int N, const void* codes);
+
+// Grouped products over offsets [E+1] already on the device.
+hipError_t launch_segment_offsets(hipStream_t st, const uint32_t* counts,
+                                  uint32_t* offsets, int rows);
+hipError_t launch_grouped_f32(hipStream_t st, const float* x, const float* w,
+                              const uint32_t* off, float* out, int E, int T, int K,
+                              int N, bool write_padding);
+hipError_t launch_int4_grouped_f32(hipStream_t st, const float* x, Int4Planes w,
+                                   const uint32_t* off, float* out, int E, int T,
+                                   int K, int N, bool write_padding);
+hipError_t launch_int4_grouped_bf16(Device* d, hipStream_t st, const uint16_t* x,
+                                    Int4Planes w, const uint32_t* off, uint16_t* out,
+                                    int E, int T, int K, int N, bool write_padding);
+
+// Device quantizer.
+hipError_t launch_int4_quantize(hipStream_t st, const float* w, int64_t n,
+                                uint32_t* packed, uint16_t* scales, uint16_t* zeros);
+
+// Host quantizer shared by the C entry point.
+void int4_quantize_host(const float* w, int64_t n, uint32_t* packed, uint16_t* scales,
+                        uint16_t* zeros);
+void int4_dequantize_host(const uint32_t* packed, const uint16_t* scales,
+                          const uint16_t* zeros, int64_t n, float* out);
+
+}  // namespace accel

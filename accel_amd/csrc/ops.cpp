@@ -1,0 +1,594 @@
+// The operator layer of the C ABI: the tensor package's int4 and grouped
+// entry points with the reference's validation and refusal messages
+// (tensor/int4.go:41-212, tensor/grouped.go:48-212, tensor/segment.go:31-50),
+// and kernel-record dispatch for the backend seam.
+//
+// Kernel selection (the analogue of a plan's selection report,
+// tensor/compile.go:36-42):
+//   f32 activations, M <= 16, N % 128 == 0   -> the decode kernels (K split)
+//   f32 activations, M > 16,  N % 128 == 0   -> the fp32 tiled kernel
+//   bf16 activations, K % 64 == 0, N % 128 == 0 -> the MFMA tiles
+//   any other shape                          -> the per-element kernel
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <string>
+
+#include "internal.hpp"
+
+namespace accel {
+hipError_t launch_zero_tail_bf16(hipStream_t st, const uint32_t* off, uint16_t* out, int E,
+                                 int T, int N);
+}
+
+using namespace accel;
+
+#define ACCEL_API extern "C" __attribute__((visibility("default")))
+
+namespace {
+
+const char* dtype_name(int32_t d) {
+    switch (d) {
+        case ACCEL_F32: return "f32";
+        case ACCEL_F16: return "f16";
+        case ACCEL_BF16: return "bf16";
+        case ACCEL_U32: return "u32";
+        default: return "an unknown dtype";
+    }
+}
+
+std::string shape_str(const accel_tensor_t* t) {
+    std::string s = "[";
+    for (int i = 0; i < t->rank && i < 4; i++) {
+        if (i) s += ' ';
+        s += std::to_string((long long)t->shape[i]);
+    }
+    return s + "]";
+}
+
+int64_t elements(const accel_tensor_t* t) {
+    int64_t n = 1;
+    for (int i = 0; i < t->rank && i < 4; i++) n *= t->shape[i];
+    return n;
+}
+
+int refuse(const char* op, const std::string& why) {
+    return fail(ACCEL_E_INVALID, "accel/tensor: %s: %s", op, why.c_str());
+}
+
+bool valid_tensor(const accel_tensor_t* t) {
+    return t && t->rank >= 0 && t->rank <= 4;
+}
+
+// checkInt4 (tensor/int4.go:41-78): why a packed matrix is not usable, or "".
+std::string check_int4(const accel_int4_t* q, const char* what) {
+    char buf[512];
+    if (!q || !q->codes || !q->scales || !q->zeros) {
+        snprintf(buf, sizeof buf,
+                 "%s needs a code plane, a scale plane and a zero plane; the zero point is "
+                 "what makes four bits usable and is not optional",
+                 what);
+        return buf;
+    }
+    if (q->weights <= 0) {
+        snprintf(buf, sizeof buf,
+                 "%s declares %lld weights; the count cannot be derived from the word count, "
+                 "because eight weights per word makes several matrices pack into the same "
+                 "words",
+                 what, (long long)q->weights);
+        return buf;
+    }
+    const int64_t want = (q->weights + 7) / 8;
+    if (q->codes_len != want) {
+        snprintf(buf, sizeof buf,
+                 "%s declares %lld weights, which is %lld words, and the code plane holds %lld",
+                 what, (long long)q->weights, (long long)want, (long long)q->codes_len);
+        return buf;
+    }
+    const int64_t groups = (q->weights + 127) / 128;
+    if (q->scales_len != groups) {
+        snprintf(buf, sizeof buf, "%s has %lld weights, which is %lld groups of 128, and %lld scales",
+                 what, (long long)q->weights, (long long)groups, (long long)q->scales_len);
+        return buf;
+    }
+    if (q->zeros_len != groups) {
+        snprintf(buf, sizeof buf, "%s has %lld weights, which is %lld groups of 128, and %lld zeros",
+                 what, (long long)q->weights, (long long)groups, (long long)q->zeros_len);
+        return buf;
+    }
+    return "";
+}
+
+Int4Planes planes(const accel_int4_t* w) { return {w->codes, w->scales, w->zeros}; }
+
+// Runs a launch and classifies its outcome.
+int finish(Device* d, hipError_t e, int status, const char* what) {
+    if (status != ACCEL_OK) return status;
+    return classify(d, e, what);
+}
+
+int check_out(const char* op, const accel_tensor_t* out, int32_t dtype, int64_t rows,
+              int64_t cols, bool vector) {
+    char buf[256];
+    if (!valid_tensor(out) || !out->data)
+        return refuse(op, "the output tensor is missing");
+    if (out->dtype != dtype) {
+        snprintf(buf, sizeof buf, "the output is %s and this product writes %s",
+                 dtype_name(out->dtype), dtype_name(dtype));
+        return refuse(op, buf);
+    }
+    const bool ok = vector ? (out->rank == 1 && out->shape[0] == cols)
+                           : (out->rank == 2 && out->shape[0] == rows && out->shape[1] == cols);
+    if (!ok) {
+        if (vector)
+            snprintf(buf, sizeof buf, "the output is %s and the product is [%lld]",
+                     shape_str(out).c_str(), (long long)cols);
+        else
+            snprintf(buf, sizeof buf, "the output is %s and the product is [%lld %lld]",
+                     shape_str(out).c_str(), (long long)rows, (long long)cols);
+        return refuse(op, buf);
+    }
+    return ACCEL_OK;
+}
+
+// The shared core of Int4MatVec and Int4MatMul once validated.
+int run_int4_product(Device* d, hipStream_t st, const void* a, int32_t dtype,
+                     const accel_int4_t* w, void* out, int M, int K, int N) {
+    int status = begin_submission(d);
+    if (status != ACCEL_OK) return status;
+    if (M == 0 || N == 0) return ACCEL_OK;
+    const Int4Planes p = planes(w);
+    const bool aligned128 = N % 128 == 0 && (uint64_t)K * (uint64_t)N < (1ull << 32);
+    hipError_t e = hipSuccess;
+    if (dtype == ACCEL_F32) {
+        const float* af = static_cast<const float*>(a);
+        float* of = static_cast<float*>(out);
+        if (int4_decode_f32_supported(M, K, N, w->codes))
+            e = launch_int4_decode_f32(d, st, af, p, of, M, K, N, &status);
+        else if (M > 16 && aligned128)
+            e = launch_int4_gemm_f32(d, st, af, p, of, M, K, N);
+        else
+            e = launch_int4_generic_f32(st, af, p, of, M, K, N);
+    } else {
+        const uint16_t* ab = static_cast<const uint16_t*>(a);
+        uint16_t* ob = static_cast<uint16_t*>(out);
+        if (int4_gemm_bf16_supported(M, K, N) && (reinterpret_cast<uintptr_t>(a) & 15) == 0)
+            e = launch_int4_gemm_bf16(d, st, ab, p, ob, M, K, N);
+        else
+            e = launch_int4_generic_bf16(st, ab, p, ob, M, K, N);
+    }
+    return finish(d, e, status, "int4 product launch");
+}
+
+}  // namespace
+
+ACCEL_API int accel_int4_matvec(int dev, void* stream, const accel_tensor_t* a,
+                                const accel_int4_t* w, accel_tensor_t* out) {
+    clear_error();
+    const char* op = "Int4MatVec";
+    std::string why = check_int4(w, "the weight matrix");
+    if (!why.empty()) return refuse(op, why);
+    if (!valid_tensor(a) || !a->data) return refuse(op, "the activations are missing");
+    char buf[512];
+    if (a->dtype != ACCEL_F32) {
+        snprintf(buf, sizeof buf, "activations are %s and this kernel reads f32",
+                 dtype_name(a->dtype));
+        return refuse(op, buf);
+    }
+    if (a->rank != 1) {
+        snprintf(buf, sizeof buf,
+                 "activations are %s; a matvec takes a vector, and a batch of them is the "
+                 "tiled form, Int4MatMul",
+                 shape_str(a).c_str());
+        return refuse(op, buf);
+    }
+    const int64_t k = a->shape[0];
+    if (k == 0 || w->weights % k != 0) {
+        snprintf(buf, sizeof buf,
+                 "activations are %lld long and the matrix holds %lld weights; the matrix is "
+                 "[K, N] with K the activation width, so the second is a multiple of the "
+                 "first",
+                 (long long)k, (long long)w->weights);
+        return refuse(op, buf);
+    }
+    const int64_t n = w->weights / k;
+    if (k > INT32_MAX || n > INT32_MAX)
+        return refuse(op, "the matrix is larger than this backend's 32-bit extents");
+    int rc = check_out(op, out, ACCEL_F32, 1, n, true);
+    if (rc != ACCEL_OK) return rc;
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    return run_int4_product(d, (hipStream_t)stream, a->data, ACCEL_F32, w, out->data, 1,
+                            (int)k, (int)n);
+}
+
+ACCEL_API int accel_int4_matmul(int dev, void* stream, const accel_tensor_t* a,
+                                const accel_int4_t* w, accel_tensor_t* out) {
+    clear_error();
+    const char* op = "Int4MatMul";
+    std::string why = check_int4(w, "the weight matrix");
+    if (!why.empty()) return refuse(op, why);
+    if (!valid_tensor(a) || !a->data) return refuse(op, "the activations are missing");
+    char buf[512];
+    if (a->dtype != ACCEL_F32 && a->dtype != ACCEL_BF16) {
+        snprintf(buf, sizeof buf, "activations are %s and this kernel reads f32 (or bf16)",
+                 dtype_name(a->dtype));
+        return refuse(op, buf);
+    }
+    if (a->rank != 2) {
+        snprintf(buf, sizeof buf,
+                 "activations are %s; this is the batched form and takes [rows, K]. One row "
+                 "is Int4MatVec, which is the decode shape and reads the matrix once per token",
+                 shape_str(a).c_str());
+        return refuse(op, buf);
+    }
+    const int64_t m = a->shape[0], k = a->shape[1];
+    if (k == 0 || w->weights % k != 0) {
+        snprintf(buf, sizeof buf,
+                 "activations are %lld wide and the matrix holds %lld weights; the matrix is "
+                 "[K, N] with K the activation width, so the second is a multiple of the "
+                 "first",
+                 (long long)k, (long long)w->weights);
+        return refuse(op, buf);
+    }
+    const int64_t n = w->weights / k;
+    if (m > INT32_MAX || k > INT32_MAX || n > INT32_MAX)
+        return refuse(op, "the product is larger than this backend's 32-bit extents");
+    int rc = check_out(op, out, a->dtype, m, n, false);
+    if (rc != ACCEL_OK) return rc;
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    return run_int4_product(d, (hipStream_t)stream, a->data, a->dtype, w, out->data, (int)m,
+                            (int)k, (int)n);
+}
+
+ACCEL_API int accel_segment_offsets(int dev, void* stream, const accel_tensor_t* counts,
+                                    accel_tensor_t* offsets) {
+    clear_error();
+    const char* op = "SegmentOffsets";
+    if (!valid_tensor(counts) || !counts->data) return refuse(op, "counts is nil");
+    if (counts->dtype != ACCEL_U32) return refuse(op, "counts must be u32");
+    const int64_t rows = elements(counts);
+    if (!valid_tensor(offsets) || !offsets->data || offsets->dtype != ACCEL_U32 ||
+        elements(offsets) != rows + 1)
+        return refuse(op, "offsets must be u32 with one more entry than counts");
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    int status = begin_submission(d);
+    if (status != ACCEL_OK) return status;
+    hipError_t e = launch_segment_offsets((hipStream_t)stream,
+                                          static_cast<const uint32_t*>(counts->data),
+                                          static_cast<uint32_t*>(offsets->data), (int)rows);
+    return classify(d, e, "SegmentOffsets launch");
+}
+
+namespace {
+
+// Shape checks shared by the two grouped operators (tensor/grouped.go:48-96).
+// On success fills T, K, N, E.
+int check_grouped(const char* op, const accel_tensor_t* x, const accel_tensor_t* w,
+                  const accel_tensor_t* counts, int64_t* T, int64_t* K, int64_t* N,
+                  int64_t* E) {
+    char buf[512];
+    if (!valid_tensor(counts) || !counts->data)
+        return refuse(op, "counts is nil; it is one token count per expert and is what says "
+                          "which rows belong to which weight matrix");
+    if (!valid_tensor(x) || !x->data || !valid_tensor(w) || !w->data)
+        return refuse(op, "an operand is missing");
+    struct {
+        const char* name;
+        const accel_tensor_t* t;
+        int32_t want;
+    } cs[] = {{"x", x, ACCEL_F32}, {"w", w, ACCEL_F32}, {"counts", counts, ACCEL_U32}};
+    for (auto& c : cs)
+        if (c.t->dtype != c.want) {
+            snprintf(buf, sizeof buf, "%s is %s and this kernel reads %s", c.name,
+                     dtype_name(c.t->dtype), dtype_name(c.want));
+            return refuse(op, buf);
+        }
+    if (x->rank != 2) {
+        snprintf(buf, sizeof buf,
+                 "x is %s; it is [tokens, K] with the tokens of every expert end to end",
+                 shape_str(x).c_str());
+        return refuse(op, buf);
+    }
+    if (w->rank != 3) {
+        snprintf(buf, sizeof buf, "w is %s; it is [experts, K, N], one matrix per expert",
+                 shape_str(w).c_str());
+        return refuse(op, buf);
+    }
+    *T = x->shape[0];
+    *K = x->shape[1];
+    *E = w->shape[0];
+    *N = w->shape[2];
+    if (w->shape[1] != *K) {
+        snprintf(buf, sizeof buf,
+                 "x is %s and w is %s; every expert contracts against the same width, so w's "
+                 "second axis is x's second",
+                 shape_str(x).c_str(), shape_str(w).c_str());
+        return refuse(op, buf);
+    }
+    if (elements(counts) != *E) {
+        snprintf(buf, sizeof buf,
+                 "counts holds %lld entries and w has %lld experts; it is one token count per "
+                 "expert",
+                 (long long)elements(counts), (long long)*E);
+        return refuse(op, buf);
+    }
+    if (*E == 0) return refuse(op, "w declares no experts");
+    return ACCEL_OK;
+}
+
+// Offsets for `experts` counts into the workspace; returns the device
+// pointer or nullptr with status set.
+uint32_t* offsets_in_workspace(Device* d, hipStream_t st, const uint32_t* counts,
+                               int64_t experts, int* status) {
+    void* ws = workspace(d, (size_t)(experts + 1) * sizeof(uint32_t), status);
+    if (!ws) return nullptr;
+    uint32_t* off =
+        reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + kWorkspaceCounterBytes);
+    hipError_t e = launch_segment_offsets(st, counts, off, (int)experts);
+    if (e != hipSuccess) {
+        *status = classify(d, e, "SegmentOffsets launch");
+        return nullptr;
+    }
+    return off;
+}
+
+int run_grouped_f32(const char* op, int dev, void* stream, const accel_tensor_t* x,
+                    const accel_tensor_t* w, const accel_tensor_t* counts, accel_tensor_t* out,
+                    bool matvec) {
+    clear_error();
+    int64_t T, K, N, E;
+    int rc = check_grouped(op, x, w, counts, &T, &K, &N, &E);
+    if (rc != ACCEL_OK) return rc;
+    rc = check_out(op, out, ACCEL_F32, T, N, false);
+    if (rc != ACCEL_OK) return rc;
+    if (T > INT32_MAX || K > INT32_MAX || N > INT32_MAX || E > INT32_MAX)
+        return refuse(op, "the product is larger than this backend's 32-bit extents");
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    int status = begin_submission(d);
+    if (status != ACCEL_OK) return status;
+    hipStream_t st = (hipStream_t)stream;
+    uint32_t* off = offsets_in_workspace(d, st, static_cast<const uint32_t*>(counts->data), E,
+                                         &status);
+    if (!off) return status;
+    hipError_t e = launch_grouped_f32(st, static_cast<const float*>(x->data),
+                                      static_cast<const float*>(w->data), off,
+                                      static_cast<float*>(out->data), (int)E, (int)T, (int)K,
+                                      (int)N, matvec);
+    return classify(d, e, "grouped launch");
+}
+
+int run_grouped_int4(const char* op, int dev, void* stream, const accel_tensor_t* x,
+                     const accel_int4_t* w, int64_t experts, const accel_tensor_t* counts,
+                     accel_tensor_t* out, bool matvec) {
+    clear_error();
+    char buf[512];
+    std::string why = check_int4(w, "the expert weights");
+    if (!why.empty()) return refuse(op, why);
+    if (!valid_tensor(counts) || !counts->data)
+        return refuse(op, "counts is nil; it is one token count per expert and is what says "
+                          "which rows belong to which weight matrix");
+    if (counts->dtype != ACCEL_U32) {
+        snprintf(buf, sizeof buf, "counts is %s and this kernel reads u32",
+                 dtype_name(counts->dtype));
+        return refuse(op, buf);
+    }
+    if (!valid_tensor(x) || !x->data) return refuse(op, "x is missing");
+    if (x->dtype != ACCEL_F32 && x->dtype != ACCEL_BF16) {
+        snprintf(buf, sizeof buf, "x is %s and this kernel reads f32 (or bf16)",
+                 dtype_name(x->dtype));
+        return refuse(op, buf);
+    }
+    if (x->rank != 2) {
+        snprintf(buf, sizeof buf,
+                 "x is %s; it is [tokens, K] with the tokens of every expert end to end",
+                 shape_str(x).c_str());
+        return refuse(op, buf);
+    }
+    if (experts <= 0) return refuse(op, "w declares no experts");
+    if (elements(counts) != experts) {
+        snprintf(buf, sizeof buf,
+                 "counts holds %lld entries and w has %lld experts; it is one token count per "
+                 "expert",
+                 (long long)elements(counts), (long long)experts);
+        return refuse(op, buf);
+    }
+    const int64_t T = x->shape[0], K = x->shape[1];
+    if (K == 0 || w->weights % (experts * K) != 0) {
+        snprintf(buf, sizeof buf,
+                 "x is %lld wide and the %lld experts hold %lld weights; each expert is [K, N] "
+                 "with K x's width",
+                 (long long)K, (long long)experts, (long long)w->weights);
+        return refuse(op, buf);
+    }
+    const int64_t N = w->weights / (experts * K);
+    if ((K * N) % 128 != 0)
+        return refuse(op, "each expert's K*N must be a multiple of 128, so no quantisation "
+                          "group straddles two experts");
+    if (T > INT32_MAX || K > INT32_MAX || N > INT32_MAX || experts > INT32_MAX ||
+        (uint64_t)w->weights >= (1ull << 40))
+        return refuse(op, "the product is larger than this backend's extents");
+    int rc = check_out(op, out, x->dtype, T, N, false);
+    if (rc != ACCEL_OK) return rc;
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    int status = begin_submission(d);
+    if (status != ACCEL_OK) return status;
+    hipStream_t st = (hipStream_t)stream;
+    uint32_t* off = offsets_in_workspace(d, st, static_cast<const uint32_t*>(counts->data),
+                                         experts, &status);
+    if (!off) return status;
+    const Int4Planes p = planes(w);
+    hipError_t e;
+    if (x->dtype == ACCEL_F32) {
+        e = launch_int4_grouped_f32(st, static_cast<const float*>(x->data), p, off,
+                                    static_cast<float*>(out->data), (int)experts, (int)T,
+                                    (int)K, (int)N, matvec);
+    } else {
+        const bool mfma = int4_gemm_bf16_supported(1, (int)K, (int)N) &&
+                          (reinterpret_cast<uintptr_t>(x->data) & 15) == 0;
+        if (!mfma)
+            return refuse(op, "bf16 grouped products need K % 64 == 0 and N % 128 == 0");
+        e = launch_int4_grouped_bf16(d, st, static_cast<const uint16_t*>(x->data), p, off,
+                                     static_cast<uint16_t*>(out->data), (int)experts, (int)T,
+                                     (int)K, (int)N, matvec);
+        if (e == hipSuccess && matvec)
+            e = launch_zero_tail_bf16(st, off, static_cast<uint16_t*>(out->data),
+                                      (int)experts, (int)T, (int)N);
+    }
+    return classify(d, e, "grouped int4 launch");
+}
+
+}  // namespace
+
+ACCEL_API int accel_grouped_matvec(int dev, void* stream, const accel_tensor_t* x,
+                                   const accel_tensor_t* w, const accel_tensor_t* counts,
+                                   accel_tensor_t* out) {
+    return run_grouped_f32("GroupedMatVec", dev, stream, x, w, counts, out, true);
+}
+
+ACCEL_API int accel_grouped_matmul(int dev, void* stream, const accel_tensor_t* x,
+                                   const accel_tensor_t* w, const accel_tensor_t* counts,
+                                   accel_tensor_t* out) {
+    return run_grouped_f32("GroupedMatMul", dev, stream, x, w, counts, out, false);
+}
+
+ACCEL_API int accel_int4_grouped_matvec(int dev, void* stream, const accel_tensor_t* x,
+                                        const accel_int4_t* w, int64_t experts,
+                                        const accel_tensor_t* counts, accel_tensor_t* out) {
+    return run_grouped_int4("Int4GroupedMatVec", dev, stream, x, w, experts, counts, out,
+                            true);
+}
+
+ACCEL_API int accel_int4_grouped_matmul(int dev, void* stream, const accel_tensor_t* x,
+                                        const accel_int4_t* w, int64_t experts,
+                                        const accel_tensor_t* counts, accel_tensor_t* out) {
+    return run_grouped_int4("Int4GroupedMatMul", dev, stream, x, w, experts, counts, out,
+                            false);
+}
+
+ACCEL_API int accel_int4_quantize_device(int dev, void* stream, const float* w, int64_t n,
+                                         uint32_t* packed, uint16_t* scales, uint16_t* zeros) {
+    clear_error();
+    if (n < 0) return fail(ACCEL_E_INVALID, "accel_int4_quantize_device: negative count");
+    if (n == 0) return ACCEL_OK;
+    if (!w || !packed || !scales || !zeros)
+        return fail(ACCEL_E_INVALID, "accel_int4_quantize_device: NULL pointer");
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    int status = begin_submission(d);
+    if (status != ACCEL_OK) return status;
+    return classify(d, launch_int4_quantize((hipStream_t)stream, w, n, packed, scales, zeros),
+                    "quantize launch");
+}
+
+// ---- backend seam: kernel records ------------------------------------------
+
+namespace {
+
+struct Record {
+    const char* name;
+    int bindings;
+};
+const Record kRecords[] = {
+    {"QuantMatVecInt4", 5}, {"QuantMatMulInt4", 5}, {"GroupedMatVec", 4},
+    {"GroupedMatMul", 4},   {"SegmentOffsets", 2},
+};
+
+uint32_t u32_at(const void* p, size_t off) {
+    uint32_t v;
+    std::memcpy(&v, static_cast<const char*>(p) + off, 4);
+    return v;
+}
+
+}  // namespace
+
+ACCEL_API int accel_hip_supports_kernel(const char* kernel) {
+    if (!kernel) return 0;
+    for (const Record& r : kRecords)
+        if (std::strcmp(r.name, kernel) == 0) return 1;
+    return 0;
+}
+
+ACCEL_API int accel_hip_dispatch(int dev, void* stream, const char* kernel,
+                                 const void* const* bindings, const uint64_t* lens,
+                                 int32_t nbindings, const void* uniform, size_t uniform_bytes,
+                                 const uint32_t count[3]) {
+    clear_error();
+    (void)count;
+    if (!kernel) return fail(ACCEL_E_INVALID, "accel_hip_dispatch: no kernel named");
+    const Record* rec = nullptr;
+    for (const Record& r : kRecords)
+        if (std::strcmp(r.name, kernel) == 0) rec = &r;
+    if (!rec)
+        return fail(ACCEL_E_UNSUPPORTED,
+                    "accel_hip: kernel %s has no gfx950 implementation in this backend", kernel);
+    if (nbindings != rec->bindings || !bindings || !lens)
+        return fail(ACCEL_E_INVALID, "accel_hip: %s takes %d bindings, got %d", kernel,
+                    rec->bindings, nbindings);
+    if (!uniform || uniform_bytes < 16)
+        return fail(ACCEL_E_INVALID, "accel_hip: %s needs its 16-byte uniform block", kernel);
+    std::string name = kernel;
+    if (name == "QuantMatVecInt4" || name == "QuantMatMulInt4") {
+        // GEMMDims std140: M@0, N@4, K@8.  The matvec's M is unused (0).
+        const uint32_t M = name == "QuantMatVecInt4" ? 1u : u32_at(uniform, 0);
+        const uint32_t N = u32_at(uniform, 4), K = u32_at(uniform, 8);
+        const uint64_t weights = (uint64_t)K * N;
+        accel_int4_t w = {static_cast<const uint32_t*>(bindings[1]), (int64_t)lens[1],
+                          static_cast<const uint16_t*>(bindings[2]), (int64_t)lens[2],
+                          static_cast<const uint16_t*>(bindings[3]), (int64_t)lens[3],
+                          (int64_t)weights};
+        if (lens[0] < (uint64_t)M * K || lens[4] < (uint64_t)M * N)
+            return fail(ACCEL_E_INVALID, "accel_hip: %s bindings are shorter than its dims",
+                        kernel);
+        accel_tensor_t a = {const_cast<void*>(bindings[0]), ACCEL_F32, 2, {M, K, 0, 0}};
+        accel_tensor_t o = {const_cast<void*>(bindings[4]), ACCEL_F32, 2, {M, N, 0, 0}};
+        if (name == "QuantMatVecInt4") {
+            a.rank = 1;
+            a.shape[0] = K;
+            o.rank = 1;
+            o.shape[0] = N;
+            return accel_int4_matvec(dev, stream, &a, &w, &o);
+        }
+        return accel_int4_matmul(dev, stream, &a, &w, &o);
+    }
+    if (name == "SegmentOffsets") {
+        const uint32_t rows = u32_at(uniform, 0);
+        if (lens[0] < rows || lens[1] < (uint64_t)rows + 1)
+            return fail(ACCEL_E_INVALID, "accel_hip: SegmentOffsets bindings are too short");
+        accel_tensor_t c = {const_cast<void*>(bindings[0]), ACCEL_U32, 1, {rows, 0, 0, 0}};
+        accel_tensor_t o = {const_cast<void*>(bindings[1]), ACCEL_U32, 1, {rows + 1, 0, 0, 0}};
+        return accel_segment_offsets(dev, stream, &c, &o);
+    }
+    // Grouped records take the offsets directly (the plan's SegmentOffsets
+    // node already ran).  GroupedDims {E@0,K@4,N@8}: tokens from out's length.
+    // GroupedTiledDims {E@0,Tokens@4,K@8,N@12}.
+    const bool tiled = name == "GroupedMatMul";
+    const uint32_t E = u32_at(uniform, 0);
+    uint32_t T, K, N;
+    if (tiled) {
+        T = u32_at(uniform, 4);
+        K = u32_at(uniform, 8);
+        N = u32_at(uniform, 12);
+    } else {
+        K = u32_at(uniform, 4);
+        N = u32_at(uniform, 8);
+        T = N ? (uint32_t)(lens[3] / N) : 0;
+    }
+    if (lens[0] < (uint64_t)T * K || lens[1] < (uint64_t)E * K * N || lens[2] < (uint64_t)E + 1 ||
+        lens[3] < (uint64_t)T * N)
+        return fail(ACCEL_E_INVALID, "accel_hip: %s bindings are shorter than its dims", kernel);
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    int status = begin_submission(d);
+    if (status != ACCEL_OK) return status;
+    hipError_t e = launch_grouped_f32((hipStream_t)stream, static_cast<const float*>(bindings[0]),
+                                      static_cast<const float*>(bindings[1]),
+                                      static_cast<const uint32_t*>(bindings[2]),
+                                      static_cast<float*>(const_cast<void*>(bindings[3])),
+                                      (int)E, (int)T, (int)K, (int)N, !tiled);
+    return classify(d, e, "grouped launch");
+}

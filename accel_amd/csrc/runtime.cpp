@@ -1,0 +1,403 @@
+// The backend seam of the C ABI: adapters, devices, blocks, streams, fences,
+// timers and kernel-record dispatch.  Mirrors what internal/driver asks of a
+// backend (internal/driver/driver.go:149-238, plan.go:31-428) as functions a
+// purego binding can call.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "internal.hpp"
+
+namespace accel {
+
+namespace {
+thread_local std::string g_last_error;
+constexpr int kMaxDevices = 64;
+Device g_devices[kMaxDevices];
+std::mutex g_open_mu;
+}  // namespace
+
+int fail(int code, const char* fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+void clear_error() { g_last_error.clear(); }
+
+Device* device(int dev) {
+    if (dev < 0 || dev >= kMaxDevices) {
+        fail(ACCEL_E_NO_DEVICE, "accel_hip: device %d does not exist", dev);
+        return nullptr;
+    }
+    Device* d = &g_devices[dev];
+    if (!d->open) {
+        fail(ACCEL_E_NO_DEVICE, "accel_hip: device %d is not open", dev);
+        return nullptr;
+    }
+    if (hipSetDevice(dev) != hipSuccess) {
+        fail(ACCEL_E_NO_DEVICE, "accel_hip: hipSetDevice(%d) failed", dev);
+        return nullptr;
+    }
+    return d;
+}
+
+int begin_submission(Device* d) {
+    std::lock_guard<std::mutex> lk(d->mu);
+    if (d->lost.load()) return fail(ACCEL_E_DEVICE_LOST, "accel: device lost");
+    d->submissions++;
+    if (d->lose_at > 0 && d->submissions >= d->lose_at) {
+        d->lost.store(1);
+        return fail(ACCEL_E_DEVICE_LOST, "accel: device lost (injected at submission %lld)",
+                    (long long)d->submissions);
+    }
+    return ACCEL_OK;
+}
+
+int classify(Device* d, hipError_t e, const char* what) {
+    if (e == hipSuccess) return ACCEL_OK;
+    switch (e) {
+        case hipErrorOutOfMemory:
+            return fail(ACCEL_E_OOM, "accel_hip: %s: %s", what, hipGetErrorString(e));
+        case hipErrorIllegalAddress:
+        case hipErrorLaunchFailure:
+        case hipErrorECCNotCorrectable:
+        case hipErrorAssert:
+        case hipErrorLaunchTimeOut:
+            if (d) d->lost.store(1);
+            return fail(ACCEL_E_DEVICE_LOST, "accel: device lost (%s: %s)", what,
+                        hipGetErrorString(e));
+        default:
+            return fail(ACCEL_E_HIP, "accel_hip: %s: %s", what, hipGetErrorString(e));
+    }
+}
+
+void* workspace(Device* d, size_t bytes, int* status) {
+    *status = ACCEL_OK;
+    size_t need = kWorkspaceCounterBytes + bytes;
+    std::lock_guard<std::mutex> lk(d->mu);
+    if (d->ws && d->ws_bytes >= need) return d->ws;
+    // Growing: nothing queued may still use the old allocation.
+    if (d->ws) {
+        (void)hipDeviceSynchronize();
+        (void)hipFree(d->ws);
+        d->ws = nullptr;
+        d->ws_bytes = 0;
+    }
+    size_t sz = need < (size_t(8) << 20) ? (size_t(8) << 20) : need;
+    hipError_t e = hipMalloc(&d->ws, sz);
+    if (e != hipSuccess) {
+        d->ws = nullptr;
+        *status = classify(d, e, "workspace allocation");
+        return nullptr;
+    }
+    e = hipMemset(d->ws, 0, kWorkspaceCounterBytes);
+    if (e != hipSuccess) {
+        *status = classify(d, e, "workspace clear");
+        return nullptr;
+    }
+    d->ws_bytes = sz;
+    return d->ws;
+}
+
+}  // namespace accel
+
+using namespace accel;
+
+#define ACCEL_API extern "C" __attribute__((visibility("default")))
+
+ACCEL_API const char* accel_hip_last_error(void) { return g_last_error.c_str(); }
+
+ACCEL_API int accel_hip_abi_version(void) { return 1; }
+
+ACCEL_API int accel_hip_probe(int* count) {
+    clear_error();
+    if (!count) return fail(ACCEL_E_INVALID, "accel_hip_probe: count is NULL");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e == hipErrorNoDevice || e == hipErrorInvalidDevice) n = 0;
+    else if (e != hipSuccess) {
+        *count = 0;
+        return fail(ACCEL_OK, "accel_hip_probe: %s", hipGetErrorString(e));
+    }
+    *count = n;
+    return ACCEL_OK;
+}
+
+ACCEL_API int accel_hip_info(int dev, accel_hip_info_t* out) {
+    clear_error();
+    if (!out) return fail(ACCEL_E_INVALID, "accel_hip_info: out is NULL");
+    hipDeviceProp_t p;
+    hipError_t e = hipGetDeviceProperties(&p, dev);
+    if (e != hipSuccess)
+        return fail(ACCEL_E_NO_DEVICE, "accel_hip_info(%d): %s", dev, hipGetErrorString(e));
+    memset(out, 0, sizeof *out);
+    snprintf(out->name, sizeof out->name, "%s", p.name);
+    snprintf(out->arch, sizeof out->arch, "%s", p.gcnArchName);
+    out->compute_units = p.multiProcessorCount;
+    out->wavefront = p.warpSize;
+    out->lds_per_block = (int32_t)p.sharedMemPerBlock;
+    out->clock_khz = p.clockRate;
+    out->mem_clock_khz = p.memoryClockRate;
+    out->mem_bus_bits = p.memoryBusWidth;
+    out->hbm_bytes = p.totalGlobalMem;
+    out->l2_bytes = p.l2CacheSize;
+    out->pci_bus = p.pciBusID;
+    return ACCEL_OK;
+}
+
+ACCEL_API int accel_hip_open(int dev) {
+    clear_error();
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || dev < 0 || dev >= n || dev >= kMaxDevices)
+        return fail(ACCEL_E_NO_DEVICE, "accel_hip_open: no HIP device %d", dev);
+    std::lock_guard<std::mutex> lk(g_open_mu);
+    Device* d = &g_devices[dev];
+    if (d->open) return ACCEL_OK;
+    hipError_t e = hipSetDevice(dev);
+    if (e != hipSuccess) return classify(nullptr, e, "hipSetDevice");
+    hipDeviceProp_t p;
+    e = hipGetDeviceProperties(&p, dev);
+    if (e != hipSuccess) return classify(nullptr, e, "hipGetDeviceProperties");
+    std::string arch = p.gcnArchName;
+    if (arch.rfind("gfx950", 0) != 0)
+        return fail(ACCEL_E_UNSUPPORTED,
+                    "accel_hip_open: device %d is %s; this library carries gfx950 code only",
+                    dev, p.gcnArchName);
+    d->ordinal = dev;
+    d->cu_count = p.multiProcessorCount;
+    d->lds_per_block = p.sharedMemPerBlock;
+    d->lost.store(0);
+    d->submissions = 0;
+    d->lose_at = 0;
+    d->open = true;
+    return ACCEL_OK;
+}
+
+ACCEL_API int accel_hip_close(int dev) {
+    clear_error();
+    if (dev < 0 || dev >= kMaxDevices) return ACCEL_OK;
+    std::lock_guard<std::mutex> lk(g_open_mu);
+    Device* d = &g_devices[dev];
+    if (!d->open) return ACCEL_OK;
+    (void)hipSetDevice(dev);
+    if (d->ws) {
+        (void)hipDeviceSynchronize();
+        (void)hipFree(d->ws);
+    }
+    d->ws = nullptr;
+    d->ws_bytes = 0;
+    d->open = false;
+    return ACCEL_OK;
+}
+
+ACCEL_API int accel_hip_lost(int dev) {
+    if (dev < 0 || dev >= kMaxDevices) return 0;
+    return g_devices[dev].lost.load() ? 1 : 0;
+}
+
+ACCEL_API int accel_hip_inject_loss(int dev, int64_t at_submission) {
+    clear_error();
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    std::lock_guard<std::mutex> lk(d->mu);
+    d->submissions = 0;
+    d->lose_at = at_submission;
+    return ACCEL_OK;
+}
+
+ACCEL_API int accel_hip_alloc(int dev, size_t bytes, void** ptr) {
+    clear_error();
+    if (!ptr) return fail(ACCEL_E_INVALID, "accel_hip_alloc: ptr is NULL");
+    *ptr = nullptr;
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    if (d->lost.load()) return fail(ACCEL_E_DEVICE_LOST, "accel: device lost");
+    if (bytes == 0) bytes = 1;
+    return classify(d, hipMalloc(ptr, bytes), "hipMalloc");
+}
+
+ACCEL_API int accel_hip_free(int dev, void* ptr) {
+    clear_error();
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    if (!ptr) return ACCEL_OK;
+    return classify(d, hipFree(ptr), "hipFree");
+}
+
+ACCEL_API int accel_hip_write(int dev, void* dst, size_t offset, const void* src,
+                              size_t bytes) {
+    clear_error();
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    if (d->lost.load()) return fail(ACCEL_E_DEVICE_LOST, "accel: device lost");
+    if (bytes == 0) return ACCEL_OK;
+    if (!dst || !src) return fail(ACCEL_E_INVALID, "accel_hip_write: NULL pointer");
+    return classify(d, hipMemcpy((char*)dst + offset, src, bytes, hipMemcpyHostToDevice),
+                    "hipMemcpy(HtoD)");
+}
+
+ACCEL_API int accel_hip_read(int dev, const void* src, size_t offset, void* dst,
+                             size_t bytes) {
+    clear_error();
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    if (d->lost.load()) return fail(ACCEL_E_DEVICE_LOST, "accel: device lost");
+    if (bytes == 0) return ACCEL_OK;
+    if (!dst || !src) return fail(ACCEL_E_INVALID, "accel_hip_read: NULL pointer");
+    return classify(d,
+                    hipMemcpy(dst, (const char*)src + offset, bytes, hipMemcpyDeviceToHost),
+                    "hipMemcpy(DtoH)");
+}
+
+ACCEL_API int accel_hip_copy(int dev, void* stream, void* dst, const void* src,
+                             size_t bytes) {
+    clear_error();
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    int st = begin_submission(d);
+    if (st != ACCEL_OK) return st;
+    if (bytes == 0) return ACCEL_OK;
+    return classify(d, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice,
+                                      (hipStream_t)stream),
+                    "hipMemcpyAsync(DtoD)");
+}
+
+ACCEL_API int accel_hip_stream_create(int dev, void** stream) {
+    clear_error();
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    if (!stream) return fail(ACCEL_E_INVALID, "accel_hip_stream_create: NULL out");
+    hipStream_t s = nullptr;
+    // Default priority only: every stream of this library is created the same way.
+    int rc = classify(d, hipStreamCreateWithFlags(&s, hipStreamNonBlocking),
+                      "hipStreamCreate");
+    *stream = s;
+    return rc;
+}
+
+ACCEL_API int accel_hip_stream_destroy(int dev, void* stream) {
+    clear_error();
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    if (!stream) return ACCEL_OK;
+    return classify(d, hipStreamDestroy((hipStream_t)stream), "hipStreamDestroy");
+}
+
+ACCEL_API int accel_hip_stream_sync(int dev, void* stream) {
+    clear_error();
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    if (d->lost.load()) return fail(ACCEL_E_DEVICE_LOST, "accel: device lost");
+    return classify(d, hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
+}
+
+ACCEL_API int accel_hip_event_create(int dev, void** event) {
+    clear_error();
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    if (!event) return fail(ACCEL_E_INVALID, "accel_hip_event_create: NULL out");
+    hipEvent_t ev = nullptr;
+    int rc = classify(d, hipEventCreate(&ev), "hipEventCreate");
+    *event = ev;
+    return rc;
+}
+
+ACCEL_API int accel_hip_event_destroy(int dev, void* event) {
+    clear_error();
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    if (!event) return ACCEL_OK;
+    return classify(d, hipEventDestroy((hipEvent_t)event), "hipEventDestroy");
+}
+
+ACCEL_API int accel_hip_event_record(int dev, void* event, void* stream) {
+    clear_error();
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    if (d->lost.load()) return fail(ACCEL_E_DEVICE_LOST, "accel: device lost");
+    return classify(d, hipEventRecord((hipEvent_t)event, (hipStream_t)stream),
+                    "hipEventRecord");
+}
+
+ACCEL_API int accel_hip_event_query(int dev, void* event) {
+    clear_error();
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    if (d->lost.load()) return 1;  // a lost device is done (plan.go:380-382)
+    hipError_t e = hipEventQuery((hipEvent_t)event);
+    if (e == hipSuccess) return 1;
+    if (e == hipErrorNotReady) return 0;
+    return classify(d, e, "hipEventQuery");
+}
+
+ACCEL_API int accel_hip_event_sync(int dev, void* event) {
+    clear_error();
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    if (d->lost.load()) return fail(ACCEL_E_DEVICE_LOST, "accel: device lost");
+    return classify(d, hipEventSynchronize((hipEvent_t)event), "hipEventSynchronize");
+}
+
+ACCEL_API int accel_hip_event_elapsed(int dev, void* start, void* end, float* ms) {
+    clear_error();
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    if (!ms) return fail(ACCEL_E_INVALID, "accel_hip_event_elapsed: NULL out");
+    return classify(d, hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)end),
+                    "hipEventElapsedTime");
+}
+
+ACCEL_API int accel_hip_capture_begin(int dev, void* stream) {
+    clear_error();
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    if (d->lost.load()) return fail(ACCEL_E_DEVICE_LOST, "accel: device lost");
+    if (!stream)
+        return fail(ACCEL_E_INVALID, "accel_hip_capture_begin: the null stream cannot capture");
+    return classify(d,
+                    hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal),
+                    "hipStreamBeginCapture");
+}
+
+ACCEL_API int accel_hip_capture_end(int dev, void* stream, void** exec) {
+    clear_error();
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    if (!exec) return fail(ACCEL_E_INVALID, "accel_hip_capture_end: NULL out");
+    *exec = nullptr;
+    hipGraph_t g = nullptr;
+    int rc = classify(d, hipStreamEndCapture((hipStream_t)stream, &g), "hipStreamEndCapture");
+    if (rc != ACCEL_OK) return rc;
+    hipGraphExec_t ge = nullptr;
+    rc = classify(d, hipGraphInstantiate(&ge, g, nullptr, nullptr, 0), "hipGraphInstantiate");
+    (void)hipGraphDestroy(g);
+    if (rc != ACCEL_OK) return rc;
+    *exec = ge;
+    return ACCEL_OK;
+}
+
+ACCEL_API int accel_hip_exec_launch(int dev, void* exec, void* stream) {
+    clear_error();
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    if (!exec) return fail(ACCEL_E_INVALID, "accel_hip_exec_launch: NULL executable");
+    int st = begin_submission(d);
+    if (st != ACCEL_OK) return st;
+    return classify(d, hipGraphLaunch((hipGraphExec_t)exec, (hipStream_t)stream),
+                    "hipGraphLaunch");
+}
+
+ACCEL_API int accel_hip_exec_destroy(int dev, void* exec) {
+    clear_error();
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    if (!exec) return ACCEL_OK;
+    return classify(d, hipGraphExecDestroy((hipGraphExec_t)exec), "hipGraphExecDestroy");
+}

@@ -1,0 +1,258 @@
+/*
+ * accel_hip.h -- C ABI of libaccel_hip.so, the MI355X (gfx950) backend for
+ * golang-design/accel's int4 weight-only linear path.
+ *
+ * Two layers are exported.
+ *
+ *  1. The backend seam.  What the reference's internal/driver interfaces ask
+ *     of a backend (Adapter, Device, Block, Executable, Fence, Timer,
+ *     KernelSupport), as plain functions over opaque handles, so a Go
+ *     internal/hip package can bind them with purego the way
+ *     internal/metal binds Metal.  A dispatch names a reference kernel record
+ *     (e.g. "QuantMatVecInt4") and passes its bindings in record order plus
+ *     the std140 uniform bytes; the library picks the gfx950 kernel.
+ *
+ *  2. The operator layer.  The tensor-package entry points of the path
+ *     (tensor.Int4MatVec, Int4MatMul, GroupedMatVec, GroupedMatMul, the
+ *     SegmentOffsets node and quant.Int4Quantize), with the reference's
+ *     validation and refusal messages, over device pointers.
+ *
+ * Conventions.  Every function returns an int status: ACCEL_OK (0) or a
+ * negative ACCEL_E_* code, with a message for the calling thread in
+ * accel_hip_last_error().  No C++ exception crosses this boundary.  Device
+ * pointers are those returned by accel_hip_alloc (or any hipMalloc'd
+ * memory of the same device).  A stream argument may be NULL for the
+ * device's null stream.  Dtype codes: ACCEL_F32, ACCEL_F16, ACCEL_BF16,
+ * ACCEL_U32.  Half-precision values cross the ABI as uint16_t bit patterns,
+ * as the reference moves them ("The host slice for an f16 buffer is
+ * []uint16", internal/kernels/differential_darwin_test.go:242-244).
+ *
+ * Workspace.  Kernels that reduce across workgroups (the decode product's
+ * K split) and the grouped products (segment offsets, tile lists) use a
+ * per-device workspace owned by the library.  Two operator calls that run
+ * concurrently on different streams of one device race on it; serialize
+ * them or use one stream per device.
+ */
+#ifndef ACCEL_HIP_H
+#define ACCEL_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes -------------------------------------------------------- */
+#define ACCEL_OK 0
+#define ACCEL_E_INVALID (-1)     /* refused by validation (tensor layer b.fail) */
+#define ACCEL_E_NO_DEVICE (-2)   /* no such device, or device not open */
+#define ACCEL_E_DEVICE_LOST (-3) /* sticky: driver.ErrDeviceLost */
+#define ACCEL_E_OOM (-4)         /* allocation failed; not loss */
+#define ACCEL_E_UNSUPPORTED (-5) /* kernel record with no gfx950 artifact */
+#define ACCEL_E_HIP (-6)         /* other HIP runtime error */
+
+/* ---- dtypes (the reference's accel.DType subset on this path) ----------- */
+#define ACCEL_F32 1
+#define ACCEL_F16 2
+#define ACCEL_BF16 3
+#define ACCEL_U32 4
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* accel_hip_last_error(void);
+
+/* ABI version: bumped on any incompatible change of this header. */
+int accel_hip_abi_version(void);
+
+/* ===================================================================== */
+/* 1. Backend seam                                                       */
+/* ===================================================================== */
+
+/* Adapter.Info (internal/driver/driver.go:149-160) plus the figures the
+ * roofline needs. */
+typedef struct accel_hip_info {
+    char name[128];          /* marketing name */
+    char arch[64];           /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+    int32_t compute_units;
+    int32_t wavefront;       /* 64 on CDNA */
+    int32_t lds_per_block;   /* bytes of LDS a workgroup may use */
+    int32_t clock_khz;       /* peak shader clock */
+    int32_t mem_clock_khz;
+    int32_t mem_bus_bits;
+    uint64_t hbm_bytes;
+    int32_t l2_bytes;
+    int32_t pci_bus;
+} accel_hip_info_t;
+
+/* Number of HIP devices; 0 (and ACCEL_OK) where there is no GPU.  Replaces
+ * platformAdapters' enumeration (adapters_other.go:18, device.go:48-52). */
+int accel_hip_probe(int* count);
+int accel_hip_info(int dev, accel_hip_info_t* out);
+
+/* Adapter.Open / Device.Close (driver.go:149-190).  open sets the device
+ * current for the calling thread and creates the per-device state;
+ * close frees the workspace.  Both are idempotent. */
+int accel_hip_open(int dev);
+int accel_hip_close(int dev);
+
+/* Device.Lost (driver.go:178-186): 1 once the device is lost, for good
+ * (internal/driver/plan.go:385-391), else 0. */
+int accel_hip_lost(int dev);
+
+/* Fault injection, the analogue of CPUOptions.LoseAtSubmission
+ * (accel.go:306-314; internal/cpu/cpu.go:179-191): the device is marked lost
+ * when the n-th accepted submission (counting from 1, from now) begins, and
+ * that submission launches nothing.  0 disables. */
+int accel_hip_inject_loss(int dev, int64_t at_submission);
+
+/* Device.Alloc / Block.Free / Block.Write / Block.Read
+ * (driver.go:163-238).  write and read are synchronous with the device. */
+int accel_hip_alloc(int dev, size_t bytes, void** ptr);
+int accel_hip_free(int dev, void* ptr);
+int accel_hip_write(int dev, void* dst, size_t offset, const void* src, size_t bytes);
+int accel_hip_read(int dev, const void* src, size_t offset, void* dst, size_t bytes);
+/* Plan copy node (internal/driver/plan.go:112-140), stream-ordered. */
+int accel_hip_copy(int dev, void* stream, void* dst, const void* src, size_t bytes);
+
+/* Streams: one per in-flight submission (Executable.Submit must not wait,
+ * plan.go:360-371). */
+int accel_hip_stream_create(int dev, void** stream);
+int accel_hip_stream_destroy(int dev, void* stream);
+int accel_hip_stream_sync(int dev, void* stream);
+
+/* Fence (plan.go:374-383) and Timer (plan.go:349-353) as HIP events. */
+int accel_hip_event_create(int dev, void** event);
+int accel_hip_event_destroy(int dev, void* event);
+int accel_hip_event_record(int dev, void* event, void* stream);
+/* 1 = done (a lost device is done), 0 = pending, <0 = error. */
+int accel_hip_event_query(int dev, void* event);
+int accel_hip_event_sync(int dev, void* event);
+int accel_hip_event_elapsed(int dev, void* start, void* end, float* ms);
+
+/* Executable (plan.go:360-371) as a HIP graph.  Operator calls and
+ * dispatches issued on `stream` between capture_begin and capture_end are
+ * recorded, not run; exec_launch replays them as one submission (the
+ * reference's resubmittable compiled plan, GraphCompiler.Compile,
+ * plan.go:398-400).  Issue every captured call once eagerly before capturing,
+ * so the workspace it needs is already allocated. */
+int accel_hip_capture_begin(int dev, void* stream);
+int accel_hip_capture_end(int dev, void* stream, void** exec);
+int accel_hip_exec_launch(int dev, void* exec, void* stream);
+int accel_hip_exec_destroy(int dev, void* exec);
+
+/* KernelSupport.SupportsKernel (plan.go:424-428): 1 if the named reference
+ * kernel record has a gfx950 implementation here, else 0.  Records without
+ * one are refused; nothing falls back to another implementation
+ * (the rule at internal/metal/exec_darwin.go:140-149). */
+int accel_hip_supports_kernel(const char* kernel);
+
+/* One PlanNode{Op: OpDispatch} (plan.go:112-201): the kernel record's name,
+ * its bindings as device pointers in record order with their element counts
+ * (the `_lens` words, internal/metal/exec_darwin.go:494-528), and its std140
+ * uniform block.  count is Dispatch.Count, advisory: the library chooses
+ * its own grid.  Supported records and their binding orders:
+ *   QuantMatVecInt4  a f32, bq u32, bs f16, bz f16, out f32; GEMMDims
+ *   QuantMatMulInt4  a f32, bq u32, bs f16, bz f16, out f32; GEMMDims
+ *   GroupedMatVec    x f32, w f32, offsets u32, out f32;      GroupedDims
+ *   GroupedMatMul    x f32, w f32, offsets u32, out f32;      GroupedTiledDims
+ *   SegmentOffsets   counts u32, offsets u32;                 SegmentDims
+ * (internal/kernels/accel_kernels.go:6799-6808,7052-7061; GEMMDims is
+ * {M@0,N@4,K@8}, GroupedDims {Experts@0,K@4,N@8}, GroupedTiledDims
+ * {Experts@0,Tokens@4,K@8,N@12}, SegmentDims {Rows@0}, :173-231). */
+int accel_hip_dispatch(int dev, void* stream, const char* kernel,
+                       const void* const* bindings, const uint64_t* lens,
+                       int32_t nbindings, const void* uniform, size_t uniform_bytes,
+                       const uint32_t count[3]);
+
+/* ===================================================================== */
+/* 2. Operator layer                                                     */
+/* ===================================================================== */
+
+/* A device tensor: data pointer, dtype and row-major shape. */
+typedef struct accel_tensor {
+    void* data;
+    int32_t dtype;
+    int32_t rank;
+    int64_t shape[4];
+} accel_tensor_t;
+
+/* tensor.Int4 (tensor/int4.go:25-38): packed u32 codes (eight weights per
+ * word, low nibble first), f16 scales and zeros (one each per 128 weights of
+ * the flattened [K,N] matrix), and the weight count.  Element counts, not
+ * bytes. */
+typedef struct accel_int4 {
+    const uint32_t* codes;
+    int64_t codes_len;
+    const uint16_t* scales;
+    int64_t scales_len;
+    const uint16_t* zeros;
+    int64_t zeros_len;
+    int64_t weights;
+} accel_int4_t;
+
+/* tensor.Int4MatVec (tensor/int4.go:99-147): out[n] = sum_k a[k] * w(k,n),
+ * w = s==0 ? z : (code-z)*s.  a is f32 [K]; out is f32 [N], N = weights/K. */
+int accel_int4_matvec(int dev, void* stream, const accel_tensor_t* a,
+                      const accel_int4_t* w, accel_tensor_t* out);
+
+/* tensor.Int4MatMul (tensor/int4.go:168-212): a [M,K] -> out [M,N].  The
+ * reference takes f32 a and gives f32 out; this also accepts bf16 a with bf16
+ * out (fp32 accumulation), the additive dtype selection QuantMatMul makes by
+ * activation dtype (tensor/quantized.go:87-113).  M <= 16 runs the decode
+ * kernels; larger M the MFMA kernels. */
+int accel_int4_matmul(int dev, void* stream, const accel_tensor_t* a,
+                      const accel_int4_t* w, accel_tensor_t* out);
+
+/* The SegmentOffsets node (tensor/segment.go:31-50;
+ * internal/kernels/segment.go:40-50): offsets[r] = sum of counts[<r],
+ * offsets[rows] = total.  counts u32 [rows], offsets u32 [rows+1]. */
+int accel_segment_offsets(int dev, void* stream, const accel_tensor_t* counts,
+                          accel_tensor_t* offsets);
+
+/* tensor.GroupedMatVec (tensor/grouped.go:48-115): x f32 [T,K], w f32
+ * [E,K,N], counts u32 [E] -> out f32 [T,N]; token t uses expert
+ * e(t) = #{r : off[r+1] <= t}; a token past the last segment is written 0. */
+int accel_grouped_matvec(int dev, void* stream, const accel_tensor_t* x,
+                         const accel_tensor_t* w, const accel_tensor_t* counts,
+                         accel_tensor_t* out);
+
+/* tensor.GroupedMatMul (tensor/grouped.go:138-212): same operands; rows
+ * [off[e], min(off[e+1], T)) use expert e and rows outside every segment are
+ * left as they were. */
+int accel_grouped_matmul(int dev, void* stream, const accel_tensor_t* x,
+                         const accel_tensor_t* w, const accel_tensor_t* counts,
+                         accel_tensor_t* out);
+
+/* The int4 composition of the two grouped operators: the weight is
+ * `experts` stacked [K,N] int4 matrices quantized as one flat [E,K,N] array
+ * (groups never straddle experts when K*N % 128 == 0, which is required).
+ * x is f32 or bf16 [T,K]; out matches x's dtype, [T,N].  The matvec form
+ * writes 0 past the last segment (grouped.go:66-77); the matmul form leaves
+ * such rows unwritten (groupedtiled.go:184-231). */
+int accel_int4_grouped_matvec(int dev, void* stream, const accel_tensor_t* x,
+                              const accel_int4_t* w, int64_t experts,
+                              const accel_tensor_t* counts, accel_tensor_t* out);
+int accel_int4_grouped_matmul(int dev, void* stream, const accel_tensor_t* x,
+                              const accel_int4_t* w, int64_t experts,
+                              const accel_tensor_t* counts, accel_tensor_t* out);
+
+/* quant.Int4Quantize (quant/int4.go:71-138) on host memory: packed holds
+ * ceil(n/8) words, scales and zeros ceil(n/128) f16 each. */
+int accel_int4_quantize(const float* w, int64_t n, uint32_t* packed,
+                        uint16_t* scales, uint16_t* zeros);
+
+/* quant.Int4Dequantize (quant/int4.go:160-175) on host memory. */
+int accel_int4_dequantize(const uint32_t* packed, const uint16_t* scales,
+                          const uint16_t* zeros, int64_t n, float* out);
+
+/* quant.Int4Quantize on the device, bit-identical to the host form: the
+ * same f32 range arithmetic, f16 narrowing and f64 divide-and-round.
+ * Pointers are device memory. */
+int accel_int4_quantize_device(int dev, void* stream, const float* w, int64_t n,
+                               uint32_t* packed, uint16_t* scales, uint16_t* zeros);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ACCEL_HIP_H */

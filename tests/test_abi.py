@@ -1,0 +1,213 @@
+"""The C ABI on the CPU: the library loads, exports every symbol the header
+declares, its host packer is bit-exact with the oracle, and the operator
+layer refuses what the reference refuses (tensor/int4_test.go:121-273,
+357-420; tensor/grouped_test.go:92-202,295-330) -- validation runs before
+any device is touched, so none of this needs a GPU.
+"""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import accel_amd
+import oracle
+from accel_amd import F16, F32, U32, BF16
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "accel_hip.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(accel_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    syms = declared_symbols()
+    assert len(syms) >= 30
+    lib = ctypes.CDLL(accel_amd.LIB_PATH)
+    for s in syms:
+        assert hasattr(lib, s), s
+    assert set(syms) == set(accel_amd.SIGNATURES), \
+        set(syms) ^ set(accel_amd.SIGNATURES)
+
+
+def test_abi_version():
+    assert accel_amd.lib().accel_hip_abi_version() == 1
+
+
+def test_probe_reports_a_count_without_failing():
+    assert accel_amd.device_count() >= 0
+
+
+@pytest.mark.parametrize("n", [1, 5, 128, 129, 1000, 4096 * 2 + 77])
+@pytest.mark.parametrize("kind", ["normal", "far", "denorm", "huge", "nan_inf", "zeros"])
+def test_host_packer_is_bit_exact_with_the_oracle(n, kind):
+    rng = np.random.default_rng(n * 7 + len(kind))
+    if kind == "normal":
+        w = rng.standard_normal(n) * 0.02
+    elif kind == "far":
+        w = 1000 + rng.random(n)
+    elif kind == "denorm":
+        w = rng.standard_normal(n) * 1e-40
+    elif kind == "huge":
+        w = rng.standard_normal(n) * 3e38
+    elif kind == "nan_inf":
+        w = np.where(rng.random(n) < 0.05, np.nan,
+                     np.where(rng.random(n) < 0.05, -np.inf, rng.standard_normal(n)))
+    else:
+        w = np.where(rng.random(n) < 0.5, -0.0, 0.0)
+    w = np.asarray(w, np.float32)
+    got = accel_amd.int4_quantize(w)
+    want = oracle.int4_quantize(w)
+    for g, x, what in zip(got, want, ("codes", "scales", "zeros")):
+        assert np.array_equal(g, x), what
+    back = accel_amd.int4_dequantize(*got, n)
+    ref = oracle.int4_dequantize(*want, n)
+    assert np.array_equal(back.view(np.uint32), ref.view(np.uint32))
+
+
+def test_host_packer_at_a_baseline_shape():
+    rng = np.random.Generator(np.random.PCG64(0))
+    w = (rng.standard_normal((1024, 4096)) * 0.02).astype(np.float32)
+    got = accel_amd.int4_quantize(w)
+    want = oracle.int4_quantize(w)
+    for g, x in zip(got, want):
+        assert np.array_equal(g, x)
+
+
+def test_kernel_support_names_the_records():
+    for k in ["QuantMatVecInt4", "QuantMatMulInt4", "GroupedMatVec", "GroupedMatMul",
+              "SegmentOffsets"]:
+        assert accel_amd.supports_kernel(k)
+    assert not accel_amd.supports_kernel("MatMulTiledF32")
+    assert not accel_amd.supports_kernel("")
+
+
+# ---- refusals ---------------------------------------------------------------
+# Fake device pointers: validation never dereferences them.
+FAKE = 0x1000
+
+
+def t(shape, dtype, data=FAKE):
+    x = accel_amd.Tensor()
+    x.data = data
+    x.dtype = dtype
+    x.rank = len(shape)
+    for i, s in enumerate(shape):
+        x.shape[i] = s
+    return x
+
+
+def w4(weights, codes=None, scales=None, zeros=None, c=FAKE, s=FAKE, z=FAKE):
+    d = accel_amd.Int4Desc()
+    d.codes, d.scales, d.zeros = c, s, z
+    d.codes_len = (weights + 7) // 8 if codes is None else codes
+    d.scales_len = (weights + 127) // 128 if scales is None else scales
+    d.zeros_len = (weights + 127) // 128 if zeros is None else zeros
+    d.weights = weights
+    return d
+
+
+def call(fn, *args):
+    lib = accel_amd.lib()
+    rc = getattr(lib, fn)(0, None, *[ctypes.byref(a) if not isinstance(a, int) else a
+                                     for a in args])
+    return rc, accel_amd.last_error()
+
+
+K, N = 128, 2
+
+
+@pytest.mark.parametrize("mut,want", [
+    (dict(z=None), "the zero point is what makes four bits usable"),
+    (dict(s=None), "needs a code plane, a scale plane and a zero plane"),
+    (dict(codes=31), "which is 32 words, and the code plane holds 31"),
+    (dict(scales=3), "which is 2 groups of 128, and 3 scales"),
+    (dict(zeros=1), "which is 2 groups of 128, and 1 zeros"),
+])
+def test_a_mismatched_triple_is_refused(mut, want):   # tensor/int4_test.go:121-172
+    kw = {k: v for k, v in mut.items() if k in ("codes", "scales", "zeros")}
+    ptrs = {k: v for k, v in mut.items() if k in ("c", "s", "z")}
+    w = w4(K * N, **kw, **ptrs)
+    rc, msg = call("accel_int4_matvec", t([K], F32), w, t([N], F32))
+    assert rc == accel_amd.E_INVALID and want in msg and "Int4MatVec" in msg, msg
+
+
+def test_zero_weights_are_refused():
+    rc, msg = call("accel_int4_matvec", t([K], F32), w4(0, codes=0, scales=0, zeros=0),
+                   t([N], F32))
+    assert rc == accel_amd.E_INVALID and "declares 0 weights" in msg
+
+
+@pytest.mark.parametrize("a,want", [
+    (t([K], BF16), "activations are bf16 and this kernel reads f32"),
+    (t([2, K], F32), "a matvec takes a vector"),
+    (t([100], F32), "activations are 100 long and the matrix holds 256 weights"),
+])
+def test_int4_matvec_refuses_wrong_activations(a, want):   # tensor/int4_test.go:224-273
+    rc, msg = call("accel_int4_matvec", a, w4(K * N), t([N], F32))
+    assert rc == accel_amd.E_INVALID and want in msg, msg
+
+
+def test_int4_matmul_refuses_a_vector_and_names_matvec():   # :357-385
+    rc, msg = call("accel_int4_matmul", t([64], F32), w4(64 * 4), t([1, 4], F32))
+    assert rc == accel_amd.E_INVALID and "Int4MatVec" in msg
+
+
+@pytest.mark.parametrize("a,out,want", [
+    (t([2, K], U32), t([2, N], F32), "activations are u32"),
+    (t([2, 100], F32), t([2, N], F32), "100 wide and the matrix holds 256"),
+    (t([2, K], F32), t([2, N + 1], F32), "the output is [2 3] and the product is [2 2]"),
+    (t([2, K], F32), t([2, N], BF16), "the output is bf16 and this product writes f32"),
+])
+def test_int4_matmul_refusals(a, out, want):   # :387-420
+    rc, msg = call("accel_int4_matmul", a, w4(K * N), out)
+    assert rc == accel_amd.E_INVALID and want in msg, msg
+
+
+def test_grouped_refusals():   # tensor/grouped_test.go:92-202,295-330
+    x = t([6, 32], F32)
+    w = t([3, 32, 4], F32)
+    c = t([3], U32)
+    o = t([6, 4], F32)
+    rc, msg = call("accel_grouped_matvec", x, w, t([2], U32), o)
+    assert rc == accel_amd.E_INVALID and "counts holds 2 entries and w has 3 experts" in msg
+    rc, msg = call("accel_grouped_matvec", x, t([3, 31, 4], F32), c, o)
+    assert rc == accel_amd.E_INVALID and "every expert contracts against the same width" in msg
+    rc, msg = call("accel_grouped_matmul", t([6, 32], BF16), w, c, o)
+    assert rc == accel_amd.E_INVALID and "x is bf16 and this kernel reads f32" in msg
+    rc, msg = call("accel_grouped_matmul", x, t([32, 4], F32), c, o)
+    assert rc == accel_amd.E_INVALID and "one matrix per expert" in msg
+    rc, msg = call("accel_grouped_matmul", x, t([0, 32, 4], F32), t([0], U32), o)
+    assert rc == accel_amd.E_INVALID and "w declares no experts" in msg
+    rc, msg = call("accel_grouped_matvec", x, w, t([3], U32, data=0), o)
+    assert rc == accel_amd.E_INVALID and "counts is nil" in msg
+
+
+def test_int4_grouped_refuses_straddling_groups():
+    lib = accel_amd.lib()
+    x = t([4, 8], F32)
+    w = w4(3 * 8 * 4)  # 96 weights per... K*N = 32, not a multiple of 128
+    rc = lib.accel_int4_grouped_matmul(0, None, ctypes.byref(x), ctypes.byref(w), 3,
+                                       ctypes.byref(t([3], U32)), ctypes.byref(t([4, 4], F32)))
+    assert rc == accel_amd.E_INVALID and "straddles" in accel_amd.last_error()
+
+
+def test_dispatch_refuses_an_unknown_record():
+    lib = accel_amd.lib()
+    u = (ctypes.c_char * 16)()
+    rc = lib.accel_hip_dispatch(0, None, b"MatMulTiledF32", None, None, 0,
+                                ctypes.cast(u, ctypes.c_void_p), 16, None)
+    assert rc == accel_amd.E_UNSUPPORTED
+    assert "no gfx950 implementation" in accel_amd.last_error()
+
+
+def test_a_closed_device_is_refused():
+    lib = accel_amd.lib()
+    p = ctypes.c_void_p()
+    assert lib.accel_hip_alloc(63, 16, ctypes.byref(p)) == accel_amd.E_NO_DEVICE
+    assert lib.accel_hip_lost(63) == 0

@@ -1,0 +1,198 @@
+"""GPU parity of the grouped (ragged, mixture-of-experts) products and the
+segment offsets, through the C ABI.  Cases follow
+internal/kernels/grouped_test.go and tensor/grouped_test.go; the f32 forms
+carry the reference's 1e-4 element bound, the int4 forms the path's rel-L2
+tolerances.
+"""
+import struct
+
+import numpy as np
+import pytest
+
+import accel_amd
+import oracle
+from accel_amd import BF16, F32, U32, workloads
+from conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def grouped_fixture(E, K, N, counts):
+    off = oracle.segment_offsets(np.array(counts, np.uint32))
+    total = int(off[E])
+    x = np.sin(np.arange(total * K) * 0.23).astype(np.float32)
+    base = np.cos(np.arange(K * N) * 0.17).astype(np.float32)
+    w = np.concatenate([base * np.float32(e + 1) for e in range(E)]).astype(np.float32)
+    return x, w, off
+
+
+def run_grouped(dev, form, x, w, counts, E, T, K, N, init=None):
+    xb = dev.upload(np.ascontiguousarray(x, np.float32).reshape(T, K))
+    wb = dev.upload(np.ascontiguousarray(w, np.float32).reshape(E, K, N))
+    cb = dev.upload(np.asarray(counts, np.uint32), U32)
+    ob = dev.alloc((T, N), F32)
+    ob.write(np.full((T, N), 7.0, np.float32) if init is None else init)
+    getattr(dev, form)(xb, wb, cb, ob)
+    got = ob.numpy()
+    for b in (xb, wb, cb, ob):
+        b.free()
+    return got
+
+
+def test_segment_offsets_on_device(dev):
+    for counts in ([3, 0, 5, 2, 0, 7], list(range(200)), [0xFFFFFFFF, 2], [9]):
+        c = np.array(counts, np.uint32)
+        cb = dev.upload(c, U32)
+        ob = dev.alloc((c.size + 1,), U32)
+        dev.SegmentOffsets(cb, ob)
+        assert np.array_equal(ob.numpy(), oracle.segment_offsets(c))
+        cb.free(); ob.free()
+
+
+@pytest.mark.parametrize("form", ["GroupedMatVec", "GroupedMatMul"])
+@pytest.mark.parametrize("E,K,N,counts", [(3, 64, 5, [2, 1, 3]), (4, 64, 3, [2, 0, 2, 0]),
+                                          (2, 64, 2, [1, 1]), (4, 40, 20, [11, 0, 3, 20])])
+def test_grouped_f32_matches_each_expert_alone(dev, form, E, K, N, counts):
+    x, w, off = grouped_fixture(E, K, N, counts)
+    T = int(off[E])
+    got = run_grouped(dev, form, x, w, counts, E, T, K, N)
+    ref = oracle.grouped_matvec if form == "GroupedMatVec" else oracle.grouped_matmul
+    want = ref(x, w, off, E, T, K, N)
+    assert np.all(np.abs(got - want) <= 1e-4)
+
+
+def test_grouped_matvec_writes_zero_past_the_last_segment(dev):
+    E, K, N = 3, 64, 4
+    x, w, _ = grouped_fixture(E, K, N, [2, 1, 2])
+    counts = [2, 0, 2]          # offsets 0,2,2,4; row 4 is padding
+    T = 5
+    xs = np.concatenate([x, np.zeros(K, np.float32)])[:T * K]
+    got = run_grouped(dev, "GroupedMatVec", xs, w, counts, E, T, K, N)
+    want = oracle.grouped_matvec(xs, w, oracle.segment_offsets(np.array(counts, np.uint32)),
+                                 E, T, K, N)
+    assert np.all(got[4] == 0)
+    assert np.all(np.abs(got - want) <= 1e-4)
+
+
+def test_grouped_matmul_clamps_and_leaves_other_rows(dev):
+    E, K, N = 2, 40, 20
+    x, w, _ = grouped_fixture(E, K, N, [4, 4])
+    T = 8
+    counts = [4, 12]            # offsets 0,4,16 clamp to the 8 rows
+    got = run_grouped(dev, "GroupedMatMul", x, w, counts, E, T, K, N)
+    want = oracle.grouped_matmul(x, w, oracle.segment_offsets(np.array(counts, np.uint32)),
+                                 E, T, K, N)
+    assert np.all(np.abs(got - want) <= 1e-4)
+    # and rows no segment covers keep their contents
+    counts = [2, 2]
+    got = run_grouped(dev, "GroupedMatMul", x, w, counts, E, T, K, N)
+    assert np.all(got[4:] == 7.0)
+
+
+def test_dispatch_of_the_grouped_records(dev):
+    E, K, N = 3, 32, 4
+    counts = [2, 0, 4]
+    x, w, off = grouped_fixture(E, K, N, counts)
+    T = int(off[E])
+    bufs = [dev.upload(x), dev.upload(w), dev.upload(off, U32), dev.alloc((T, N), F32)]
+    dev.dispatch("GroupedMatVec", bufs, [T * K, E * K * N, E + 1, T * N],
+                 struct.pack("<IIII", E, K, N, 0))
+    assert np.all(np.abs(bufs[3].numpy() - oracle.grouped_matvec(x, w, off, E, T, K, N))
+                  <= 1e-4)
+    dev.dispatch("GroupedMatMul", bufs, [T * K, E * K * N, E + 1, T * N],
+                 struct.pack("<IIII", E, T, K, N))
+    assert np.all(np.abs(bufs[3].numpy() - oracle.grouped_matmul(x, w, off, E, T, K, N))
+                  <= 1e-4)
+    cb = dev.upload(np.array(counts, np.uint32), U32)
+    ob = dev.alloc((E + 1,), U32)
+    dev.dispatch("SegmentOffsets", [cb, ob], [E, E + 1], struct.pack("<IIII", E, 0, 0, 0))
+    assert np.array_equal(ob.numpy(), off)
+    for b in bufs + [cb, ob]:
+        b.free()
+
+
+# ---- int4 grouped -------------------------------------------------------------
+
+def int4_case(E, K, N, counts, pad, seed, bf16):
+    rng = np.random.default_rng(seed)
+    off = oracle.segment_offsets(np.array(counts, np.uint32))
+    T = int(off[E]) + pad
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    if bf16:
+        x = workloads.bf16_to_f32(workloads.bf16_bits(x))
+    w = (rng.standard_normal(E * K * N) * 0.02).astype(np.float32)
+    p, s, z = oracle.int4_quantize(w)
+    return x, p, s, z, off, T
+
+
+def run_int4_grouped(dev, form, x, p, s, z, counts, E, T, K, N, bf16):
+    w = dev.upload_int4(p, s, z, E * K * N)
+    if bf16:
+        xb = dev.upload(workloads.bf16_bits(x), BF16)
+        ob = dev.alloc((T, N), BF16)
+        ob.write(workloads.bf16_bits(np.full((T, N), 7.0, np.float32)))
+    else:
+        xb = dev.upload(x)
+        ob = dev.alloc((T, N), F32)
+        ob.write(np.full((T, N), 7.0, np.float32))
+    cb = dev.upload(np.asarray(counts, np.uint32), U32)
+    getattr(dev, form)(xb, w, E, cb, ob)
+    got = ob.numpy()
+    if bf16:
+        got = workloads.bf16_to_f32(got)
+    for b in (xb, ob, cb):
+        b.free()
+    w.free()
+    return got
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("form", ["Int4GroupedMatVec", "Int4GroupedMatMul"])
+@pytest.mark.parametrize("E,K,N,counts,pad", [(3, 128, 128, [5, 0, 9], 2),
+                                              (8, 256, 384, [1, 130, 0, 7, 64, 0, 3, 260], 3),
+                                              (2, 64, 256, [0, 0], 4)])
+def test_int4_grouped_matches_the_oracle(dev, bf16, form, E, K, N, counts, pad):
+    x, p, s, z, off, T = int4_case(E, K, N, counts, pad, seed=E + K, bf16=bf16)
+    got = run_int4_grouped(dev, form, x, p, s, z, counts, E, T, K, N, bf16)
+    init = np.full(T * N, 7.0, np.float32)
+    if form == "Int4GroupedMatVec":
+        want = oracle.int4_grouped_matvec(x, p, s, z, off, E, T, K, N, threads=8, out=init)
+    else:
+        want = oracle.int4_grouped_matmul(x, p, s, z, off, E, T, K, N, threads=8, out=init)
+    if bf16:
+        want = oracle.round_bf16(want)
+    tol = 2e-2 if bf16 else 1e-5
+    assert rel_l2(got, want) <= tol
+    covered = int(off[E])
+    if form == "Int4GroupedMatVec":
+        assert np.all(got[covered:] == 0)
+    else:
+        assert np.all(got[covered:] == 7.0)
+
+
+def test_config4_moe_full_size_sampled(dev):
+    m = workloads.moe()
+    R = int(m.counts.sum())
+    assert R == 1024
+    w = dev.upload_int4(m.packed, m.scales, m.zeros, m.E * m.K * m.N)
+    xb = dev.upload(workloads.bf16_bits(m.x), BF16)
+    cb = dev.upload(m.counts, U32)
+    ob = dev.alloc((R, m.N), BF16)
+    dev.Int4GroupedMatMul(xb, w, m.E, cb, ob)
+    got = workloads.bf16_to_f32(ob.numpy())
+    off = oracle.segment_offsets(m.counts)
+    # the first and last rows of every expert's segment, against the oracle
+    for e in range(m.E):
+        if off[e] == off[e + 1]:
+            continue
+        rows = np.unique([off[e], off[e + 1] - 1])
+        base = e * m.K * m.N
+        pe = m.packed[base // 8:(base + m.K * m.N) // 8]
+        se = m.scales[base // 128:(base + m.K * m.N) // 128]
+        ze = m.zeros[base // 128:(base + m.K * m.N) // 128]
+        want = oracle.quant_matmul_int4(np.ascontiguousarray(m.x[rows]), pe, se, ze,
+                                        len(rows), m.K, m.N, threads=8)
+        assert rel_l2(got[rows], oracle.round_bf16(want)) <= 2e-2
+    for b in (xb, cb, ob):
+        b.free()
+    w.free()
