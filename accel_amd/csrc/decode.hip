@@ -8,24 +8,39 @@
 // w = s == 0 ? z : (code - z) * s.  With N % 128 == 0 a group is 128
 // consecutive columns of one row k.
 //
-// Kernel shape.  A workgroup of 256 lanes owns a 256-column tile (two groups,
-// 128 bytes of codes per row) and a slice of K.  Each lane owns CPL adjacent
-// columns and walks the rows of its row-phase; a row of the tile is read by
-// 256/CPL adjacent lanes as one 128-byte segment (16-byte loads for CPL=32).
-// Per (row, group) the lane folds the dequantisation into two scalars,
+// Kernel shape.  A workgroup of 256 lanes owns a tile of TILE columns and a
+// slice of K rows.  Each lane owns CPL adjacent columns (CPL/8 words: one 4-,
+// 8- or 16-byte load per row) and walks the slice's rows of its row phase;
+// the TILE/CPL lanes of a row read it as one contiguous segment.  Rows are
+// fetched R at a time into registers, the next batch issued before the
+// current one is used.  Per (row, group) the dequantisation folds into two
+// scalars,
 //     x*w = (x*s)*code + b,   b = -(x*s)*z   (or x*z for a zero scale),
-// so the inner loop is one conversion and one FMA per weight, and b is summed
-// once per row.  Nibbles become floats through the fp8 converter: a byte
-// 0000qqqq read as OCP e4m3 is exactly q * 2^-9 (codes 0..7 are subnormals
-// q/8 * 2^-6, codes 8..15 the first binade (1 + (q-8)/8) * 2^-6), so
-// v_cvt_pk_f32_fp8 turns two nibbles into two exact floats and the 2^9 is
-// folded into x*s.
+// so the inner loop is one conversion per two weights and one FMA per
+// weight, and b is summed once per row.  Nibbles become floats through the
+// fp8 converter: a byte 0000qqqq read as OCP e4m3 is exactly q * 2^-9 (codes
+// 0..7 are the subnormals q/8 * 2^-6, codes 8..15 the first binade
+// (1 + (q-8)/8) * 2^-6), so v_cvt_pk_f32_fp8 turns two nibbles into two exact
+// floats and the 2^9 is folded into x*s.
 //
-// The row-phases of a workgroup are summed through LDS.  When K is split
-// across workgroups, each writes its column partials to the workspace and
-// the last workgroup of the tile to finish (an atomic ticket) adds the
-// partials in slice order and writes the output, so the result does not
-// depend on scheduling.  The ticket is reset by that workgroup.
+// Reduction.  The row phases of a workgroup are summed through LDS.  With
+// one slice those sums are the output.  Otherwise every workgroup stores its
+// column sums to the workspace with device-scope stores, waits until they
+// are acknowledged, and draws a ticket for its tile with a device-scope
+// atomic; the workgroup that draws the last ticket reads all slices' sums
+// with device-scope loads, adds them in slice order -- so the result does not
+// depend on scheduling -- writes the output and returns the ticket to zero.
+// Device-scope ("sc1") stores and loads go through the device's coherence
+// point, so only the data of the hand-off pays for it: no L2-wide writeback
+// or invalidate (what an agent-scope release/acquire fence costs on CDNA) is
+// issued.
+//
+// Placement.  Workgroups are dealt to the eight XCDs round robin by launch
+// index.  Logical workgroups are renumbered so that consecutive ones -- the
+// tiles of one K slice, which share scale and zero rows, activations and
+// 128-byte code lines -- run on one XCD and its L2 fetches those once.  The
+// placement affects speed only: every cross-workgroup access above is
+// device-coherent.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -39,8 +54,8 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kTile = 256;     // columns per workgroup
-constexpr int kThreads = 256;  // lanes per workgroup
+constexpr int kThreads = 256;           // lanes per workgroup
+constexpr int kRows = 4;                // rows per lane per fetch batch
 constexpr float kNibbleScale = 512.0f;  // 1 / (e4m3 value of code 1)
 
 __device__ __forceinline__ float half_bits_to_float(uint16_t h) {
@@ -61,53 +76,67 @@ __device__ __forceinline__ void unpack8(uint32_t w, float* f) {
     f[1] = c.x; f[3] = c.y; f[5] = d.x; f[7] = d.y;
 }
 
-template <int CPL>
-struct CodeLoad;
-template <>
-struct CodeLoad<32> {
-    static __device__ __forceinline__ void load(const uint32_t* p, uint32_t* w) {
+// WPL consecutive code words of one row, streamed past the caches.
+template <int WPL>
+__device__ __forceinline__ void load_words(const uint32_t* p, uint32_t* w) {
+    if constexpr (WPL == 4) {
         const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
         w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
-    }
-};
-template <>
-struct CodeLoad<16> {
-    static __device__ __forceinline__ void load(const uint32_t* p, uint32_t* w) {
+    } else if constexpr (WPL == 2) {
         const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
         w[0] = v.x; w[1] = v.y;
-    }
-};
-template <>
-struct CodeLoad<8> {
-    static __device__ __forceinline__ void load(const uint32_t* p, uint32_t* w) {
+    } else {
         w[0] = __builtin_nontemporal_load(p);
     }
+}
+
+__device__ __forceinline__ void store_device(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_device(float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One fetch batch: kRows rows of a lane's segment, with their scale, zero and
+// (for M <= 2) activations.  Rows past the slice are not fetched.
+template <int M, int WPL>
+struct Batch {
+    uint32_t q[kRows][WPL];
+    uint16_t s[kRows], z[kRows];
+    float x[kRows][M <= 2 ? M : 1];
 };
 
-// M rows of activations, CPL columns per lane.
-template <int M, int CPL>
+// M rows of activations; TILE columns per workgroup, CPL per lane.
+template <int M, int TILE, int CPL>
 __global__ __launch_bounds__(kThreads) void int4_decode_f32_kernel(
     const float* __restrict__ a, const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
-    float* __restrict__ out, float* __restrict__ partial, uint32_t* __restrict__ tickets,
-    int K, int N, int rows_per_slice) {
-    constexpr int LPR = kTile / CPL;       // lanes per row
-    constexpr int RP = kThreads / LPR;     // row phases
-    constexpr int WPL = CPL / 8;           // words per lane per row
-    __shared__ float red[RP][kTile];
+    float* __restrict__ out, float* partial, uint32_t* tickets, int K, int N,
+    int rows_per_slice, int slices) {
+    constexpr int LPR = TILE / CPL;     // lanes per row
+    constexpr int RP = kThreads / LPR;  // row phases
+    constexpr int WPL = CPL / 8;        // code words per lane per row
+    constexpr bool kXInBatch = M <= 2;
+    __shared__ __attribute__((aligned(16))) float red[RP][TILE];
     __shared__ int last_flag;
+
+    const int tiles = N / TILE;
+    const int grid = tiles * slices;
+    int b = blockIdx.x;
+    if ((grid & 7) == 0) b = (b & 7) * (grid >> 3) + (b >> 3);
+    const int tile = b % tiles;
+    const int slice = b / tiles;
 
     const int tid = threadIdx.x;
     const int lane = tid % LPR;
     const int rp = tid / LPR;
-    const int tile0 = blockIdx.x * kTile;
-    const int col0 = tile0 + lane * CPL;
-    const bool active = col0 < N;
-    const int groups_per_row = N >> 7;
+    const int col0 = tile * TILE + lane * CPL;
     const int g = col0 >> 7;
-    const int k_begin = blockIdx.y * rows_per_slice;
-    const int k_end = min(K, k_begin + rows_per_slice);
+    const size_t groups_per_row = (size_t)(N >> 7);
     const size_t words_per_row = (size_t)(N >> 3);
+    const int k_begin = slice * rows_per_slice;
+    const int k_end = min(K, k_begin + rows_per_slice);
+    const uint32_t* qcol = codes + (col0 >> 3);
 
     float acc[M][CPL];
     float bias[M];
@@ -118,59 +147,85 @@ __global__ __launch_bounds__(kThreads) void int4_decode_f32_kernel(
         for (int j = 0; j < CPL; j++) acc[m][j] = 0.0f;
     }
 
-    if (active) {
-        const uint32_t* qp = codes + (size_t)(k_begin + rp) * words_per_row + (col0 >> 3);
-        const uint16_t* sp = scales + (size_t)(k_begin + rp) * groups_per_row + g;
-        const uint16_t* zp = zeros + (size_t)(k_begin + rp) * groups_per_row + g;
-        const float* ap = a + k_begin + rp;
-#pragma unroll 2
-        for (int k = k_begin + rp; k < k_end; k += RP) {
-            uint32_t w[WPL];
-            CodeLoad<CPL>::load(qp, w);
-            const float s = half_bits_to_float(*sp);
-            const float z = half_bits_to_float(*zp);
-            float xs[M];
+    auto fetch = [&](Batch<M, WPL>& bt, int k) {
 #pragma unroll
-            for (int m = 0; m < M; m++) {
-                const float x = ap[(size_t)m * K];
-                const float xsm = x * s;
-                bias[m] += (s == 0.0f) ? x * z : -(xsm * z);
-                xs[m] = xsm * kNibbleScale;
+        for (int i = 0; i < kRows; i++) {
+            const int row = k + i * RP;
+            if (row < k_end) {
+                load_words<WPL>(qcol + (size_t)row * words_per_row, bt.q[i]);
+                bt.s[i] = scales[(size_t)row * groups_per_row + g];
+                bt.z[i] = zeros[(size_t)row * groups_per_row + g];
+                if constexpr (kXInBatch) {
+#pragma unroll
+                    for (int m = 0; m < M; m++) bt.x[i][m] = a[(size_t)m * K + row];
+                }
             }
-#pragma unroll
-            for (int i = 0; i < WPL; i++) {
-                float f[8];
-                unpack8(w[i], f);
-#pragma unroll
-                for (int m = 0; m < M; m++)
-#pragma unroll
-                    for (int j = 0; j < 8; j++)
-                        acc[m][i * 8 + j] = __builtin_fmaf(xs[m], f[j], acc[m][i * 8 + j]);
-            }
-            qp += RP * words_per_row;
-            sp += RP * groups_per_row;
-            zp += RP * groups_per_row;
-            ap += RP;
         }
+    };
+    auto compute = [&](const Batch<M, WPL>& bt, int k) {
+#pragma unroll
+        for (int i = 0; i < kRows; i++) {
+            const int row = k + i * RP;
+            if (row < k_end) {
+                const float s = half_bits_to_float(bt.s[i]);
+                const float z = half_bits_to_float(bt.z[i]);
+                float xs[M];
+#pragma unroll
+                for (int m = 0; m < M; m++) {
+                    float x;
+                    if constexpr (kXInBatch) x = bt.x[i][m];
+                    else x = a[(size_t)m * K + row];
+                    const float xsm = x * s;
+                    bias[m] += (s == 0.0f) ? x * z : -(xsm * z);
+                    xs[m] = xsm * kNibbleScale;
+                }
+#pragma unroll
+                for (int wi = 0; wi < WPL; wi++) {
+                    float f[8];
+                    unpack8(bt.q[i][wi], f);
+#pragma unroll
+                    for (int m = 0; m < M; m++)
+#pragma unroll
+                        for (int j = 0; j < 8; j++)
+                            acc[m][wi * 8 + j] =
+                                __builtin_fmaf(xs[m], f[j], acc[m][wi * 8 + j]);
+                }
+            }
+        }
+    };
+
+    // Two named buffers so the next batch is in flight while one is used.
+    constexpr int kStep = kRows * RP;
+    Batch<M, WPL> b0, b1;
+    int k = k_begin + rp;
+    if (k < k_end) fetch(b0, k);
+    while (k < k_end) {
+        if (k + kStep < k_end) fetch(b1, k + kStep);
+        compute(b0, k);
+        k += kStep;
+        if (k >= k_end) break;
+        if (k + kStep < k_end) fetch(b0, k + kStep);
+        compute(b1, k);
+        k += kStep;
     }
 
-    const bool split = gridDim.y > 1;
-    const int col = tile0 + tid;
+    const bool split = slices > 1;
 #pragma unroll
     for (int m = 0; m < M; m++) {
 #pragma unroll
         for (int j = 0; j < CPL; j += 4) {
-            float4 v = make_float4(acc[m][j] + bias[m], acc[m][j + 1] + bias[m],
-                                   acc[m][j + 2] + bias[m], acc[m][j + 3] + bias[m]);
+            const float4 v = make_float4(acc[m][j] + bias[m], acc[m][j + 1] + bias[m],
+                                         acc[m][j + 2] + bias[m], acc[m][j + 3] + bias[m]);
             *reinterpret_cast<float4*>(&red[rp][lane * CPL + j]) = v;
         }
         __syncthreads();
-        float sum = 0.0f;
-#pragma unroll
-        for (int p = 0; p < RP; p++) sum += red[p][tid];
-        if (col < N) {
+        for (int c = tid; c < TILE; c += kThreads) {
+            float sum = 0.0f;
+#pragma unroll 8
+            for (int p = 0; p < RP; p++) sum += red[p][c];
+            const int col = tile * TILE + c;
             if (split)
-                partial[((size_t)blockIdx.y * M + m) * N + col] = sum;
+                store_device(&partial[((size_t)slice * M + m) * N + col], sum);
             else
                 out[(size_t)m * N + col] = sum;
         }
@@ -178,41 +233,51 @@ __global__ __launch_bounds__(kThreads) void int4_decode_f32_kernel(
     }
     if (!split) return;
 
-    // Publish this slice's partials, then take a ticket; the last slice of
-    // the tile to arrive adds all slices in slice order.
-    __threadfence();
+    // Hand-off: this workgroup's sums are acknowledged by the coherence point
+    // before its ticket is drawn; the last of the tile's slices adds them up.
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __syncthreads();
     if (tid == 0) {
-        const uint32_t prev = atomicAdd(&tickets[blockIdx.x], 1u);
-        last_flag = (prev == gridDim.y - 1);
+        const uint32_t prev = __hip_atomic_fetch_add(&tickets[tile], 1u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+        last_flag = prev == (uint32_t)(slices - 1);
     }
     __syncthreads();
     if (!last_flag) return;
-    __threadfence();
-    if (col < N) {
+    const size_t slice_stride = (size_t)M * N;
+    for (int idx = tid; idx < M * TILE; idx += kThreads) {
+        const int m = idx / TILE;
+        const int col = tile * TILE + idx % TILE;
+        float* p = partial + (size_t)m * N + col;
+        float sum = 0.0f;
+        int sl = 0;
+        for (; sl + 8 <= slices; sl += 8) {
+            float v[8];
 #pragma unroll
-        for (int m = 0; m < M; m++) {
-            float sum = 0.0f;
-            for (int sl = 0; sl < (int)gridDim.y; sl++)
-                sum += __builtin_nontemporal_load(&partial[((size_t)sl * M + m) * N + col]);
-            out[(size_t)m * N + col] = sum;
+            for (int u = 0; u < 8; u++) v[u] = load_device(p + (size_t)(sl + u) * slice_stride);
+#pragma unroll
+            for (int u = 0; u < 8; u++) sum += v[u];
         }
+        for (; sl < slices; sl++) sum += load_device(p + (size_t)sl * slice_stride);
+        out[(size_t)m * N + col] = sum;
     }
-    if (tid == 0) tickets[blockIdx.x] = 0;
+    if (tid == 0)
+        __hip_atomic_store(&tickets[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int M, int CPL>
+// Slices so the launch has about two workgroups per CU, each lane at least
+// kRows rows of work.
+template <int M, int TILE, int CPL>
 hipError_t launch_decode(Device* d, hipStream_t st, const float* a, Int4Planes w,
                          float* out, int K, int N, int* status) {
-    constexpr int LPR = kTile / CPL;
+    constexpr int LPR = TILE / CPL;
     constexpr int RP = kThreads / LPR;
-    const int tiles = (N + kTile - 1) / kTile;
-    // Enough workgroups to give every CU a few, each slice at least a few rows
-    // per lane; the split costs M*N*4 bytes per slice of workspace traffic.
+    const int tiles = N / TILE;
     const int target_blocks = d->cu_count * 2;
-    int slices = std::max(1, target_blocks / tiles);
-    const int min_rows = RP * 4;
-    slices = std::min(slices, std::max(1, K / min_rows));
+    int slices = std::max(1, (target_blocks + tiles - 1) / tiles);
+    slices = std::min(slices, std::max(1, K / (RP * kRows)));
     int rows = (K + slices - 1) / slices;
     rows = (rows + RP - 1) / RP * RP;
     slices = (K + rows - 1) / rows;
@@ -220,8 +285,8 @@ hipError_t launch_decode(Device* d, hipStream_t st, const float* a, Int4Planes w
     uint32_t* tickets = nullptr;
     if (slices > 1) {
         if ((size_t)tiles * sizeof(uint32_t) > kWorkspaceCounterBytes) {
-            *status = fail(ACCEL_E_INVALID, "decode product: N=%d needs more tickets than "
-                                            "the workspace holds", N);
+            *status = fail(ACCEL_E_INVALID,
+                           "decode product: N=%d needs more tickets than the workspace holds", N);
             return hipSuccess;
         }
         void* ws = workspace(d, (size_t)slices * M * N * sizeof(float), status);
@@ -229,10 +294,19 @@ hipError_t launch_decode(Device* d, hipStream_t st, const float* a, Int4Planes w
         tickets = static_cast<uint32_t*>(ws);
         partial = reinterpret_cast<float*>(static_cast<char*>(ws) + kWorkspaceCounterBytes);
     }
-    dim3 grid(tiles, slices);
-    hipLaunchKernelGGL((int4_decode_f32_kernel<M, CPL>), grid, dim3(kThreads), 0, st, a,
-                       w.codes, w.scales, w.zeros, out, partial, tickets, K, N, rows);
+    hipLaunchKernelGGL((int4_decode_f32_kernel<M, TILE, CPL>), dim3(tiles * slices),
+                       dim3(kThreads), 0, st, a, w.codes, w.scales, w.zeros, out, partial,
+                       tickets, K, N, rows, slices);
     return hipGetLastError();
+}
+
+// Columns per lane by row count: the accumulators (M * CPL) stay near 64.
+template <int M>
+hipError_t launch_decode_m(Device* d, hipStream_t st, const float* a, Int4Planes w,
+                           float* out, int K, int N, int* status) {
+    constexpr int CPL = M <= 2 ? 32 : (M <= 4 ? 16 : 8);
+    if (N % 256 == 0) return launch_decode<M, 256, CPL>(d, st, a, w, out, K, N, status);
+    return launch_decode<M, 128, CPL>(d, st, a, w, out, K, N, status);
 }
 
 // Any shape: one lane per output element, decoding with the flat index.
@@ -289,30 +363,28 @@ __global__ void int4_generic_bf16_kernel(const uint16_t* __restrict__ a,
 
 bool int4_decode_f32_supported(int M, int K, int N, const void* codes) {
     return M >= 1 && M <= 16 && K >= 1 && N >= 128 && N % 128 == 0 &&
-           (reinterpret_cast<uintptr_t>(codes) & 15) == 0 &&
-           (uint64_t)K * (uint64_t)N < (1ull << 32);
+           (reinterpret_cast<uintptr_t>(codes) & 15) == 0 && K < (1 << 30) && N < (1 << 30);
 }
 
 hipError_t launch_int4_decode_f32(Device* d, hipStream_t st, const float* a, Int4Planes w,
                                   float* out, int M, int K, int N, int* status) {
     *status = ACCEL_OK;
     switch (M) {
-        case 1: return launch_decode<1, 32>(d, st, a, w, out, K, N, status);
-        case 2: return launch_decode<2, 32>(d, st, a, w, out, K, N, status);
-        case 3: return launch_decode<3, 16>(d, st, a, w, out, K, N, status);
-        case 4: return launch_decode<4, 16>(d, st, a, w, out, K, N, status);
-        case 5: return launch_decode<5, 16>(d, st, a, w, out, K, N, status);
-        case 6: return launch_decode<6, 16>(d, st, a, w, out, K, N, status);
-        case 7: return launch_decode<7, 8>(d, st, a, w, out, K, N, status);
-        case 8: return launch_decode<8, 8>(d, st, a, w, out, K, N, status);
+        case 1: return launch_decode_m<1>(d, st, a, w, out, K, N, status);
+        case 2: return launch_decode_m<2>(d, st, a, w, out, K, N, status);
+        case 3: return launch_decode_m<3>(d, st, a, w, out, K, N, status);
+        case 4: return launch_decode_m<4>(d, st, a, w, out, K, N, status);
+        case 5: return launch_decode_m<5>(d, st, a, w, out, K, N, status);
+        case 6: return launch_decode_m<6>(d, st, a, w, out, K, N, status);
+        case 7: return launch_decode_m<7>(d, st, a, w, out, K, N, status);
+        case 8: return launch_decode_m<8>(d, st, a, w, out, K, N, status);
         default: break;
     }
-    // 9..16 rows: two passes of up to eight rows each.
-    const int first = 8;
-    hipError_t e = launch_decode<8, 8>(d, st, a, w, out, K, N, status);
+    // 9..16 rows: eight, then the rest.
+    hipError_t e = launch_decode_m<8>(d, st, a, w, out, K, N, status);
     if (e != hipSuccess || *status != ACCEL_OK) return e;
-    return launch_int4_decode_f32(d, st, a + (size_t)first * K, w, out + (size_t)first * N,
-                                  M - first, K, N, status);
+    return launch_int4_decode_f32(d, st, a + (size_t)8 * K, w, out + (size_t)8 * N, M - 8, K,
+                                  N, status);
 }
 
 hipError_t launch_int4_generic_f32(hipStream_t st, const float* a, Int4Planes w, float* out,
