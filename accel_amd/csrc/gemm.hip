@@ -3,23 +3,37 @@
 // CDNA4's bf16 matrix cores.
 //
 // bf16 path (activations and output bf16, fp32 accumulation).  A workgroup
-// of 256 lanes (four waves, 2x2) computes a 128x128 output tile; each wave a
-// 64x64 block as 4x4 v_mfma_f32_16x16x32_bf16 tiles.  Per K step of 64:
-//   * the activation tile (128 rows x 128 bytes) is loaded with 16-byte loads
-//     and stored to LDS as rows of 64 k;
-//   * the code tile (64 rows x 64 bytes) is loaded as 4-row x 8-column
-//     blocks, one per lane, dequantised in registers to bf16 and written to
-//     LDS transposed, as columns of 64 k -- the layout the MFMA B operand
-//     reads, 8 consecutive k per lane;
-// both LDS tiles use a 16-byte XOR swizzle so the operand reads (16 rows x
-// 4 chunks per wave) hit every bank slot equally.  LDS is double buffered,
-// and the next step's global loads are issued before the current step's
-// MFMAs.  The 128-column tile is one quantisation group wide, so a K row of
-// the tile has one (scale, zero) pair.
+// of 256 lanes (four waves) computes a 128 x 256 output tile; wave w owns
+// all 128 rows and the 64 columns [64w, 64w+64), as 4 x 2 tiles of
+// v_mfma_f32_32x32x16_bf16 (the 32x32 form: on gfx950 the 16x16x32 form
+// issues at well under the matrix cores' peak).  Per K stage of 64:
+//   * the activation tile (128 rows x 128 bytes) goes to LDS through 16-byte
+//     loads, rows XOR-swizzled in 16-byte chunks so the fragment reads
+//     (32 rows x 2 chunks per wave) spread over the banks;
+//   * the packed codes (64 rows x 128 bytes) go to LDS as they are, four
+//     bits a weight, transposed in 4 x 4-byte blocks so that each u32 holds
+//     one byte (two adjacent columns) of four consecutive rows;
+//   * per (row, group) the fold (512*s, s == 0 ? z : -z*s) goes to LDS.
+// Each wave then dequantises its own B fragments in registers: the lane of
+// MFMA column c and k-group h reads one u32 per four rows, turns the nibbles
+// into exact floats with the fp8 converter (byte 0000qqqq as OCP e4m3 is
+// q*2^-9; a converter pair is the same column of two rows, the pairing the
+// bf16x2 operand wants), applies w = f*(512 s) + add in fp32 and packs to
+// bf16.  The MFMA's n-tile j, column c is mapped to the physical column
+// 2c + j, so a lane's two n-tiles are the two columns of one code byte and
+// its outputs are bf16 pairs.  A 64-column wave tile lies inside one
+// 128-column quantisation group, so a row has one (s, z) per wave.
+// LDS is double buffered; the next stage's global loads are issued before
+// the current stage's MFMAs and written to LDS after them.
+//
+// Placement: consecutive logical tiles (the column tiles of one row band,
+// which share its activations) are dealt to one XCD so its L2 serves them.
 //
 // f32 path (the reference API's f32 activations and output, M > 16): an
 // LDS-tiled fp32 VALU product, exact up to f32 rounding order.
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
 
 #include "internal.hpp"
 
@@ -28,12 +42,16 @@ namespace {
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int BM = 128, BN = 128, BK = 64;
+constexpr int BM = 128, BN = 256, BK = 64;
 constexpr int kThreads = 256;
-constexpr int kRowBytes = BK * 2;  // one LDS row: 64 bf16
+constexpr int kARowBytes = BK * 2;   // one LDS activation row: 64 bf16
+constexpr int kBQuadWords = BN / 2;  // u32 words per row quad: one per code byte
 
 __device__ __forceinline__ float half_bits_to_float(uint16_t h) {
     _Float16 v;
@@ -41,174 +59,285 @@ __device__ __forceinline__ float half_bits_to_float(uint16_t h) {
     return (float)v;
 }
 
-__device__ __forceinline__ void unpack8(uint32_t w, float* f) {
-    const uint32_t lo = w & 0x0F0F0F0Fu;
-    const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;
-    const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);
-    const f32x2 b = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
-    const f32x2 c = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
-    const f32x2 d = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
-    f[0] = a.x; f[2] = a.y; f[4] = b.x; f[6] = b.y;
-    f[1] = c.x; f[3] = c.y; f[5] = d.x; f[7] = d.y;
+// Byte offset of 16-byte chunk `c` of activation row `r` under the swizzle:
+// LDS has 64 banks (256 bytes), two rows wide; each row pair puts a chunk
+// index on its own 16-byte bank group, so a fragment read (32 rows, one
+// chunk) and a staging write (one row, eight chunks) do not conflict.
+__device__ __forceinline__ int a_off(int r, int c) {
+    return r * kARowBytes + ((c ^ ((r >> 1) & 7)) << 4);
+}
+// Word offset of code byte `bc` of row quad `rq`: odd quad pairs are
+// shifted by half a bank width, so the two k-groups of a fragment read
+// (quads 2h and 2h+1 apart by two) use different banks.
+__device__ __forceinline__ int b_off(int rq, int bc) {
+    return rq * kBQuadWords + (bc ^ (((rq >> 1) & 1) << 5));
 }
 
-// Byte offset of 16-byte chunk `c` of LDS row `r` under the swizzle.
-__device__ __forceinline__ int swz(int r, int c) {
-    return r * kRowBytes + ((c ^ ((r >> 1) & 7)) << 4);
+// 4 x 4 byte transpose: out[b] = byte b of r0, r1, r2, r3 (low to high).
+__device__ __forceinline__ u32x4 transpose4(uint32_t r0, uint32_t r1, uint32_t r2,
+                                            uint32_t r3) {
+    const uint32_t lo01 = __builtin_amdgcn_perm(r1, r0, 0x05010400u);  // r0b0 r1b0 r0b1 r1b1
+    const uint32_t lo23 = __builtin_amdgcn_perm(r3, r2, 0x05010400u);
+    const uint32_t hi01 = __builtin_amdgcn_perm(r1, r0, 0x07030602u);  // r0b2 r1b2 r0b3 r1b3
+    const uint32_t hi23 = __builtin_amdgcn_perm(r3, r2, 0x07030602u);
+    u32x4 o;
+    o.x = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);
+    o.y = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);
+    o.z = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
+    o.w = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
+    return o;
 }
 
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-    bf16x2 v;
-    v.x = (__bf16)lo;
-    v.y = (__bf16)hi;
-    return __builtin_bit_cast(uint32_t, v);
-}
+constexpr int kStages = 3;   // LDS ring depth (and register sets in flight)
 
-// One 128x128 output tile: rows [m0, m_end) of a/out are valid (rows past
-// m_end are computed from a clamped row and never stored); the codes,
-// scales and zeros pointers are those of the [K, N] matrix in use.
-__device__ __forceinline__ void gemm_tile_bf16(
-    char (*lds)[2][BM * kRowBytes], const uint16_t* __restrict__ a,
-    const uint32_t* __restrict__ codes, const uint16_t* __restrict__ scales,
-    const uint16_t* __restrict__ zeros, uint16_t* __restrict__ out, int m0, int m_end,
-    int n0, int K, int N) {
+struct __attribute__((aligned(16))) GemmLds {
+    char a[kStages][BM * kARowBytes];               // 3 x 16 KB
+    uint32_t b[kStages][(BK / 4) * kBQuadWords];    // 3 x 8 KB: [row quad][code byte]
+    f32x2 fold[kStages][2][BK];                     // [buf][group of the tile][row]
+};
+
+// One stage's global loads, held in registers until written to LDS.
+struct StageRegs {
+    u32x4 a[4];
+    u32x2 b[4];
+    uint16_t s, z;
+};
+
+// One 16-k substep's operands for a wave.
+struct SubstepRegs {
+    bf16x8 af[4];      // A fragments of the four 32-row tiles
+    uint32_t tw[2];    // codes of rows 8*kg .. 8*kg+7 (two quads)
+    f32x4 fr[4];       // (mul, add) of those rows, two per vector
+};
+
+// One 128 x 256 output tile.  Rows [m0, m_end) of a/out are valid; rows
+// past m_end are computed from a clamped row and not stored.  Columns
+// [n0, n0 + 256) with n0 + 128 == N allowed (the upper half is computed
+// from clamped columns and not stored).  codes/scales/zeros describe the
+// [K, N] matrix in use.
+//
+// Pipeline.  Stage kt (64 k) reads LDS buffer kt % 3.  During it the wave
+// issues the global loads of stage kt+3 into register set kt % 3, writes set
+// (kt+2) % 3 (stage kt+2, loaded one stage earlier) into buffer (kt+2) % 3,
+// and runs the stage's four 16-k substeps so that the LDS reads of substep
+// s+2 and the dequantisation of substep s+1 overlap the MFMAs of substep s;
+// the last substeps read ahead into buffer (kt+1) % 3, completed before the
+// previous barrier.  One barrier per stage.
+__device__ __forceinline__ void gemm_tile_bf16(GemmLds& lds, const uint16_t* __restrict__ a,
+                                               const uint32_t* __restrict__ codes,
+                                               const uint16_t* __restrict__ scales,
+                                               const uint16_t* __restrict__ zeros,
+                                               uint16_t* __restrict__ out, int m0, int m_end,
+                                               int n0, int K, int N) {
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int lane = tid & 63;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int groups_per_row = N >> 7;
-    const int g = n0 >> 7;
+    const int c32 = lane & 31;   // MFMA row (A) / column (B, D) within a 32 x 32 tile
+    const int kg = lane >> 5;    // MFMA k-group (8 consecutive k)
+    const size_t groups_per_row = (size_t)(N >> 7);
     const size_t words_per_row = (size_t)(N >> 3);
+    const bool half_tile = n0 + BN > N;   // only the first 128 columns exist
 
-    // A loader: row t/2, 64 bytes at (t&1)*64.
-    const int a_row = tid >> 1;
-    const int a_half = tid & 1;
-    const int a_grow = min(m0 + a_row, m_end - 1);
-    const uint16_t* a_src = a + (size_t)a_grow * K + a_half * 32;
-    // B loader: 8 columns (one word) x 4 rows.
-    const int b_cw = tid & 15;
-    const int b_rq = tid >> 4;
-    const uint32_t* b_src = codes + (size_t)(b_rq * 4) * words_per_row + (n0 >> 3) + b_cw;
-    const uint16_t* s_src = scales + (size_t)(b_rq * 4) * groups_per_row + g;
-    const uint16_t* z_src = zeros + (size_t)(b_rq * 4) * groups_per_row + g;
-
-    uint4 a_reg[4];
-    uint32_t b_reg[4];
-    uint16_t s_reg[4], z_reg[4];
-
-    auto load_global = [&](int k0) {
-        const uint4* ap = reinterpret_cast<const uint4*>(a_src + k0);
-#pragma unroll
-        for (int i = 0; i < 4; i++) a_reg[i] = ap[i];
-        const size_t roff = (size_t)k0 * words_per_row;
-        const size_t goff = (size_t)k0 * groups_per_row;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            b_reg[i] = __builtin_nontemporal_load(b_src + roff + i * words_per_row);
-            s_reg[i] = s_src[goff + i * groups_per_row];
-            z_reg[i] = z_src[goff + i * groups_per_row];
-        }
-    };
-
-    auto store_lds = [&](int buf) {
-        char* As = lds[buf][0];
-        char* Bs = lds[buf][1];
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-            *reinterpret_cast<uint4*>(As + swz(a_row, a_half * 4 + i)) = a_reg[i];
-        // Dequantise the 4x8 block and write it transposed: column n gets
-        // k = 4*b_rq .. 4*b_rq+3 (half of one 16-byte chunk).
-        float v[4][8];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float s = half_bits_to_float(s_reg[i]);
-            const float z = half_bits_to_float(z_reg[i]);
-            const float mul = s * 512.0f;
-            const float add = (s == 0.0f) ? z : -(z * s);
-            float f[8];
-            unpack8(b_reg[i], f);
-#pragma unroll
-            for (int j = 0; j < 8; j++) v[i][j] = __builtin_fmaf(f[j], mul, add);
-        }
-        const int chunk = b_rq >> 1;
-        const int sub = (b_rq & 1) * 8;
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int n = b_cw * 8 + j;
-            uint2 pr;
-            pr.x = pack_bf16x2(v[0][j], v[1][j]);
-            pr.y = pack_bf16x2(v[2][j], v[3][j]);
-            *reinterpret_cast<uint2*>(Bs + swz(n, chunk) + sub) = pr;
-        }
-    };
-
-    f32x4 acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
-
-    const int ktiles = K / BK;
-    load_global(0);
-    store_lds(0);
-    __syncthreads();
-
-    const int r16 = lane & 15;
-    const int kq = lane >> 4;  // which 8-k chunk within a 32-k MFMA step
-    for (int kt = 0; kt < ktiles; kt++) {
-        const int cur = kt & 1;
-        if (kt + 1 < ktiles) load_global((kt + 1) * BK);
-        const char* As = lds[cur][0];
-        const char* Bs = lds[cur][1];
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
-            bf16x8 af[4], bfr[4];
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-                af[t] = *reinterpret_cast<const bf16x8*>(
-                    As + swz(wm * 64 + t * 16 + r16, ks * 4 + kq));
-                bfr[t] = *reinterpret_cast<const bf16x8*>(
-                    Bs + swz(wn * 64 + t * 16 + r16, ks * 4 + kq));
-            }
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int j = 0; j < 4; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[j],
-                                                                        acc[i][j], 0, 0, 0);
-        }
-        if (kt + 1 < ktiles) store_lds(cur ^ 1);
-        __syncthreads();
-    }
-
-    // D layout of a 16x16 tile: lane holds column lane%16, rows 4*(lane/16)+i.
+    // Activation staging: 1024 chunks of 16 bytes, four per lane.
+    const uint16_t* a_src[4];
+    int a_dst[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
+        const int q = tid + kThreads * i;
+        const int r = q >> 3, c = q & 7;
+        const int row = min(m0 + r, m_end - 1);
+        a_src[i] = a + (size_t)row * K + c * 8;
+        a_dst[i] = a_off(r, c);
+    }
+    // Code staging: row quad tid / 16, 16-column chunk tid % 16 (8 bytes of
+    // each of the quad's four rows).
+    const int b_rq = tid >> 4;
+    const int b_ch = tid & 15;
+    const int b_col = (half_tile && b_ch >= 8) ? n0 + (b_ch - 8) * 16 : n0 + b_ch * 16;
+    const uint32_t* b_src = codes + (size_t)(4 * b_rq) * words_per_row + (b_col >> 3);
+    const int b_dst0 = b_off(b_rq, 8 * b_ch), b_dst1 = b_off(b_rq, 8 * b_ch + 4);
+    // Fold staging: one (row, group of the tile) per lane, lanes 128..255
+    // repeating lanes 0..127 (the same value to the same place) so the stage
+    // body has no branch.
+    const int f_row = tid & 63;
+    const int f_grp = (tid >> 6) & 1;
+    const size_t f_g = (size_t)(n0 >> 7) + ((half_tile && f_grp) ? 0 : f_grp);
+    const uint16_t* s_src = scales + (size_t)f_row * groups_per_row + f_g;
+    const uint16_t* z_src = zeros + (size_t)f_row * groups_per_row + f_g;
+    const int ktiles = K / BK;
+
+    // Loads of stage kt, clamped to the last stage (a load past the end is
+    // repeated work, never used).
+    auto load_global = [&](StageRegs& g, int kt) {
+        const int k0 = min(kt, ktiles - 1) * BK;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int col = n0 + wn * 64 + j * 16 + r16;
+        for (int i = 0; i < 4; i++) g.a[i] = *reinterpret_cast<const u32x4*>(a_src[i] + k0);
+        const uint32_t* bp = b_src + (size_t)k0 * words_per_row;
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int row = m0 + wm * 64 + i * 16 + kq * 4 + r;
-                if (row < m_end) {
-                    const __bf16 v = (__bf16)acc[i][j][r];
-                    out[(size_t)row * N + col] = __builtin_bit_cast(uint16_t, v);
-                }
+        for (int i = 0; i < 4; i++)
+            g.b[i] = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x2*>(bp + (size_t)i * words_per_row));
+        g.s = s_src[(size_t)k0 * groups_per_row];
+        g.z = z_src[(size_t)k0 * groups_per_row];
+    };
+    auto store_lds = [&](const StageRegs& g, int buf) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) *reinterpret_cast<u32x4*>(lds.a[buf] + a_dst[i]) = g.a[i];
+        *reinterpret_cast<u32x4*>(&lds.b[buf][b_dst0]) =
+            transpose4(g.b[0].x, g.b[1].x, g.b[2].x, g.b[3].x);
+        *reinterpret_cast<u32x4*>(&lds.b[buf][b_dst1]) =
+            transpose4(g.b[0].y, g.b[1].y, g.b[2].y, g.b[3].y);
+        const float s = half_bits_to_float(g.s);
+        const float z = half_bits_to_float(g.z);
+        f32x2 f;
+        f.x = s * 512.0f;
+        f.y = (s == 0.0f) ? z : -(z * s);
+        lds.fold[buf][f_grp][f_row] = f;
+    };
+
+    // This wave's code byte: columns 64*wave + 2*c32 and +1 of the tile.
+    const int my_bc = 32 * wave + c32;
+    const int my_grp = wave >> 1;
+
+    auto read_substep = [&](SubstepRegs& r, int buf, int ks) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) r.tw[i] = lds.b[buf][b_off(ks * 4 + 2 * kg + i, my_bc)];
+        const f32x4* fp =
+            reinterpret_cast<const f32x4*>(&lds.fold[buf][my_grp][ks * 16 + 8 * kg]);
+#pragma unroll
+        for (int i = 0; i < 4; i++) r.fr[i] = fp[i];   // (mul, add) of rows 2i, 2i+1
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+            r.af[t] = *reinterpret_cast<const bf16x8*>(lds.a[buf] +
+                                                      a_off(t * 32 + c32, ks * 2 + kg));
+    };
+    auto dequant = [&](const SubstepRegs& r, bf16x8 (&bfr)[2]) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const uint32_t t = r.tw[i];
+            const uint32_t lo = t & 0x0F0F0F0Fu;          // column 0 of rows 0..3
+            const uint32_t hi = (t >> 4) & 0x0F0F0F0Fu;   // column 1
+            const f32x2 c0a = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);  // rows 0, 1
+            const f32x2 c0b = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);   // rows 2, 3
+            const f32x2 c1a = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
+            const f32x2 c1b = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
+            const f32x4 f01 = r.fr[2 * i], f23 = r.fr[2 * i + 1];
+            const int p = 4 * i;
+            bfr[0][p + 0] = (__bf16)__builtin_fmaf(c0a.x, f01.x, f01.y);
+            bfr[0][p + 1] = (__bf16)__builtin_fmaf(c0a.y, f01.z, f01.w);
+            bfr[0][p + 2] = (__bf16)__builtin_fmaf(c0b.x, f23.x, f23.y);
+            bfr[0][p + 3] = (__bf16)__builtin_fmaf(c0b.y, f23.z, f23.w);
+            bfr[1][p + 0] = (__bf16)__builtin_fmaf(c1a.x, f01.x, f01.y);
+            bfr[1][p + 1] = (__bf16)__builtin_fmaf(c1a.y, f01.z, f01.w);
+            bfr[1][p + 2] = (__bf16)__builtin_fmaf(c1b.x, f23.x, f23.y);
+            bfr[1][p + 3] = (__bf16)__builtin_fmaf(c1b.y, f23.z, f23.w);
+        }
+    };
+
+    f32x16 acc[4][2];
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[t][j][r] = 0.0f;
+
+    auto mfmas = [&](const SubstepRegs& r, const bf16x8 (&bfr)[2]) {
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+                acc[t][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(r.af[t], bfr[j], acc[t][j],
+                                                                   0, 0, 0);
+    };
+
+    // Register sets rotate with the LDS ring: stage kt loads stage kt+3 into
+    // g[kt % 3] and writes g[(kt+2) % 3] (stage kt+2) to buffer (kt+2) % 3.
+    StageRegs g[kStages];
+    load_global(g[0], 0);
+    store_lds(g[0], 0);
+    load_global(g[1], 1);
+    store_lds(g[1], 1);
+    load_global(g[2], 2);
+    __syncthreads();
+
+    // cur: substep being multiplied (A fragments + dequantised B);
+    // nxt: substep being dequantised (its LDS reads went out a substep
+    // earlier); far: substep whose LDS reads go out now.
+    SubstepRegs cur, nxt, far;
+    bf16x8 bcur[2], bnxt[2];
+    read_substep(cur, 0, 0);
+    dequant(cur, bcur);
+    read_substep(nxt, 0, 1);
+
+    // One stage, branch free: past the last stage the loads repeat the last
+    // stage, the LDS writes land in a buffer no later stage reads, and the
+    // reads of the stage after the last are of a buffer nothing uses.
+    auto stage = [&](int kt, auto BUF) {
+        constexpr int buf = decltype(BUF)::value;
+        load_global(g[buf], kt + 3);
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            // LDS reads two substeps ahead go out first (a scheduling fence
+            // keeps the compiler from sinking them next to their use); this
+            // substep's MFMAs then interleave with the next one's dequant,
+            // whose operands arrived during the previous substep.
+            if (ks < 2) read_substep(far, buf, ks + 2);
+            else read_substep(far, (buf + 1) % kStages, ks - 2);
+            if (ks == 2) store_lds(g[(buf + 2) % kStages], (buf + 2) % kStages);
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(cur, bcur);
+            dequant(nxt, bnxt);
+            __builtin_amdgcn_sched_barrier(0);
+            cur = nxt;
+            nxt = far;
+            bcur[0] = bnxt[0];
+            bcur[1] = bnxt[1];
+        }
+        __syncthreads();
+    };
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+    using B2 = std::integral_constant<int, 2>;
+    int kt = 0;
+    for (; kt + 3 <= ktiles; kt += 3) {
+        stage(kt, B0{});
+        stage(kt + 1, B1{});
+        stage(kt + 2, B2{});
+    }
+    if (kt < ktiles) stage(kt, B0{});
+    if (kt + 1 < ktiles) stage(kt + 1, B1{});
+
+    // D of a 32 x 32 tile: lane holds column lane % 32; register r is row
+    // 8*(r/4) + 4*(lane/32) + r%4.
+    const int col = n0 + 64 * wave + 2 * c32;
+    if (col >= N) return;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int row = m0 + t * 32 + 8 * (r >> 2) + 4 * kg + (r & 3);
+            if (row < m_end) {
+                bf16x2 v;
+                v[0] = (__bf16)acc[t][0][r];
+                v[1] = (__bf16)acc[t][1][r];
+                *reinterpret_cast<bf16x2*>(out + (size_t)row * N + col) = v;
             }
         }
     }
 }
 
-__global__ __launch_bounds__(kThreads, 2) void int4_gemm_bf16_kernel(
+__global__ __launch_bounds__(kThreads, 1) void int4_gemm_bf16_kernel(
     const uint16_t* __restrict__ a, const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
     uint16_t* __restrict__ out, int M, int K, int N) {
-    __shared__ __attribute__((aligned(16))) char lds[2][2][BM * kRowBytes];  // [buf][A|B]
-    // Consecutive workgroups walk N within a band of M rows, so the band's
-    // activations stay cache-resident while the codes stream.
-    const int tiles_n = N / BN;
-    const int m0 = (blockIdx.x / tiles_n) * BM;
-    const int n0 = (blockIdx.x % tiles_n) * BN;
+    __shared__ GemmLds lds;
+    const int tiles_n = (N + BN - 1) / BN;
+    const int grid = gridDim.x;
+    int b = blockIdx.x;
+    if ((grid & 7) == 0) b = (b & 7) * (grid >> 3) + (b >> 3);
+    const int m0 = (b / tiles_n) * BM;
+    const int n0 = (b % tiles_n) * BN;
     gemm_tile_bf16(lds, a, codes, scales, zeros, out, m0, M, n0, K, N);
 }
 
@@ -216,12 +345,12 @@ __global__ __launch_bounds__(kThreads, 2) void int4_gemm_bf16_kernel(
 // position in the list of (expert, 128-row block) pairs, walked from the
 // offsets; blocks past the list's end exit.  Expert e's rows are
 // [off[e], min(off[e+1], T)) (groupedtiled.go:184-188).
-__global__ __launch_bounds__(kThreads, 2) void int4_grouped_bf16_kernel(
+__global__ __launch_bounds__(kThreads, 1) void int4_grouped_bf16_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
     const uint32_t* __restrict__ off, uint16_t* __restrict__ out, int E, int T, int K,
     int N) {
-    __shared__ __attribute__((aligned(16))) char lds[2][2][BM * kRowBytes];
+    __shared__ GemmLds lds;
     int idx = blockIdx.y;
     int e = 0, m0 = 0, m_end = 0;
     bool found = false;
@@ -322,13 +451,13 @@ __global__ __launch_bounds__(256) void int4_gemm_f32_kernel(
 }  // namespace
 
 bool int4_gemm_bf16_supported(int M, int K, int N) {
-    return M >= 1 && K >= BK && K % BK == 0 && N >= BN && N % BN == 0 &&
-           (uint64_t)K * (uint64_t)N < (1ull << 32);
+    return M >= 1 && K >= BK && K % BK == 0 && N >= 128 && N % 128 == 0 &&
+           K < (1 << 30) && N < (1 << 30);
 }
 
 hipError_t launch_int4_gemm_bf16(Device*, hipStream_t st, const uint16_t* a, Int4Planes w,
                                  uint16_t* out, int M, int K, int N) {
-    const int tiles = ((M + BM - 1) / BM) * (N / BN);
+    const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
     hipLaunchKernelGGL(int4_gemm_bf16_kernel, dim3(tiles), dim3(kThreads), 0, st, a, w.codes,
                        w.scales, w.zeros, out, M, K, N);
     return hipGetLastError();
@@ -341,7 +470,7 @@ hipError_t launch_int4_grouped_bf16(Device*, hipStream_t st, const uint16_t* x,
     // partial block.
     const int max_blocks = (T + BM - 1) / BM + E;
     if (max_blocks > 65535) return hipErrorInvalidConfiguration;
-    dim3 grid(N / BN, max_blocks);
+    dim3 grid((N + BN - 1) / BN, max_blocks);
     hipLaunchKernelGGL(int4_grouped_bf16_kernel, grid, dim3(kThreads), 0, st, x, w.codes,
                        w.scales, w.zeros, off, out, E, T, K, N);
     return hipGetLastError();
