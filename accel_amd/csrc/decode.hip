@@ -267,17 +267,22 @@ __global__ __launch_bounds__(kThreads) void int4_decode_f32_kernel(
         __hip_atomic_store(&tickets[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Slices so the launch has about two workgroups per CU, each lane at least
-// kRows rows of work.
+// Slices: each lane gets two fetch batches (2 * kRows rows) when that still
+// gives every CU a workgroup, else more slices down to one batch per lane.
+// Every slice costs the tail a device-coherent store, ticket and load, so
+// the split stops as soon as the launch fills the chip.
 template <int M, int TILE, int CPL>
 hipError_t launch_decode(Device* d, hipStream_t st, const float* a, Int4Planes w,
                          float* out, int K, int N, int* status) {
     constexpr int LPR = TILE / CPL;
     constexpr int RP = kThreads / LPR;
     const int tiles = N / TILE;
-    const int target_blocks = d->cu_count * 2;
-    int slices = std::max(1, (target_blocks + tiles - 1) / tiles);
-    slices = std::min(slices, std::max(1, K / (RP * kRows)));
+    int slices = std::max(1, K / (RP * 2 * kRows));
+    if (tiles * slices < d->cu_count)
+        slices = std::min(std::max(1, K / (RP * kRows)), (d->cu_count + tiles - 1) / tiles);
+    // Partial sums (M * N * 4 bytes a slice) stay within 1/8 of the codes.
+    slices = std::min(slices, std::max(1, K / (64 * M)));
+    slices = std::max(1, slices);
     int rows = (K + slices - 1) / slices;
     rows = (rows + RP - 1) / RP * RP;
     slices = (K + rows - 1) / rows;

@@ -103,3 +103,42 @@ def moe(tokens: int = 512, E: int = 8, top: int = 2, K: int = 4096, N: int = 143
 def algorithmic_bytes(M: int, K: int, N: int, act_bytes: int = 4, out_bytes: int = 4) -> int:
     """Bytes one product must move: codes + f16 scale/zero + activations + output."""
     return K * N // 2 + 4 * (K * N // 128) + act_bytes * M * K + out_bytes * M * N
+
+
+# Config 5: one Llama-3-8B-shaped decoder layer's seven projections, (K, N)
+# in the reference layout [K=in, N=out].
+LAYER_SHAPES = {
+    "q": (4096, 4096), "k": (4096, 1024), "v": (4096, 1024), "o": (4096, 4096),
+    "gate": (4096, 14336), "up": (4096, 14336), "down": (14336, 4096),
+}
+
+
+def fast_int4(K: int, N: int, rng) -> tuple:
+    """Packed int4 planes of a [K, N] ~ N(0, 0.02) weight drawn in float32
+    (benchmark inputs: fast to make, not the parity fixtures' f64 draw)."""
+    import accel_amd
+    w = rng.standard_normal((K, N), dtype=np.float32) * np.float32(0.02)
+    return accel_amd.int4_quantize(w)
+
+
+def moe_fast(tokens: int = 512, E: int = 8, top: int = 2, K: int = 4096, N: int = 14336,
+             seed: int = 3) -> MoE:
+    """Config 4's shape with float32 draws (benchmark inputs): top-2 routing of
+    a seeded softmax, rows sorted by expert, stable by token."""
+    import accel_amd
+    rng = np.random.Generator(np.random.PCG64(seed))
+    x = rng.standard_normal((tokens, K), dtype=np.float32)
+    x = bf16_to_f32(bf16_bits(x))
+    planes = [fast_int4(K, N, rng) for _ in range(E)]
+    logits = rng.standard_normal((tokens, E))
+    p = np.exp(logits - logits.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    chosen = np.argsort(-p, axis=1, kind="stable")[:, :top]
+    pairs = sorted(((int(e), t) for t in range(tokens) for e in chosen[t]))
+    order = np.array([t for _, t in pairs], np.int64)
+    experts = np.array([e for e, _ in pairs], np.int64)
+    counts = np.bincount(experts, minlength=E).astype(np.uint32)
+    packed = np.concatenate([pl[0] for pl in planes])
+    scales = np.concatenate([pl[1] for pl in planes])
+    zeros = np.concatenate([pl[2] for pl in planes])
+    return MoE(x[order], counts, packed, scales, zeros, E, K, N, tokens, order)

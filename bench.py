@@ -2,20 +2,27 @@
 """Benchmark of the int4 weight-only linear path on one MI355X.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-extra]
+                    [--configs]
 
-Headline (BASELINE.json's metric, M=1 leg): the decode product
+Headline (the M=1 leg of BASELINE.json's metric): the decode product
 Int4MatVec at M=1, K=N=4096, in the reference's int4 format (128-weight
 groups, f16 scale and zero), f32 activations and output.  One step is one
-product.  The weights rotate over enough device copies (> 512 MB in all) that
-the 256 MB Infinity Cache cannot hold them, so each step reads its weights
-from HBM.  K steps are captured into one HIP graph and replayed, bracketed
-by events on the stream they run on; ``value`` is algorithmic bytes per step
-over the per-step time.
+product.  The weights rotate over enough device copies (> 512 MB in all)
+that the 256 MB Infinity Cache cannot hold them, so each step reads its
+weights from HBM.  K steps are captured into one HIP graph and replayed,
+bracketed by HIP events on the stream they run on; ``value`` is algorithmic
+bytes per step over the per-step time, and ``roofline`` prices the same
+kernel against the HBM peak.  ``roofline.traffic`` is the HBM bytes a
+launch of that kernel moves, from the rocprofv3 FETCH_SIZE / WRITE_SIZE
+summary committed under profiles/ (null when absent).
 
-The M=2048 leg (bf16 prefill product, TFLOP/s against the dense bf16 MFMA
-peak) and the M=16 decode are reported under ``extra``.  ``cpu_baseline`` is
-the oracle's restatement of the reference CPU backend's algorithm
-(``oracle/``), timed on this host's cores on a bounded sample.
+The M=2048 leg of the metric (bf16 prefill product on the matrix cores,
+TFLOP/s against the dense bf16 peak) is reported under ``extra`` with a
+roofline object of its own.  ``--configs`` adds the other BASELINE shapes
+(M=16 decode, the ragged MoE product, the layer chain) to ``extra``.
+``cpu_baseline`` is the oracle's restatement of the reference CPU
+backend's algorithm (``oracle/``), timed on this host's cores on a bounded
+sample of the headline workload.
 
 Prints one JSON line.
 """
@@ -29,10 +36,14 @@ import time
 
 import numpy as np
 
+HERE = os.path.dirname(os.path.abspath(__file__))
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, vendor figure
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, vendor figure
 METRIC = ("int4 linear: HBM GB/s (% peak) at M=1; TFLOP/s (% MFMA peak) at M=2048")
 ROTATE_BYTES = 544 << 20       # weight copies in rotation, > 2x the Infinity Cache
+TRAFFIC_FILE = os.path.join(HERE, "profiles", "traffic.json")
+GEMV_KERNEL = "int4_decode_f32_kernel<1, 256, 32>"
+GEMM_KERNEL = "int4_gemm_bf16_kernel"
 
 
 def parse():
@@ -42,6 +53,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--configs", action="store_true",
+                    help="also time BASELINE configs 2, 4 and 5 (slower)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     return ap.parse_args()
 
@@ -52,8 +65,19 @@ def cpu_threads() -> int:
     return max(1, min(n, 16))
 
 
+def traffic_of(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed PMC summary."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)["kernels"][kernel]
+        return int(t["hbm_bytes_per_launch"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 class Timed:
-    """Captures `count` calls of `issue(i)` into a graph and times replays."""
+    """Captures `count` calls of `issue(i)` into a graph and times replays
+    with HIP events on the stream the graph runs on."""
 
     def __init__(self, dev, stream, issue, count):
         self.dev, self.stream = dev, stream
@@ -63,7 +87,7 @@ class Timed:
         self.exec = dev.capture_end(stream)
         self.e0, self.e1 = dev.event(), dev.event()
 
-    def run(self, replays: int) -> float:
+    def run(self, replays: int = 1) -> float:
         d = self.dev
         d.sync(self.stream)
         d.record(self.e0, self.stream)
@@ -80,75 +104,154 @@ class Timed:
         self.dev.destroy_event(self.e1)
 
 
-def bench_gemv(dev, stream, steps, warmup):
+def rotated_weights(dev, stream, L, total_bytes=ROTATE_BYTES):
+    """Device copies of L's int4 planes, enough that they exceed the cache."""
     import accel_amd
-    from accel_amd import F32, workloads
-    cfg = workloads.CONFIGS["gemv_m1"]
-    L = workloads.linear(**cfg)
-    K, N = L.K, L.N
     per_copy = L.packed.nbytes + L.scales.nbytes + L.zeros.nbytes
-    copies = max(1, -(-ROTATE_BYTES // per_copy))
-    w0 = dev.upload_int4(L.packed, L.scales, L.zeros, K * N)
+    copies = max(1, -(-total_bytes // per_copy))
+    w0 = dev.upload_int4(L.packed, L.scales, L.zeros, L.K * L.N)
     ws = [w0]
     for _ in range(copies - 1):
         w = accel_amd.Int4Weights(dev.alloc(w0.codes.shape, accel_amd.U32),
                                   dev.alloc(w0.scales.shape, accel_amd.F16),
-                                  dev.alloc(w0.zeros.shape, accel_amd.F16), K * N)
+                                  dev.alloc(w0.zeros.shape, accel_amd.F16), L.K * L.N)
         for src, dst in ((w0.codes, w.codes), (w0.scales, w.scales), (w0.zeros, w.zeros)):
             accel_amd._check(accel_amd.lib().accel_hip_copy(dev.index, stream, dst.ptr,
                                                             src.ptr, src.nbytes))
         ws.append(w)
     dev.sync(stream)
-    a = dev.upload(L.x[0])
-    out = dev.alloc((N,), F32)
-    # eager once per copy: sizes the workspace and checks the result
-    for w in ws:
-        dev.Int4MatVec(a, w, out, stream=stream)
+    return ws
+
+
+def time_product(dev, stream, L, call, steps, warmup, bf16=False):
+    """Per-call time of `call(a, w, out)` over rotated weights, in ms."""
+    from accel_amd import BF16, F32, workloads
+    ws = rotated_weights(dev, stream, L)
+    if bf16:
+        a = dev.upload(workloads.bf16_bits(L.x), BF16)
+        out = dev.alloc((L.M, L.N), BF16)
+    else:
+        a = dev.upload(L.x if L.M > 1 else L.x[0])
+        out = dev.alloc((L.M, L.N) if L.M > 1 else (L.N,), F32)
+    for w in ws:  # eager once per copy: sizes the workspace
+        call(a, w, out, stream)
     dev.sync(stream)
-    t = Timed(dev, stream, lambda i: dev.Int4MatVec(a, ws[i % copies], out, stream=stream),
-              steps)
     if warmup:
-        wt = Timed(dev, stream, lambda i: dev.Int4MatVec(a, ws[i % copies], out,
-                                                         stream=stream), warmup)
-        wt.run(1)
+        wt = Timed(dev, stream, lambda i: call(a, ws[i % len(ws)], out, stream), warmup)
+        wt.run()
         wt.close()
-    ms = t.run(1)
+    t = Timed(dev, stream, lambda i: call(a, ws[i % len(ws)], out, stream), steps)
+    ms = t.run() / steps
     t.close()
     got = out.numpy()
-    bytes_per = workloads.algorithmic_bytes(1, K, N)
-    ms_per = ms / steps
     for w in ws:
         w.free()
     a.free()
     out.free()
-    return dict(ms_per_step=ms_per, bytes=bytes_per, gbs=bytes_per / (ms_per * 1e-3) / 1e9,
-                copies=copies, L=L, out=got)
+    return ms, got, len(ws)
 
 
-def bench_gemm(dev, stream, name, reps=20):
-    from accel_amd import BF16, F32, workloads
-    cfg = workloads.CONFIGS[name]
-    L = workloads.linear(**cfg)
-    M, K, N = L.M, L.K, L.N
-    w = dev.upload_int4(L.packed, L.scales, L.zeros, K * N)
-    if L.bf16:
-        a = dev.upload(workloads.bf16_bits(L.x), BF16)
-        out = dev.alloc((M, N), BF16)
-    else:
-        a = dev.upload(L.x)
-        out = dev.alloc((M, N), F32)
-    dev.Int4MatMul(a, w, out, stream=stream)
-    dev.sync(stream)
-    t = Timed(dev, stream, lambda i: dev.Int4MatMul(a, w, out, stream=stream), reps)
-    t.run(1)
-    ms = t.run(1) / reps
-    t.close()
-    flops = 2.0 * M * N * K
+def bench_gemv(dev, stream, steps, warmup):
+    from accel_amd import workloads
+    L = workloads.linear(**workloads.CONFIGS["gemv_m1"])
+    ms, got, copies = time_product(dev, stream, L, lambda a, w, o, s: dev.Int4MatVec(a, w, o, s),
+                                   steps, warmup)
+    bytes_per = workloads.algorithmic_bytes(1, L.K, L.N)
+    return dict(ms=ms, bytes=bytes_per, gbs=bytes_per / (ms * 1e-3) / 1e9, copies=copies,
+                L=L, out=got)
+
+
+def bench_gemm(dev, stream, name, steps=40, warmup=4):
+    from accel_amd import workloads
+    L = workloads.linear(**workloads.CONFIGS[name])
+    ms, _, copies = time_product(dev, stream, L,
+                                 lambda a, w, o, s: dev.Int4MatMul(a, w, o, s), steps, warmup,
+                                 bf16=L.bf16)
+    flops = 2.0 * L.M * L.N * L.K
     act = 2 if L.bf16 else 4
-    bytes_per = workloads.algorithmic_bytes(M, K, N, act, act)
-    w.free(); a.free(); out.free()
+    bytes_per = workloads.algorithmic_bytes(L.M, L.K, L.N, act, act)
     return dict(ms=ms, us=ms * 1e3, tflops=flops / (ms * 1e-3) / 1e12,
-                gbs=bytes_per / (ms * 1e-3) / 1e9)
+                gbs=bytes_per / (ms * 1e-3) / 1e9, copies=copies, bytes=bytes_per)
+
+
+def bench_moe(dev, stream, steps=20):
+    """Config 4: Int4GroupedMatMul over 1024 routed bf16 rows, 8 experts."""
+    from accel_amd import BF16, U32, workloads
+    m = workloads.moe_fast()
+    R = int(m.counts.sum())
+    w = dev.upload_int4(m.packed, m.scales, m.zeros, m.E * m.K * m.N)
+    xb = dev.upload(workloads.bf16_bits(m.x), BF16)
+    cb = dev.upload(m.counts, U32)
+    ob = dev.alloc((R, m.N), BF16)
+    dev.Int4GroupedMatMul(xb, w, m.E, cb, ob, stream=stream)
+    dev.sync(stream)
+    t = Timed(dev, stream, lambda i: dev.Int4GroupedMatMul(xb, w, m.E, cb, ob, stream=stream),
+              steps)
+    t.run()
+    ms = t.run() / steps
+    t.close()
+    flops = 2.0 * R * m.K * m.N
+    for b in (xb, cb, ob):
+        b.free()
+    w.free()
+    return dict(us=round(ms * 1e3, 2), tflops=round(flops / (ms * 1e-3) / 1e12, 1),
+                rows=R, experts=m.E)
+
+
+_LAYER_PLANES = {}
+
+
+def bench_layer_chain(dev, stream, batch, steps=100):
+    """Config 5: one Llama-3-8B-shaped decoder layer's seven int4 products
+    as a decode step: q,k,v <- x; o <- q; gate,up <- o; down <- gate*up
+    (the gate*up product is the caller's; the step times the seven
+    products, chained on one stream)."""
+    import accel_amd
+    from accel_amd import F32, workloads
+    shapes = workloads.LAYER_SHAPES  # name -> (K, N)
+    rng = np.random.Generator(np.random.PCG64(4))
+    x = rng.standard_normal((batch, 4096)).astype(np.float32)
+    if not _LAYER_PLANES:
+        for name, (K, N) in shapes.items():
+            _LAYER_PLANES[name] = workloads.fast_int4(K, N, rng)
+    ws, bufs = {}, {}
+    total_bytes = 0
+    for name, (K, N) in shapes.items():
+        packed, scales, zeros = _LAYER_PLANES[name]
+        ws[name] = dev.upload_int4(packed, scales, zeros, K * N)
+        total_bytes += packed.nbytes + scales.nbytes + zeros.nbytes
+        bufs[name] = dev.alloc((batch, N) if batch > 1 else (N,), F32)
+    xin = dev.upload(x if batch > 1 else x[0])
+    inter = dev.alloc((batch, 14336) if batch > 1 else (14336,), F32)
+
+    def op(a, w, o):
+        if batch > 1:
+            dev.Int4MatMul(a, w, o, stream)
+        else:
+            dev.Int4MatVec(a, w, o, stream)
+
+    def step(i):
+        op(xin, ws["q"], bufs["q"])
+        op(xin, ws["k"], bufs["k"])
+        op(xin, ws["v"], bufs["v"])
+        op(bufs["q"], ws["o"], bufs["o"])
+        op(bufs["o"], ws["gate"], bufs["gate"])
+        op(bufs["o"], ws["up"], bufs["up"])
+        op(inter, ws["down"], bufs["down"])
+
+    step(0)
+    dev.sync(stream)
+    t = Timed(dev, stream, step, steps)
+    t.run()
+    ms = t.run() / steps
+    t.close()
+    for w in ws.values():
+        w.free()
+    for b in list(bufs.values()) + [xin, inter]:
+        b.free()
+    return dict(us_per_step=round(ms * 1e3, 2),
+                gbs=round(total_bytes / (ms * 1e-3) / 1e9, 1),
+                weight_bytes=total_bytes, batch=batch)
 
 
 def cpu_baseline(L, seconds):
@@ -168,18 +271,18 @@ def cpu_baseline(L, seconds):
     return dict(value=round(bytes_per * n / el / 1e9, 3), unit="GB/s", cores=threads,
                 kind="port",
                 sample=f"{n} calls of QuantMatVecInt4 at M=1 K=N=4096 in {el:.1f} s "
-                       f"(oracle/oracle.c, reference order, {threads} threads)")
+                       f"(oracle/oracle.c: the reference CPU algorithm restated in C, "
+                       f"reference evaluation order, {threads} threads)")
 
 
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported "
-              "(this build runs on a single MI355X; see DESIGN.md for how the path "
-              "would shard)", file=sys.stderr)
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (this build "
+              "runs on a single MI355X; DESIGN.md describes how the path would shard)",
+              file=sys.stderr)
         sys.exit(2)
     import accel_amd
-    from accel_amd import workloads
     if accel_amd.device_count() < 1:
         print("no HIP device", file=sys.stderr)
         sys.exit(1)
@@ -195,16 +298,17 @@ def main():
         "n_gpus": 1,
         "steps": steps,
         "warmup": args.warmup,
-        "ms_per_step": round(r["ms_per_step"], 6),
+        "ms_per_step": round(r["ms"], 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
         "config": {
-            "workload": "Int4MatVec M=1 K=4096 N=4096, int4 G=128 f16 scale+zero "
-                        "(BASELINE config 1 shape in the reference format), f32 x/out, "
-                        f"weights rotated over {r['copies']} device copies (HBM, not MALL)",
+            "workload": "Int4MatVec M=1 K=4096 N=4096 (BASELINE config 1's shape and the "
+                        "metric's M=1 leg) in the reference int4 format: 128-weight groups, "
+                        "f16 scale+zero; f32 activations and output; weights rotated over "
+                        f"{r['copies']} device copies so every step reads HBM",
             "seed": 0,
         },
         "roofline": {
@@ -213,21 +317,31 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "kernel": "int4_decode_f32_kernel<1, 32>",
+            "traffic": traffic_of(GEMV_KERNEL),
+            "kernel": GEMV_KERNEL,
             "bytes_per_launch": r["bytes"],
-            "us_per_launch": round(r["ms_per_step"] * 1e3, 4),
+            "us_per_launch": round(r["ms"] * 1e3, 4),
         },
     }
     if not args.no_extra:
-        extra = {}
         p = bench_gemm(dev, stream, "prefill_m2048")
-        extra["prefill_m2048_bf16"] = {
-            "tflops": round(p["tflops"], 2), "us": round(p["us"], 2),
-            "frac_of_bf16_peak": round(p["tflops"] / BF16_PEAK_TFLOPS, 4)}
-        d = bench_gemm(dev, stream, "decode_m16")
-        extra["decode_m16_f32"] = {"us": round(d["us"], 2), "gbs": round(d["gbs"], 1),
-                                   "frac_of_hbm": round(d["gbs"] / HBM_PEAK_GBS, 4)}
+        extra = {"prefill_m2048_bf16": {
+            "workload": "Int4MatMul M=2048 K=4096 N=4096, bf16 x/out, fp32 accumulate "
+                        "(BASELINE config 3, the metric's M=2048 leg)",
+            "us": round(p["us"], 2),
+            "roofline": {"bound": "mfma", "achieved": round(p["tflops"], 1),
+                         "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(p["tflops"] / BF16_PEAK_TFLOPS, 4),
+                         "traffic": traffic_of(GEMM_KERNEL), "kernel": GEMM_KERNEL,
+                         "flops_per_launch": 2 * 2048 * 4096 * 4096},
+        }}
+        if args.configs:
+            d = bench_gemm(dev, stream, "decode_m16", steps=200, warmup=10)
+            extra["decode_m16_f32"] = {"us": round(d["us"], 2), "gbs": round(d["gbs"], 1),
+                                       "frac_of_hbm": round(d["gbs"] / HBM_PEAK_GBS, 4)}
+            extra["moe_grouped_bf16"] = bench_moe(dev, stream)
+            extra["layer_chain_b1"] = bench_layer_chain(dev, stream, 1)
+            extra["layer_chain_b8"] = bench_layer_chain(dev, stream, 8)
         line["extra"] = extra
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(L, args.cpu_seconds)
