@@ -97,6 +97,58 @@ __device__ __forceinline__ float load_device(float* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Split-K hand-off, called by every lane of a workgroup after it stored its
+// sums for columns [col0, col0 + cols) of slice `slice` with store_device:
+// the stores are acknowledged by the device coherence point before the
+// tile's ticket is drawn, and the workgroup drawing the last ticket reads all
+// slices' sums with device-scope loads, adds them in slice order (so the
+// result does not depend on scheduling), writes `out` and returns the ticket
+// to zero for the next launch.
+__device__ __forceinline__ void split_k_finish(float* partial, uint32_t* tickets, float* out,
+                                               int tile, int col0, int cols, int M, int N,
+                                               int slices, int* last_flag) {
+    const int tid = threadIdx.x;
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t prev = __hip_atomic_fetch_add(&tickets[tile], 1u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+        *last_flag = prev == (uint32_t)(slices - 1);
+    }
+    __syncthreads();
+    if (!*last_flag) return;
+    const size_t slice_stride = (size_t)M * N;
+    for (int idx = tid; idx < M * cols; idx += blockDim.x) {
+        const int m = idx / cols;
+        const int col = col0 + idx % cols;
+        float* p = partial + (size_t)m * N + col;
+        float sum = 0.0f;
+        int sl = 0;
+        // up to sixteen slices' loads in flight at once
+        for (; sl + 16 <= slices; sl += 16) {
+            float v[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) v[u] = load_device(p + (size_t)(sl + u) * slice_stride);
+#pragma unroll
+            for (int u = 0; u < 16; u++) sum += v[u];
+        }
+        if (sl < slices) {
+            float v[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++)
+                v[u] = sl + u < slices ? load_device(p + (size_t)(sl + u) * slice_stride) : 0.0f;
+#pragma unroll
+            for (int u = 0; u < 16; u++)
+                if (sl + u < slices) sum += v[u];
+        }
+        out[(size_t)m * N + col] = sum;
+    }
+    if (tid == 0)
+        __hip_atomic_store(&tickets[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // One fetch batch: kRows rows of a lane's segment, with their scale, zero and
 // (for M <= 2) activations.  Rows past the slice are not fetched.
 template <int M, int WPL>
@@ -233,38 +285,7 @@ __global__ __launch_bounds__(kThreads) void int4_decode_f32_kernel(
     }
     if (!split) return;
 
-    // Hand-off: this workgroup's sums are acknowledged by the coherence point
-    // before its ticket is drawn; the last of the tile's slices adds them up.
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t prev = __hip_atomic_fetch_add(&tickets[tile], 1u, __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT);
-        last_flag = prev == (uint32_t)(slices - 1);
-    }
-    __syncthreads();
-    if (!last_flag) return;
-    const size_t slice_stride = (size_t)M * N;
-    for (int idx = tid; idx < M * TILE; idx += kThreads) {
-        const int m = idx / TILE;
-        const int col = tile * TILE + idx % TILE;
-        float* p = partial + (size_t)m * N + col;
-        float sum = 0.0f;
-        int sl = 0;
-        for (; sl + 8 <= slices; sl += 8) {
-            float v[8];
-#pragma unroll
-            for (int u = 0; u < 8; u++) v[u] = load_device(p + (size_t)(sl + u) * slice_stride);
-#pragma unroll
-            for (int u = 0; u < 8; u++) sum += v[u];
-        }
-        for (; sl < slices; sl++) sum += load_device(p + (size_t)sl * slice_stride);
-        out[(size_t)m * N + col] = sum;
-    }
-    if (tid == 0)
-        __hip_atomic_store(&tickets[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    split_k_finish(partial, tickets, out, tile, tile * TILE, TILE, M, N, slices, &last_flag);
 }
 
 // Slices: each lane gets two fetch batches (2 * kRows rows) when that still
@@ -364,6 +385,238 @@ __global__ void int4_generic_bf16_kernel(const uint16_t* __restrict__ a,
     out[i] = float_to_bf16_bits(acc);
 }
 
+// ---- 3..16 rows: the matrix cores ------------------------------------------
+//
+// With M rows of activations every weight feeds M FMAs, and past two rows the
+// VALU (not HBM) bounds the product.  This kernel moves the arithmetic onto
+// v_mfma_f32_16x16x32_bf16 and keeps f32 accuracy:
+//   * the activation rows are the MFMA's A side (16 rows; rows >= M are zero),
+//     scaled per (row k, group) to v = x * (512 s) and split exactly into three
+//     bf16 terms hi + mid + lo (each the RNE rounding of what is left; the
+//     residue is below 2^-27 |v|), so three MFMAs per tile give the product of
+//     v with an exact B to f32 accuracy;
+//   * B is the code itself, q * 2^-9, exact in bf16 (fp8 converter), so
+//     A' * B = x * s * q;
+//   * the zero point is the per-(row m, group) bias sum_k x * add,
+//     add = s == 0 ? z : -z*s, accumulated in f32 on the VALU.
+// A workgroup owns one 128-column group and a K slice; its four waves take
+// the slice's 32-k steps in turn and are summed through LDS.  The MFMA column
+// c of n-tile j is the physical column 8c + j, so lane c's eight n-tiles are
+// the eight nibbles of code word c, read straight from HBM (one u32 per row)
+// and paired (row, row+1) with v_perm for the bf16x2 operand.  Slices are
+// combined by split_k_finish.
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kMfmaCols = 128;      // one quantisation group
+constexpr int kMfmaMaxRows = 2048;  // rows of a slice whose fold fits in LDS
+
+struct MfmaDecodeLds {
+    f32x2 fold[kMfmaMaxRows];            // (512 s, add) per row of the slice
+    float red[4][16][kMfmaCols];         // per-wave sums
+    float bias[4][16];
+};
+
+__global__ __launch_bounds__(kThreads) void int4_decode_mfma_kernel(
+    const float* __restrict__ a, const uint32_t* __restrict__ codes,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
+    float* __restrict__ out, float* partial, uint32_t* tickets, int M, int K, int N,
+    int rows_per_slice, int slices) {
+    __shared__ __attribute__((aligned(16))) MfmaDecodeLds lds;
+    __shared__ int last_flag;
+
+    const int tiles = N / kMfmaCols;
+    const int grid = tiles * slices;
+    int b = blockIdx.x;
+    if ((grid & 7) == 0) b = (b & 7) * (grid >> 3) + (b >> 3);
+    const int tile = b % tiles;
+    const int slice = b / tiles;
+    const int n0 = tile * kMfmaCols;
+    const size_t g = (size_t)(n0 >> 7);
+    const size_t groups_per_row = (size_t)(N >> 7);
+    const size_t words_per_row = (size_t)(N >> 3);
+    const int k_begin = slice * rows_per_slice;
+    const int k_end = min(K, k_begin + rows_per_slice);
+    const int nrows = k_end - k_begin;
+    const int tid = threadIdx.x;
+
+    for (int r = tid; r < nrows; r += kThreads) {
+        const float s = half_bits_to_float(scales[(size_t)(k_begin + r) * groups_per_row + g]);
+        const float z = half_bits_to_float(zeros[(size_t)(k_begin + r) * groups_per_row + g]);
+        f32x2 f;
+        f.x = s * kNibbleScale;
+        f.y = (s == 0.0f) ? z : -(z * s);
+        lds.fold[r] = f;
+    }
+    __syncthreads();
+
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int c16 = lane & 15;   // A row (activation row m) / B and D column
+    const int kg = lane >> 4;    // k-group: 8 consecutive k of a 32-k step
+    const bool mrow = c16 < M;
+    const float* arow = a + (size_t)(mrow ? c16 : 0) * K;
+    const uint32_t* qcol = codes + (n0 >> 3) + c16;
+
+    f32x4 acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) acc[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    float bias = 0.0f;
+
+    // One step's global operands; the next step's are in flight while the
+    // current one is converted and multiplied.
+    struct StepRegs {
+        uint32_t wv[8];
+        f32x4 x0, x1;
+    };
+    auto fetch = [&](StepRegs& r, int stp) {
+        const int k = k_begin + stp * 32 + 8 * kg;
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            r.wv[e] = __builtin_nontemporal_load(qcol + (size_t)(k + e) * words_per_row);
+        r.x0 = (f32x4){0.f, 0.f, 0.f, 0.f};
+        r.x1 = r.x0;
+        if (mrow) {
+            r.x0 = *reinterpret_cast<const f32x4*>(arow + k);
+            r.x1 = *reinterpret_cast<const f32x4*>(arow + k + 4);
+        }
+    };
+    auto compute = [&](const StepRegs& r, int stp) {
+        const int r0 = stp * 32 + 8 * kg;          // first row of this lane, in the slice
+        const f32x4* fp = reinterpret_cast<const f32x4*>(&lds.fold[r0]);
+        const f32x4 f01 = fp[0], f23 = fp[1], f45 = fp[2], f67 = fp[3];
+        const float xv[8] = {r.x0.x, r.x0.y, r.x0.z, r.x0.w, r.x1.x, r.x1.y, r.x1.z, r.x1.w};
+        const float mul[8] = {f01.x, f01.z, f23.x, f23.z, f45.x, f45.z, f67.x, f67.z};
+        const float add[8] = {f01.y, f01.w, f23.y, f23.w, f45.y, f45.w, f67.y, f67.w};
+        bf16x8 ah, am, al;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float v = xv[e] * mul[e];
+            bias = __builtin_fmaf(xv[e], add[e], bias);
+            const __bf16 h = (__bf16)v;
+            const float r1 = v - (float)h;
+            const __bf16 md = (__bf16)r1;
+            const float r2 = r1 - (float)md;
+            ah[e] = h;
+            am[e] = md;
+            al[e] = (__bf16)r2;
+        }
+        // B: the code itself as bf16 pairs (row 2p, row 2p+1) straight from
+        // the fp8 bytes (scale 1).
+        uint32_t bw[8][4];
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const uint32_t w0 = r.wv[2 * p], w1 = r.wv[2 * p + 1];
+            const uint32_t t01 = __builtin_amdgcn_perm(w1, w0, 0x05010400u);  // bytes 0,1
+            const uint32_t t23 = __builtin_amdgcn_perm(w1, w0, 0x07030602u);  // bytes 2,3
+            const uint32_t q[4] = {t01 & 0x0F0F0F0Fu, (t01 >> 4) & 0x0F0F0F0Fu,
+                                   t23 & 0x0F0F0F0Fu, (t23 >> 4) & 0x0F0F0F0Fu};
+            // q[0]: columns 0, 2; q[1]: 1, 3; q[2]: 4, 6; q[3]: 5, 7
+#pragma unroll
+            for (int h = 0; h < 4; h++) {
+                const int c0 = (h >> 1) * 4 + (h & 1);   // 0, 1, 4, 5
+                bw[c0][p] = __builtin_bit_cast(
+                    uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q[h], 1.0f, false));
+                bw[c0 + 2][p] = __builtin_bit_cast(
+                    uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q[h], 1.0f, true));
+            }
+        }
+        bf16x8 bfr[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            bfr[j] = __builtin_bit_cast(bf16x8, (u32x4){bw[j][0], bw[j][1], bw[j][2], bw[j][3]});
+        // All hi products, then all mid, then all lo: each accumulator's
+        // consecutive MFMAs are eight apart.
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bfr[j], acc[j], 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(am, bfr[j], acc[j], 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bfr[j], acc[j], 0, 0, 0);
+    };
+
+    // A ring of kDepth steps in flight per wave: the loads of a step go out
+    // kDepth steps (of this wave) before it is used, which covers HBM
+    // latency with a wave's own strided row loads.
+    constexpr int kDepth = 4;
+    const int nsteps = nrows / 32;   // slices are whole 32-k steps
+    StepRegs ring[kDepth];
+#pragma unroll
+    for (int i = 0; i < kDepth; i++)
+        if (wave + 4 * i < nsteps) fetch(ring[i], wave + 4 * i);
+    for (int base = wave; base < nsteps; base += 4 * kDepth) {
+#pragma unroll
+        for (int i = 0; i < kDepth; i++) {
+            const int stp = base + 4 * i;
+            if (stp < nsteps) {
+                compute(ring[i], stp);
+                if (stp + 4 * kDepth < nsteps) fetch(ring[i], stp + 4 * kDepth);
+            }
+        }
+    }
+
+    // D of a 16 x 16 tile: lane holds column lane % 16, rows 4*(lane/16)+i.
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) lds.red[wave][kg * 4 + i][8 * c16 + j] = acc[j][i];
+    bias += __shfl_xor(bias, 16, 64);
+    bias += __shfl_xor(bias, 32, 64);
+    if (kg == 0) lds.bias[wave][c16] = bias;
+    __syncthreads();
+
+    const bool split = slices > 1;
+    for (int idx = tid; idx < M * kMfmaCols; idx += kThreads) {
+        const int m = idx / kMfmaCols;
+        const int c = idx % kMfmaCols;
+        const float v = ((lds.red[0][m][c] + lds.red[1][m][c]) +
+                         (lds.red[2][m][c] + lds.red[3][m][c])) +
+                        ((lds.bias[0][m] + lds.bias[1][m]) + (lds.bias[2][m] + lds.bias[3][m]));
+        if (split)
+            store_device(&partial[((size_t)slice * M + m) * N + n0 + c], v);
+        else
+            out[(size_t)m * N + n0 + c] = v;
+    }
+    if (!split) return;
+    split_k_finish(partial, tickets, out, tile, n0, kMfmaCols, M, N, slices, &last_flag);
+}
+
+// Slices: two workgroups per CU, partial sums within 1/8 of the codes, and
+// every slice a whole number of 32-k steps for each of the four waves.
+hipError_t launch_decode_mfma(Device* d, hipStream_t st, const float* a, Int4Planes w,
+                              float* out, int M, int K, int N, int* status) {
+    const int tiles = N / kMfmaCols;
+    constexpr int kQuantum = 32 * 4;
+    int slices = std::max(1, (2 * d->cu_count + tiles - 1) / tiles);
+    slices = std::min(slices, std::max(1, K / (64 * M)));
+    slices = std::min(slices, std::max(1, K / kQuantum));
+    slices = std::max(slices, (K + kMfmaMaxRows - 1) / kMfmaMaxRows);
+    int rows = (K + slices - 1) / slices;
+    rows = (rows + kQuantum - 1) / kQuantum * kQuantum;
+    if (rows > kMfmaMaxRows) rows = kMfmaMaxRows;
+    slices = (K + rows - 1) / rows;
+    float* partial = nullptr;
+    uint32_t* tickets = nullptr;
+    if (slices > 1) {
+        if ((size_t)tiles * sizeof(uint32_t) > kWorkspaceCounterBytes) {
+            *status = fail(ACCEL_E_INVALID,
+                           "decode product: N=%d needs more tickets than the workspace holds", N);
+            return hipSuccess;
+        }
+        void* ws = workspace(d, (size_t)slices * M * N * sizeof(float), status);
+        if (!ws) return hipSuccess;
+        tickets = static_cast<uint32_t*>(ws);
+        partial = reinterpret_cast<float*>(static_cast<char*>(ws) + kWorkspaceCounterBytes);
+    }
+    hipLaunchKernelGGL(int4_decode_mfma_kernel, dim3(tiles * slices), dim3(kThreads), 0, st, a,
+                       w.codes, w.scales, w.zeros, out, partial, tickets, M, K, N, rows, slices);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 bool int4_decode_f32_supported(int M, int K, int N, const void* codes) {
@@ -374,6 +627,9 @@ bool int4_decode_f32_supported(int M, int K, int N, const void* codes) {
 hipError_t launch_int4_decode_f32(Device* d, hipStream_t st, const float* a, Int4Planes w,
                                   float* out, int M, int K, int N, int* status) {
     *status = ACCEL_OK;
+    // Three or more rows: the matrix-core kernel, where its shape holds.
+    if (M >= 3 && K % 32 == 0 && (reinterpret_cast<uintptr_t>(a) & 15) == 0)
+        return launch_decode_mfma(d, st, a, w, out, M, K, N, status);
     switch (M) {
         case 1: return launch_decode_m<1>(d, st, a, w, out, K, N, status);
         case 2: return launch_decode_m<2>(d, st, a, w, out, K, N, status);
