@@ -100,20 +100,22 @@ __device__ __forceinline__ float load_device(float* p) {
 // Split-K hand-off, called by every lane of a workgroup after it stored its
 // sums for columns [col0, col0 + cols) of slice `slice` with store_device:
 // the stores are acknowledged by the device coherence point before the
-// tile's ticket is drawn, and the workgroup drawing the last ticket reads all
+// tile's ticket is drawn (each tile's ticket has a 128-byte line of its own
+// where the workspace allows, so the atomics of different tiles do not queue
+// behind each other), and the workgroup drawing the last ticket reads all
 // slices' sums with device-scope loads, adds them in slice order (so the
 // result does not depend on scheduling), writes `out` and returns the ticket
 // to zero for the next launch.
-__device__ __forceinline__ void split_k_finish(float* partial, uint32_t* tickets, float* out,
-                                               int tile, int col0, int cols, int M, int N,
-                                               int slices, int* last_flag) {
+__device__ __forceinline__ void split_k_finish(float* partial, uint32_t* ticket, float* out,
+                                               int col0, int cols, int M, int N, int slices,
+                                               int* last_flag) {
     const int tid = threadIdx.x;
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(0);
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __syncthreads();
     if (tid == 0) {
-        const uint32_t prev = __hip_atomic_fetch_add(&tickets[tile], 1u, __ATOMIC_RELAXED,
+        const uint32_t prev = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED,
                                                      __HIP_MEMORY_SCOPE_AGENT);
         *last_flag = prev == (uint32_t)(slices - 1);
     }
@@ -146,30 +148,104 @@ __device__ __forceinline__ void split_k_finish(float* partial, uint32_t* tickets
         out[(size_t)m * N + col] = sum;
     }
     if (tid == 0)
-        __hip_atomic_store(&tickets[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// One fetch batch: kRows rows of a lane's segment, with their scale, zero and
-// (for M <= 2) activations.  Rows past the slice are not fetched.
+// Cross-lane sums over the row phases of a wave.  A wave holds 64 / LPR row
+// phases of LPR lanes each (lane l belongs to row phase l / LPR); every lane
+// has n accumulators for its columns.  Each stage halves the values a lane
+// holds and doubles the row phases they cover: lanes whose bit D is clear
+// keep the first half of the columns, the others the second half, and each
+// adds its partner's (lane l ^ D) copy of the half it keeps.  D = 32 and 16
+// use the swap-permutes (one instruction moves a pair of values between the
+// two halves of the wave, or between adjacent 16-lane rows), D = 8 a DPP
+// rotation within 16-lane rows, smaller D a cross-lane read.  Stages run
+// from D = 32 down to D = LPR, so the result sums all row phases of the
+// wave; lane l ends with n * LPR / 64 values, the columns given by
+// reduced_offset.
+template <int D>
+__device__ __forceinline__ float xor_partner(float x, int l) {
+    if constexpr (D == 8) {
+        // row_ror:8 within 16-lane rows: lane l reads lane l ^ 8
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xf, 0xf,
+                                                          false));
+    } else {
+        return __int_as_float(__builtin_amdgcn_ds_bpermute((l ^ D) << 2, __float_as_int(x)));
+    }
+}
+template <int n, int D, int LPR>
+__device__ __forceinline__ void transpose_reduce(float* v, int l) {
+    if constexpr (D >= LPR) {
+        constexpr int h = n / 2;
+        if constexpr (D == 32 || D == 16) {
+#pragma unroll
+            for (int j = 0; j < h; j++) {
+                const auto r = D == 32 ? __builtin_amdgcn_permlane32_swap(
+                                             __float_as_uint(v[j]), __float_as_uint(v[h + j]),
+                                             false, false)
+                                       : __builtin_amdgcn_permlane16_swap(
+                                             __float_as_uint(v[j]), __float_as_uint(v[h + j]),
+                                             false, false);
+                v[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+            }
+        } else {
+            const bool upper = (l & D) != 0;
+#pragma unroll
+            for (int j = 0; j < h; j++) {
+                const float keep = upper ? v[h + j] : v[j];
+                const float send = upper ? v[j] : v[h + j];
+                v[j] = keep + xor_partner<D>(send, l);
+            }
+        }
+        transpose_reduce<h, D / 2, LPR>(v, l);
+    }
+}
+// Column offset (within the lane's CPL columns) of the values transpose_reduce
+// leaves in lane l.
+template <int n, int D, int LPR>
+__device__ __forceinline__ int reduced_offset(int l) {
+    if constexpr (D >= LPR) {
+        return ((l & D) ? n / 2 : 0) + reduced_offset<n / 2, D / 2, LPR>(l);
+    } else {
+        return 0;
+    }
+}
+
+// One fetch batch: the codes of kRows rows of a lane's segment, plus the
+// one (row, group) of the wave's batch whose scale, zero and activations
+// this lane loads (see the kernel).
 template <int M, int WPL>
 struct Batch {
     uint32_t q[kRows][WPL];
-    uint16_t s[kRows], z[kRows];
-    float x[kRows][M <= 2 ? M : 1];
+    uint16_t s, z;
+    float x[M];
 };
 
 // M rows of activations; TILE columns per workgroup, CPL per lane.
+//
+// Scales and zeros.  A wave's batch spans RPW = 64 / LPR row phases times
+// kRows rows and GPT = TILE / 128 groups per row: V = 2 * CPL <= 64 (row,
+// group) pairs.  Lane v < V of the wave loads pair v's scale, zero and
+// activations with one 2-byte load each, folds them into x*s*512 and the
+// bias term, and the lanes that decode that pair's codes fetch the two
+// values with a cross-lane read (ds_bpermute).  One load per pair instead
+// of one per lane and row keeps the small, scattered scale reads off the
+// memory pipeline's critical path.
 template <int M, int TILE, int CPL>
 __global__ __launch_bounds__(kThreads) void int4_decode_f32_kernel(
     const float* __restrict__ a, const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
-    float* __restrict__ out, float* partial, uint32_t* tickets, int K, int N,
+    float* __restrict__ out, float* partial, uint32_t* tickets, int ticket_stride, int K, int N,
     int rows_per_slice, int slices) {
     constexpr int LPR = TILE / CPL;     // lanes per row
     constexpr int RP = kThreads / LPR;  // row phases
+    constexpr int RPW = 64 / LPR;       // row phases per wave
+    constexpr int GPT = TILE / 128;     // groups per row of a tile
     constexpr int WPL = CPL / 8;        // code words per lane per row
-    constexpr bool kXInBatch = M <= 2;
-    __shared__ __attribute__((aligned(16))) float red[RP][TILE];
+    constexpr int V = RPW * kRows * GPT;
+    static_assert(V <= 64, "one (row, group) pair per lane");
+    static_assert(kThreads == 256, "four waves per workgroup");
+    __shared__ __attribute__((aligned(16))) float red[4][TILE];
     __shared__ int last_flag;
 
     const int tiles = N / TILE;
@@ -183,12 +259,23 @@ __global__ __launch_bounds__(kThreads) void int4_decode_f32_kernel(
     const int lane = tid % LPR;
     const int rp = tid / LPR;
     const int col0 = tile * TILE + lane * CPL;
-    const int g = col0 >> 7;
     const size_t groups_per_row = (size_t)(N >> 7);
     const size_t words_per_row = (size_t)(N >> 3);
     const int k_begin = slice * rows_per_slice;
     const int k_end = min(K, k_begin + rows_per_slice);
     const uint32_t* qcol = codes + (col0 >> 3);
+
+    // The pair this lane loads: row phase (wave, pj), batch row pi, group ph.
+    const int l64 = tid & 63;
+    const int wave = tid >> 6;
+    const int ph = l64 % GPT;
+    const int pi = (l64 / GPT) / RPW;
+    const int pj = (l64 / GPT) % RPW;
+    const bool loader = l64 < V;
+    const int prow_off = pi * RP + wave * RPW + pj;  // row offset within a batch
+    const size_t pgroup = (size_t)tile * GPT + ph;
+    // The lanes holding this lane's pairs, row i of a batch at src + i*RPW*GPT.
+    const int src0 = ((l64 / LPR) * GPT + (lane * CPL) / 128) << 2;
 
     float acc[M][CPL];
     float bias[M];
@@ -199,38 +286,50 @@ __global__ __launch_bounds__(kThreads) void int4_decode_f32_kernel(
         for (int j = 0; j < CPL; j++) acc[m][j] = 0.0f;
     }
 
-    auto fetch = [&](Batch<M, WPL>& bt, int k) {
+    // kb: the batch's first row; this lane's rows are kb + rp + i*RP.
+    auto fetch = [&](Batch<M, WPL>& bt, int kb) {
 #pragma unroll
         for (int i = 0; i < kRows; i++) {
-            const int row = k + i * RP;
-            if (row < k_end) {
-                load_words<WPL>(qcol + (size_t)row * words_per_row, bt.q[i]);
-                bt.s[i] = scales[(size_t)row * groups_per_row + g];
-                bt.z[i] = zeros[(size_t)row * groups_per_row + g];
-                if constexpr (kXInBatch) {
+            const int row = kb + rp + i * RP;
+            if (row < k_end) load_words<WPL>(qcol + (size_t)row * words_per_row, bt.q[i]);
+        }
+        const int prow = kb + prow_off;
+        if (loader && prow < k_end) {
+            bt.s = scales[(size_t)prow * groups_per_row + pgroup];
+            bt.z = zeros[(size_t)prow * groups_per_row + pgroup];
 #pragma unroll
-                    for (int m = 0; m < M; m++) bt.x[i][m] = a[(size_t)m * K + row];
-                }
-            }
+            for (int m = 0; m < M; m++) bt.x[m] = a[(size_t)m * K + prow];
+        } else {
+            bt.s = 0;
+            bt.z = 0;
+#pragma unroll
+            for (int m = 0; m < M; m++) bt.x[m] = 0.0f;
         }
     };
-    auto compute = [&](const Batch<M, WPL>& bt, int k) {
+    auto compute = [&](const Batch<M, WPL>& bt, int kb) {
+        // Fold the loaded pair: x*w = (x*s*512) * (q * 2^-9) + add.
+        const float s = half_bits_to_float(bt.s);
+        const float z = half_bits_to_float(bt.z);
+        float pxs[M], padd[M];
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            const float xsm = bt.x[m] * s;
+            padd[m] = (s == 0.0f) ? bt.x[m] * z : -(xsm * z);
+            pxs[m] = xsm * kNibbleScale;
+        }
 #pragma unroll
         for (int i = 0; i < kRows; i++) {
-            const int row = k + i * RP;
-            if (row < k_end) {
-                const float s = half_bits_to_float(bt.s[i]);
-                const float z = half_bits_to_float(bt.z[i]);
-                float xs[M];
+            const int src = src0 + ((i * RPW * GPT) << 2);
+            float xs[M];
 #pragma unroll
-                for (int m = 0; m < M; m++) {
-                    float x;
-                    if constexpr (kXInBatch) x = bt.x[i][m];
-                    else x = a[(size_t)m * K + row];
-                    const float xsm = x * s;
-                    bias[m] += (s == 0.0f) ? x * z : -(xsm * z);
-                    xs[m] = xsm * kNibbleScale;
-                }
+            for (int m = 0; m < M; m++) {
+                xs[m] = __int_as_float(
+                    __builtin_amdgcn_ds_bpermute(src, __float_as_int(pxs[m])));
+                const float add = __int_as_float(
+                    __builtin_amdgcn_ds_bpermute(src, __float_as_int(padd[m])));
+                if (kb + rp + i * RP < k_end) bias[m] += add;
+            }
+            if (kb + rp + i * RP < k_end) {
 #pragma unroll
                 for (int wi = 0; wi < WPL; wi++) {
                     float f[8];
@@ -247,34 +346,39 @@ __global__ __launch_bounds__(kThreads) void int4_decode_f32_kernel(
     };
 
     // Two named buffers so the next batch is in flight while one is used.
+    // The loop runs on the wave-uniform batch base, so every lane takes part
+    // in the cross-lane reads.
     constexpr int kStep = kRows * RP;
     Batch<M, WPL> b0, b1;
-    int k = k_begin + rp;
-    if (k < k_end) fetch(b0, k);
-    while (k < k_end) {
-        if (k + kStep < k_end) fetch(b1, k + kStep);
-        compute(b0, k);
-        k += kStep;
-        if (k >= k_end) break;
-        if (k + kStep < k_end) fetch(b0, k + kStep);
-        compute(b1, k);
-        k += kStep;
+    int kb = k_begin;
+    fetch(b0, kb);
+    while (kb < k_end) {
+        if (kb + kStep < k_end) fetch(b1, kb + kStep);
+        compute(b0, kb);
+        kb += kStep;
+        if (kb >= k_end) break;
+        if (kb + kStep < k_end) fetch(b0, kb + kStep);
+        compute(b1, kb);
+        kb += kStep;
     }
 
+    // Row-phase sums: first across the wave's RPW row phases in registers
+    // (transpose_reduce), then across the four waves through LDS.
     const bool split = slices > 1;
+    constexpr int NV = CPL / RPW;  // column sums a lane holds after the wave stage
 #pragma unroll
     for (int m = 0; m < M; m++) {
+        float v[CPL];
 #pragma unroll
-        for (int j = 0; j < CPL; j += 4) {
-            const float4 v = make_float4(acc[m][j] + bias[m], acc[m][j + 1] + bias[m],
-                                         acc[m][j + 2] + bias[m], acc[m][j + 3] + bias[m]);
-            *reinterpret_cast<float4*>(&red[rp][lane * CPL + j]) = v;
-        }
+        for (int j = 0; j < CPL; j++) v[j] = acc[m][j] + bias[m];
+        transpose_reduce<CPL, 64 / 2, LPR>(v, l64);
+        // Lane l64 now holds the wave's sums of columns c0 .. c0 + NV - 1.
+        const int c0 = lane * CPL + reduced_offset<CPL, 64 / 2, LPR>(l64);
+#pragma unroll
+        for (int e = 0; e < NV; e++) red[wave][c0 + e] = v[e];
         __syncthreads();
         for (int c = tid; c < TILE; c += kThreads) {
-            float sum = 0.0f;
-#pragma unroll 8
-            for (int p = 0; p < RP; p++) sum += red[p][c];
+            const float sum = (red[0][c] + red[1][c]) + (red[2][c] + red[3][c]);
             const int col = tile * TILE + c;
             if (split)
                 store_device(&partial[((size_t)slice * M + m) * N + col], sum);
@@ -285,7 +389,18 @@ __global__ __launch_bounds__(kThreads) void int4_decode_f32_kernel(
     }
     if (!split) return;
 
-    split_k_finish(partial, tickets, out, tile, tile * TILE, TILE, M, N, slices, &last_flag);
+    split_k_finish(partial, tickets + (size_t)tile * ticket_stride, out, tile * TILE, TILE, M, N,
+                   slices, &last_flag);
+}
+
+// Spacing of the tiles' tickets in u32 words: 32 (one 128-byte line each)
+// when the counter area holds that many, else the widest power of two that
+// fits; 0 when not even one word per tile fits.
+int ticket_stride(int tiles) {
+    const size_t words = kWorkspaceCounterBytes / sizeof(uint32_t);
+    for (int stride = 32; stride >= 1; stride >>= 1)
+        if ((size_t)tiles * stride <= words) return stride;
+    return 0;
 }
 
 // Slices: each lane gets two fetch batches (2 * kRows rows) when that still
@@ -309,8 +424,10 @@ hipError_t launch_decode(Device* d, hipStream_t st, const float* a, Int4Planes w
     slices = (K + rows - 1) / rows;
     float* partial = nullptr;
     uint32_t* tickets = nullptr;
+    int stride = 0;
     if (slices > 1) {
-        if ((size_t)tiles * sizeof(uint32_t) > kWorkspaceCounterBytes) {
+        stride = ticket_stride(tiles);
+        if (stride == 0) {
             *status = fail(ACCEL_E_INVALID,
                            "decode product: N=%d needs more tickets than the workspace holds", N);
             return hipSuccess;
@@ -322,7 +439,7 @@ hipError_t launch_decode(Device* d, hipStream_t st, const float* a, Int4Planes w
     }
     hipLaunchKernelGGL((int4_decode_f32_kernel<M, TILE, CPL>), dim3(tiles * slices),
                        dim3(kThreads), 0, st, a, w.codes, w.scales, w.zeros, out, partial,
-                       tickets, K, N, rows, slices);
+                       tickets, stride, K, N, rows, slices);
     return hipGetLastError();
 }
 
@@ -421,7 +538,8 @@ struct MfmaDecodeLds {
 __global__ __launch_bounds__(kThreads) void int4_decode_mfma_kernel(
     const float* __restrict__ a, const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
-    float* __restrict__ out, float* partial, uint32_t* tickets, int M, int K, int N,
+    float* __restrict__ out, float* partial, uint32_t* tickets, int ticket_stride, int M, int K,
+    int N,
     int rows_per_slice, int slices) {
     __shared__ __attribute__((aligned(16))) MfmaDecodeLds lds;
     __shared__ int last_flag;
@@ -582,7 +700,8 @@ __global__ __launch_bounds__(kThreads) void int4_decode_mfma_kernel(
             out[(size_t)m * N + n0 + c] = v;
     }
     if (!split) return;
-    split_k_finish(partial, tickets, out, tile, n0, kMfmaCols, M, N, slices, &last_flag);
+    split_k_finish(partial, tickets + (size_t)tile * ticket_stride, out, n0, kMfmaCols, M, N,
+                   slices, &last_flag);
 }
 
 // Slices: two workgroups per CU, partial sums within 1/8 of the codes, and
@@ -601,8 +720,10 @@ hipError_t launch_decode_mfma(Device* d, hipStream_t st, const float* a, Int4Pla
     slices = (K + rows - 1) / rows;
     float* partial = nullptr;
     uint32_t* tickets = nullptr;
+    int stride = 0;
     if (slices > 1) {
-        if ((size_t)tiles * sizeof(uint32_t) > kWorkspaceCounterBytes) {
+        stride = ticket_stride(tiles);
+        if (stride == 0) {
             *status = fail(ACCEL_E_INVALID,
                            "decode product: N=%d needs more tickets than the workspace holds", N);
             return hipSuccess;
@@ -613,7 +734,8 @@ hipError_t launch_decode_mfma(Device* d, hipStream_t st, const float* a, Int4Pla
         partial = reinterpret_cast<float*>(static_cast<char*>(ws) + kWorkspaceCounterBytes);
     }
     hipLaunchKernelGGL(int4_decode_mfma_kernel, dim3(tiles * slices), dim3(kThreads), 0, st, a,
-                       w.codes, w.scales, w.zeros, out, partial, tickets, M, K, N, rows, slices);
+                       w.codes, w.scales, w.zeros, out, partial, tickets, stride, M, K, N, rows,
+                       slices);
     return hipGetLastError();
 }
 
