@@ -49,9 +49,10 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int BM = 128, BN = 256, BK = 64;
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;        // eight waves: two per SIMD
 constexpr int kARowBytes = BK * 2;   // one LDS activation row: 64 bf16
 constexpr int kBQuadWords = BN / 2;  // u32 words per row quad: one per code byte
+constexpr int kStages = 2;           // LDS ring depth
 
 __device__ __forceinline__ float half_bits_to_float(uint16_t h) {
     _Float16 v;
@@ -62,7 +63,7 @@ __device__ __forceinline__ float half_bits_to_float(uint16_t h) {
 // Byte offset of 16-byte chunk `c` of activation row `r` under the swizzle:
 // LDS has 64 banks (256 bytes), two rows wide; each row pair puts a chunk
 // index on its own 16-byte bank group, so a fragment read (32 rows, one
-// chunk) and a staging write (one row, eight chunks) do not conflict.
+// chunk) does not conflict.
 __device__ __forceinline__ int a_off(int r, int c) {
     return r * kARowBytes + ((c ^ ((r >> 1) & 7)) << 4);
 }
@@ -88,18 +89,23 @@ __device__ __forceinline__ u32x4 transpose4(uint32_t r0, uint32_t r1, uint32_t r
     return o;
 }
 
-constexpr int kStages = 3;   // LDS ring depth (and register sets in flight)
-
-struct __attribute__((aligned(16))) GemmLds {
-    char a[kStages][BM * kARowBytes];               // 3 x 16 KB
-    uint32_t b[kStages][(BK / 4) * kBQuadWords];    // 3 x 8 KB: [row quad][code byte]
+struct __attribute__((aligned(16))) GemmRing {
+    char a[kStages][BM * kARowBytes];               // 2 x 16 KB
+    uint32_t b[kStages][(BK / 4) * kBQuadWords];    // 2 x 8 KB: [row quad][code byte]
     f32x2 fold[kStages][2][BK];                     // [buf][group of the tile][row]
+};
+struct __attribute__((aligned(16))) GemmLds {
+    union {
+        GemmRing ring;
+        // Accumulator hand-off of the wave pairs: [column quarter][quad][lane].
+        f32x4 red[4][32][64];
+    };
 };
 
 // One stage's global loads, held in registers until written to LDS.
 struct StageRegs {
-    u32x4 a[4];
-    u32x2 b[4];
+    u32x4 a[2];
+    uint32_t b[4];
     uint16_t s, z;
 };
 
@@ -116,12 +122,16 @@ struct SubstepRegs {
 // from clamped columns and not stored).  codes/scales/zeros describe the
 // [K, N] matrix in use.
 //
-// Pipeline.  Stage kt (64 k) reads LDS buffer kt % 3.  During it the wave
-// issues the global loads of stage kt+3 into register set kt % 3, writes set
-// (kt+2) % 3 (stage kt+2, loaded one stage earlier) into buffer (kt+2) % 3,
-// and runs the stage's four 16-k substeps so that the LDS reads of substep
-// s+2 and the dequantisation of substep s+1 overlap the MFMAs of substep s;
-// the last substeps read ahead into buffer (kt+1) % 3, completed before the
+// Waves.  Wave w owns columns [64 (w%4), 64 (w%4) + 64) and all 128 rows;
+// waves w and w + 4 (one per SIMD pair slot) split every 64-k stage, the
+// first taking its 16-k substeps 0 and 2, the second 1 and 3, and their
+// accumulators are added at the end.  Two waves per SIMD let one wave's
+// dequantisation and LDS reads issue while the other's MFMAs run.
+//
+// Pipeline.  Stage kt (64 k) reads LDS buffer kt % 2.  During it the
+// workgroup issues the global loads of stage kt+2 into register set kt % 2
+// and at its end writes set (kt+1) % 2 (stage kt+1, loaded a stage earlier)
+// into buffer (kt+1) % 2, which every wave finished reading before the
 // previous barrier.  One barrier per stage.
 __device__ __forceinline__ void gemm_tile_bf16(GemmLds& lds, const uint16_t* __restrict__ a,
                                                const uint32_t* __restrict__ codes,
@@ -131,34 +141,37 @@ __device__ __forceinline__ void gemm_tile_bf16(GemmLds& lds, const uint16_t* __r
                                                int n0, int K, int N) {
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
+    const int wq = wave & 3;     // column quarter
+    const int wp = wave >> 2;    // substep parity
     const int lane = tid & 63;
     const int c32 = lane & 31;   // MFMA row (A) / column (B, D) within a 32 x 32 tile
     const int kg = lane >> 5;    // MFMA k-group (8 consecutive k)
     const size_t groups_per_row = (size_t)(N >> 7);
     const size_t words_per_row = (size_t)(N >> 3);
     const bool half_tile = n0 + BN > N;   // only the first 128 columns exist
+    GemmRing& ring = lds.ring;
 
-    // Activation staging: 1024 chunks of 16 bytes, four per lane.
-    const uint16_t* a_src[4];
-    int a_dst[4];
+    // Activation staging: 1024 chunks of 16 bytes a stage, two per lane.
+    const uint16_t* a_src[2];
+    int a_dst[2];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < 2; i++) {
         const int q = tid + kThreads * i;
         const int r = q >> 3, c = q & 7;
         const int row = min(m0 + r, m_end - 1);
         a_src[i] = a + (size_t)row * K + c * 8;
         a_dst[i] = a_off(r, c);
     }
-    // Code staging: row quad tid / 16, 16-column chunk tid % 16 (8 bytes of
-    // each of the quad's four rows).
-    const int b_rq = tid >> 4;
-    const int b_ch = tid & 15;
-    const int b_col = (half_tile && b_ch >= 8) ? n0 + (b_ch - 8) * 16 : n0 + b_ch * 16;
-    const uint32_t* b_src = codes + (size_t)(4 * b_rq) * words_per_row + (b_col >> 3);
-    const int b_dst0 = b_off(b_rq, 8 * b_ch), b_dst1 = b_off(b_rq, 8 * b_ch + 4);
-    // Fold staging: one (row, group of the tile) per lane, lanes 128..255
-    // repeating lanes 0..127 (the same value to the same place) so the stage
-    // body has no branch.
+    // Code staging: row quad tid / 32, word column tid % 32 (four code bytes
+    // of each of the quad's four rows).
+    const int b_rq = tid >> 5;
+    const int b_wc = tid & 31;
+    const int b_src_wc = (half_tile && b_wc >= 16) ? b_wc - 16 : b_wc;
+    const uint32_t* b_src = codes + (size_t)(4 * b_rq) * words_per_row + (n0 >> 3) + b_src_wc;
+    const int b_dst = b_off(b_rq, 4 * b_wc);
+    // Fold staging: one (row, group of the tile) per lane, lanes 128..511
+    // repeating lanes 0..127 (the same value to the same place) so the
+    // stage body has no branch and every lane issues the same loads.
     const int f_row = tid & 63;
     const int f_grp = (tid >> 6) & 1;
     const size_t f_g = (size_t)(n0 >> 7) + ((half_tile && f_grp) ? 0 : f_grp);
@@ -166,49 +179,46 @@ __device__ __forceinline__ void gemm_tile_bf16(GemmLds& lds, const uint16_t* __r
     const uint16_t* z_src = zeros + (size_t)f_row * groups_per_row + f_g;
     const int ktiles = K / BK;
 
-    // Loads of stage kt, clamped to the last stage (a load past the end is
-    // repeated work, never used).
+    // Stage indices past the end are clamped to the last stage: the loads
+    // repeat valid data and land in buffers no later stage reads.
     auto load_global = [&](StageRegs& g, int kt) {
         const int k0 = min(kt, ktiles - 1) * BK;
 #pragma unroll
-        for (int i = 0; i < 4; i++) g.a[i] = *reinterpret_cast<const u32x4*>(a_src[i] + k0);
+        for (int i = 0; i < 2; i++) g.a[i] = *reinterpret_cast<const u32x4*>(a_src[i] + k0);
         const uint32_t* bp = b_src + (size_t)k0 * words_per_row;
 #pragma unroll
         for (int i = 0; i < 4; i++)
-            g.b[i] = __builtin_nontemporal_load(
-                reinterpret_cast<const u32x2*>(bp + (size_t)i * words_per_row));
+            g.b[i] = __builtin_nontemporal_load(bp + (size_t)i * words_per_row);
         g.s = s_src[(size_t)k0 * groups_per_row];
         g.z = z_src[(size_t)k0 * groups_per_row];
     };
-    auto store_lds = [&](const StageRegs& g, int buf) {
+    auto store_lds = [&](const StageRegs& g, auto BUF) {
+        constexpr int buf = decltype(BUF)::value;
 #pragma unroll
-        for (int i = 0; i < 4; i++) *reinterpret_cast<u32x4*>(lds.a[buf] + a_dst[i]) = g.a[i];
-        *reinterpret_cast<u32x4*>(&lds.b[buf][b_dst0]) =
-            transpose4(g.b[0].x, g.b[1].x, g.b[2].x, g.b[3].x);
-        *reinterpret_cast<u32x4*>(&lds.b[buf][b_dst1]) =
-            transpose4(g.b[0].y, g.b[1].y, g.b[2].y, g.b[3].y);
+        for (int i = 0; i < 2; i++) *reinterpret_cast<u32x4*>(ring.a[buf] + a_dst[i]) = g.a[i];
+        *reinterpret_cast<u32x4*>(&ring.b[buf][b_dst]) = transpose4(g.b[0], g.b[1], g.b[2], g.b[3]);
         const float s = half_bits_to_float(g.s);
         const float z = half_bits_to_float(g.z);
         f32x2 f;
         f.x = s * 512.0f;
         f.y = (s == 0.0f) ? z : -(z * s);
-        lds.fold[buf][f_grp][f_row] = f;
+        ring.fold[buf][f_grp][f_row] = f;
     };
+    // This wave's code byte: columns 64*wq + 2*c32 and +1 of the tile.
+    const int my_bc = 32 * wq + c32;
+    const int my_grp = wq >> 1;
 
-    // This wave's code byte: columns 64*wave + 2*c32 and +1 of the tile.
-    const int my_bc = 32 * wave + c32;
-    const int my_grp = wave >> 1;
-
-    auto read_substep = [&](SubstepRegs& r, int buf, int ks) {
+    auto read_substep = [&](SubstepRegs& r, auto BUF, int ks) {
+        constexpr int buf = decltype(BUF)::value;
 #pragma unroll
-        for (int i = 0; i < 2; i++) r.tw[i] = lds.b[buf][b_off(ks * 4 + 2 * kg + i, my_bc)];
+        for (int i = 0; i < 2; i++) r.tw[i] = ring.b[buf][b_off(ks * 4 + 2 * kg + i, my_bc)];
         const f32x4* fp =
-            reinterpret_cast<const f32x4*>(&lds.fold[buf][my_grp][ks * 16 + 8 * kg]);
+            reinterpret_cast<const f32x4*>(&ring.fold[buf][my_grp][ks * 16 + 8 * kg]);
 #pragma unroll
         for (int i = 0; i < 4; i++) r.fr[i] = fp[i];   // (mul, add) of rows 2i, 2i+1
 #pragma unroll
         for (int t = 0; t < 4; t++)
-            r.af[t] = *reinterpret_cast<const bf16x8*>(lds.a[buf] +
+            r.af[t] = *reinterpret_cast<const bf16x8*>(ring.a[buf] +
                                                       a_off(t * 32 + c32, ks * 2 + kg));
     };
     auto dequant = [&](const SubstepRegs& r, bf16x8 (&bfr)[2]) {
@@ -251,66 +261,76 @@ __device__ __forceinline__ void gemm_tile_bf16(GemmLds& lds, const uint16_t* __r
                                                                    0, 0, 0);
     };
 
-    // Register sets rotate with the LDS ring: stage kt loads stage kt+3 into
-    // g[kt % 3] and writes g[(kt+2) % 3] (stage kt+2) to buffer (kt+2) % 3.
-    StageRegs g[kStages];
-    load_global(g[0], 0);
-    store_lds(g[0], 0);
-    load_global(g[1], 1);
-    store_lds(g[1], 1);
-    load_global(g[2], 2);
-    __syncthreads();
-
-    // cur: substep being multiplied (A fragments + dequantised B);
-    // nxt: substep being dequantised (its LDS reads went out a substep
-    // earlier); far: substep whose LDS reads go out now.
-    SubstepRegs cur, nxt, far;
-    bf16x8 bcur[2], bnxt[2];
-    read_substep(cur, 0, 0);
-    dequant(cur, bcur);
-    read_substep(nxt, 0, 1);
-
-    // One stage, branch free: past the last stage the loads repeat the last
-    // stage, the LDS writes land in a buffer no later stage reads, and the
-    // reads of the stage after the last are of a buffer nothing uses.
-    auto stage = [&](int kt, auto BUF) {
-        constexpr int buf = decltype(BUF)::value;
-        load_global(g[buf], kt + 3);
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-            // LDS reads two substeps ahead go out first (a scheduling fence
-            // keeps the compiler from sinking them next to their use); this
-            // substep's MFMAs then interleave with the next one's dequant,
-            // whose operands arrived during the previous substep.
-            if (ks < 2) read_substep(far, buf, ks + 2);
-            else read_substep(far, (buf + 1) % kStages, ks - 2);
-            if (ks == 2) store_lds(g[(buf + 2) % kStages], (buf + 2) % kStages);
-            __builtin_amdgcn_sched_barrier(0);
-            mfmas(cur, bcur);
-            dequant(nxt, bnxt);
-            __builtin_amdgcn_sched_barrier(0);
-            cur = nxt;
-            nxt = far;
-            bcur[0] = bnxt[0];
-            bcur[1] = bnxt[1];
-        }
-        __syncthreads();
-    };
     using B0 = std::integral_constant<int, 0>;
     using B1 = std::integral_constant<int, 1>;
-    using B2 = std::integral_constant<int, 2>;
+
+    // Prologue: stage 0 in LDS, stage 1 in register set 1.
+    StageRegs g[2];
+    load_global(g[0], 0);
+    load_global(g[1], 1);
+    store_lds(g[0], B0{});
+    __syncthreads();
+
+    // One stage, branch free (see the pipeline above).  BUF = kt % 2.
+    auto stage = [&](int kt, auto BUF) {
+        constexpr int buf = decltype(BUF)::value;
+        using Next = std::integral_constant<int, (buf + 1) % kStages>;
+        // One substep's operands live at a time; the SIMD's other wave
+        // covers the LDS latency.
+        SubstepRegs cur;
+        bf16x8 bcur[2];
+        read_substep(cur, BUF, wp);
+        load_global(g[buf], kt + 2);
+        dequant(cur, bcur);
+        mfmas(cur, bcur);
+        __builtin_amdgcn_sched_barrier(0);
+        read_substep(cur, BUF, wp + 2);
+        dequant(cur, bcur);
+        mfmas(cur, bcur);
+        store_lds(g[(buf + 1) % kStages], Next{});
+        __syncthreads();
+    };
     int kt = 0;
-    for (; kt + 3 <= ktiles; kt += 3) {
+    for (; kt + 2 <= ktiles; kt += 2) {
         stage(kt, B0{});
         stage(kt + 1, B1{});
-        stage(kt + 2, B2{});
     }
     if (kt < ktiles) stage(kt, B0{});
-    if (kt + 1 < ktiles) stage(kt + 1, B1{});
+
+    // The odd-substep wave of each pair hands its accumulators over.
+    if (wp == 1) {
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    f32x4 v;
+                    v.x = acc[t][j][4 * q];
+                    v.y = acc[t][j][4 * q + 1];
+                    v.z = acc[t][j][4 * q + 2];
+                    v.w = acc[t][j][4 * q + 3];
+                    lds.red[wq][(t * 2 + j) * 4 + q][lane] = v;
+                }
+    }
+    __syncthreads();
+    if (wp == 1) return;
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const f32x4 v = lds.red[wq][(t * 2 + j) * 4 + q][lane];
+                acc[t][j][4 * q] += v.x;
+                acc[t][j][4 * q + 1] += v.y;
+                acc[t][j][4 * q + 2] += v.z;
+                acc[t][j][4 * q + 3] += v.w;
+            }
 
     // D of a 32 x 32 tile: lane holds column lane % 32; register r is row
     // 8*(r/4) + 4*(lane/32) + r%4.
-    const int col = n0 + 64 * wave + 2 * c32;
+    const int col = n0 + 64 * wq + 2 * c32;
     if (col >= N) return;
 #pragma unroll
     for (int t = 0; t < 4; t++) {
