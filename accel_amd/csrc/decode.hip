@@ -8,20 +8,24 @@
 // w = s == 0 ? z : (code - z) * s.  With N % 128 == 0 a group is 128
 // consecutive columns of one row k.
 //
-// Kernel shape.  A workgroup of 256 lanes owns a tile of TILE columns and a
-// slice of K rows.  Each lane owns CPL adjacent columns (CPL/8 words: one 4-,
-// 8- or 16-byte load per row) and walks the slice's rows of its row phase;
-// the TILE/CPL lanes of a row read it as one contiguous segment.  Rows are
-// fetched R at a time into registers, the next batch issued before the
-// current one is used.  Per (row, group) the dequantisation folds into two
-// scalars,
+// Kernel shape.  A workgroup of 512 lanes (eight waves) owns a tile of TILE
+// columns and a slice of K rows.  Each lane owns CPL adjacent columns (CPL/8
+// words: one 4-, 8- or 16-byte load per row) and kBatch rows of its row
+// phase; the TILE/CPL lanes of a row read it as one contiguous segment (128
+// bytes for a 256-column tile).  A lane issues all its loads -- codes, then
+// the scale, zero and activations of each of its rows -- before it uses
+// any, branch free, so a workgroup waits for one memory latency; the slice
+// count grows with K instead of a loop (only past kMaxSlices slices does a
+// workgroup loop over batches).  Per (row, group) the dequantisation folds
+// into two scalars,
 //     x*w = (x*s)*code + b,   b = -(x*s)*z   (or x*z for a zero scale),
 // so the inner loop is one conversion per two weights and one FMA per
-// weight, and b is summed once per row.  Nibbles become floats through the
-// fp8 converter: a byte 0000qqqq read as OCP e4m3 is exactly q * 2^-9 (codes
-// 0..7 are the subnormals q/8 * 2^-6, codes 8..15 the first binade
-// (1 + (q-8)/8) * 2^-6), so v_cvt_pk_f32_fp8 turns two nibbles into two exact
-// floats and the 2^9 is folded into x*s.
+// weight, and b is summed per lane and added once to each of its column
+// sums.  Nibbles become floats through the fp8 converter: a byte 0000qqqq
+// read as OCP e4m3 is exactly q * 2^-9 (codes 0..7 are the subnormals
+// q/8 * 2^-6, codes 8..15 the first binade (1 + (q-8)/8) * 2^-6), so
+// v_cvt_pk_f32_fp8 turns two nibbles into two exact floats and the 2^9 is
+// folded into x*s.
 //
 // Reduction.  The row phases of a workgroup are summed through LDS.  With
 // one slice those sums are the output.  Otherwise every workgroup stores its
@@ -54,8 +58,10 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kThreads = 256;           // lanes per workgroup
-constexpr int kRows = 4;                // rows per lane per fetch batch
+constexpr int kThreads = 256;           // lanes per workgroup of the matrix-core kernel
+constexpr int kDecThreads = 512;        // lanes per workgroup of the VALU kernel
+constexpr int kBatch = 4;               // rows per lane per fetch batch
+constexpr int kMaxSlices = 64;          // K slices of a VALU decode launch, at most
 constexpr float kNibbleScale = 512.0f;  // 1 / (e4m3 value of code 1)
 
 __device__ __forceinline__ float half_bits_to_float(uint16_t h) {
@@ -211,41 +217,29 @@ __device__ __forceinline__ int reduced_offset(int l) {
     }
 }
 
-// One fetch batch: the codes of kRows rows of a lane's segment, plus the
-// one (row, group) of the wave's batch whose scale, zero and activations
-// this lane loads (see the kernel).
-template <int M, int WPL>
-struct Batch {
-    uint32_t q[kRows][WPL];
-    uint16_t s, z;
-    float x[M];
-};
-
 // M rows of activations; TILE columns per workgroup, CPL per lane.
 //
-// Scales and zeros.  A wave's batch spans RPW = 64 / LPR row phases times
-// kRows rows and GPT = TILE / 128 groups per row: V = 2 * CPL <= 64 (row,
-// group) pairs.  Lane v < V of the wave loads pair v's scale, zero and
-// activations with one 2-byte load each, folds them into x*s*512 and the
-// bias term, and the lanes that decode that pair's codes fetch the two
-// values with a cross-lane read (ds_bpermute).  One load per pair instead
-// of one per lane and row keeps the small, scattered scale reads off the
-// memory pipeline's critical path.
+// A workgroup of eight waves owns TILE columns and the rows
+// [k_begin, k_end) of its slice, kBatch rows per lane: lane (row phase rp,
+// segment lane) decodes rows k_begin + rp + i * RP, i < kBatch.  All of a
+// lane's loads -- its codes, then the scale, zero and activations of each
+// of its rows -- are issued at once, before any is used, and are branch
+// free (rows past the end are clamped into the slice, loaded again and
+// given a zero factor), so the workgroup waits for one memory latency.
+// Matrices longer than the slices the launch can take loop over such
+// batches.
 template <int M, int TILE, int CPL>
-__global__ __launch_bounds__(kThreads) void int4_decode_f32_kernel(
+__global__ __launch_bounds__(kDecThreads) void int4_decode_f32_kernel(
     const float* __restrict__ a, const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
     float* __restrict__ out, float* partial, uint32_t* tickets, int ticket_stride, int K, int N,
     int rows_per_slice, int slices) {
-    constexpr int LPR = TILE / CPL;     // lanes per row
-    constexpr int RP = kThreads / LPR;  // row phases
-    constexpr int RPW = 64 / LPR;       // row phases per wave
-    constexpr int GPT = TILE / 128;     // groups per row of a tile
-    constexpr int WPL = CPL / 8;        // code words per lane per row
-    constexpr int V = RPW * kRows * GPT;
-    static_assert(V <= 64, "one (row, group) pair per lane");
-    static_assert(kThreads == 256, "four waves per workgroup");
-    __shared__ __attribute__((aligned(16))) float red[4][TILE];
+    constexpr int LPR = TILE / CPL;        // lanes per row
+    constexpr int RP = kDecThreads / LPR;  // row phases
+    constexpr int RPW = 64 / LPR;          // row phases per wave
+    constexpr int WPL = CPL / 8;           // code words per lane per row
+    constexpr int NWAVE = kDecThreads / 64;
+    __shared__ __attribute__((aligned(16))) float red[NWAVE][TILE];
     __shared__ int last_flag;
 
     const int tiles = N / TILE;
@@ -256,129 +250,89 @@ __global__ __launch_bounds__(kThreads) void int4_decode_f32_kernel(
     const int slice = b / tiles;
 
     const int tid = threadIdx.x;
+    const int l64 = tid & 63;
+    const int wave = tid >> 6;
     const int lane = tid % LPR;
     const int rp = tid / LPR;
     const int col0 = tile * TILE + lane * CPL;
     const size_t groups_per_row = (size_t)(N >> 7);
     const size_t words_per_row = (size_t)(N >> 3);
+    const size_t group = (size_t)((col0) >> 7);
     const int k_begin = slice * rows_per_slice;
     const int k_end = min(K, k_begin + rows_per_slice);
     const uint32_t* qcol = codes + (col0 >> 3);
 
-    // The pair this lane loads: row phase (wave, pj), batch row pi, group ph.
-    const int l64 = tid & 63;
-    const int wave = tid >> 6;
-    const int ph = l64 % GPT;
-    const int pi = (l64 / GPT) / RPW;
-    const int pj = (l64 / GPT) % RPW;
-    const bool loader = l64 < V;
-    const int prow_off = pi * RP + wave * RPW + pj;  // row offset within a batch
-    const size_t pgroup = (size_t)tile * GPT + ph;
-    // The lanes holding this lane's pairs, row i of a batch at src + i*RPW*GPT.
-    const int src0 = ((l64 / LPR) * GPT + (lane * CPL) / 128) << 2;
-
     float acc[M][CPL];
-    float bias[M];
+    float bsum[M];
 #pragma unroll
     for (int m = 0; m < M; m++) {
-        bias[m] = 0.0f;
+        bsum[m] = 0.0f;
 #pragma unroll
         for (int j = 0; j < CPL; j++) acc[m][j] = 0.0f;
     }
 
-    // kb: the batch's first row; this lane's rows are kb + rp + i*RP.
-    auto fetch = [&](Batch<M, WPL>& bt, int kb) {
+    for (int kb = k_begin; kb < k_end; kb += kBatch * RP) {
+        uint32_t q[kBatch][WPL];
+        uint16_t sb[kBatch], zb[kBatch];
+        float xv[kBatch][M];
 #pragma unroll
-        for (int i = 0; i < kRows; i++) {
-            const int row = kb + rp + i * RP;
-            if (row < k_end) load_words<WPL>(qcol + (size_t)row * words_per_row, bt.q[i]);
-        }
-        const int prow = kb + prow_off;
-        if (loader && prow < k_end) {
-            bt.s = scales[(size_t)prow * groups_per_row + pgroup];
-            bt.z = zeros[(size_t)prow * groups_per_row + pgroup];
-#pragma unroll
-            for (int m = 0; m < M; m++) bt.x[m] = a[(size_t)m * K + prow];
-        } else {
-            bt.s = 0;
-            bt.z = 0;
-#pragma unroll
-            for (int m = 0; m < M; m++) bt.x[m] = 0.0f;
-        }
-    };
-    auto compute = [&](const Batch<M, WPL>& bt, int kb) {
-        // Fold the loaded pair: x*w = (x*s*512) * (q * 2^-9) + add.
-        const float s = half_bits_to_float(bt.s);
-        const float z = half_bits_to_float(bt.z);
-        float pxs[M], padd[M];
-#pragma unroll
-        for (int m = 0; m < M; m++) {
-            const float xsm = bt.x[m] * s;
-            padd[m] = (s == 0.0f) ? bt.x[m] * z : -(xsm * z);
-            pxs[m] = xsm * kNibbleScale;
+        for (int i = 0; i < kBatch; i++) {
+            const int row = min(kb + rp + i * RP, k_end - 1);
+            load_words<WPL>(qcol + (size_t)row * words_per_row, q[i]);
         }
 #pragma unroll
-        for (int i = 0; i < kRows; i++) {
-            const int src = src0 + ((i * RPW * GPT) << 2);
-            float xs[M];
+        for (int i = 0; i < kBatch; i++) {
+            const int row = min(kb + rp + i * RP, k_end - 1);
+            sb[i] = scales[(size_t)row * groups_per_row + group];
+            zb[i] = zeros[(size_t)row * groups_per_row + group];
+#pragma unroll
+            for (int m = 0; m < M; m++) xv[i][m] = a[(size_t)m * K + row];
+        }
+#pragma unroll
+        for (int i = 0; i < kBatch; i++) {
+            const bool valid = kb + rp + i * RP < k_end;
+            const float s = half_bits_to_float(sb[i]);
+            const float z = half_bits_to_float(zb[i]);
+            float c[M];
 #pragma unroll
             for (int m = 0; m < M; m++) {
-                xs[m] = __int_as_float(
-                    __builtin_amdgcn_ds_bpermute(src, __float_as_int(pxs[m])));
-                const float add = __int_as_float(
-                    __builtin_amdgcn_ds_bpermute(src, __float_as_int(padd[m])));
-                if (kb + rp + i * RP < k_end) bias[m] += add;
+                const float xs = xv[i][m] * s;
+                const float bterm = (s == 0.0f) ? xv[i][m] * z : -(xs * z);
+                c[m] = valid ? xs * kNibbleScale : 0.0f;
+                bsum[m] += valid ? bterm : 0.0f;
             }
-            if (kb + rp + i * RP < k_end) {
 #pragma unroll
-                for (int wi = 0; wi < WPL; wi++) {
-                    float f[8];
-                    unpack8(bt.q[i][wi], f);
+            for (int wi = 0; wi < WPL; wi++) {
+                float f[8];
+                unpack8(q[i][wi], f);
 #pragma unroll
-                    for (int m = 0; m < M; m++)
+                for (int m = 0; m < M; m++)
 #pragma unroll
-                        for (int j = 0; j < 8; j++)
-                            acc[m][wi * 8 + j] =
-                                __builtin_fmaf(xs[m], f[j], acc[m][wi * 8 + j]);
-                }
+                    for (int j = 0; j < 8; j++)
+                        acc[m][wi * 8 + j] = __builtin_fmaf(c[m], f[j], acc[m][wi * 8 + j]);
             }
         }
-    };
-
-    // Two named buffers so the next batch is in flight while one is used.
-    // The loop runs on the wave-uniform batch base, so every lane takes part
-    // in the cross-lane reads.
-    constexpr int kStep = kRows * RP;
-    Batch<M, WPL> b0, b1;
-    int kb = k_begin;
-    fetch(b0, kb);
-    while (kb < k_end) {
-        if (kb + kStep < k_end) fetch(b1, kb + kStep);
-        compute(b0, kb);
-        kb += kStep;
-        if (kb >= k_end) break;
-        if (kb + kStep < k_end) fetch(b0, kb + kStep);
-        compute(b1, kb);
-        kb += kStep;
     }
 
-    // Row-phase sums: first across the wave's RPW row phases in registers
-    // (transpose_reduce), then across the four waves through LDS.
+    // Row-phase sums: across the wave's RPW row phases in registers
+    // (transpose_reduce), then across the waves through LDS.  A lane's
+    // zero-point sum is a constant of each of its columns.
     const bool split = slices > 1;
     constexpr int NV = CPL / RPW;  // column sums a lane holds after the wave stage
 #pragma unroll
     for (int m = 0; m < M; m++) {
         float v[CPL];
 #pragma unroll
-        for (int j = 0; j < CPL; j++) v[j] = acc[m][j] + bias[m];
+        for (int j = 0; j < CPL; j++) v[j] = acc[m][j] + bsum[m];
         transpose_reduce<CPL, 64 / 2, LPR>(v, l64);
-        // Lane l64 now holds the wave's sums of columns c0 .. c0 + NV - 1.
         const int c0 = lane * CPL + reduced_offset<CPL, 64 / 2, LPR>(l64);
 #pragma unroll
         for (int e = 0; e < NV; e++) red[wave][c0 + e] = v[e];
         __syncthreads();
-        for (int c = tid; c < TILE; c += kThreads) {
-            const float sum = (red[0][c] + red[1][c]) + (red[2][c] + red[3][c]);
+        for (int c = tid; c < TILE; c += kDecThreads) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int w = 0; w < NWAVE; w++) sum += red[w][c];
             const int col = tile * TILE + c;
             if (split)
                 store_device(&partial[((size_t)slice * M + m) * N + col], sum);
@@ -403,25 +357,21 @@ int ticket_stride(int tiles) {
     return 0;
 }
 
-// Slices: each lane gets two fetch batches (2 * kRows rows) when that still
-// gives every CU a workgroup, else more slices down to one batch per lane.
-// Every slice costs the tail a device-coherent store, ticket and load, so
-// the split stops as soon as the launch fills the chip.
+// Slices: one batch (kBatch rows a lane) per workgroup, so every workgroup
+// waits for one memory latency; past kMaxSlices slices a workgroup loops
+// over several batches instead, which bounds the partial sums and the
+// hand-off's reads.
 template <int M, int TILE, int CPL>
 hipError_t launch_decode(Device* d, hipStream_t st, const float* a, Int4Planes w,
                          float* out, int K, int N, int* status) {
     constexpr int LPR = TILE / CPL;
-    constexpr int RP = kThreads / LPR;
+    constexpr int RP = kDecThreads / LPR;
+    constexpr int kRowsPerBatch = kBatch * RP;
     const int tiles = N / TILE;
-    int slices = std::max(1, K / (RP * 2 * kRows));
-    if (tiles * slices < d->cu_count)
-        slices = std::min(std::max(1, K / (RP * kRows)), (d->cu_count + tiles - 1) / tiles);
-    // Partial sums (M * N * 4 bytes a slice) stay within 1/8 of the codes.
-    slices = std::min(slices, std::max(1, K / (64 * M)));
-    slices = std::max(1, slices);
-    int rows = (K + slices - 1) / slices;
-    rows = (rows + RP - 1) / RP * RP;
-    slices = (K + rows - 1) / rows;
+    const int batches = (K + kRowsPerBatch - 1) / kRowsPerBatch;
+    const int per_slice = (batches + kMaxSlices - 1) / kMaxSlices;
+    const int rows = per_slice * kRowsPerBatch;
+    const int slices = (K + rows - 1) / rows;
     float* partial = nullptr;
     uint32_t* tickets = nullptr;
     int stride = 0;
@@ -438,7 +388,7 @@ hipError_t launch_decode(Device* d, hipStream_t st, const float* a, Int4Planes w
         partial = reinterpret_cast<float*>(static_cast<char*>(ws) + kWorkspaceCounterBytes);
     }
     hipLaunchKernelGGL((int4_decode_f32_kernel<M, TILE, CPL>), dim3(tiles * slices),
-                       dim3(kThreads), 0, st, a, w.codes, w.scales, w.zeros, out, partial,
+                       dim3(kDecThreads), 0, st, a, w.codes, w.scales, w.zeros, out, partial,
                        tickets, stride, K, N, rows, slices);
     return hipGetLastError();
 }

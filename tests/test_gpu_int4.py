@@ -103,6 +103,9 @@ SHAPES_F32 = [
     # the VALU decode kernel at its other widths: K % 32 != 0 keeps M >= 3 off
     # the matrix cores; 128-column tiles; two passes of eight rows
     (3, 200, 640), (6, 100, 1024), (12, 72, 512), (2, 4096, 14336), (1, 4096, 640),
+    # K long enough that a workgroup loops over several batches of rows (256-
+    # and 128-column tiles), and the layer chain's down projection
+    (1, 16640, 256), (2, 33000, 128), (1, 14336, 4096),
 ]
 
 
