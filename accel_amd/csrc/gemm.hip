@@ -3,28 +3,34 @@
 // CDNA4's bf16 matrix cores.
 //
 // bf16 path (activations and output bf16, fp32 accumulation).  A workgroup
-// of 256 lanes (four waves) computes a 128 x 256 output tile; wave w owns
-// all 128 rows and the 64 columns [64w, 64w+64), as 4 x 2 tiles of
-// v_mfma_f32_32x32x16_bf16 (the 32x32 form: on gfx950 the 16x16x32 form
-// issues at well under the matrix cores' peak).  Per K stage of 64:
+// of 256 lanes (four waves, one per SIMD) computes a 128 x 256 output tile.
+// Wave w owns the column half ch = w & 1 (128 columns: one quantisation
+// group) and all 128 rows, as 4 x 4 tiles of v_mfma_f32_32x32x16_bf16,
+// for the 16-k substeps of parity w >> 1 of every 64-k stage; the two
+// parities' accumulators are added through LDS at the end.  Per stage:
 //   * the activation tile (128 rows x 128 bytes) goes to LDS through 16-byte
 //     loads, rows XOR-swizzled in 16-byte chunks so the fragment reads
-//     (32 rows x 2 chunks per wave) spread over the banks;
+//     (32 rows x one chunk) spread over the banks;
 //   * the packed codes (64 rows x 128 bytes) go to LDS as they are, four
 //     bits a weight, transposed in 4 x 4-byte blocks so that each u32 holds
 //     one byte (two adjacent columns) of four consecutive rows;
 //   * per (row, group) the fold (512*s, s == 0 ? z : -z*s) goes to LDS.
-// Each wave then dequantises its own B fragments in registers: the lane of
-// MFMA column c and k-group h reads one u32 per four rows, turns the nibbles
-// into exact floats with the fp8 converter (byte 0000qqqq as OCP e4m3 is
-// q*2^-9; a converter pair is the same column of two rows, the pairing the
-// bf16x2 operand wants), applies w = f*(512 s) + add in fp32 and packs to
-// bf16.  The MFMA's n-tile j, column c is mapped to the physical column
-// 2c + j, so a lane's two n-tiles are the two columns of one code byte and
-// its outputs are bf16 pairs.  A 64-column wave tile lies inside one
-// 128-column quantisation group, so a row has one (s, z) per wave.
-// LDS is double buffered; the next stage's global loads are issued before
-// the current stage's MFMAs and written to LDS after them.
+// Each wave dequantises its own B fragments in registers: a lane reads two
+// code bytes of its eight rows, turns the nibbles into exact floats with
+// the fp8 converter (byte 0000qqqq as OCP e4m3 is q*2^-9; a converter pair
+// is the same column of two rows, the pairing the bf16x2 operand wants),
+// applies w = f*(512 s) + add in fp32 and packs to bf16.  The MFMA's
+// n-tile j, column c is the tile column 128 ch + 4c + j, so a lane's four
+// n-tiles are the four nibbles of two adjacent code bytes and its outputs
+// are four adjacent bf16.  Every weight is dequantised once.
+//
+// Measured on gfx950 (one wave per SIMD, 16 independent 32x32x16 MFMAs a
+// step): the matrix cores sustain about 2.1 PFLOP/s alone; up to ~32 VALU
+// instructions per 16 MFMAs are free, ~64 cost a few percent, and more make
+// the VALU the bound; LDS reads and vector-memory loads interleaved with the
+// MFMAs cost more (eight 16-byte LDS reads per 16 MFMAs: -18%; eight
+// L1-hitting global loads: -40%), which is why the activations are shared
+// through LDS and each wave's tile is as wide as a group.
 //
 // Placement: consecutive logical tiles (the column tiles of one row band,
 // which share its activations) are dealt to one XCD so its L2 serves them.
@@ -45,14 +51,14 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int BM = 128, BN = 256, BK = 64;
-constexpr int kThreads = 512;        // eight waves: two per SIMD
+constexpr int kThreads = 256;        // four waves, one per SIMD
 constexpr int kARowBytes = BK * 2;   // one LDS activation row: 64 bf16
 constexpr int kBQuadWords = BN / 2;  // u32 words per row quad: one per code byte
-constexpr int kStages = 2;           // LDS ring depth
 
 __device__ __forceinline__ float half_bits_to_float(uint16_t h) {
     _Float16 v;
@@ -89,30 +95,32 @@ __device__ __forceinline__ u32x4 transpose4(uint32_t r0, uint32_t r1, uint32_t r
     return o;
 }
 
-struct __attribute__((aligned(16))) GemmRing {
-    char a[kStages][BM * kARowBytes];               // 2 x 16 KB
-    uint32_t b[kStages][(BK / 4) * kBQuadWords];    // 2 x 8 KB: [row quad][code byte]
-    f32x2 fold[kStages][2][BK];                     // [buf][group of the tile][row]
+// One 64-k stage in LDS.
+struct __attribute__((aligned(16))) GemmStage {
+    char a[BM * kARowBytes];                  // 16 KB, swizzled rows
+    uint32_t b[(BK / 4) * kBQuadWords];       // 8 KB: [row quad][code byte]
+    f32x2 fold[2][BK];                        // (512 s, add) per [group of the tile][row]
 };
 struct __attribute__((aligned(16))) GemmLds {
     union {
-        GemmRing ring;
-        // Accumulator hand-off of the wave pairs: [column quarter][quad][lane].
-        f32x4 red[4][32][64];
+        GemmStage st[2];
+        // Accumulator hand-off of the k-parity wave pairs, half a tile at a
+        // time: [column half][n-tile pair][row tile][register quad][lane].
+        f32x4 red[2][2][4][4][64];
     };
 };
 
 // One stage's global loads, held in registers until written to LDS.
 struct StageRegs {
-    u32x4 a[2];
-    uint32_t b[4];
+    u32x4 a[4];       // four 16-byte activation chunks
+    u32x2 b[4];       // 8 bytes of codes of each of four consecutive rows
     uint16_t s, z;
 };
 
-// One 16-k substep's operands for a wave.
+// One 16-k substep's LDS operands for a wave.
 struct SubstepRegs {
     bf16x8 af[4];      // A fragments of the four 32-row tiles
-    uint32_t tw[2];    // codes of rows 8*kg .. 8*kg+7 (two quads)
+    u32x2 tw[2];       // two code bytes (four columns) of rows 8*kg .. 8*kg+7, two quads
     f32x4 fr[4];       // (mul, add) of those rows, two per vector
 };
 
@@ -122,17 +130,22 @@ struct SubstepRegs {
 // from clamped columns and not stored).  codes/scales/zeros describe the
 // [K, N] matrix in use.
 //
-// Waves.  Wave w owns columns [64 (w%4), 64 (w%4) + 64) and all 128 rows;
-// waves w and w + 4 (one per SIMD pair slot) split every 64-k stage, the
-// first taking its 16-k substeps 0 and 2, the second 1 and 3, and their
-// accumulators are added at the end.  Two waves per SIMD let one wave's
-// dequantisation and LDS reads issue while the other's MFMAs run.
+// Waves.  Wave w (one per SIMD) owns the column half ch = w & 1 -- 128
+// columns, one quantisation group -- and all 128 rows, as 4 x 4 tiles of
+// v_mfma_f32_32x32x16_bf16, for the 16-k substeps of parity kp = w >> 1 of
+// every 64-k stage; the two parities' accumulators are added at the end.
+// MFMA column c of n-tile j is the column 128 ch + 4c + j, so a lane's four
+// n-tiles are the four nibbles of two adjacent code bytes.  Every weight is
+// dequantised once, and each wave reads the activation tile only for its
+// own substeps.  A wave pipelines its substeps: while the 16 MFMAs of one
+// run, it dequantises the next one's codes, read from LDS at the start of
+// the current one.
 //
-// Pipeline.  Stage kt (64 k) reads LDS buffer kt % 2.  During it the
-// workgroup issues the global loads of stage kt+2 into register set kt % 2
-// and at its end writes set (kt+1) % 2 (stage kt+1, loaded a stage earlier)
-// into buffer (kt+1) % 2, which every wave finished reading before the
-// previous barrier.  One barrier per stage.
+// Stages.  Stage kt (64 k) sits in LDS buffer kt % 2.  At its first
+// substep a wave writes its share of stage kt+1 (loaded two stages
+// earlier) into the other buffer and issues the global loads of stage
+// kt+3; the stage's one barrier, before its second substep, makes stage
+// kt+1 visible before that substep reads the next stage's operands.
 __device__ __forceinline__ void gemm_tile_bf16(GemmLds& lds, const uint16_t* __restrict__ a,
                                                const uint32_t* __restrict__ codes,
                                                const uint16_t* __restrict__ scales,
@@ -141,196 +154,225 @@ __device__ __forceinline__ void gemm_tile_bf16(GemmLds& lds, const uint16_t* __r
                                                int n0, int K, int N) {
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
-    const int wq = wave & 3;     // column quarter
-    const int wp = wave >> 2;    // substep parity
+    const int ch = wave & 1;     // column half
+    const int kp = wave >> 1;    // substep parity
     const int lane = tid & 63;
     const int c32 = lane & 31;   // MFMA row (A) / column (B, D) within a 32 x 32 tile
     const int kg = lane >> 5;    // MFMA k-group (8 consecutive k)
     const size_t groups_per_row = (size_t)(N >> 7);
     const size_t words_per_row = (size_t)(N >> 3);
     const bool half_tile = n0 + BN > N;   // only the first 128 columns exist
-    GemmRing& ring = lds.ring;
+    const int ktiles = K / BK;
 
-    // Activation staging: 1024 chunks of 16 bytes a stage, two per lane.
-    const uint16_t* a_src[2];
-    int a_dst[2];
+    // Activation staging: 1024 chunks of 16 bytes a stage, four per lane.
+    const uint16_t* a_src[4];
+    int a_dst[4];
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < 4; i++) {
         const int q = tid + kThreads * i;
         const int r = q >> 3, c = q & 7;
         const int row = min(m0 + r, m_end - 1);
         a_src[i] = a + (size_t)row * K + c * 8;
         a_dst[i] = a_off(r, c);
     }
-    // Code staging: row quad tid / 32, word column tid % 32 (four code bytes
-    // of each of the quad's four rows).
-    const int b_rq = tid >> 5;
-    const int b_wc = tid & 31;
-    const int b_src_wc = (half_tile && b_wc >= 16) ? b_wc - 16 : b_wc;
-    const uint32_t* b_src = codes + (size_t)(4 * b_rq) * words_per_row + (n0 >> 3) + b_src_wc;
-    const int b_dst = b_off(b_rq, 4 * b_wc);
-    // Fold staging: one (row, group of the tile) per lane, lanes 128..511
-    // repeating lanes 0..127 (the same value to the same place) so the
-    // stage body has no branch and every lane issues the same loads.
+    // Code staging: row quad tid / 16 and 8-byte column chunk tid % 16 (16
+    // columns, two words) of each of the quad's four rows.
+    const int b_rq = tid >> 4;
+    const int b_cc = tid & 15;
+    const int b_cc_src = (half_tile && b_cc >= 8) ? b_cc - 8 : b_cc;
+    const uint32_t* b_src = codes + (size_t)(4 * b_rq) * words_per_row + (n0 >> 3) + 2 * b_cc_src;
+    const int b_dst = b_off(b_rq, 8 * b_cc);
+    // Fold staging: one (row, group of the tile) per lane, lanes 128..255
+    // repeating lanes 0..127 (the same value to the same place).
     const int f_row = tid & 63;
     const int f_grp = (tid >> 6) & 1;
     const size_t f_g = (size_t)(n0 >> 7) + ((half_tile && f_grp) ? 0 : f_grp);
     const uint16_t* s_src = scales + (size_t)f_row * groups_per_row + f_g;
     const uint16_t* z_src = zeros + (size_t)f_row * groups_per_row + f_g;
-    const int ktiles = K / BK;
 
     // Stage indices past the end are clamped to the last stage: the loads
     // repeat valid data and land in buffers no later stage reads.
     auto load_global = [&](StageRegs& g, int kt) {
         const int k0 = min(kt, ktiles - 1) * BK;
 #pragma unroll
-        for (int i = 0; i < 2; i++) g.a[i] = *reinterpret_cast<const u32x4*>(a_src[i] + k0);
+        for (int i = 0; i < 4; i++) g.a[i] = *reinterpret_cast<const u32x4*>(a_src[i] + k0);
         const uint32_t* bp = b_src + (size_t)k0 * words_per_row;
 #pragma unroll
         for (int i = 0; i < 4; i++)
-            g.b[i] = __builtin_nontemporal_load(bp + (size_t)i * words_per_row);
+            g.b[i] = *reinterpret_cast<const u32x2*>(bp + (size_t)i * words_per_row);
         g.s = s_src[(size_t)k0 * groups_per_row];
         g.z = z_src[(size_t)k0 * groups_per_row];
     };
-    auto store_lds = [&](const StageRegs& g, auto BUF) {
-        constexpr int buf = decltype(BUF)::value;
+    auto store_lds = [&](const StageRegs& g, int buf) {
+        GemmStage& S = lds.st[buf];
 #pragma unroll
-        for (int i = 0; i < 2; i++) *reinterpret_cast<u32x4*>(ring.a[buf] + a_dst[i]) = g.a[i];
-        *reinterpret_cast<u32x4*>(&ring.b[buf][b_dst]) = transpose4(g.b[0], g.b[1], g.b[2], g.b[3]);
+        for (int i = 0; i < 4; i++) *reinterpret_cast<u32x4*>(S.a + a_dst[i]) = g.a[i];
+#pragma unroll
+        for (int w = 0; w < 2; w++)
+            *reinterpret_cast<u32x4*>(&S.b[b_dst + 4 * w]) =
+                transpose4(g.b[0][w], g.b[1][w], g.b[2][w], g.b[3][w]);
         const float s = half_bits_to_float(g.s);
         const float z = half_bits_to_float(g.z);
         f32x2 f;
         f.x = s * 512.0f;
         f.y = (s == 0.0f) ? z : -(z * s);
-        ring.fold[buf][f_grp][f_row] = f;
+        S.fold[f_grp][f_row] = f;
     };
-    // This wave's code byte: columns 64*wq + 2*c32 and +1 of the tile.
-    const int my_bc = 32 * wq + c32;
-    const int my_grp = wq >> 1;
+    // This lane's code bytes: 64*ch + 2*c32 and +1 (columns 128ch + 4c32 .. +3).
+    const int my_bc = 64 * ch + 2 * c32;
 
-    auto read_substep = [&](SubstepRegs& r, auto BUF, int ks) {
-        constexpr int buf = decltype(BUF)::value;
+    auto read_substep = [&](SubstepRegs& r, int buf, int ks) {
+        const GemmStage& S = lds.st[buf];
 #pragma unroll
-        for (int i = 0; i < 2; i++) r.tw[i] = ring.b[buf][b_off(ks * 4 + 2 * kg + i, my_bc)];
-        const f32x4* fp =
-            reinterpret_cast<const f32x4*>(&ring.fold[buf][my_grp][ks * 16 + 8 * kg]);
+        for (int i = 0; i < 2; i++)
+            r.tw[i] = *reinterpret_cast<const u32x2*>(&S.b[b_off(ks * 4 + 2 * kg + i, my_bc)]);
+        const f32x4* fp = reinterpret_cast<const f32x4*>(&S.fold[ch][ks * 16 + 8 * kg]);
 #pragma unroll
         for (int i = 0; i < 4; i++) r.fr[i] = fp[i];   // (mul, add) of rows 2i, 2i+1
 #pragma unroll
         for (int t = 0; t < 4; t++)
-            r.af[t] = *reinterpret_cast<const bf16x8*>(ring.a[buf] +
-                                                      a_off(t * 32 + c32, ks * 2 + kg));
+            r.af[t] = *reinterpret_cast<const bf16x8*>(S.a + a_off(t * 32 + c32, ks * 2 + kg));
     };
-    auto dequant = [&](const SubstepRegs& r, bf16x8 (&bfr)[2]) {
+    // B fragments of the four n-tiles: code byte e of tw (e = 0, 1) holds
+    // columns 2e (low nibble) and 2e + 1 (high nibble); u32 h of a u32x2
+    // pair is quad h (rows 4h .. 4h+3).
+    auto dequant = [&](const SubstepRegs& r, bf16x8 (&bfr)[4]) {
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const uint32_t t = r.tw[i];
-            const uint32_t lo = t & 0x0F0F0F0Fu;          // column 0 of rows 0..3
-            const uint32_t hi = (t >> 4) & 0x0F0F0F0Fu;   // column 1
-            const f32x2 c0a = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);  // rows 0, 1
-            const f32x2 c0b = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);   // rows 2, 3
-            const f32x2 c1a = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
-            const f32x2 c1b = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
-            const f32x4 f01 = r.fr[2 * i], f23 = r.fr[2 * i + 1];
-            const int p = 4 * i;
-            bfr[0][p + 0] = (__bf16)__builtin_fmaf(c0a.x, f01.x, f01.y);
-            bfr[0][p + 1] = (__bf16)__builtin_fmaf(c0a.y, f01.z, f01.w);
-            bfr[0][p + 2] = (__bf16)__builtin_fmaf(c0b.x, f23.x, f23.y);
-            bfr[0][p + 3] = (__bf16)__builtin_fmaf(c0b.y, f23.z, f23.w);
-            bfr[1][p + 0] = (__bf16)__builtin_fmaf(c1a.x, f01.x, f01.y);
-            bfr[1][p + 1] = (__bf16)__builtin_fmaf(c1a.y, f01.z, f01.w);
-            bfr[1][p + 2] = (__bf16)__builtin_fmaf(c1b.x, f23.x, f23.y);
-            bfr[1][p + 3] = (__bf16)__builtin_fmaf(c1b.y, f23.z, f23.w);
+        for (int e = 0; e < 2; e++) {
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const uint32_t t = r.tw[h][e];
+                const uint32_t lo = t & 0x0F0F0F0Fu;          // column 2e of rows 0..3
+                const uint32_t hi = (t >> 4) & 0x0F0F0F0Fu;   // column 2e + 1
+                const f32x2 c0a = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);  // rows 0, 1
+                const f32x2 c0b = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);   // rows 2, 3
+                const f32x2 c1a = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
+                const f32x2 c1b = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
+                const f32x4 f01 = r.fr[2 * h], f23 = r.fr[2 * h + 1];
+                const int p = 4 * h;
+                bfr[2 * e][p + 0] = (__bf16)__builtin_fmaf(c0a.x, f01.x, f01.y);
+                bfr[2 * e][p + 1] = (__bf16)__builtin_fmaf(c0a.y, f01.z, f01.w);
+                bfr[2 * e][p + 2] = (__bf16)__builtin_fmaf(c0b.x, f23.x, f23.y);
+                bfr[2 * e][p + 3] = (__bf16)__builtin_fmaf(c0b.y, f23.z, f23.w);
+                bfr[2 * e + 1][p + 0] = (__bf16)__builtin_fmaf(c1a.x, f01.x, f01.y);
+                bfr[2 * e + 1][p + 1] = (__bf16)__builtin_fmaf(c1a.y, f01.z, f01.w);
+                bfr[2 * e + 1][p + 2] = (__bf16)__builtin_fmaf(c1b.x, f23.x, f23.y);
+                bfr[2 * e + 1][p + 3] = (__bf16)__builtin_fmaf(c1b.y, f23.z, f23.w);
+            }
         }
     };
 
-    f32x16 acc[4][2];
+    f32x16 acc[4][4];
 #pragma unroll
     for (int t = 0; t < 4; t++)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+        for (int j = 0; j < 4; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[t][j][r] = 0.0f;
 
-    auto mfmas = [&](const SubstepRegs& r, const bf16x8 (&bfr)[2]) {
+    auto mfmas = [&](const SubstepRegs& r, const bf16x8 (&bfr)[4]) {
 #pragma unroll
         for (int t = 0; t < 4; t++)
 #pragma unroll
-            for (int j = 0; j < 2; j++)
+            for (int j = 0; j < 4; j++)
                 acc[t][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(r.af[t], bfr[j], acc[t][j],
                                                                    0, 0, 0);
     };
 
-    using B0 = std::integral_constant<int, 0>;
-    using B1 = std::integral_constant<int, 1>;
-
-    // Prologue: stage 0 in LDS, stage 1 in register set 1.
+    // Prologue: stage 0 in LDS buffer 0, stage 1 in register set 1, stage 2
+    // in flight into register set 0, this wave's first substep read and
+    // dequantised.
     StageRegs g[2];
+    SubstepRegs fr[2];
+    bf16x8 bq[2][4];
     load_global(g[0], 0);
     load_global(g[1], 1);
-    store_lds(g[0], B0{});
+    store_lds(g[0], 0);
+    load_global(g[0], 2);
     __syncthreads();
+    read_substep(fr[0], 0, kp);
+    dequant(fr[0], bq[0]);
 
-    // One stage, branch free (see the pipeline above).  BUF = kt % 2.
-    auto stage = [&](int kt, auto BUF) {
-        constexpr int buf = decltype(BUF)::value;
-        using Next = std::integral_constant<int, (buf + 1) % kStages>;
-        // One substep's operands live at a time; the SIMD's other wave
-        // covers the LDS latency.
-        SubstepRegs cur;
-        bf16x8 bcur[2];
-        read_substep(cur, BUF, wp);
-        load_global(g[buf], kt + 2);
-        dequant(cur, bcur);
-        mfmas(cur, bcur);
-        __builtin_amdgcn_sched_barrier(0);
-        read_substep(cur, BUF, wp + 2);
-        dequant(cur, bcur);
-        mfmas(cur, bcur);
-        store_lds(g[(buf + 1) % kStages], Next{});
-        __syncthreads();
+    // The wave's substep u (0, 1) of stage kt is ks = 2u + kp.  SET = kt % 2
+    // names the register set that holds stage kt+2 (the other one holds
+    // stage kt+1 until it is written).
+    auto substep = [&](int kt, auto U, auto SET) {
+        constexpr int u = decltype(U)::value;
+        constexpr int set = decltype(SET)::value;
+        const int buf = kt & 1;
+        if constexpr (u == 0) {
+            store_lds(g[set ^ 1], buf ^ 1);      // stage kt+1
+            load_global(g[set ^ 1], kt + 3);
+            read_substep(fr[1], buf, 2 + kp);
+        } else {
+            __syncthreads();                      // stage kt+1 visible
+            read_substep(fr[0], buf ^ 1, kp);
+        }
+        mfmas(fr[u], bq[u]);
+        dequant(fr[u ^ 1], bq[u ^ 1]);
+        // The MFMAs in issue order, each followed by a share of the next
+        // substep's LDS reads and dequant VALU.
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
+            __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);   // VALU
+        }
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    auto stage = [&](int kt, auto SET) {
+        substep(kt, I0{}, SET);
+        substep(kt, I1{}, SET);
     };
     int kt = 0;
     for (; kt + 2 <= ktiles; kt += 2) {
-        stage(kt, B0{});
-        stage(kt + 1, B1{});
+        stage(kt, I0{});
+        stage(kt + 1, I1{});
     }
-    if (kt < ktiles) stage(kt, B0{});
+    if (kt < ktiles) stage(kt, I0{});
 
-    // The odd-substep wave of each pair hands its accumulators over.
-    if (wp == 1) {
-#pragma unroll
-        for (int t = 0; t < 4; t++)
-#pragma unroll
-            for (int j = 0; j < 2; j++)
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    f32x4 v;
-                    v.x = acc[t][j][4 * q];
-                    v.y = acc[t][j][4 * q + 1];
-                    v.z = acc[t][j][4 * q + 2];
-                    v.w = acc[t][j][4 * q + 3];
-                    lds.red[wq][(t * 2 + j) * 4 + q][lane] = v;
-                }
-    }
+    // The odd-parity waves hand their accumulators to the even ones through
+    // LDS, one pair of n-tiles at a time.
     __syncthreads();
-    if (wp == 1) return;
 #pragma unroll
-    for (int t = 0; t < 4; t++)
+    for (int jp = 0; jp < 2; jp++) {
+        if (kp == 1) {
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+            for (int jj = 0; jj < 2; jj++)
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const f32x4 v = lds.red[wq][(t * 2 + j) * 4 + q][lane];
-                acc[t][j][4 * q] += v.x;
-                acc[t][j][4 * q + 1] += v.y;
-                acc[t][j][4 * q + 2] += v.z;
-                acc[t][j][4 * q + 3] += v.w;
-            }
+                for (int t = 0; t < 4; t++)
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const f32x16& v = acc[t][2 * jp + jj];
+                        lds.red[ch][jj][t][q][lane] =
+                            (f32x4){v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+                    }
+        }
+        __syncthreads();
+        if (kp == 0) {
+#pragma unroll
+            for (int jj = 0; jj < 2; jj++)
+#pragma unroll
+                for (int t = 0; t < 4; t++)
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const f32x4 v = lds.red[ch][jj][t][q][lane];
+                        f32x16& d = acc[t][2 * jp + jj];
+                        d[4 * q] += v.x;
+                        d[4 * q + 1] += v.y;
+                        d[4 * q + 2] += v.z;
+                        d[4 * q + 3] += v.w;
+                    }
+        }
+        __syncthreads();
+    }
+    if (kp == 1) return;
 
     // D of a 32 x 32 tile: lane holds column lane % 32; register r is row
-    // 8*(r/4) + 4*(lane/32) + r%4.
-    const int col = n0 + 64 * wq + 2 * c32;
+    // 8*(r/4) + 4*(lane/32) + r%4.  A lane's four n-tiles are four adjacent
+    // columns.
+    const int col = n0 + 128 * ch + 4 * c32;
     if (col >= N) return;
 #pragma unroll
     for (int t = 0; t < 4; t++) {
@@ -338,10 +380,12 @@ __device__ __forceinline__ void gemm_tile_bf16(GemmLds& lds, const uint16_t* __r
         for (int r = 0; r < 16; r++) {
             const int row = m0 + t * 32 + 8 * (r >> 2) + 4 * kg + (r & 3);
             if (row < m_end) {
-                bf16x2 v;
+                bf16x4 v;
                 v[0] = (__bf16)acc[t][0][r];
                 v[1] = (__bf16)acc[t][1][r];
-                *reinterpret_cast<bf16x2*>(out + (size_t)row * N + col) = v;
+                v[2] = (__bf16)acc[t][2][r];
+                v[3] = (__bf16)acc[t][3][r];
+                *reinterpret_cast<bf16x4*>(out + (size_t)row * N + col) = v;
             }
         }
     }

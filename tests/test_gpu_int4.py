@@ -161,7 +161,10 @@ def test_decode_is_deterministic(dev):
 # ---- bf16 prefill -------------------------------------------------------------
 
 SHAPES_BF16 = [(1, 64, 128), (64, 256, 256), (100, 512, 384), (128, 128, 128),
-               (257, 1024, 640), (512, 2048, 1024)]
+               (257, 1024, 640), (512, 2048, 1024),
+               # the 256-row tiles with one stage, an odd stage count and a
+               # ragged last row band
+               (300, 64, 128), (256, 192, 384), (511, 320, 256)]
 
 
 def _bf16_oracle(x, p, s, z, M, K, N, rows=None):
