@@ -58,7 +58,6 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kThreads = 256;           // lanes per workgroup of the matrix-core kernel
 constexpr int kDecThreads = 512;        // lanes per workgroup of the VALU kernel
 constexpr int kBatch = 4;               // rows per lane per fetch batch
 constexpr int kMaxSlices = 64;          // K slices of a VALU decode launch, at most
@@ -455,238 +454,645 @@ __global__ void int4_generic_bf16_kernel(const uint16_t* __restrict__ a,
 // ---- 3..16 rows: the matrix cores ------------------------------------------
 //
 // With M rows of activations every weight feeds M FMAs, and past two rows the
-// VALU (not HBM) bounds the product.  This kernel moves the arithmetic onto
-// v_mfma_f32_16x16x32_bf16 and keeps f32 accuracy:
-//   * the activation rows are the MFMA's A side (16 rows; rows >= M are zero),
-//     scaled per (row k, group) to v = x * (512 s) and split exactly into three
-//     bf16 terms hi + mid + lo (each the RNE rounding of what is left; the
-//     residue is below 2^-27 |v|), so three MFMAs per tile give the product of
-//     v with an exact B to f32 accuracy;
+// VALU (not HBM) bounds a VALU product.  This kernel moves the arithmetic
+// onto v_mfma_f32_16x16x32_bf16 and keeps f32 accuracy:
+//   * the activation rows are the MFMA's A side (16 rows; rows >= M are
+//     clamped copies whose results are never stored), scaled per (row k,
+//     group) to v = x * (512 s) and split exactly into three bf16 terms
+//     hi + mid + lo (each the RNE rounding of what is left; the residue is
+//     below 2^-27 |v|), so three MFMAs per tile give the product of v with
+//     an exact B to f32 accuracy;
 //   * B is the code itself, q * 2^-9, exact in bf16 (fp8 converter), so
 //     A' * B = x * s * q;
 //   * the zero point is the per-(row m, group) bias sum_k x * add,
 //     add = s == 0 ? z : -z*s, accumulated in f32 on the VALU.
-// A workgroup owns one 128-column group and a K slice; its four waves take
-// the slice's 32-k steps in turn and are summed through LDS.  The MFMA column
-// c of n-tile j is the physical column 8c + j, so lane c's eight n-tiles are
-// the eight nibbles of code word c, read straight from HBM (one u32 per row)
-// and paired (row, row+1) with v_perm for the bf16x2 operand.  Slices are
-// combined by split_k_finish.
+// The MFMA column c of n-tile j of group g is the tile column
+// 128 g + 8 c + j, so a lane's eight n-tiles of a group are the eight
+// nibbles of one code word (word 16 g + c of a tile row), and the sixteen
+// columns of every n-tile lie in one quantisation group, as the A side's
+// per-group scale requires.
+//
+// Memory.  A workgroup (eight waves) owns a tile of 128 G columns (64 G bytes
+// of every code row) and a K slice; its waves take the slice's 32-row steps
+// in turn.  A step's codes reach LDS with global_load_lds_dwordx4 (no
+// registers: each lane's 16 bytes land at the instruction's LDS base + 16 *
+// lane, and every lane may name any global chunk), so each instruction reads
+// whole 64 G-byte row segments, and the MFMA layout -- one word of eight rows
+// per lane -- is read back with ds_read2(st64)_b32.  Rows are placed (row
+// slot, XOR of the 16-byte chunk) so that those reads are free of bank
+// conflicts.  The step's scales and zeros arrive the same way; one lane per
+// (row, group) folds them into (512 s, add) in LDS for the whole wave.  Each
+// wave keeps kDepth steps in flight in its own LDS ring, so no barrier is
+// needed until the epilogue.  The compiler does not order LDS reads after
+// LDS-direct loads, so each step waits for its own loads explicitly
+// (s_waitcnt vmcnt counting the loads issued after it).
+//
+// The waves' sums meet in LDS; with one slice they are the output, else the
+// split-K hand-off below combines the slices (in slice order).
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int kMfmaCols = 128;      // one quantisation group
-constexpr int kMfmaMaxRows = 2048;  // rows of a slice whose fold fits in LDS
+constexpr int kMfLdsBytes = 155648;   // 152 KiB of the 160 KiB a workgroup may hold
 
-struct MfmaDecodeLds {
-    f32x2 fold[kMfmaMaxRows];            // (512 s, add) per row of the slice
-    float red[4][16][kMfmaCols];         // per-wave sums
-    float bias[4][16];
+// Geometry of a tile of G quantisation groups (128 G columns) worked by NW
+// waves.  A step is 32 rows; its LDS buffer holds the codes, the 16 x 32
+// activations, the raw scales and zeros and their fold.
+template <int G, int NW>
+struct MfTile {
+    static constexpr int kThreads = 64 * NW;
+    static constexpr int kCols = 128 * G;
+    static constexpr int kRowBytes = 64 * G;            // codes of one tile row
+    static constexpr int kChunks = 4 * G;               // 16-byte chunks per tile row
+    static constexpr int kCodeBytes = 32 * kRowBytes;
+    static constexpr int kXBytes = 16 * 32 * 4;
+    static constexpr int kRawBytes = 256;               // scales, then zeros: a dword per row
+    static constexpr int kFoldBytes = 256 * G;          // (512 s, add) per (row, group)
+    static constexpr int kXOff = kCodeBytes;
+    static constexpr int kRawOff = kXOff + kXBytes;
+    static constexpr int kFoldOff = kRawOff + kRawBytes;
+    static constexpr int kStepBytes = kFoldOff + kFoldBytes;
+    static constexpr int kDepth = kMfLdsBytes / (NW * kStepBytes);
+    static constexpr int kCodeDma = kCodeBytes / 1024;  // 1 KiB per instruction
+    static constexpr int kVmemPerStep = kCodeDma + 2 + 1;   // + activations, scale/zero
+    static constexpr int kItems = 16 * kCols / 4 / kThreads;  // f32x4 outputs per lane
+    static_assert(kDepth >= 2 && kDepth <= 8, "ring depth");
+    static_assert(NW * 16 * (kCols + G) * 4 <= kMfLdsBytes, "reduction LDS");
+    static_assert(kItems >= 1 && 16 * kCols / 4 == kItems * kThreads, "items");
 };
 
-__global__ __launch_bounds__(kThreads) void int4_decode_mfma_kernel(
+// LDS row slot of step row r (0..31) and the XOR applied to its 16-byte
+// chunk index.  Lane (c, kg) reads word 16 g + c of rows 8 kg + e; these
+// place the four kg rows of one read in four different 16-bank ranges (and
+// two different ones within each half wave).
+template <int G>
+__device__ __forceinline__ int mf_row_slot(int r) {
+    if constexpr (G == 1) return r ^ ((r >> 3) & 3);
+    else return r ^ ((r >> 4) & 1);
+}
+template <int G>
+__device__ __forceinline__ int mf_chunk_xor(int r) {
+    if constexpr (G == 1) return 0;
+    else return 4 * ((r >> 3) & 1);
+}
+// Position of 16-byte chunk q (0..7) of activation row m in its 128-byte LDS
+// row: the sixteen rows' reads of one chunk fall in sixteen bank groups.
+__device__ __forceinline__ int mf_x_pos(int m, int q) { return q ^ ((m >> 1) & 7); }
+
+// LDS-direct loads: `bytes` per lane from `src` to lds_dst + bytes * lane
+// (lds_dst uniform).  Non-template wrappers, so that host compilation of
+// the kernel templates never instantiates the LDS address-space casts.
+__device__ __forceinline__ void lds_load16(const void* src, uint8_t* lds_dst) {
+    __builtin_amdgcn_global_load_lds(src, (lds_void*)lds_dst, 16, 0, 0);
+}
+__device__ __forceinline__ void lds_load4(const void* src, uint8_t* lds_dst) {
+    __builtin_amdgcn_global_load_lds(src, (lds_void*)lds_dst, 4, 0, 0);
+}
+__device__ __forceinline__ void lds_load2(const void* src, uint8_t* lds_dst) {
+    __builtin_amdgcn_global_load_lds(src, (lds_void*)lds_dst, 2, 0, 0);
+}
+// Byte address of an LDS location, as ds_* instructions take it.
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+    return (uint32_t)(uintptr_t)(lds_void*)p;
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// Waits until at most V * q vector-memory loads are outstanding, q < D.
+template <int V, int D>
+__device__ __forceinline__ void wait_vmem_steps(int q) {
+    if constexpr (D > 1) {
+        if (q == D - 1) {
+            wait_vmem<V * (D - 1)>();
+            return;
+        }
+        wait_vmem_steps<V, D - 1>(q);
+    } else {
+        wait_vmem<0>();
+    }
+}
+
+// Two values -> three bf16 pairs whose sum is (v0, v1) to 2^-27 relative:
+// each term is the RNE bf16 of what the previous ones leave, and the
+// remainder v - term is exact in f32, taken with one v_dot2 (-1 * term + v).
+// The pairs (-1, 0) and (0, -1) come in as SGPRs: the compiler would encode
+// the first as the inline constant -1.0, which the hardware does not expand
+// to bf16 -1 in the low half.
+__device__ __forceinline__ bf16x2 bf16_pair_bits(uint32_t bits) {
+    uint32_t r;
+    asm("s_mov_b32 %0, %1" : "=s"(r) : "i"(bits));
+    return __builtin_bit_cast(bf16x2, r);
+}
+__device__ __forceinline__ void split3(float v0, float v1, uint32_t& hi, uint32_t& mid,
+                                       uint32_t& lo) {
+    const bf16x2 m10 = bf16_pair_bits(0x0000BF80u);   // (-1, 0)
+    const bf16x2 m01 = bf16_pair_bits(0xBF800000u);   // (0, -1)
+    const bf16x2 h = __builtin_convertvector((f32x2){v0, v1}, bf16x2);
+    const float r0 = __builtin_amdgcn_fdot2_f32_bf16(h, m10, v0, false);
+    const float r1 = __builtin_amdgcn_fdot2_f32_bf16(h, m01, v1, false);
+    const bf16x2 m = __builtin_convertvector((f32x2){r0, r1}, bf16x2);
+    const float s0 = __builtin_amdgcn_fdot2_f32_bf16(m, m10, r0, false);
+    const float s1 = __builtin_amdgcn_fdot2_f32_bf16(m, m01, r1, false);
+    const bf16x2 l = __builtin_convertvector((f32x2){s0, s1}, bf16x2);
+    hi = __builtin_bit_cast(uint32_t, h);
+    mid = __builtin_bit_cast(uint32_t, m);
+    lo = __builtin_bit_cast(uint32_t, l);
+}
+
+// Eight code words (rows 2p, 2p+1 paired) -> the B operands of the eight
+// n-tiles (nibble j of each word), as bf16 q * 2^-9.
+__device__ __forceinline__ void codes_to_b(const uint32_t (&w)[8], bf16x8 (&b)[8]) {
+    uint32_t bw[8][4];
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        const uint32_t w0 = w[2 * p], w1 = w[2 * p + 1];
+        const uint32_t t01 = __builtin_amdgcn_perm(w1, w0, 0x05010400u);  // bytes 0,1
+        const uint32_t t23 = __builtin_amdgcn_perm(w1, w0, 0x07030602u);  // bytes 2,3
+        const uint32_t q[4] = {t01 & 0x0F0F0F0Fu, (t01 >> 4) & 0x0F0F0F0Fu,
+                               t23 & 0x0F0F0F0Fu, (t23 >> 4) & 0x0F0F0F0Fu};
+        // q[0]: nibbles 0, 2; q[1]: 1, 3; q[2]: 4, 6; q[3]: 5, 7
+#pragma unroll
+        for (int h = 0; h < 4; h++) {
+            const int c0 = (h >> 1) * 4 + (h & 1);
+            bw[c0][p] = __builtin_bit_cast(
+                uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q[h], 1.0f, false));
+            bw[c0 + 2][p] = __builtin_bit_cast(
+                uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q[h], 1.0f, true));
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+        b[j] = __builtin_bit_cast(bf16x8, (u32x4){bw[j][0], bw[j][1], bw[j][2], bw[j][3]});
+}
+
+template <int G, int NW>
+__global__ __launch_bounds__(64 * NW) void int4_decode_mfma_kernel(
     const float* __restrict__ a, const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
     float* __restrict__ out, float* partial, uint32_t* tickets, int ticket_stride, int M, int K,
-    int N,
-    int rows_per_slice, int slices) {
-    __shared__ __attribute__((aligned(16))) MfmaDecodeLds lds;
+    int N, int rows_per_slice, int slices) {
+    using T = MfTile<G, NW>;
+    constexpr int D = T::kDepth;
+    constexpr int V = T::kVmemPerStep;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kMfLdsBytes];
     __shared__ int last_flag;
 
-    const int tiles = N / kMfmaCols;
+    const int tiles = N / T::kCols;
     const int grid = tiles * slices;
     int b = blockIdx.x;
     if ((grid & 7) == 0) b = (b & 7) * (grid >> 3) + (b >> 3);
     const int tile = b % tiles;
     const int slice = b / tiles;
-    const int n0 = tile * kMfmaCols;
-    const size_t g = (size_t)(n0 >> 7);
-    const size_t groups_per_row = (size_t)(N >> 7);
-    const size_t words_per_row = (size_t)(N >> 3);
+    const int n0 = tile * T::kCols;
+    const int g0 = tile * G;
+    const size_t gpr = (size_t)(N >> 7);           // groups per row
+    const size_t row_bytes = (size_t)(N >> 1);
     const int k_begin = slice * rows_per_slice;
     const int k_end = min(K, k_begin + rows_per_slice);
-    const int nrows = k_end - k_begin;
+    const int nsteps = (k_end - k_begin) >> 5;
     const int tid = threadIdx.x;
-
-    for (int r = tid; r < nrows; r += kThreads) {
-        const float s = half_bits_to_float(scales[(size_t)(k_begin + r) * groups_per_row + g]);
-        const float z = half_bits_to_float(zeros[(size_t)(k_begin + r) * groups_per_row + g]);
-        f32x2 f;
-        f.x = s * kNibbleScale;
-        f.y = (s == 0.0f) ? z : -(z * s);
-        lds.fold[r] = f;
-    }
-    __syncthreads();
-
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
-    const int c16 = lane & 15;   // A row (activation row m) / B and D column
-    const int kg = lane >> 4;    // k-group: 8 consecutive k of a 32-k step
-    const bool mrow = c16 < M;
-    const float* arow = a + (size_t)(mrow ? c16 : 0) * K;
-    const uint32_t* qcol = codes + (n0 >> 3) + c16;
+    const int c16 = lane & 15;
+    const int kg = lane >> 4;
+    const int my_steps = wave < nsteps ? (nsteps - wave + NW - 1) / NW : 0;
 
-    f32x4 acc[8];
+    uint8_t* ring = lds + wave * (D * T::kStepBytes);
+
+    // This lane's global sources, relative to a step's first row.
+    const uint8_t* code_tile = reinterpret_cast<const uint8_t*>(codes) + (size_t)n0 / 2;
+    uint32_t code_off[T::kCodeDma];
 #pragma unroll
-    for (int j = 0; j < 8; j++) acc[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    float bias = 0.0f;
+    for (int i = 0; i < T::kCodeDma; i++) {
+        const int s = 64 * i + lane;
+        const int r = mf_row_slot<G>(s / T::kChunks);   // the slot map is an involution
+        const int ch = (s % T::kChunks) ^ mf_chunk_xor<G>(r);
+        code_off[i] = (uint32_t)r * (uint32_t)row_bytes + 16u * (uint32_t)ch;
+    }
+    // activations: instruction j, lane l fills position (64 j + l) % 8 of row
+    // (64 j + l) / 8 of the step's 16 x 32 block (rows >= M repeat row M - 1)
+    const float* x_src[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int s = 64 * j + lane;
+        const int m = s >> 3;
+        x_src[j] = a + (size_t)min(m, M - 1) * K + 4 * mf_x_pos(m, s & 7);
+    }
+    // scales (lanes 0..31) or zeros (32..63) of row lane % 32: G f16 values,
+    // landing in dword `lane` of the step's raw block
+    const uint16_t* raw_src = (lane < 32 ? scales : zeros) + (size_t)(lane & 31) * gpr + g0;
 
-    // One step's global operands; the next step's are in flight while the
-    // current one is converted and multiplied.
-    struct StepRegs {
-        uint32_t wv[8];
+    auto issue = [&](int i, int slot) {
+        const int row0 = k_begin + 32 * (wave + NW * i);
+        uint8_t* buf = ring + slot * T::kStepBytes;
+        const uint8_t* src = code_tile + (size_t)row0 * row_bytes;
+#pragma unroll
+        for (int c = 0; c < T::kCodeDma; c++) lds_load16(src + code_off[c], buf + 1024 * c);
+#pragma unroll
+        for (int j = 0; j < 2; j++) lds_load16(x_src[j] + row0, buf + T::kXOff + 1024 * j);
+        if constexpr (G == 1)
+            lds_load2(raw_src + (size_t)row0 * gpr, buf + T::kRawOff);
+        else
+            lds_load4(raw_src + (size_t)row0 * gpr, buf + T::kRawOff);
+    };
+
+    // LDS byte addresses (within a step buffer) of this lane's reads.
+    // Codes: row 8 kg + e of word 16 g + c16 (see mf_row_slot); two bases
+    // per group whose rows sit 256 bytes apart.
+    const uint32_t ring_lds = lds_address(ring);
+    uint32_t cbase[4];
+    if constexpr (G == 1) {
+        // row 8 kg + 4 h + l sits in slot 8 kg + 4 h + (l ^ kg): base l, + 256 h
+#pragma unroll
+        for (int l = 0; l < 4; l++) cbase[l] = 512 * kg + 64 * (l ^ kg) + 4 * c16;
+    } else {
+        // row 8 kg + e sits in slot 8 kg + (e ^ (kg >> 1)), its chunks XOR
+        // 4 (kg & 1): even e from one base, odd e from the other, + 256 (e / 2)
+        const int bb = kg >> 1;
+#pragma unroll
+        for (int g = 0; g < 2; g++) {
+            const uint32_t goff = 64 * (g ^ (kg & 1)) + 4 * c16 + 1024 * kg;
+            cbase[2 * g] = goff + 128 * bb;
+            cbase[2 * g + 1] = goff + 128 * (1 - bb);
+        }
+    }
+    // activations: row c16, columns 8 kg .. 8 kg + 7
+    const uint32_t xoff0 = T::kXOff + 128 * c16 + 16 * mf_x_pos(c16, 2 * kg);
+    const uint32_t xoff1 = T::kXOff + 128 * c16 + 16 * mf_x_pos(c16, 2 * kg + 1);
+    // fold: rows 8 kg .. 8 kg + 7, all groups; the lane folding (row, group)
+    // pair `fold_p` (G == 1: lanes 16 r + e, e < 8, fold row 8 r + e)
+    const uint32_t foff = T::kFoldOff + 64 * G * kg;
+    const int fold_p = G == 2 ? lane : 8 * (lane >> 4) + (lane & 7);
+    // LDS-direct loads of fewer than 16 bytes land one dword per lane: the
+    // scales of row r at 4 r (group g at + 2 g), the zeros 128 bytes on
+    const uint32_t raw_off = G == 2 ? 2 * fold_p : 4 * fold_p;
+    const bool folds = G == 2 || (lane & 15) < 8;
+
+    f32x4 acc[G][8];
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc[g][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    float bias[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) bias[g] = 0.0f;
+
+    // Reads of LDS-direct data are inline asm with their own lgkmcnt wait:
+    // the compiler cannot tell LDS-direct loads' addresses from other LDS
+    // accesses and would wait for every outstanding load (vmcnt(0)) before
+    // them, which drains the ring.  Their order is fixed by the asm blocks;
+    // LDS operations of one wave complete in order.
+    auto compute = [&](int slot) {
+        const uint32_t sb = ring_lds + slot * T::kStepBytes;
+        // one lane per (row, group): (512 s, add), written back for the wave
+        if (folds) {
+            uint32_t sr, zr;
+            asm volatile(
+                "ds_read_u16 %0, %2\n\t"
+                "ds_read_u16 %1, %2 offset:128\n\t"
+                "s_waitcnt lgkmcnt(0)"
+                : "=&v"(sr), "=&v"(zr)
+                : "v"(sb + T::kRawOff + raw_off));
+            const float s = half_bits_to_float((uint16_t)sr);
+            const float z = half_bits_to_float((uint16_t)zr);
+            const f32x2 f = {s * kNibbleScale, s == 0.0f ? z : -(z * s)};
+            asm volatile("ds_write_b64 %0, %1" ::"v"(sb + T::kFoldOff + 8 * fold_p),
+                         "v"(__builtin_bit_cast(uint64_t, f))
+                         : "memory");
+        }
         f32x4 x0, x1;
-    };
-    auto fetch = [&](StepRegs& r, int stp) {
-        const int k = k_begin + stp * 32 + 8 * kg;
-#pragma unroll
-        for (int e = 0; e < 8; e++)
-            r.wv[e] = __builtin_nontemporal_load(qcol + (size_t)(k + e) * words_per_row);
-        r.x0 = (f32x4){0.f, 0.f, 0.f, 0.f};
-        r.x1 = r.x0;
-        if (mrow) {
-            r.x0 = *reinterpret_cast<const f32x4*>(arow + k);
-            r.x1 = *reinterpret_cast<const f32x4*>(arow + k + 4);
+        f32x4 fv[4 * G];
+        u32x2 wp[G][4];   // (rows e, e + 2) for G == 2, (l, l + 4) for G == 1
+        if constexpr (G == 1) {
+            asm volatile(
+                "ds_read_b128 %0, %10\n\t"
+                "ds_read_b128 %1, %11\n\t"
+                "ds_read_b128 %2, %12\n\t"
+                "ds_read_b128 %3, %12 offset:16\n\t"
+                "ds_read_b128 %4, %12 offset:32\n\t"
+                "ds_read_b128 %5, %12 offset:48\n\t"
+                "ds_read2_b32 %6, %13 offset1:64\n\t"
+                "ds_read2_b32 %7, %14 offset1:64\n\t"
+                "ds_read2_b32 %8, %15 offset1:64\n\t"
+                "ds_read2_b32 %9, %16 offset1:64\n\t"
+                "s_waitcnt lgkmcnt(0)"
+                : "=&v"(x0), "=&v"(x1), "=&v"(fv[0]), "=&v"(fv[1]), "=&v"(fv[2]),
+                  "=&v"(fv[3]), "=&v"(wp[0][0]), "=&v"(wp[0][1]), "=&v"(wp[0][2]),
+                  "=&v"(wp[0][3])
+                : "v"(sb + xoff0), "v"(sb + xoff1), "v"(sb + foff), "v"(sb + cbase[0]),
+                  "v"(sb + cbase[1]), "v"(sb + cbase[2]), "v"(sb + cbase[3])
+                : "memory");
+        } else {
+            asm volatile(
+                "ds_read_b128 %0, %18\n\t"
+                "ds_read_b128 %1, %19\n\t"
+                "ds_read_b128 %2, %20\n\t"
+                "ds_read_b128 %3, %20 offset:16\n\t"
+                "ds_read_b128 %4, %20 offset:32\n\t"
+                "ds_read_b128 %5, %20 offset:48\n\t"
+                "ds_read_b128 %6, %20 offset:64\n\t"
+                "ds_read_b128 %7, %20 offset:80\n\t"
+                "ds_read_b128 %8, %20 offset:96\n\t"
+                "ds_read_b128 %9, %20 offset:112\n\t"
+                "ds_read2st64_b32 %10, %21 offset1:1\n\t"
+                "ds_read2st64_b32 %11, %21 offset0:2 offset1:3\n\t"
+                "ds_read2st64_b32 %12, %22 offset1:1\n\t"
+                "ds_read2st64_b32 %13, %22 offset0:2 offset1:3\n\t"
+                "ds_read2st64_b32 %14, %23 offset1:1\n\t"
+                "ds_read2st64_b32 %15, %23 offset0:2 offset1:3\n\t"
+                "ds_read2st64_b32 %16, %24 offset1:1\n\t"
+                "ds_read2st64_b32 %17, %24 offset0:2 offset1:3\n\t"
+                "s_waitcnt lgkmcnt(0)"
+                : "=&v"(x0), "=&v"(x1), "=&v"(fv[0]), "=&v"(fv[1]), "=&v"(fv[2]),
+                  "=&v"(fv[3]), "=&v"(fv[4]), "=&v"(fv[5]), "=&v"(fv[6]), "=&v"(fv[7]),
+                  "=&v"(wp[0][0]), "=&v"(wp[0][1]), "=&v"(wp[0][2]), "=&v"(wp[0][3]),
+                  "=&v"(wp[1][0]), "=&v"(wp[1][1]), "=&v"(wp[1][2]), "=&v"(wp[1][3])
+                : "v"(sb + xoff0), "v"(sb + xoff1), "v"(sb + foff), "v"(sb + cbase[0]),
+                  "v"(sb + cbase[1]), "v"(sb + cbase[2]), "v"(sb + cbase[3])
+                : "memory");
         }
-    };
-    auto compute = [&](const StepRegs& r, int stp) {
-        const int r0 = stp * 32 + 8 * kg;          // first row of this lane, in the slice
-        const f32x4* fp = reinterpret_cast<const f32x4*>(&lds.fold[r0]);
-        const f32x4 f01 = fp[0], f23 = fp[1], f45 = fp[2], f67 = fp[3];
-        const float xv[8] = {r.x0.x, r.x0.y, r.x0.z, r.x0.w, r.x1.x, r.x1.y, r.x1.z, r.x1.w};
-        const float mul[8] = {f01.x, f01.z, f23.x, f23.z, f45.x, f45.z, f67.x, f67.z};
-        const float add[8] = {f01.y, f01.w, f23.y, f23.w, f45.y, f45.w, f67.y, f67.w};
-        bf16x8 ah, am, al;
+        const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        f32x2 fe[G][8];
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const float v = xv[e] * mul[e];
-            bias = __builtin_fmaf(xv[e], add[e], bias);
-            const __bf16 h = (__bf16)v;
-            const float r1 = v - (float)h;
-            const __bf16 md = (__bf16)r1;
-            const float r2 = r1 - (float)md;
-            ah[e] = h;
-            am[e] = md;
-            al[e] = (__bf16)r2;
+        for (int q = 0; q < 4 * G; q++) {
+            const int p0 = 2 * q, p1 = 2 * q + 1;   // (row, group) pairs p = e * G + g
+            fe[p0 % G][p0 / G] = (f32x2){fv[q].x, fv[q].y};
+            fe[p1 % G][p1 / G] = (f32x2){fv[q].z, fv[q].w};
         }
-        // B: the code itself as bf16 pairs (row 2p, row 2p+1) straight from
-        // the fp8 bytes (scale 1).
-        uint32_t bw[8][4];
 #pragma unroll
-        for (int p = 0; p < 4; p++) {
-            const uint32_t w0 = r.wv[2 * p], w1 = r.wv[2 * p + 1];
-            const uint32_t t01 = __builtin_amdgcn_perm(w1, w0, 0x05010400u);  // bytes 0,1
-            const uint32_t t23 = __builtin_amdgcn_perm(w1, w0, 0x07030602u);  // bytes 2,3
-            const uint32_t q[4] = {t01 & 0x0F0F0F0Fu, (t01 >> 4) & 0x0F0F0F0Fu,
-                                   t23 & 0x0F0F0F0Fu, (t23 >> 4) & 0x0F0F0F0Fu};
-            // q[0]: columns 0, 2; q[1]: 1, 3; q[2]: 4, 6; q[3]: 5, 7
+        for (int g = 0; g < G; g++) {
+            uint32_t w[8];
+            if constexpr (G == 1) {
 #pragma unroll
-            for (int h = 0; h < 4; h++) {
-                const int c0 = (h >> 1) * 4 + (h & 1);   // 0, 1, 4, 5
-                bw[c0][p] = __builtin_bit_cast(
-                    uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q[h], 1.0f, false));
-                bw[c0 + 2][p] = __builtin_bit_cast(
-                    uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q[h], 1.0f, true));
+                for (int l = 0; l < 4; l++) {
+                    w[l] = wp[0][l].x;
+                    w[l + 4] = wp[0][l].y;
+                }
+            } else {
+                // even base: (0, 2), (4, 6); odd base: (1, 3), (5, 7)
+                w[0] = wp[g][0].x; w[2] = wp[g][0].y; w[4] = wp[g][1].x; w[6] = wp[g][1].y;
+                w[1] = wp[g][2].x; w[3] = wp[g][2].y; w[5] = wp[g][3].x; w[7] = wp[g][3].y;
             }
+            uint32_t ah[4], am[4], al[4];
+#pragma unroll
+            for (int p = 0; p < 4; p++) {
+                const float v0 = xv[2 * p] * fe[g][2 * p].x;
+                const float v1 = xv[2 * p + 1] * fe[g][2 * p + 1].x;
+                bias[g] = __builtin_fmaf(xv[2 * p], fe[g][2 * p].y, bias[g]);
+                bias[g] = __builtin_fmaf(xv[2 * p + 1], fe[g][2 * p + 1].y, bias[g]);
+                split3(v0, v1, ah[p], am[p], al[p]);
+            }
+            const bf16x8 Ah = __builtin_bit_cast(bf16x8, (u32x4){ah[0], ah[1], ah[2], ah[3]});
+            const bf16x8 Am = __builtin_bit_cast(bf16x8, (u32x4){am[0], am[1], am[2], am[3]});
+            const bf16x8 Al = __builtin_bit_cast(bf16x8, (u32x4){al[0], al[1], al[2], al[3]});
+            bf16x8 bq[8];
+            codes_to_b(w, bq);
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                acc[g][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Ah, bq[j], acc[g][j], 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                acc[g][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Am, bq[j], acc[g][j], 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                acc[g][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Al, bq[j], acc[g][j], 0, 0, 0);
         }
-        bf16x8 bfr[8];
-#pragma unroll
-        for (int j = 0; j < 8; j++)
-            bfr[j] = __builtin_bit_cast(bf16x8, (u32x4){bw[j][0], bw[j][1], bw[j][2], bw[j][3]});
-        // All hi products, then all mid, then all lo: each accumulator's
-        // consecutive MFMAs are eight apart.
-#pragma unroll
-        for (int j = 0; j < 8; j++)
-            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bfr[j], acc[j], 0, 0, 0);
-#pragma unroll
-        for (int j = 0; j < 8; j++)
-            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(am, bfr[j], acc[j], 0, 0, 0);
-#pragma unroll
-        for (int j = 0; j < 8; j++)
-            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bfr[j], acc[j], 0, 0, 0);
     };
 
-    // A ring of kDepth steps in flight per wave: the loads of a step go out
-    // kDepth steps (of this wave) before it is used, which covers HBM
-    // latency with a wave's own strided row loads.
-    constexpr int kDepth = 4;
-    const int nsteps = nrows / 32;   // slices are whole 32-k steps
-    StepRegs ring[kDepth];
+    // The ring: D - 1 steps in flight ahead of the one being computed.  A
+    // slot is refilled only after the step that used it has been computed
+    // (its LDS reads have returned: their values fed that step's MFMAs).
+    // Every load of a step is issued before any load of a later step, so
+    // "at most V * q loads outstanding", q = the steps issued after it,
+    // means the step has landed.
 #pragma unroll
-    for (int i = 0; i < kDepth; i++)
-        if (wave + 4 * i < nsteps) fetch(ring[i], wave + 4 * i);
-    for (int base = wave; base < nsteps; base += 4 * kDepth) {
+    for (int u = 0; u < D - 1; u++)
+        if (u < my_steps) issue(u, u);
+    for (int base = 0; base < my_steps; base += D) {
 #pragma unroll
-        for (int i = 0; i < kDepth; i++) {
-            const int stp = base + 4 * i;
-            if (stp < nsteps) {
-                compute(ring[i], stp);
-                if (stp + 4 * kDepth < nsteps) fetch(ring[i], stp + 4 * kDepth);
+        for (int u = 0; u < D; u++) {
+            const int i = base + u;
+            if (i < my_steps) {
+                __builtin_amdgcn_sched_barrier(0);
+                if (i + D - 1 < my_steps) issue(i + D - 1, (u + D - 1) % D);
+                wait_vmem_steps<V, D>(min(D - 1, my_steps - 1 - i));
+                __builtin_amdgcn_sched_barrier(0);
+                compute(u);
             }
         }
     }
 
-    // D of a 16 x 16 tile: lane holds column lane % 16, rows 4*(lane/16)+i.
+    // ---- epilogue: the waves' sums meet in LDS --------------------------
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(lds);                       // [wave][16][kCols]
+    float* red_bias = red + NW * 16 * T::kCols;                 // [wave][16][G]
 #pragma unroll
-    for (int j = 0; j < 8; j++)
+    for (int g = 0; g < G; g++) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) lds.red[wave][kg * 4 + i][8 * c16 + j] = acc[j][i];
-    bias += __shfl_xor(bias, 16, 64);
-    bias += __shfl_xor(bias, 32, 64);
-    if (kg == 0) lds.bias[wave][c16] = bias;
+        for (int i = 0; i < 4; i++) {
+            float* dst = red + (size_t)(wave * 16 + 4 * kg + i) * T::kCols + 128 * g + 8 * c16;
+            *reinterpret_cast<f32x4*>(dst) =
+                (f32x4){acc[g][0][i], acc[g][1][i], acc[g][2][i], acc[g][3][i]};
+            *reinterpret_cast<f32x4*>(dst + 4) =
+                (f32x4){acc[g][4][i], acc[g][5][i], acc[g][6][i], acc[g][7][i]};
+        }
+        float bs = bias[g];
+        bs += __shfl_xor(bs, 16, 64);
+        bs += __shfl_xor(bs, 32, 64);
+        if (kg == 0) red_bias[(wave * 16 + c16) * G + g] = bs;
+    }
     __syncthreads();
 
-    const bool split = slices > 1;
-    for (int idx = tid; idx < M * kMfmaCols; idx += kThreads) {
-        const int m = idx / kMfmaCols;
-        const int c = idx % kMfmaCols;
-        const float v = ((lds.red[0][m][c] + lds.red[1][m][c]) +
-                         (lds.red[2][m][c] + lds.red[3][m][c])) +
-                        ((lds.bias[0][m] + lds.bias[1][m]) + (lds.bias[2][m] + lds.bias[3][m]));
-        if (split)
-            store_device(&partial[((size_t)slice * M + m) * N + n0 + c], v);
-        else
-            out[(size_t)m * N + n0 + c] = v;
+    constexpr int C4 = T::kCols / 4;
+    f32x4 val[T::kItems];
+    int item_m[T::kItems], item_c[T::kItems];
+#pragma unroll
+    for (int u = 0; u < T::kItems; u++) {
+        const int it = tid + T::kThreads * u;
+        const int m = it / C4;
+        const int c = 4 * (it % C4);
+        item_m[u] = m;
+        item_c[u] = c;
+        f32x4 s = (f32x4){0.f, 0.f, 0.f, 0.f};
+        float bsum = 0.0f;
+        if (m < M) {
+#pragma unroll
+            for (int w = 0; w < NW; w++)
+                s += *reinterpret_cast<const f32x4*>(red + (size_t)(w * 16 + m) * T::kCols + c);
+#pragma unroll
+            for (int w = 0; w < NW; w++) bsum += red_bias[(w * 16 + m) * G + c / 128];
+        }
+        val[u] = s + bsum;
     }
-    if (!split) return;
-    split_k_finish(partial, tickets + (size_t)tile * ticket_stride, out, n0, kMfmaCols, M, N,
-                   slices, &last_flag);
+
+    if (slices == 1) {
+#pragma unroll
+        for (int u = 0; u < T::kItems; u++) {
+            if (item_m[u] >= M) continue;
+            float* o = out + (size_t)item_m[u] * N + n0 + item_c[u];
+            o[0] = val[u].x; o[1] = val[u].y; o[2] = val[u].z; o[3] = val[u].w;
+        }
+        return;
+    }
+
+    // ---- split-K hand-off -----------------------------------------------
+    // Arrival first: a workgroup draws its tile's arrival ticket as soon as
+    // its sums are ready.  Every workgroup but the last stores its sums
+    // (device scope), waits until they are acknowledged and then counts
+    // itself done.  The last arriver keeps its own sums in registers, waits
+    // until the others -- all of which hold tickets, so all are running and
+    // none waits on anything -- are done, and adds the slices in slice order.
+    // This takes the last arriver's store round trip off the critical path.
+    const size_t slice_stride = (size_t)M * N;
+    uint32_t* arrive = tickets + (size_t)tile * ticket_stride;
+    uint32_t* done = arrive + 1;
+    if (tid == 0) {
+        const uint32_t prev = __hip_atomic_fetch_add(arrive, 1u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+        last_flag = prev == (uint32_t)(slices - 1);
+    }
+    __syncthreads();
+    if (!last_flag) {
+#pragma unroll
+        for (int u = 0; u < T::kItems; u++) {
+            if (item_m[u] >= M) continue;
+            uint64_t* p = reinterpret_cast<uint64_t*>(partial + slice * slice_stride +
+                                                      (size_t)item_m[u] * N + n0 + item_c[u]);
+            __hip_atomic_store(p, __builtin_bit_cast(uint64_t, (f32x2){val[u].x, val[u].y}),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(p + 1, __builtin_bit_cast(uint64_t, (f32x2){val[u].z, val[u].w}),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __syncthreads();
+        if (tid == 0)
+            __hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    if (tid == 0) {
+        // bounded: every workgroup counted in `arrive` is running toward `done`
+        for (int spin = 0; spin < (1 << 22); spin++) {
+            if (__hip_atomic_load(done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                (uint32_t)(slices - 1))
+                break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
+    __syncthreads();
+    // every slice's sums in slice order, eight slices' loads in flight at a
+    // time; this workgroup's own come from registers
+    f32x4 sum[T::kItems];
+#pragma unroll
+    for (int u = 0; u < T::kItems; u++) sum[u] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < slices; s0 += 8) {
+        f32x4 v[T::kItems][8];
+#pragma unroll
+        for (int u = 0; u < T::kItems; u++) {
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const int sl = s0 + q;
+                v[u][q] = val[u];
+                if (item_m[u] < M && sl < slices && sl != slice) {
+                    uint64_t* p = reinterpret_cast<uint64_t*>(
+                        partial + sl * slice_stride + (size_t)item_m[u] * N + n0 + item_c[u]);
+                    const f32x2 lo = __builtin_bit_cast(
+                        f32x2, __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+                    const f32x2 hi = __builtin_bit_cast(
+                        f32x2,
+                        __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+                    v[u][q] = (f32x4){lo.x, lo.y, hi.x, hi.y};
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < T::kItems; u++)
+#pragma unroll
+            for (int q = 0; q < 8; q++)
+                if (s0 + q < slices) sum[u] += v[u][q];
+    }
+#pragma unroll
+    for (int u = 0; u < T::kItems; u++) {
+        if (item_m[u] >= M) continue;
+        float* o = out + (size_t)item_m[u] * N + n0 + item_c[u];
+        o[0] = sum[u].x; o[1] = sum[u].y; o[2] = sum[u].z; o[3] = sum[u].w;
+    }
+    if (tid == 0) {
+        __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
-// Slices: two workgroups per CU, partial sums within 1/8 of the codes, and
-// every slice a whole number of 32-k steps for each of the four waves.
-hipError_t launch_decode_mfma(Device* d, hipStream_t st, const float* a, Int4Planes w,
-                              float* out, int M, int K, int N, int* status) {
-    const int tiles = N / kMfmaCols;
-    constexpr int kQuantum = 32 * 4;
-    int slices = std::max(1, (2 * d->cu_count + tiles - 1) / tiles);
-    slices = std::min(slices, std::max(1, K / (64 * M)));
-    slices = std::min(slices, std::max(1, K / kQuantum));
-    slices = std::max(slices, (K + kMfmaMaxRows - 1) / kMfmaMaxRows);
-    int rows = (K + slices - 1) / slices;
-    rows = (rows + kQuantum - 1) / kQuantum * kQuantum;
-    if (rows > kMfmaMaxRows) rows = kMfmaMaxRows;
-    slices = (K + rows - 1) / rows;
+struct MfPlan {
+    int groups;   // G
+    int slices;
+    int rows;     // per slice, a multiple of 32
+};
+
+// Tile width and K slices: at most one workgroup per CU (a workgroup holds
+// 152 KiB of LDS, so more would wait for a second round), and the last
+// workgroup of a tile reads at most 128 / (G M) slices' sums (64 KiB at
+// M = 16).  Two-group tiles (128-byte
+// row segments) when the planes allow them and they fill the CUs as well
+// as one-group tiles do.
+MfPlan plan_decode_mfma(const Device* d, int M, int K, int N, bool planes_4b) {
+    MfPlan best{1, 1, K};
+    int best_wgs = -1;
+    for (int G = 2; G >= 1; G--) {
+        if (G == 2 && (N % 256 != 0 || !planes_4b)) continue;
+        const int tiles = N / (128 * G);
+        // one workgroup per CU: more would run in a second round
+        int slices = std::max(1, d->cu_count / tiles);
+        slices = std::max(1, std::min(slices, 128 / (G * M)));
+        slices = std::min(slices, std::max(1, K / 256));
+        const int rows = (K / 32 + slices - 1) / slices * 32;
+        slices = (K + rows - 1) / rows;
+        const int wgs = std::min(tiles * slices, d->cu_count);
+        if (wgs > best_wgs) {
+            best_wgs = wgs;
+            best = MfPlan{G, slices, rows};
+        }
+    }
+    return best;
+}
+
+template <int G, int NW>
+hipError_t launch_mfma(Device* d, hipStream_t st, const float* a, Int4Planes w, float* out,
+                       int M, int K, int N, const MfPlan& p, int* status) {
+    const int tiles = N / (128 * G);
     float* partial = nullptr;
     uint32_t* tickets = nullptr;
     int stride = 0;
-    if (slices > 1) {
-        stride = ticket_stride(tiles);
-        if (stride == 0) {
+    if (p.slices > 1) {
+        stride = ticket_stride(tiles);   // two counters a tile: arrivals, stores done
+        if (stride < 2) {
             *status = fail(ACCEL_E_INVALID,
                            "decode product: N=%d needs more tickets than the workspace holds", N);
             return hipSuccess;
         }
-        void* ws = workspace(d, (size_t)slices * M * N * sizeof(float), status);
+        void* ws = workspace(d, (size_t)p.slices * M * N * sizeof(float), status);
         if (!ws) return hipSuccess;
         tickets = static_cast<uint32_t*>(ws);
         partial = reinterpret_cast<float*>(static_cast<char*>(ws) + kWorkspaceCounterBytes);
     }
-    hipLaunchKernelGGL(int4_decode_mfma_kernel, dim3(tiles * slices), dim3(kThreads), 0, st, a,
-                       w.codes, w.scales, w.zeros, out, partial, tickets, stride, M, K, N, rows,
-                       slices);
+    hipLaunchKernelGGL((int4_decode_mfma_kernel<G, NW>), dim3(tiles * p.slices), dim3(64 * NW),
+                       0, st, a, w.codes, w.scales, w.zeros, out, partial, tickets, stride, M, K,
+                       N, p.rows, p.slices);
     return hipGetLastError();
+}
+
+hipError_t launch_decode_mfma(Device* d, hipStream_t st, const float* a, Int4Planes w,
+                              float* out, int M, int K, int N, int* status) {
+    const bool planes_4b = ((reinterpret_cast<uintptr_t>(w.scales) |
+                             reinterpret_cast<uintptr_t>(w.zeros)) & 3) == 0;
+    const MfPlan p = plan_decode_mfma(d, M, K, N, planes_4b);
+    if (p.groups == 2) return launch_mfma<2, 8>(d, st, a, w, out, M, K, N, p, status);
+    return launch_mfma<1, 8>(d, st, a, w, out, M, K, N, p, status);
 }
 
 }  // namespace
@@ -699,8 +1105,9 @@ bool int4_decode_f32_supported(int M, int K, int N, const void* codes) {
 hipError_t launch_int4_decode_f32(Device* d, hipStream_t st, const float* a, Int4Planes w,
                                   float* out, int M, int K, int N, int* status) {
     *status = ACCEL_OK;
-    // Three or more rows: the matrix-core kernel, where its shape holds.
-    if (M >= 3 && K % 32 == 0 && (reinterpret_cast<uintptr_t>(a) & 15) == 0)
+    // Three or more rows: the matrix-core kernel, where its shape holds (its
+    // per-lane code offsets within a 32-row step are 32-bit).
+    if (M >= 3 && K % 32 == 0 && N < (1 << 27) && (reinterpret_cast<uintptr_t>(a) & 15) == 0)
         return launch_decode_mfma(d, st, a, w, out, M, K, N, status);
     switch (M) {
         case 1: return launch_decode_m<1>(d, st, a, w, out, K, N, status);

@@ -106,6 +106,10 @@ SHAPES_F32 = [
     # K long enough that a workgroup loops over several batches of rows (256-
     # and 128-column tiles), and the layer chain's down projection
     (1, 16640, 256), (2, 33000, 128), (1, 14336, 4096),
+    # the matrix-core decode kernel: one- and two-group tiles, one step, a few
+    # steps, several slices, the layer chain's down projection
+    (4, 4096, 4096), (9, 1024, 384), (11, 2048, 768), (15, 14336, 4096), (16, 96, 256),
+    (6, 32, 128), (10, 4096, 1024),
 ]
 
 
