@@ -519,7 +519,7 @@ struct MfTile {
     static constexpr int kVmemPerStep = kCodeDma + 2 + 1;   // + activations, scale/zero
     static constexpr int kItems = 16 * kCols / 4 / kThreads;  // f32x4 outputs per lane
     static_assert(kDepth >= 2 && kDepth <= 8, "ring depth");
-    static_assert(NW * 16 * (kCols + G) * 4 <= kMfLdsBytes, "reduction LDS");
+    static_assert(NW * 16 * (kCols + 4 + G) * 4 <= kMfLdsBytes, "reduction LDS");
     static_assert(kItems >= 1 && 16 * kCols / 4 == kItems * kThreads, "items");
 };
 
@@ -888,13 +888,16 @@ __global__ __launch_bounds__(64 * NW) void int4_decode_mfma_kernel(
 
     // ---- epilogue: the waves' sums meet in LDS --------------------------
     __syncthreads();
-    float* red = reinterpret_cast<float*>(lds);                       // [wave][16][kCols]
-    float* red_bias = red + NW * 16 * T::kCols;                 // [wave][16][G]
+    // rows padded by four floats: the four kg rows a store instruction
+    // writes land in different banks
+    constexpr int RS = T::kCols + 4;
+    float* red = reinterpret_cast<float*>(lds);                       // [wave][16][RS]
+    float* red_bias = red + NW * 16 * RS;                             // [wave][16][G]
 #pragma unroll
     for (int g = 0; g < G; g++) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            float* dst = red + (size_t)(wave * 16 + 4 * kg + i) * T::kCols + 128 * g + 8 * c16;
+            float* dst = red + (size_t)(wave * 16 + 4 * kg + i) * RS + 128 * g + 8 * c16;
             *reinterpret_cast<f32x4*>(dst) =
                 (f32x4){acc[g][0][i], acc[g][1][i], acc[g][2][i], acc[g][3][i]};
             *reinterpret_cast<f32x4*>(dst + 4) =
@@ -922,7 +925,7 @@ __global__ __launch_bounds__(64 * NW) void int4_decode_mfma_kernel(
         if (m < M) {
 #pragma unroll
             for (int w = 0; w < NW; w++)
-                s += *reinterpret_cast<const f32x4*>(red + (size_t)(w * 16 + m) * T::kCols + c);
+                s += *reinterpret_cast<const f32x4*>(red + (size_t)(w * 16 + m) * RS + c);
 #pragma unroll
             for (int w = 0; w < NW; w++) bsum += red_bias[(w * 16 + m) * G + c / 128];
         }
