@@ -122,6 +122,9 @@ SIGNATURES = {
                                    _P(Tensor), _P(Tensor)], _i),
     "accel_int4_grouped_matmul": ([_i, _vp, _P(Tensor), _P(Int4Desc), ctypes.c_int64,
                                    _P(Tensor), _P(Tensor)], _i),
+    "accel_swiglu": ([_i, _vp, _P(Tensor), _P(Tensor), _P(Tensor)], _i),
+    "accel_rmsnorm": ([_i, _vp, _P(Tensor), _P(Tensor), ctypes.c_float, _P(Tensor)], _i),
+    "accel_matvec_f32_f16": ([_i, _vp, _P(Tensor), _P(Tensor), _P(Tensor)], _i),
     "accel_int4_quantize": ([_vp, ctypes.c_int64, _vp, _vp, _vp], _i),
     "accel_int4_dequantize": ([_vp, _vp, _vp, ctypes.c_int64, _vp], _i),
     "accel_int4_quantize_device": ([_i, _vp, _vp, ctypes.c_int64, _vp, _vp, _vp], _i),
@@ -389,6 +392,25 @@ class Device:
         _check(_lib.accel_int4_grouped_matmul(self.index, stream, ctypes.byref(tx),
                                               ctypes.byref(tw), experts, ctypes.byref(tc),
                                               ctypes.byref(to)))
+
+    def SwiGLU(self, gate: Buffer, value: Buffer, out: Buffer, stream=None) -> None:
+        """tensor.SwiGLU (tensor/elementwise.go:161-189)."""
+        tg, tv, to = gate.tensor(), value.tensor(), out.tensor()
+        _check(_lib.accel_swiglu(self.index, stream, ctypes.byref(tg), ctypes.byref(tv),
+                                 ctypes.byref(to)))
+
+    def RMSNorm(self, x: Buffer, gain: Buffer, eps: float, out: Buffer, stream=None) -> None:
+        """tensor.RMSNorm (tensor/ops.go:105-135)."""
+        tx, tg, to = x.tensor(), gain.tensor(), out.tensor()
+        _check(_lib.accel_rmsnorm(self.index, stream, ctypes.byref(tx), ctypes.byref(tg),
+                                  ctypes.c_float(eps), ctypes.byref(to)))
+
+    def MatVecF32F16(self, x: Buffer, w: Buffer, out: Buffer, stream=None) -> None:
+        """tensor.MatMul's M = 1 selection for f32 x and f16 w (MatVecF32F16,
+        tensor/matmul.go:113-121)."""
+        tx, tw, to = x.tensor(), w.tensor(), out.tensor()
+        _check(_lib.accel_matvec_f32_f16(self.index, stream, ctypes.byref(tx), ctypes.byref(tw),
+                                         ctypes.byref(to)))
 
     def int4_quantize(self, w: Buffer, n: int, packed: Buffer, scales: Buffer, zeros: Buffer,
                       stream=None) -> None:

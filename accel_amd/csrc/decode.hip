@@ -401,6 +401,143 @@ hipError_t launch_decode_m(Device* d, hipStream_t st, const float* a, Int4Planes
     return launch_decode<M, 128, CPL>(d, st, a, w, out, K, N, status);
 }
 
+// ---- MatVecF32F16: f32 activations against f16 weights --------------------
+//
+// The reference's MatVecF32F16 (internal/kernels/matvec.go:79-105) is the
+// M = 1 product a transformer decode step has besides the int4 ones (f16
+// weights such as an output projection).  HBM-bound like the int4 matvec and
+// built the same way: a 512-lane workgroup owns TILE columns and a K slice;
+// a lane owns eight adjacent columns (one 16-byte load a row) and kBatch rows
+// of its row phase, all its loads issued before any is used; the row phases
+// meet through the same cross-lane and LDS stages, and the slices through
+// the same deterministic hand-off.  The f32 sums are formed in a different
+// order from the reference's 16-phase one, so results agree to f32 rounding,
+// not bit for bit.
+template <int TILE>
+__global__ __launch_bounds__(kDecThreads) void matvec_f16_kernel(
+    const float* __restrict__ a, const uint16_t* __restrict__ w, float* __restrict__ out,
+    float* partial, uint32_t* tickets, int ticket_stride, int K, int N, int rows_per_slice,
+    int slices) {
+    constexpr int CPL = 8;
+    constexpr int LPR = TILE / CPL;
+    constexpr int RP = kDecThreads / LPR;
+    constexpr int RPW = 64 / LPR;
+    constexpr int NWAVE = kDecThreads / 64;
+    __shared__ __attribute__((aligned(16))) float red[NWAVE][TILE];
+    __shared__ int last_flag;
+
+    const int tiles = N / TILE;
+    const int grid = tiles * slices;
+    int b = blockIdx.x;
+    if ((grid & 7) == 0) b = (b & 7) * (grid >> 3) + (b >> 3);
+    const int tile = b % tiles;
+    const int slice = b / tiles;
+    const int tid = threadIdx.x;
+    const int l64 = tid & 63;
+    const int wave = tid >> 6;
+    const int lane = tid % LPR;
+    const int rp = tid / LPR;
+    const int col0 = tile * TILE + lane * CPL;
+    const int k_begin = slice * rows_per_slice;
+    const int k_end = min(K, k_begin + rows_per_slice);
+    const uint16_t* wcol = w + col0;
+
+    float acc[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; j++) acc[j] = 0.0f;
+    for (int kb = k_begin; kb < k_end; kb += kBatch * RP) {
+        u32x4 q[kBatch];
+        float xv[kBatch];
+#pragma unroll
+        for (int i = 0; i < kBatch; i++) {
+            const int row = min(kb + rp + i * RP, k_end - 1);
+            q[i] = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4*>(wcol + (size_t)row * N));
+        }
+#pragma unroll
+        for (int i = 0; i < kBatch; i++) xv[i] = a[min(kb + rp + i * RP, k_end - 1)];
+#pragma unroll
+        for (int i = 0; i < kBatch; i++) {
+            const float c = kb + rp + i * RP < k_end ? xv[i] : 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t pair = q[i][j];
+                acc[2 * j] = __builtin_fmaf(c, half_bits_to_float((uint16_t)pair), acc[2 * j]);
+                acc[2 * j + 1] =
+                    __builtin_fmaf(c, half_bits_to_float((uint16_t)(pair >> 16)), acc[2 * j + 1]);
+            }
+        }
+    }
+
+    constexpr int NV = CPL / RPW;
+    transpose_reduce<CPL, 64 / 2, LPR>(acc, l64);
+    const int c0 = lane * CPL + reduced_offset<CPL, 64 / 2, LPR>(l64);
+#pragma unroll
+    for (int e = 0; e < NV; e++) red[wave][c0 + e] = acc[e];
+    __syncthreads();
+    const bool split = slices > 1;
+    for (int c = tid; c < TILE; c += kDecThreads) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int wv = 0; wv < NWAVE; wv++) sum += red[wv][c];
+        const int col = tile * TILE + c;
+        if (split)
+            store_device(&partial[(size_t)slice * N + col], sum);
+        else
+            out[col] = sum;
+    }
+    if (!split) return;
+    split_k_finish(partial, tickets + (size_t)tile * ticket_stride, out, tile * TILE, TILE, 1, N,
+                   slices, &last_flag);
+}
+
+// Any shape: one lane per column, the reference's 16-phase order.
+__global__ void matvec_f16_generic_kernel(const float* __restrict__ a,
+                                          const uint16_t* __restrict__ w,
+                                          float* __restrict__ out, int K, int N) {
+    const int col = blockIdx.x * blockDim.x + threadIdx.x;
+    if (col >= N) return;
+    float sum = 0.0f;
+    for (int p = 0; p < 16; p++) {
+        float acc = 0.0f;
+        for (int k = p; k < K; k += 16)
+            acc = __builtin_fmaf(a[k], half_bits_to_float(w[(size_t)k * N + col]), acc);
+        sum += acc;
+    }
+    out[col] = sum;
+}
+
+template <int TILE>
+hipError_t launch_matvec_f16_tiled(Device* d, hipStream_t st, const float* a, const uint16_t* w,
+                                   float* out, int K, int N, int* status) {
+    constexpr int LPR = TILE / 8;
+    constexpr int RP = kDecThreads / LPR;
+    constexpr int kRowsPerBatch = kBatch * RP;
+    const int tiles = N / TILE;
+    const int batches = (K + kRowsPerBatch - 1) / kRowsPerBatch;
+    const int per_slice = (batches + kMaxSlices - 1) / kMaxSlices;
+    const int rows = per_slice * kRowsPerBatch;
+    const int slices = (K + rows - 1) / rows;
+    float* partial = nullptr;
+    uint32_t* tickets = nullptr;
+    int stride = 0;
+    if (slices > 1) {
+        stride = ticket_stride(tiles);
+        if (stride == 0) {
+            *status = fail(ACCEL_E_INVALID,
+                           "matvec: N=%d needs more tickets than the workspace holds", N);
+            return hipSuccess;
+        }
+        void* ws = workspace(d, (size_t)slices * N * sizeof(float), status);
+        if (!ws) return hipSuccess;
+        tickets = static_cast<uint32_t*>(ws);
+        partial = reinterpret_cast<float*>(static_cast<char*>(ws) + kWorkspaceCounterBytes);
+    }
+    hipLaunchKernelGGL((matvec_f16_kernel<TILE>), dim3(tiles * slices), dim3(kDecThreads), 0, st,
+                       a, w, out, partial, tickets, stride, K, N, rows, slices);
+    return hipGetLastError();
+}
+
 // Any shape: one lane per output element, decoding with the flat index.
 __global__ void int4_generic_f32_kernel(const float* __restrict__ a,
                                         const uint32_t* __restrict__ codes,
@@ -1099,6 +1236,20 @@ hipError_t launch_decode_mfma(Device* d, hipStream_t st, const float* a, Int4Pla
 }
 
 }  // namespace
+
+hipError_t launch_matvec_f32_f16(Device* d, hipStream_t st, const float* a, const uint16_t* w,
+                                 float* out, int K, int N, int* status) {
+    *status = ACCEL_OK;
+    if (K <= 0 || N <= 0) return hipSuccess;
+    const bool aligned = (reinterpret_cast<uintptr_t>(w) & 15) == 0;
+    if (aligned && N % 256 == 0 && N < (1 << 30))
+        return launch_matvec_f16_tiled<256>(d, st, a, w, out, K, N, status);
+    if (aligned && N % 128 == 0 && N < (1 << 30))
+        return launch_matvec_f16_tiled<128>(d, st, a, w, out, K, N, status);
+    hipLaunchKernelGGL(matvec_f16_generic_kernel, dim3((N + 255) / 256), dim3(256), 0, st, a, w,
+                       out, K, N);
+    return hipGetLastError();
+}
 
 bool int4_decode_f32_supported(int M, int K, int N, const void* codes) {
     return M >= 1 && M <= 16 && K >= 1 && N >= 128 && N % 128 == 0 &&

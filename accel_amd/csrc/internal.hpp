@@ -91,6 +91,14 @@ hipError_t launch_int4_grouped_bf16(Device* d, hipStream_t st, const uint16_t* x
                                     Int4Planes w, const uint32_t* off, uint16_t* out,
                                     int E, int T, int K, int N, bool write_padding);
 
+// Decode-step neighbours: MatVecF32F16 (f32 a [K], f16 w [K,N] -> f32 [N]),
+// SwiGLU over n elements, RMSNorm over `rows` rows of `width`.
+hipError_t launch_matvec_f32_f16(Device* d, hipStream_t st, const float* a, const uint16_t* w,
+                                 float* out, int K, int N, int* status);
+hipError_t launch_swiglu(hipStream_t st, const float* a, const float* b, float* out, int64_t n);
+hipError_t launch_rmsnorm(hipStream_t st, const float* x, const float* w, float* out, int rows,
+                          int width, float eps);
+
 // Device quantizer.
 hipError_t launch_int4_quantize(hipStream_t st, const float* w, int64_t n,
                                 uint32_t* packed, uint16_t* scales, uint16_t* zeros);

@@ -11,6 +11,7 @@
 //   any other shape                          -> the per-element kernel
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstring>
 #include <string>
 
@@ -485,6 +486,147 @@ ACCEL_API int accel_int4_quantize_device(int dev, void* stream, const float* w, 
                     "quantize launch");
 }
 
+// ---- decode-step neighbours -------------------------------------------------
+
+namespace {
+
+bool same_shape(const accel_tensor_t* a, const accel_tensor_t* b) {
+    if (a->rank != b->rank) return false;
+    for (int i = 0; i < a->rank; i++)
+        if (a->shape[i] != b->shape[i]) return false;
+    return true;
+}
+
+}  // namespace
+
+// tensor.SwiGLU (tensor/elementwise.go:161-189) over the registered f32
+// kernel: gate, value and out share one shape.
+ACCEL_API int accel_swiglu(int dev, void* stream, const accel_tensor_t* gate,
+                           const accel_tensor_t* value, accel_tensor_t* out) {
+    clear_error();
+    const char* op = "SwiGLU";
+    char buf[256];
+    if (!valid_tensor(gate) || !gate->data || !valid_tensor(value) || !value->data)
+        return refuse(op, "an operand is missing");
+    if (gate->dtype != value->dtype) {
+        snprintf(buf, sizeof buf, "operands are %s and %s", dtype_name(gate->dtype),
+                 dtype_name(value->dtype));
+        return refuse(op, buf);
+    }
+    if (gate->dtype != ACCEL_F32) {
+        snprintf(buf, sizeof buf, "%s has no SwiGLU kernel here; the registered kernel reads f32",
+                 dtype_name(gate->dtype));
+        return refuse(op, buf);
+    }
+    if (!same_shape(gate, value)) {
+        snprintf(buf, sizeof buf,
+                 "shapes %s and %s differ; the fused kernel indexes both operands together, so "
+                 "broadcasting one would need the composed form",
+                 shape_str(gate).c_str(), shape_str(value).c_str());
+        return refuse(op, buf);
+    }
+    if (!valid_tensor(out) || !out->data || out->dtype != ACCEL_F32 || !same_shape(out, gate))
+        return refuse(op, "the output must be f32 with the operands' shape");
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    int status = begin_submission(d);
+    if (status != ACCEL_OK) return status;
+    hipError_t e = launch_swiglu((hipStream_t)stream, static_cast<const float*>(gate->data),
+                                 static_cast<const float*>(value->data),
+                                 static_cast<float*>(out->data), elements(gate));
+    return classify(d, e, "SwiGLU launch");
+}
+
+// tensor.RMSNorm (tensor/ops.go:105-135): x f32 of any rank >= 1, gain f32
+// [width] with width x's last axis, eps positive and finite.
+ACCEL_API int accel_rmsnorm(int dev, void* stream, const accel_tensor_t* x,
+                            const accel_tensor_t* gain, float eps, accel_tensor_t* out) {
+    clear_error();
+    const char* op = "RMSNorm";
+    char buf[256];
+    if (!valid_tensor(x) || !x->data || !valid_tensor(gain) || !gain->data)
+        return refuse(op, "an operand is missing");
+    if (x->dtype != ACCEL_F32 || gain->dtype != ACCEL_F32) {
+        snprintf(buf, sizeof buf,
+                 "x is %s and gain is %s; the registered kernel reads f32",
+                 dtype_name(x->dtype), dtype_name(gain->dtype));
+        return refuse(op, buf);
+    }
+    if (x->rank < 1) return refuse(op, "x has no shape");
+    const int64_t width = x->shape[x->rank - 1];
+    if (gain->rank != 1 || gain->shape[0] != width) {
+        snprintf(buf, sizeof buf,
+                 "gain is %s and x's last axis is %lld; the gain is one value per feature",
+                 shape_str(gain).c_str(), (long long)width);
+        return refuse(op, buf);
+    }
+    if (!(eps > 0) || !(eps < INFINITY)) {
+        snprintf(buf, sizeof buf,
+                 "eps is %g and must be positive and finite: it is what keeps a row of zeros "
+                 "from dividing by zero",
+                 (double)eps);
+        return refuse(op, buf);
+    }
+    if (!valid_tensor(out) || !out->data || out->dtype != ACCEL_F32 || !same_shape(out, x))
+        return refuse(op, "the output must be f32 with x's shape");
+    const int64_t rows = width ? elements(x) / width : 0;
+    if (width > INT32_MAX || rows > INT32_MAX)
+        return fail(ACCEL_E_UNSUPPORTED, "accel/tensor: RMSNorm: %lld rows of %lld are more than "
+                    "this kernel's 32-bit grid indexes", (long long)rows, (long long)width);
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    int status = begin_submission(d);
+    if (status != ACCEL_OK) return status;
+    hipError_t e = launch_rmsnorm((hipStream_t)stream, static_cast<const float*>(x->data),
+                                  static_cast<const float*>(gain->data),
+                                  static_cast<float*>(out->data), (int)rows, (int)width, eps);
+    return classify(d, e, "RMSNorm launch");
+}
+
+// tensor.MatMul's M = 1 selection for f32 activations against f16 weights
+// (tensor/matmul.go:113-121 -> MatVecF32F16): x f32 [1,K] or [K], w f16
+// [K,N] (raw f16 bits) -> out f32 [1,N] or [N].  Larger M selects the mixed
+// tiled GEMM in the reference, which is not built here.
+ACCEL_API int accel_matvec_f32_f16(int dev, void* stream, const accel_tensor_t* x,
+                                   const accel_tensor_t* w, accel_tensor_t* out) {
+    clear_error();
+    const char* op = "MatMul";
+    char buf[256];
+    if (!valid_tensor(x) || !x->data || !valid_tensor(w) || !w->data)
+        return refuse(op, "an operand is missing");
+    if (x->dtype != ACCEL_F32 || w->dtype != ACCEL_F16) {
+        snprintf(buf, sizeof buf,
+                 "operands are %s and %s; this entry point is the f32-activation, f16-weight "
+                 "pair", dtype_name(x->dtype), dtype_name(w->dtype));
+        return refuse(op, buf);
+    }
+    if (w->rank != 2) return refuse(op, "w must be [K N]");
+    const int64_t K = w->shape[0], N = w->shape[1];
+    const bool vec = x->rank == 1;
+    if (!(vec ? x->shape[0] == K : (x->rank == 2 && x->shape[1] == K))) {
+        snprintf(buf, sizeof buf, "x is %s and w is %s; the inner dimensions must agree",
+                 shape_str(x).c_str(), shape_str(w).c_str());
+        return refuse(op, buf);
+    }
+    if (!vec && x->shape[0] != 1)
+        return fail(ACCEL_E_UNSUPPORTED,
+                    "accel/tensor: MatMul: x has %lld rows; the f32 x f16 product is built for "
+                    "M = 1 (MatVecF32F16) only",
+                    (long long)x->shape[0]);
+    const int rc = check_out(op, out, ACCEL_F32, 1, N, vec);
+    if (rc != ACCEL_OK) return rc;
+    if (K > INT32_MAX || N > INT32_MAX)
+        return fail(ACCEL_E_UNSUPPORTED, "accel/tensor: MatMul: dimensions past 2^31");
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    int status = begin_submission(d);
+    if (status != ACCEL_OK) return status;
+    hipError_t e = launch_matvec_f32_f16(d, (hipStream_t)stream, static_cast<const float*>(x->data),
+                                         static_cast<const uint16_t*>(w->data),
+                                         static_cast<float*>(out->data), (int)K, (int)N, &status);
+    return finish(d, e, status, "MatVecF32F16 launch");
+}
+
 // ---- backend seam: kernel records ------------------------------------------
 
 namespace {
@@ -495,7 +637,8 @@ struct Record {
 };
 const Record kRecords[] = {
     {"QuantMatVecInt4", 5}, {"QuantMatMulInt4", 5}, {"GroupedMatVec", 4},
-    {"GroupedMatMul", 4},   {"SegmentOffsets", 2},
+    {"GroupedMatMul", 4},   {"SegmentOffsets", 2},  {"SwiGLU", 3},
+    {"RMSNorm", 3},         {"MatVecF32F16", 3},
 };
 
 uint32_t u32_at(const void* p, size_t off) {
@@ -529,9 +672,42 @@ ACCEL_API int accel_hip_dispatch(int dev, void* stream, const char* kernel,
     if (nbindings != rec->bindings || !bindings || !lens)
         return fail(ACCEL_E_INVALID, "accel_hip: %s takes %d bindings, got %d", kernel,
                     rec->bindings, nbindings);
+    std::string name = kernel;
+    if (name == "SwiGLU") {
+        // no uniform: the length is out's (elementwise.go:85-91)
+        const uint64_t n = lens[2];
+        if (lens[0] < n || lens[1] < n)
+            return fail(ACCEL_E_INVALID, "accel_hip: SwiGLU bindings are shorter than out");
+        accel_tensor_t g = {const_cast<void*>(bindings[0]), ACCEL_F32, 1, {(int64_t)n, 0, 0, 0}};
+        accel_tensor_t v = {const_cast<void*>(bindings[1]), ACCEL_F32, 1, {(int64_t)n, 0, 0, 0}};
+        accel_tensor_t o = {const_cast<void*>(bindings[2]), ACCEL_F32, 1, {(int64_t)n, 0, 0, 0}};
+        return accel_swiglu(dev, stream, &g, &v, &o);
+    }
     if (!uniform || uniform_bytes < 16)
         return fail(ACCEL_E_INVALID, "accel_hip: %s needs its 16-byte uniform block", kernel);
-    std::string name = kernel;
+    if (name == "RMSNorm") {
+        // RowDims {Rows@0, Width@4, Eps@8} (norm.go:13-22)
+        const uint32_t rows = u32_at(uniform, 0), width = u32_at(uniform, 4);
+        float eps;
+        std::memcpy(&eps, static_cast<const char*>(uniform) + 8, 4);
+        if (lens[0] < (uint64_t)rows * width || lens[1] < width || lens[2] < (uint64_t)rows * width)
+            return fail(ACCEL_E_INVALID, "accel_hip: RMSNorm bindings are shorter than its dims");
+        accel_tensor_t x = {const_cast<void*>(bindings[0]), ACCEL_F32, 2, {rows, width, 0, 0}};
+        accel_tensor_t g = {const_cast<void*>(bindings[1]), ACCEL_F32, 1, {width, 0, 0, 0}};
+        accel_tensor_t o = {const_cast<void*>(bindings[2]), ACCEL_F32, 2, {rows, width, 0, 0}};
+        return accel_rmsnorm(dev, stream, &x, &g, eps, &o);
+    }
+    if (name == "MatVecF32F16") {
+        // GEMMDims {M@0, N@4, K@8}
+        const uint32_t N = u32_at(uniform, 4), K = u32_at(uniform, 8);
+        if (lens[0] < K || lens[1] < (uint64_t)K * N || lens[2] < N)
+            return fail(ACCEL_E_INVALID,
+                        "accel_hip: MatVecF32F16 bindings are shorter than its dims");
+        accel_tensor_t a = {const_cast<void*>(bindings[0]), ACCEL_F32, 1, {K, 0, 0, 0}};
+        accel_tensor_t wt = {const_cast<void*>(bindings[1]), ACCEL_F16, 2, {K, N, 0, 0}};
+        accel_tensor_t o = {const_cast<void*>(bindings[2]), ACCEL_F32, 1, {N, 0, 0, 0}};
+        return accel_matvec_f32_f16(dev, stream, &a, &wt, &o);
+    }
     if (name == "QuantMatVecInt4" || name == "QuantMatMulInt4") {
         // GEMMDims std140: M@0, N@4, K@8.  The matvec's M is unused (0).
         const uint32_t M = name == "QuantMatVecInt4" ? 1u : u32_at(uniform, 0);

@@ -232,7 +232,9 @@ def bench_layer_chain(dev, stream, batch, steps=100):
         total_bytes += packed.nbytes + scales.nbytes + zeros.nbytes
         bufs[name] = dev.alloc((batch, N) if batch > 1 else (N,), F32)
     xin = dev.upload(x if batch > 1 else x[0])
-    inter = dev.alloc((batch, 14336) if batch > 1 else (14336,), F32)
+    # the down projection's input (the caller's gate*up), as activations
+    hmid = rng.standard_normal((batch, 14336)).astype(np.float32)
+    inter = dev.upload(hmid if batch > 1 else hmid[0])
 
     def op(a, w, o):
         if batch > 1:
@@ -261,6 +263,89 @@ def bench_layer_chain(dev, stream, batch, steps=100):
     return dict(us_per_step=round(ms * 1e3, 2),
                 gbs=round(total_bytes / (ms * 1e-3) / 1e9, 1),
                 weight_bytes=total_bytes, batch=batch)
+
+
+def bench_matvec_f16(dev, stream, K=4096, N=4096, steps=200):
+    """MatVecF32F16 (f32 x [K], f16 w [K,N]) over f16 weight copies totalling
+    more than 512 MB, so every call reads HBM."""
+    from accel_amd import F16, F32
+    rng = np.random.Generator(np.random.PCG64(5))
+    wbits = (rng.standard_normal(K * N, dtype=np.float32) * 0.02).astype(np.float16)
+    wbits = wbits.view(np.uint16).reshape(K, N)
+    copies = max(1, -(-ROTATE_BYTES // wbits.nbytes))
+    ws = [dev.upload(wbits, F16) for _ in range(copies)]
+    a = dev.upload(rng.standard_normal(K).astype(np.float32))
+    out = dev.alloc((N,), F32)
+    for w in ws:
+        dev.MatVecF32F16(a, w, out, stream)
+    dev.sync(stream)
+    t = Timed(dev, stream, lambda i: dev.MatVecF32F16(a, ws[i % copies], out, stream), steps)
+    ms = median_replay(t) / steps
+    t.close()
+    for b in ws + [a, out]:
+        b.free()
+    nbytes = K * N * 2 + 4 * K + 4 * N
+    return dict(us=round(ms * 1e3, 3), gbs=round(nbytes / (ms * 1e-3) / 1e9, 1),
+                frac_of_hbm=round(nbytes / (ms * 1e-3) / 8e12, 4), K=K, N=N, copies=copies)
+
+
+def bench_decode_step(dev, stream, batch, steps=100):
+    """Config 5's layer as a whole decode step with its on-device neighbours:
+    h = RMSNorm(x); q,k,v <- h; o <- q; h2 = RMSNorm(o); gate,up <- h2;
+    a = SwiGLU(gate, up); down <- a.  Ten launches a step, captured in one
+    HIP graph and replayed (attention itself is outside the int4 path)."""
+    from accel_amd import F32, workloads
+    shapes = workloads.LAYER_SHAPES
+    rng = np.random.Generator(np.random.PCG64(4))
+    x = rng.standard_normal((batch, 4096)).astype(np.float32)
+    g1 = (rng.standard_normal(4096) * 0.1 + 1).astype(np.float32)
+    g2 = (rng.standard_normal(4096) * 0.1 + 1).astype(np.float32)
+    if not _LAYER_PLANES:
+        for name, (K, N) in shapes.items():
+            _LAYER_PLANES[name] = workloads.fast_int4(K, N, rng)
+    ws, bufs = {}, {}
+    total_bytes = 0
+    shape = (lambda n: (batch, n)) if batch > 1 else (lambda n: (n,))
+    for name, (K, N) in shapes.items():
+        packed, scales, zeros = _LAYER_PLANES[name]
+        ws[name] = dev.upload_int4(packed, scales, zeros, K * N)
+        total_bytes += packed.nbytes + scales.nbytes + zeros.nbytes
+        bufs[name] = dev.alloc(shape(N), F32)
+    xin = dev.upload(x if batch > 1 else x[0])
+    gb1, gb2 = dev.upload(g1), dev.upload(g2)
+    h1, h2 = dev.alloc(shape(4096), F32), dev.alloc(shape(4096), F32)
+    act = dev.alloc(shape(14336), F32)
+
+    def op(a, w, o):
+        if batch > 1:
+            dev.Int4MatMul(a, w, o, stream)
+        else:
+            dev.Int4MatVec(a, w, o, stream)
+
+    def step(i):
+        dev.RMSNorm(xin, gb1, 1e-5, h1, stream)
+        op(h1, ws["q"], bufs["q"])
+        op(h1, ws["k"], bufs["k"])
+        op(h1, ws["v"], bufs["v"])
+        op(bufs["q"], ws["o"], bufs["o"])
+        dev.RMSNorm(bufs["o"], gb2, 1e-5, h2, stream)
+        op(h2, ws["gate"], bufs["gate"])
+        op(h2, ws["up"], bufs["up"])
+        dev.SwiGLU(bufs["gate"], bufs["up"], act, stream)
+        op(act, ws["down"], bufs["down"])
+
+    step(0)
+    dev.sync(stream)
+    t = Timed(dev, stream, step, steps)
+    ms = median_replay(t) / steps
+    t.close()
+    for w in ws.values():
+        w.free()
+    for b in list(bufs.values()) + [xin, gb1, gb2, h1, h2, act]:
+        b.free()
+    return dict(us_per_step=round(ms * 1e3, 2),
+                gbs=round(total_bytes / (ms * 1e-3) / 1e9, 1),
+                weight_bytes=total_bytes, batch=batch, launches=10)
 
 
 def cpu_baseline(L, seconds):
@@ -351,6 +436,9 @@ def main():
             extra["moe_grouped_bf16"] = bench_moe(dev, stream)
             extra["layer_chain_b1"] = bench_layer_chain(dev, stream, 1)
             extra["layer_chain_b8"] = bench_layer_chain(dev, stream, 8)
+            extra["matvec_f32_f16"] = bench_matvec_f16(dev, stream)
+            extra["decode_step_b1"] = bench_decode_step(dev, stream, 1)
+            extra["decode_step_b8"] = bench_decode_step(dev, stream, 8)
         line["extra"] = extra
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(L, args.cpu_seconds)

@@ -156,9 +156,14 @@ int accel_hip_supports_kernel(const char* kernel);
  *   GroupedMatVec    x f32, w f32, offsets u32, out f32;      GroupedDims
  *   GroupedMatMul    x f32, w f32, offsets u32, out f32;      GroupedTiledDims
  *   SegmentOffsets   counts u32, offsets u32;                 SegmentDims
+ *   SwiGLU           a f32, b f32, out f32;                   (no uniform)
+ *   RMSNorm          x f32, w f32, out f32;                   RowDims
+ *   MatVecF32F16     a f32, b f16, out f32;                   GEMMDims
  * (internal/kernels/accel_kernels.go:6799-6808,7052-7061; GEMMDims is
  * {M@0,N@4,K@8}, GroupedDims {Experts@0,K@4,N@8}, GroupedTiledDims
- * {Experts@0,Tokens@4,K@8,N@12}, SegmentDims {Rows@0}, :173-231). */
+ * {Experts@0,Tokens@4,K@8,N@12}, SegmentDims {Rows@0}, :173-231; RowDims
+ * {Rows@0,Width@4,Eps@8 f32}, internal/kernels/norm.go:13-22; SwiGLU's length
+ * is out's, elementwise.go:85-91). */
 int accel_hip_dispatch(int dev, void* stream, const char* kernel,
                        const void* const* bindings, const uint64_t* lens,
                        int32_t nbindings, const void* uniform, size_t uniform_bytes,
@@ -235,6 +240,29 @@ int accel_int4_grouped_matvec(int dev, void* stream, const accel_tensor_t* x,
 int accel_int4_grouped_matmul(int dev, void* stream, const accel_tensor_t* x,
                               const accel_int4_t* w, int64_t experts,
                               const accel_tensor_t* counts, accel_tensor_t* out);
+
+/* ---- decode-step neighbours of the int4 products ---------------------- */
+
+/* tensor.SwiGLU (tensor/elementwise.go:161-189; kernel
+ * internal/kernels/elementwise.go:85-91): out = gate / (1 + Exp(-gate)) *
+ * value, f32, one shape for all three; Exp is the f64 exponential rounded to
+ * f32 (kmath/kmath.go:55).  Bit-identical to the reference CPU backend. */
+int accel_swiglu(int dev, void* stream, const accel_tensor_t* gate,
+                 const accel_tensor_t* value, accel_tensor_t* out);
+
+/* tensor.RMSNorm (tensor/ops.go:105-135; kernel internal/kernels/norm.go:
+ * 47-80): each row of x (f32, any rank >= 1) times RSqrt(mean(x^2) + eps),
+ * times gain (f32 [width]); eps > 0 and finite.  The reference's reduction
+ * order, so bit-identical to the reference CPU backend. */
+int accel_rmsnorm(int dev, void* stream, const accel_tensor_t* x,
+                  const accel_tensor_t* gain, float eps, accel_tensor_t* out);
+
+/* tensor.MatMul's M = 1 selection for f32 activations and f16 weights
+ * (tensor/matmul.go:113-121; kernel MatVecF32F16, internal/kernels/
+ * matvec.go:79-105): x f32 [K] or [1,K], w f16 [K,N] -> out f32 [N] or
+ * [1,N].  Other M are ACCEL_E_UNSUPPORTED. */
+int accel_matvec_f32_f16(int dev, void* stream, const accel_tensor_t* x,
+                         const accel_tensor_t* w, accel_tensor_t* out);
 
 /* quant.Int4Quantize (quant/int4.go:71-138) on host memory: packed holds
  * ceil(n/8) words, scales and zeros ceil(n/128) f16 each. */

@@ -83,6 +83,9 @@ def lib():
                                           _u16p, _u32p, _f32p, ctypes.c_int]
     L.orc_int4_grouped_matmul.argtypes = [_u32, _u32, _u32, _u32, _f32p, _u32p, _u16p,
                                           _u16p, _u32p, _f32p, ctypes.c_int]
+    L.orc_swiglu.argtypes = [_f32p, _f32p, _f32p, _i64]
+    L.orc_rmsnorm.argtypes = [_u32, _u32, ctypes.c_float, _f32p, _f32p, _f32p]
+    L.orc_matvec_f32_f16.argtypes = [_u32, _u32, _f32p, _u16p, _f32p]
     _lib = L
     return L
 
@@ -256,3 +259,38 @@ def matmul_f64(a, wdq, M: int, K: int, N: int) -> np.ndarray:
     """Exact-ish product of f32 activations and dequantized weights in f64."""
     return (np.asarray(a, np.float64).reshape(M, K) @
             np.asarray(wdq, np.float64).reshape(K, N))
+
+
+# ---- decode-step neighbours -------------------------------------------------
+
+def swiglu(a, b) -> np.ndarray:
+    """SwiGLU (internal/kernels/elementwise.go:85-91), f32 in reference order."""
+    a = _f32(a)
+    b = _f32(b)
+    assert a.shape == b.shape
+    out = np.empty_like(a)
+    lib().orc_swiglu(a.reshape(-1), b.reshape(-1), out.reshape(-1), a.size)
+    return out
+
+
+def rmsnorm(x, w, eps: float) -> np.ndarray:
+    """RMSNorm over the last axis (internal/kernels/norm.go:47-80)."""
+    x = _f32(x)
+    w = _f32(w)
+    width = x.shape[-1]
+    assert w.shape == (width,)
+    rows = x.size // width
+    out = np.empty_like(x)
+    lib().orc_rmsnorm(rows, width, eps, x.reshape(-1), w, out.reshape(-1))
+    return out
+
+
+def matvec_f32_f16(a, b_bits, K: int, N: int) -> np.ndarray:
+    """MatVecF32F16 (internal/kernels/matvec.go:79-105): a f32 [K], b f16 bits
+    [K, N] -> f32 [N]."""
+    a = _f32(a).reshape(-1)
+    b_bits = np.ascontiguousarray(b_bits, np.uint16).reshape(-1)
+    assert a.size == K and b_bits.size == K * N
+    out = np.empty(N, np.float32)
+    lib().orc_matvec_f32_f16(K, N, a, b_bits, out)
+    return out

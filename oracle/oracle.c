@@ -35,6 +35,14 @@
  *   orc_grouped_*       per-expert f64 brute force, empty expert, wrong-expert,
  *                       padding row, clamp (internal/kernels/grouped_test.go)
  *   orc_segment_offsets exclusive prefix sum against numpy.cumsum
+ *   orc_swiglu          f64 closed form x*b/(1+e^-x) within one f32 rounding
+ *                       chain, exact special values (0, +-inf limits, NaN)
+ *   orc_rmsnorm         the reference's tests (norm_test.go:34-191): widths
+ *                       1, 63, 128, 129, 500, 1024 against a straight f64
+ *                       loop within the reduction budget, a zero row reads 0;
+ *                       a row of ones equals w / sqrt(1 + eps) exactly
+ *   orc_matvec_f32_f16  f64 brute force within the f32 reduction bound, and
+ *                       exact sums where every partial is an exact integer
  */
 #include <math.h>
 #include <pthread.h>
@@ -586,4 +594,77 @@ void orc_int4_grouped_matmul(uint32_t E, uint32_t T, uint32_t K, uint32_t N,
                              int threads) {
     grouped_ctx c = {E, T, K, N, x, NULL, bq, bs, bz, off, out};
     grouped_matmul_run(&c, threads);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Decode-step neighbours of the int4 products.                              */
+/* ------------------------------------------------------------------------ */
+
+/* kmath.Exp and kmath.RSqrt (kmath/kmath.go:52,55): the f64 function, rounded
+ * once to f32. */
+static inline float kmath_exp(float x) { return (float)exp((double)x); }
+static inline float kmath_rsqrt(float x) { return (float)(1.0 / sqrt((double)x)); }
+
+/* SwiGLU (internal/kernels/elementwise.go:85-91):
+ * out[i] = a[i] / (1 + Exp(-a[i])) * b[i], each operation rounded to f32. */
+void orc_swiglu(const float* a, const float* b, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; i++) {
+        const float x = a[i];
+        const float e = kmath_exp(-x);
+        const float d = 1.0f + e;
+        const float q = x / d;
+        out[i] = q * b[i];
+    }
+}
+
+/* RMSNorm (internal/kernels/norm.go:47-80), one 128-invocation workgroup a
+ * row: invocation l sums x[i]^2 over i = l, l+128, ... in increasing i; the
+ * 128 partials are added by the halving tree (stride 64, 32, ..., 1; slot l
+ * += slot l+stride); mean = total / width, scale = RSqrt(mean + eps), and
+ * out[i] = (x[i] * scale) * w[i]. */
+void orc_rmsnorm(uint32_t rows, uint32_t width, float eps, const float* x, const float* w,
+                 float* out) {
+    for (uint32_t r = 0; r < rows; r++) {
+        const float* xr = x + (size_t)r * width;
+        float* orow = out + (size_t)r * width;
+        float sh[128];
+        for (uint32_t l = 0; l < 128; l++) {
+            float acc = 0.0f;
+            for (uint32_t i = l; i < width; i += 128) {
+                const float v = xr[i];
+                const float sq = v * v;
+                acc = acc + sq;
+            }
+            sh[l] = acc;
+        }
+        for (uint32_t stride = 64; stride > 0; stride /= 2)
+            for (uint32_t l = 0; l < stride; l++) sh[l] = sh[l] + sh[l + stride];
+        const float mean = sh[0] / (float)width;
+        const float scale = kmath_rsqrt(mean + eps);
+        for (uint32_t i = 0; i < width; i++) {
+            const float t = xr[i] * scale;
+            orow[i] = t * w[i];
+        }
+    }
+}
+
+/* MatVecF32F16 (internal/kernels/matvec.go:79-105): 32 columns x 16 phases a
+ * workgroup; phase p accumulates acc = acc + a[k] * F32(b[k*N+col]) over
+ * k = p, p+16, ...; the column is the sum of the 16 partials in phase order. */
+void orc_matvec_f32_f16(uint32_t K, uint32_t N, const float* a, const uint16_t* b,
+                        float* out) {
+    for (uint32_t col = 0; col < N; col++) {
+        float ph[16];
+        for (uint32_t p = 0; p < 16; p++) {
+            float acc = 0.0f;
+            for (uint32_t k = p; k < K; k += 16) {
+                const float prod = a[k] * orc_f16_to_f32(b[(size_t)k * N + col]);
+                acc = acc + prod;
+            }
+            ph[p] = acc;
+        }
+        float sum = 0.0f;
+        for (uint32_t p = 0; p < 16; p++) sum = sum + ph[p];
+        out[col] = sum;
+    }
 }

@@ -81,7 +81,7 @@ def test_host_packer_at_a_baseline_shape():
 
 def test_kernel_support_names_the_records():
     for k in ["QuantMatVecInt4", "QuantMatMulInt4", "GroupedMatVec", "GroupedMatMul",
-              "SegmentOffsets"]:
+              "SegmentOffsets", "SwiGLU", "RMSNorm", "MatVecF32F16"]:
         assert accel_amd.supports_kernel(k)
     assert not accel_amd.supports_kernel("MatMulTiledF32")
     assert not accel_amd.supports_kernel("")
@@ -195,6 +195,42 @@ def test_int4_grouped_refuses_straddling_groups():
     rc = lib.accel_int4_grouped_matmul(0, None, ctypes.byref(x), ctypes.byref(w), 3,
                                        ctypes.byref(t([3], U32)), ctypes.byref(t([4, 4], F32)))
     assert rc == accel_amd.E_INVALID and "straddles" in accel_amd.last_error()
+
+
+def test_swiglu_refusals():   # tensor/elementwise.go:161-189; ops_test.go:563-569
+    rc, msg = call("accel_swiglu", t([8], F32), t([8], F16), t([8], F32))
+    assert rc == accel_amd.E_INVALID and "operands are f32 and f16" in msg, msg
+    rc, msg = call("accel_swiglu", t([8], F32), t([4, 2], F32), t([8], F32))
+    assert rc == accel_amd.E_INVALID and "the fused kernel indexes both operands" in msg, msg
+    rc, msg = call("accel_swiglu", t([8], BF16), t([8], BF16), t([8], BF16))
+    assert rc == accel_amd.E_INVALID and "reads f32" in msg, msg
+
+
+def test_rmsnorm_refusals():   # tensor/ops.go:105-135; ops_test.go:448-456
+    lib = accel_amd.lib()
+
+    def rms(x, g, eps, o):
+        rc = lib.accel_rmsnorm(0, None, ctypes.byref(x), ctypes.byref(g), ctypes.c_float(eps),
+                               ctypes.byref(o))
+        return rc, accel_amd.last_error()
+
+    rc, msg = rms(t([4, 8], F32), t([4], F32), 1e-5, t([4, 8], F32))
+    assert rc == accel_amd.E_INVALID and "the gain is one value per feature" in msg, msg
+    rc, msg = rms(t([4, 8], F32), t([8], F32), 0.0, t([4, 8], F32))
+    assert rc == accel_amd.E_INVALID and "must be positive and finite" in msg, msg
+    rc, msg = rms(t([4, 8], F16), t([8], F16), 1e-5, t([4, 8], F16))
+    assert rc == accel_amd.E_INVALID and "x is f16 and gain is f16" in msg, msg
+    rc, msg = rms(t([], F32), t([1], F32), 1e-5, t([], F32))
+    assert rc == accel_amd.E_INVALID and "x has no shape" in msg, msg
+
+
+def test_matvec_f32_f16_refusals():   # tensor/matmul.go:45-121
+    rc, msg = call("accel_matvec_f32_f16", t([16], F32), t([16, 4], F32), t([4], F32))
+    assert rc == accel_amd.E_INVALID and "operands are f32 and f32" in msg, msg
+    rc, msg = call("accel_matvec_f32_f16", t([15], F32), t([16, 4], F16), t([4], F32))
+    assert rc == accel_amd.E_INVALID and "the inner dimensions must agree" in msg, msg
+    rc, msg = call("accel_matvec_f32_f16", t([2, 16], F32), t([16, 4], F16), t([2, 4], F32))
+    assert rc == accel_amd.E_UNSUPPORTED and "M = 1" in msg, msg
 
 
 def test_dispatch_refuses_an_unknown_record():
