@@ -38,8 +38,8 @@ E_OOM = -4
 E_UNSUPPORTED = -5
 E_HIP = -6
 
-F32, F16, BF16, U32 = 1, 2, 3, 4
-_NP_DTYPE = {F32: np.float32, F16: np.uint16, BF16: np.uint16, U32: np.uint32}
+F32, F16, BF16, U32, I8 = 1, 2, 3, 4, 5
+_NP_DTYPE = {F32: np.float32, F16: np.uint16, BF16: np.uint16, U32: np.uint32, I8: np.int8}
 
 
 class AccelError(RuntimeError):
@@ -125,6 +125,9 @@ SIGNATURES = {
     "accel_swiglu": ([_i, _vp, _P(Tensor), _P(Tensor), _P(Tensor)], _i),
     "accel_rmsnorm": ([_i, _vp, _P(Tensor), _P(Tensor), ctypes.c_float, _P(Tensor)], _i),
     "accel_matvec_f32_f16": ([_i, _vp, _P(Tensor), _P(Tensor), _P(Tensor)], _i),
+    "accel_quant_matmul": ([_i, _vp, _P(Tensor), _P(Tensor), _P(Tensor), _P(Tensor)], _i),
+    "accel_int8_quantize": ([_vp, ctypes.c_int64, _vp, _vp], _i),
+    "accel_int8_dequantize": ([_vp, _vp, ctypes.c_int64, _vp], _i),
     "accel_int4_quantize": ([_vp, ctypes.c_int64, _vp, _vp, _vp], _i),
     "accel_int4_dequantize": ([_vp, _vp, _vp, ctypes.c_int64, _vp], _i),
     "accel_int4_quantize_device": ([_i, _vp, _vp, ctypes.c_int64, _vp, _vp, _vp], _i),
@@ -177,6 +180,25 @@ def int4_quantize(w: np.ndarray):
     if n:
         _check(_lib.accel_int4_quantize(_ptr(w), n, _ptr(packed), _ptr(scales), _ptr(zeros)))
     return packed, scales, zeros
+
+
+def int8_quantize(w: np.ndarray):
+    """quant.Int8Quantize through the library's host packer: (quants i8,
+    scales f16 bits)."""
+    w = np.ascontiguousarray(w, np.float32).reshape(-1)
+    n = w.size
+    q = np.zeros(n, np.int8)
+    s = np.zeros((n + 31) // 32, np.uint16)
+    _check(_lib.accel_int8_quantize(_ptr(w), n, _ptr(q), _ptr(s)))
+    return q, s
+
+
+def int8_dequantize(quants, scales) -> np.ndarray:
+    q = np.ascontiguousarray(quants, np.int8).reshape(-1)
+    s = np.ascontiguousarray(scales, np.uint16)
+    out = np.empty(q.size, np.float32)
+    _check(_lib.accel_int8_dequantize(_ptr(q), _ptr(s), q.size, _ptr(out)))
+    return out
 
 
 def int4_dequantize(packed, scales, zeros, n: int) -> np.ndarray:
@@ -292,7 +314,7 @@ class Device:
         host = np.ascontiguousarray(host)
         if dtype is None:
             dtype = {np.dtype(np.float32): F32, np.dtype(np.uint32): U32,
-                     np.dtype(np.uint16): F16}[host.dtype]
+                     np.dtype(np.uint16): F16, np.dtype(np.int8): I8}[host.dtype]
         buf = self.alloc(host.shape if host.shape else (1,), dtype)
         buf.write(host)
         return buf
@@ -404,6 +426,13 @@ class Device:
         tx, tg, to = x.tensor(), gain.tensor(), out.tensor()
         _check(_lib.accel_rmsnorm(self.index, stream, ctypes.byref(tx), ctypes.byref(tg),
                                   ctypes.c_float(eps), ctypes.byref(to)))
+
+    def QuantMatMul(self, x: Buffer, quants: Buffer, scales: Buffer, out: Buffer,
+                    stream=None) -> None:
+        """tensor.QuantMatMul (tensor/quantized.go:72-163): int8 weights."""
+        tx, tq, ts, to = x.tensor(), quants.tensor(), scales.tensor(), out.tensor()
+        _check(_lib.accel_quant_matmul(self.index, stream, ctypes.byref(tx), ctypes.byref(tq),
+                                       ctypes.byref(ts), ctypes.byref(to)))
 
     def MatVecF32F16(self, x: Buffer, w: Buffer, out: Buffer, stream=None) -> None:
         """tensor.MatMul's M = 1 selection for f32 x and f16 w (MatVecF32F16,

@@ -99,6 +99,12 @@ hipError_t launch_swiglu(hipStream_t st, const float* a, const float* b, float* 
 hipError_t launch_rmsnorm(hipStream_t st, const float* x, const float* w, float* out, int rows,
                           int width, float eps);
 
+// int8 weights (one f16 scale per 32 flat weights): a [M,K] f32 or f16 bits
+// -> f32 [M,N].
+hipError_t launch_int8_product(Device* d, hipStream_t st, const void* a, bool f16_act,
+                               const int8_t* quants, const uint16_t* scales, float* out, int M,
+                               int K, int N, int* status);
+
 // Device quantizer.
 hipError_t launch_int4_quantize(hipStream_t st, const float* w, int64_t n,
                                 uint32_t* packed, uint16_t* scales, uint16_t* zeros);

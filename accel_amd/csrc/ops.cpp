@@ -34,6 +34,7 @@ const char* dtype_name(int32_t d) {
         case ACCEL_F16: return "f16";
         case ACCEL_BF16: return "bf16";
         case ACCEL_U32: return "u32";
+        case ACCEL_I8: return "i8";
         default: return "an unknown dtype";
     }
 }
@@ -627,6 +628,71 @@ ACCEL_API int accel_matvec_f32_f16(int dev, void* stream, const accel_tensor_t* 
     return finish(d, e, status, "MatVecF32F16 launch");
 }
 
+// ---- int8 weights ------------------------------------------------------------
+
+// tensor.QuantMatMul (tensor/quantized.go:72-163) with checkQuantized
+// (:32-52): the reference's validation order and wording.
+ACCEL_API int accel_quant_matmul(int dev, void* stream, const accel_tensor_t* x,
+                                 const accel_tensor_t* quants, const accel_tensor_t* scales,
+                                 accel_tensor_t* out) {
+    clear_error();
+    const char* op = "QuantMatMul";
+    char buf[320];
+    if (!valid_tensor(quants) || !quants->data || !valid_tensor(scales) || !scales->data)
+        return refuse(op, "the weight needs both a quant plane and a scale plane");
+    if (quants->dtype != ACCEL_I8) {
+        snprintf(buf, sizeof buf, "the weight quants are %s and must be i8",
+                 dtype_name(quants->dtype));
+        return refuse(op, buf);
+    }
+    if (scales->dtype != ACCEL_F16) {
+        snprintf(buf, sizeof buf, "the weight scales are %s and must be f16",
+                 dtype_name(scales->dtype));
+        return refuse(op, buf);
+    }
+    const int64_t nq = elements(quants);
+    const int64_t want = (nq + 31) / 32;
+    if (elements(scales) != want) {
+        snprintf(buf, sizeof buf, "the weight has %lld quants, which is %lld blocks of 32, and "
+                 "%lld scales", (long long)nq, (long long)want, (long long)elements(scales));
+        return refuse(op, buf);
+    }
+    if (!valid_tensor(x) || !x->data) return refuse(op, "the activations are missing");
+    if (x->dtype != ACCEL_F16 && x->dtype != ACCEL_F32) {
+        snprintf(buf, sizeof buf, "activations are %s; specs/010-kernel-corpus.md registers f16 "
+                 "and f32 activations against int8 weights", dtype_name(x->dtype));
+        return refuse(op, buf);
+    }
+    if (x->rank != 2 || quants->rank != 2) {
+        snprintf(buf, sizeof buf, "operands are %s and %s; v0 multiplies two matrices",
+                 shape_str(x).c_str(), shape_str(quants).c_str());
+        return refuse(op, buf);
+    }
+    if (x->shape[1] != quants->shape[0]) {
+        snprintf(buf, sizeof buf, "%s times %s: the contracted axes are %lld and %lld",
+                 shape_str(x).c_str(), shape_str(quants).c_str(), (long long)x->shape[1],
+                 (long long)quants->shape[0]);
+        return refuse(op, buf);
+    }
+    const int64_t M = x->shape[0], K = x->shape[1], N = quants->shape[1];
+    const int rc = check_out(op, out, ACCEL_F32, M, N, false);
+    if (rc != ACCEL_OK) return rc;
+    if (M > INT32_MAX || K > INT32_MAX || N > INT32_MAX || (uint64_t)K * N >= (1ull << 40))
+        return fail(ACCEL_E_UNSUPPORTED, "accel/tensor: QuantMatMul: dimensions past this "
+                    "library's indexing");
+    if (M == 0 || N == 0) return ACCEL_OK;
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    int status = begin_submission(d);
+    if (status != ACCEL_OK) return status;
+    hipError_t e = launch_int8_product(d, (hipStream_t)stream, x->data, x->dtype == ACCEL_F16,
+                                       static_cast<const int8_t*>(quants->data),
+                                       static_cast<const uint16_t*>(scales->data),
+                                       static_cast<float*>(out->data), (int)M, (int)K, (int)N,
+                                       &status);
+    return finish(d, e, status, "QuantMatMul launch");
+}
+
 // ---- backend seam: kernel records ------------------------------------------
 
 namespace {
@@ -638,7 +704,8 @@ struct Record {
 const Record kRecords[] = {
     {"QuantMatVecInt4", 5}, {"QuantMatMulInt4", 5}, {"GroupedMatVec", 4},
     {"GroupedMatMul", 4},   {"SegmentOffsets", 2},  {"SwiGLU", 3},
-    {"RMSNorm", 3},         {"MatVecF32F16", 3},
+    {"RMSNorm", 3},         {"MatVecF32F16", 3},    {"QuantMatVecF32", 4},
+    {"QuantMatVec", 4},     {"QuantMatMulTiledF32", 4}, {"QuantMatMulTiled", 4},
 };
 
 uint32_t u32_at(const void* p, size_t off) {
@@ -696,6 +763,25 @@ ACCEL_API int accel_hip_dispatch(int dev, void* stream, const char* kernel,
         accel_tensor_t g = {const_cast<void*>(bindings[1]), ACCEL_F32, 1, {width, 0, 0, 0}};
         accel_tensor_t o = {const_cast<void*>(bindings[2]), ACCEL_F32, 2, {rows, width, 0, 0}};
         return accel_rmsnorm(dev, stream, &x, &g, eps, &o);
+    }
+    if (name.rfind("QuantMat", 0) == 0) {
+        // GEMMDims {M@0, N@4, K@8}; the M = 1 records ignore M
+        const bool vec = name == "QuantMatVecF32" || name == "QuantMatVec";
+        const bool f16 = name == "QuantMatVec" || name == "QuantMatMulTiled";
+        const uint32_t M = vec ? 1u : u32_at(uniform, 0);
+        const uint32_t N = u32_at(uniform, 4), K = u32_at(uniform, 8);
+        const uint64_t W = (uint64_t)K * N;
+        if (lens[0] < (uint64_t)M * K || lens[1] < W || lens[2] < (W + 31) / 32 ||
+            lens[3] < (uint64_t)M * N)
+            return fail(ACCEL_E_INVALID, "accel_hip: %s bindings are shorter than its dims",
+                        kernel);
+        accel_tensor_t a = {const_cast<void*>(bindings[0]), f16 ? ACCEL_F16 : ACCEL_F32, 2,
+                            {M, K, 0, 0}};
+        accel_tensor_t q = {const_cast<void*>(bindings[1]), ACCEL_I8, 2, {K, N, 0, 0}};
+        accel_tensor_t sc = {const_cast<void*>(bindings[2]), ACCEL_F16, 1,
+                             {(int64_t)((W + 31) / 32), 0, 0, 0}};
+        accel_tensor_t o = {const_cast<void*>(bindings[3]), ACCEL_F32, 2, {M, N, 0, 0}};
+        return accel_quant_matmul(dev, stream, &a, &q, &sc, &o);
     }
     if (name == "MatVecF32F16") {
         // GEMMDims {M@0, N@4, K@8}

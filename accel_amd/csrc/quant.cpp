@@ -5,6 +5,7 @@
 // The packer is bit-exact with the reference: the range arithmetic is f32,
 // the scale and zero point are narrowed to f16 and read back before use, and
 // each code is round-half-even of an f64 quotient, clamped to [0, 15].
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 
@@ -116,9 +117,68 @@ void int4_dequantize_host(const uint32_t* packed, const uint16_t* scales,
     }
 }
 
+// quant.Int8Quantize (quant/quant.go:60-123): per block of 32 flat weights
+// the peak magnitude (f32), s = f16(peak / 127) read back as f32, each quant
+// the round-half-even of the f64 quotient w / s clamped to [-127, 127].  A
+// zero peak, or a scale that narrows to zero, leaves the block's quants 0.
+void int8_quantize_host(const float* w, int64_t n, int8_t* quants, uint16_t* scales) {
+    const int64_t blocks = (n + 31) / 32;
+    for (int64_t b = 0; b < blocks; b++) {
+        const int64_t lo = b * 32, hi = std::min(lo + 32, n);
+        float peak = 0.0f;
+        for (int64_t i = lo; i < hi; i++) {
+            const float a = std::fabs(w[i]);
+            if (a > peak) peak = a;   // a NaN never compares greater
+        }
+        for (int64_t i = lo; i < hi; i++) quants[i] = 0;
+        if (peak == 0.0f) {
+            scales[b] = narrow_f16(0.0f);
+            continue;
+        }
+        const float s = peak / 127.0f;
+        scales[b] = narrow_f16(s);
+        const float s16 = widen_f16(scales[b]);
+        if (s16 == 0.0f) continue;
+        for (int64_t i = lo; i < hi; i++) {
+            double q = std::nearbyint((double)w[i] / (double)s16);
+            if (q > 127.0) q = 127.0;
+            if (q < -127.0) q = -127.0;
+            // a NaN weight: Go's int8 conversion on amd64 gives 0
+            quants[i] = q == q ? (int8_t)q : 0;
+        }
+    }
+}
+
+// quant.Int8Dequantize (quant/quant.go:129-135).
+void int8_dequantize_host(const int8_t* quants, const uint16_t* scales, int64_t n, float* out) {
+    for (int64_t i = 0; i < n; i++) out[i] = (float)quants[i] * widen_f16(scales[i / 32]);
+}
+
 }  // namespace accel
 
 #define ACCEL_API extern "C" __attribute__((visibility("default")))
+
+ACCEL_API int accel_int8_quantize(const float* w, int64_t n, int8_t* quants,
+                                  uint16_t* scales) {
+    accel::clear_error();
+    if (n < 0) return accel::fail(ACCEL_E_INVALID, "accel_int8_quantize: negative count");
+    if (n == 0) return ACCEL_OK;
+    if (!w || !quants || !scales)
+        return accel::fail(ACCEL_E_INVALID, "accel_int8_quantize: NULL pointer");
+    accel::int8_quantize_host(w, n, quants, scales);
+    return ACCEL_OK;
+}
+
+ACCEL_API int accel_int8_dequantize(const int8_t* quants, const uint16_t* scales, int64_t n,
+                                    float* out) {
+    accel::clear_error();
+    if (n < 0) return accel::fail(ACCEL_E_INVALID, "accel_int8_dequantize: negative count");
+    if (n == 0) return ACCEL_OK;
+    if (!quants || !scales || !out)
+        return accel::fail(ACCEL_E_INVALID, "accel_int8_dequantize: NULL pointer");
+    accel::int8_dequantize_host(quants, scales, n, out);
+    return ACCEL_OK;
+}
 
 ACCEL_API int accel_int4_quantize(const float* w, int64_t n, uint32_t* packed,
                                   uint16_t* scales, uint16_t* zeros) {

@@ -289,6 +289,37 @@ def bench_matvec_f16(dev, stream, K=4096, N=4096, steps=200):
                 frac_of_hbm=round(nbytes / (ms * 1e-3) / 8e12, 4), K=K, N=N, copies=copies)
 
 
+def bench_int8(dev, stream, M=1, K=4096, N=4096, steps=200):
+    """QuantMatMul on int8 weights (f32 x [M,K], i8 [K,N] with one f16 scale
+    per 32 weights) over weight copies totalling more than 512 MB, so every
+    call reads HBM.  Algorithmic bytes: K N (quants) + K N / 16 (scales) +
+    4 M K + 4 M N."""
+    from accel_amd import F32
+    rng = np.random.Generator(np.random.PCG64(6))
+    q = rng.integers(-127, 128, K * N, dtype=np.int8).reshape(K, N)
+    s = np.full((K * N) // 32, 0x1c00, np.uint16)   # f16 2^-8
+    per = q.nbytes + s.nbytes
+    copies = max(1, -(-ROTATE_BYTES // per))
+    ws = [(dev.upload(q), dev.upload(s)) for _ in range(copies)]
+    a = dev.upload(rng.standard_normal((M, K)).astype(np.float32))
+    out = dev.alloc((M, N), F32)
+    for qb, sb in ws:
+        dev.QuantMatMul(a, qb, sb, out, stream)
+    dev.sync(stream)
+    t = Timed(dev, stream, lambda i: dev.QuantMatMul(a, *ws[i % copies], out, stream), steps)
+    ms = median_replay(t) / steps
+    t.close()
+    for qb, sb in ws:
+        qb.free()
+        sb.free()
+    a.free()
+    out.free()
+    nbytes = per + 4 * M * K + 4 * M * N
+    return dict(us=round(ms * 1e3, 3), gbs=round(nbytes / (ms * 1e-3) / 1e9, 1),
+                frac_of_hbm=round(nbytes / (ms * 1e-3) / 8e12, 4), M=M, K=K, N=N,
+                copies=copies)
+
+
 def bench_decode_step(dev, stream, batch, steps=100):
     """Config 5's layer as a whole decode step with its on-device neighbours:
     h = RMSNorm(x); q,k,v <- h; o <- q; h2 = RMSNorm(o); gate,up <- h2;
@@ -437,6 +468,9 @@ def main():
             extra["layer_chain_b1"] = bench_layer_chain(dev, stream, 1)
             extra["layer_chain_b8"] = bench_layer_chain(dev, stream, 8)
             extra["matvec_f32_f16"] = bench_matvec_f16(dev, stream)
+            extra["int8_gemv_4096"] = bench_int8(dev, stream, 1)
+            extra["int8_m8_4096"] = bench_int8(dev, stream, 8)
+            extra["int8_m1_4096x14336"] = bench_int8(dev, stream, 1, 4096, 14336)
             extra["decode_step_b1"] = bench_decode_step(dev, stream, 1)
             extra["decode_step_b8"] = bench_decode_step(dev, stream, 8)
         line["extra"] = extra

@@ -57,6 +57,7 @@ extern "C" {
 #define ACCEL_F16 2
 #define ACCEL_BF16 3
 #define ACCEL_U32 4
+#define ACCEL_I8 5
 
 /* Message for the last failing call on this thread ("" if none). */
 const char* accel_hip_last_error(void);
@@ -159,6 +160,10 @@ int accel_hip_supports_kernel(const char* kernel);
  *   SwiGLU           a f32, b f32, out f32;                   (no uniform)
  *   RMSNorm          x f32, w f32, out f32;                   RowDims
  *   MatVecF32F16     a f32, b f16, out f32;                   GEMMDims
+ *   QuantMatVecF32   a f32, bq i8, bs f16, out f32;           GEMMDims (M = 1)
+ *   QuantMatVec      a f16, bq i8, bs f16, out f32;           GEMMDims (M = 1)
+ *   QuantMatMulTiledF32  a f32, bq i8, bs f16, out f32;       GEMMDims
+ *   QuantMatMulTiled     a f16, bq i8, bs f16, out f32;       GEMMDims
  * (internal/kernels/accel_kernels.go:6799-6808,7052-7061; GEMMDims is
  * {M@0,N@4,K@8}, GroupedDims {Experts@0,K@4,N@8}, GroupedTiledDims
  * {Experts@0,Tokens@4,K@8,N@12}, SegmentDims {Rows@0}, :173-231; RowDims
@@ -263,6 +268,22 @@ int accel_rmsnorm(int dev, void* stream, const accel_tensor_t* x,
  * [1,N].  Other M are ACCEL_E_UNSUPPORTED. */
 int accel_matvec_f32_f16(int dev, void* stream, const accel_tensor_t* x,
                          const accel_tensor_t* w, accel_tensor_t* out);
+
+/* ---- int8 weights ------------------------------------------------------ */
+
+/* tensor.QuantMatMul (tensor/quantized.go:72-163): x f32 or f16 [M,K] times
+ * the int8 weight {quants i8 [K,N], scales f16 [ceil(K*N/32)]} -> out f32
+ * [M,N], w(k,n) = q[kN+n] * s[(kN+n)/32].  M = 1 is the reference's
+ * QuantMatVec(F32) selection, larger M its tiled kernel; both run here. */
+int accel_quant_matmul(int dev, void* stream, const accel_tensor_t* x,
+                       const accel_tensor_t* quants, const accel_tensor_t* scales,
+                       accel_tensor_t* out);
+
+/* quant.Int8Quantize / Int8Dequantize (quant/quant.go:60-135) on host memory:
+ * quants one per weight, scales ceil(n/32) f16. */
+int accel_int8_quantize(const float* w, int64_t n, int8_t* quants, uint16_t* scales);
+int accel_int8_dequantize(const int8_t* quants, const uint16_t* scales, int64_t n,
+                          float* out);
 
 /* quant.Int4Quantize (quant/int4.go:71-138) on host memory: packed holds
  * ceil(n/8) words, scales and zeros ceil(n/128) f16 each. */

@@ -86,6 +86,8 @@ def lib():
     L.orc_swiglu.argtypes = [_f32p, _f32p, _f32p, _i64]
     L.orc_rmsnorm.argtypes = [_u32, _u32, ctypes.c_float, _f32p, _f32p, _f32p]
     L.orc_matvec_f32_f16.argtypes = [_u32, _u32, _f32p, _u16p, _f32p]
+    L.orc_quant_matvec_i8.argtypes = [_u32, _u32, _f32p, _i8p, _u16p, _f32p]
+    L.orc_quant_matmul_i8.argtypes = [_u32, _u32, _u32, _f32p, _i8p, _u16p, _f32p]
     _lib = L
     return L
 
@@ -293,4 +295,29 @@ def matvec_f32_f16(a, b_bits, K: int, N: int) -> np.ndarray:
     assert a.size == K and b_bits.size == K * N
     out = np.empty(N, np.float32)
     lib().orc_matvec_f32_f16(K, N, a, b_bits, out)
+    return out
+
+
+# ---- int8 weights -------------------------------------------------------------
+
+def quant_matvec_i8(a, quants, scales, K: int, N: int) -> np.ndarray:
+    """QuantMatVecF32 (internal/kernels/matvec.go:204-235); pass f16
+    activations widened to f32 for QuantMatVec."""
+    a = _f32(a).reshape(-1)
+    q = np.ascontiguousarray(quants, np.int8).reshape(-1)
+    s = np.ascontiguousarray(scales, np.uint16)
+    assert a.size == K and q.size == K * N and s.size == (K * N + 31) // 32
+    out = np.empty(N, np.float32)
+    lib().orc_quant_matvec_i8(K, N, a, q, s, out)
+    return out
+
+
+def quant_matmul_i8(a, quants, scales, M: int, K: int, N: int) -> np.ndarray:
+    """QuantMatMulTiledF32 (internal/kernels/quant.go:195-238)."""
+    a = _f32(a).reshape(-1)
+    q = np.ascontiguousarray(quants, np.int8).reshape(-1)
+    s = np.ascontiguousarray(scales, np.uint16)
+    assert a.size == M * K and q.size == K * N and s.size == (K * N + 31) // 32
+    out = np.empty((M, N), np.float32)
+    lib().orc_quant_matmul_i8(M, K, N, a, q, s, out.reshape(-1))
     return out

@@ -43,6 +43,12 @@
  *                       a row of ones equals w / sqrt(1 + eps) exactly
  *   orc_matvec_f32_f16  f64 brute force within the f32 reduction bound, and
  *                       exact sums where every partial is an exact integer
+ *   orc_quant_matvec_i8 / orc_quant_matmul_i8  the reference's exact-input
+ *                       cases (prefill_test.go:934-978, differential_cases_
+ *                       test.go:950-1010: a = i%7-3, q = i%201-100, dyadic
+ *                       scales) against f64, f64 brute force within the
+ *                       reduction bound, independent numpy restatements of
+ *                       the phase and sequential orders, bit for bit
  */
 #include <math.h>
 #include <pthread.h>
@@ -289,7 +295,8 @@ void orc_int8_quantize(const float* w, int64_t n, int8_t* quants, uint16_t* scal
             double q = nearbyint((double)w[i] / (double)s16);
             if (q > 127) q = 127;
             if (q < -127) q = -127;
-            quants[i] = (int8_t)q;
+            /* int8(NaN) is implementation-defined in Go; amd64 gives 0 */
+            quants[i] = q == q ? (int8_t)q : 0;
         }
     }
 }
@@ -667,4 +674,56 @@ void orc_matvec_f32_f16(uint32_t K, uint32_t N, const float* a, const uint16_t* 
         for (uint32_t p = 0; p < 16; p++) sum = sum + ph[p];
         out[col] = sum;
     }
+}
+
+/* ------------------------------------------------------------------------ */
+/* int8 weights (quant/quant.go; internal/kernels/matvec.go, quant.go).      */
+/* ------------------------------------------------------------------------ */
+
+/* One int8 weight as the kernels read it: float32(q) * F32(s), one f16 scale
+ * per 32 flat weights (QuantBlock, internal/kernels/quant.go:16). */
+static inline float int8_weight(const int8_t* bq, const uint16_t* bs, uint64_t w) {
+    const float q = (float)bq[w];
+    const float s = orc_f16_to_f32(bs[w / 32]);
+    return q * s;
+}
+
+/* QuantMatVecF32 / QuantMatVec (internal/kernels/matvec.go:157-235): 32
+ * columns x 16 phases; phase p accumulates acc = acc + a[k] * (q * s) over
+ * k = p, p+16, ...; the column adds the 16 partials in phase order.  `a` is
+ * f32 (the f16 variant's activations are widened exactly by the caller). */
+void orc_quant_matvec_i8(uint32_t K, uint32_t N, const float* a, const int8_t* bq,
+                         const uint16_t* bs, float* out) {
+    for (uint32_t col = 0; col < N; col++) {
+        float ph[16];
+        for (uint32_t p = 0; p < 16; p++) {
+            float acc = 0.0f;
+            for (uint32_t k = p; k < K; k += 16) {
+                const float wv = int8_weight(bq, bs, (uint64_t)k * N + col);
+                const float prod = a[k] * wv;
+                acc = acc + prod;
+            }
+            ph[p] = acc;
+        }
+        float sum = 0.0f;
+        for (uint32_t p = 0; p < 16; p++) sum = sum + ph[p];
+        out[col] = sum;
+    }
+}
+
+/* QuantMatMulTiledF32 / QuantMatMulTiled (internal/kernels/quant.go:126-238),
+ * which accumulate exactly as QuantMatMul(F32) (:43-124): per output,
+ * acc = acc + a[m,k] * (q * s) in increasing k. */
+void orc_quant_matmul_i8(uint32_t M, uint32_t K, uint32_t N, const float* a, const int8_t* bq,
+                         const uint16_t* bs, float* out) {
+    for (uint32_t m = 0; m < M; m++)
+        for (uint32_t col = 0; col < N; col++) {
+            float acc = 0.0f;
+            for (uint32_t k = 0; k < K; k++) {
+                const float wv = int8_weight(bq, bs, (uint64_t)k * N + col);
+                const float prod = a[(size_t)m * K + k] * wv;
+                acc = acc + prod;
+            }
+            out[(size_t)m * N + col] = acc;
+        }
 }

@@ -81,7 +81,8 @@ def test_host_packer_at_a_baseline_shape():
 
 def test_kernel_support_names_the_records():
     for k in ["QuantMatVecInt4", "QuantMatMulInt4", "GroupedMatVec", "GroupedMatMul",
-              "SegmentOffsets", "SwiGLU", "RMSNorm", "MatVecF32F16"]:
+              "SegmentOffsets", "SwiGLU", "RMSNorm", "MatVecF32F16", "QuantMatVecF32",
+              "QuantMatVec", "QuantMatMulTiledF32", "QuantMatMulTiled"]:
         assert accel_amd.supports_kernel(k)
     assert not accel_amd.supports_kernel("MatMulTiledF32")
     assert not accel_amd.supports_kernel("")
@@ -231,6 +232,32 @@ def test_matvec_f32_f16_refusals():   # tensor/matmul.go:45-121
     assert rc == accel_amd.E_INVALID and "the inner dimensions must agree" in msg, msg
     rc, msg = call("accel_matvec_f32_f16", t([2, 16], F32), t([16, 4], F16), t([2, 4], F32))
     assert rc == accel_amd.E_UNSUPPORTED and "M = 1" in msg, msg
+
+
+def test_quant_matmul_refusals():   # tensor/quantized.go:32-110
+    I8 = accel_amd.I8
+    lib = accel_amd.lib()
+
+    def qmm(x, q, sc, o):
+        rc = lib.accel_quant_matmul(0, None, ctypes.byref(x), ctypes.byref(q), ctypes.byref(sc),
+                                    ctypes.byref(o))
+        return rc, accel_amd.last_error()
+
+    x, q, sc, o = t([2, 64], F32), t([64, 8], I8), t([16], F16), t([2, 8], F32)
+    rc, msg = qmm(x, t([64, 8], I8, data=0), sc, o)
+    assert rc == accel_amd.E_INVALID and "needs both a quant plane and a scale plane" in msg
+    rc, msg = qmm(x, t([64, 8], U32), sc, o)
+    assert rc == accel_amd.E_INVALID and "quants are u32 and must be i8" in msg, msg
+    rc, msg = qmm(x, q, t([15], F16), o)
+    assert rc == accel_amd.E_INVALID and "512 quants, which is 16 blocks of 32, and 15" in msg
+    rc, msg = qmm(t([2, 64], BF16), q, sc, o)
+    assert rc == accel_amd.E_INVALID and "registers f16 and f32 activations" in msg, msg
+    rc, msg = qmm(t([64], F32), q, sc, o)
+    assert rc == accel_amd.E_INVALID and "v0 multiplies two matrices" in msg, msg
+    rc, msg = qmm(t([2, 63], F32), t([63, 8], I8), t([17], F16), o)
+    assert rc == accel_amd.E_INVALID and "504 quants, which is 16 blocks of 32, and 17" in msg, msg
+    rc, msg = qmm(t([2, 32], F32), q, sc, o)
+    assert rc == accel_amd.E_INVALID and "the contracted axes are 32 and 64" in msg, msg
 
 
 def test_dispatch_refuses_an_unknown_record():
