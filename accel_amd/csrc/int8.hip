@@ -227,7 +227,10 @@ hipError_t launch_int8_decode(Device* d, hipStream_t st, const ACT* a, const int
     constexpr int kRowsPerBatch = kBatch * RP;
     const int tiles = N / TILE;
     const int batches = (K + kRowsPerBatch - 1) / kRowsPerBatch;
-    const int per_slice = (batches + kMaxSlices - 1) / kMaxSlices;
+    // slices <= K / (16 M): the f32 partials (slices x M x N x 4 bytes) stay
+    // within a quarter of the quant bytes they summarise
+    const int max_slices = std::max(1, std::min(kMaxSlices, K / (16 * M)));
+    const int per_slice = (batches + max_slices - 1) / max_slices;
     const int rows = per_slice * kRowsPerBatch;
     const int slices = (K + rows - 1) / rows;
     float* partial = nullptr;

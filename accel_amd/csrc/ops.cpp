@@ -764,7 +764,8 @@ ACCEL_API int accel_hip_dispatch(int dev, void* stream, const char* kernel,
         accel_tensor_t o = {const_cast<void*>(bindings[2]), ACCEL_F32, 2, {rows, width, 0, 0}};
         return accel_rmsnorm(dev, stream, &x, &g, eps, &o);
     }
-    if (name.rfind("QuantMat", 0) == 0) {
+    if (name == "QuantMatVecF32" || name == "QuantMatVec" || name == "QuantMatMulTiledF32" ||
+        name == "QuantMatMulTiled") {
         // GEMMDims {M@0, N@4, K@8}; the M = 1 records ignore M
         const bool vec = name == "QuantMatVecF32" || name == "QuantMatVec";
         const bool f16 = name == "QuantMatVec" || name == "QuantMatMulTiled";

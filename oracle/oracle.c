@@ -28,6 +28,9 @@
  *   orc_int4_error_bound  the reference's bound tests, including the case that
  *                       exceeds range/30 (quant/int4_test.go:102-158)
  *   orc_int8_quantize   the int4-vs-int8 KATs (quant/int4_test.go:166-219)
+ *                       and the int8 quantizer's tests (quant/quant_test.go:
+ *                       22-240: half-step bound, the clamp, scales that
+ *                       underflow f16, the dequantize KAT)
  *   orc_quant_matvec_int4 / _matmul_int4  closed-form differential cases
  *                       (differential_cases_test.go:1347-1425), nibble-order
  *                       KAT (=40, not 4), constant-group KAT, f64 brute force

@@ -5,6 +5,7 @@ layer refuses what the reference refuses (tensor/int4_test.go:121-273,
 any device is touched, so none of this needs a GPU.
 """
 import ctypes
+import struct
 import os
 import re
 
@@ -267,6 +268,44 @@ def test_dispatch_refuses_an_unknown_record():
                                 ctypes.cast(u, ctypes.c_void_p), 16, None)
     assert rc == accel_amd.E_UNSUPPORTED
     assert "no gfx950 implementation" in accel_amd.last_error()
+
+
+def _record_cases():
+    M, K, N, E, T, rows, width = 2, 256, 256, 4, 6, 3, 64
+    g = struct.pack("<IIII", M, N, K, 0)
+    v = struct.pack("<IIII", 0, N, K, 0)
+    W = K * N
+    return {
+        "QuantMatVecInt4": ([K, W // 8, W // 128, W // 128, N], v),
+        "QuantMatMulInt4": ([M * K, W // 8, W // 128, W // 128, M * N], g),
+        "GroupedMatVec": ([T * K, E * K * N, E + 1, T * N], struct.pack("<IIII", E, K, N, 0)),
+        "GroupedMatMul": ([T * K, E * K * N, E + 1, T * N], struct.pack("<IIII", E, T, K, N)),
+        "SegmentOffsets": ([rows, rows + 1], struct.pack("<IIII", rows, 0, 0, 0)),
+        "SwiGLU": ([77, 77, 77], b""),
+        "RMSNorm": ([rows * width, width, rows * width], struct.pack("<IIfI", rows, width, 1e-5, 0)),
+        "MatVecF32F16": ([K, W, N], struct.pack("<IIII", 1, N, K, 0)),
+        "QuantMatVecF32": ([K, W, W // 32, N], v),
+        "QuantMatVec": ([K, W, W // 32, N], v),
+        "QuantMatMulTiledF32": ([M * K, W, W // 32, M * N], g),
+        "QuantMatMulTiled": ([M * K, W, W // 32, M * N], g),
+    }
+
+
+@pytest.mark.parametrize("kernel", sorted(_record_cases()))
+def test_every_record_with_full_bindings_reaches_the_device(kernel):
+    # each record routes to its own operator: bindings long enough for its
+    # dims pass validation and stop only at the unopened device
+    lens, uniform = _record_cases()[kernel]
+    lib = accel_amd.lib()
+    host = (ctypes.c_uint8 * 256)()
+    n = len(lens)
+    b = (ctypes.c_void_p * n)(*[ctypes.addressof(host)] * n)
+    ln = (ctypes.c_uint64 * n)(*lens)
+    u = ctypes.create_string_buffer(uniform, max(len(uniform), 1))
+    rc = lib.accel_hip_dispatch(63, None, kernel.encode(), b, ln, n,
+                                ctypes.cast(u, ctypes.c_void_p) if uniform else None,
+                                len(uniform), None)
+    assert rc == accel_amd.E_NO_DEVICE, (kernel, rc, accel_amd.last_error())
 
 
 def test_a_closed_device_is_refused():
