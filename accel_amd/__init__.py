@@ -115,6 +115,7 @@ SIGNATURES = {
                             ctypes.c_int32, _vp, _sz, _P(ctypes.c_uint32)], _i),
     "accel_int4_matvec": ([_i, _vp, _P(Tensor), _P(Int4Desc), _P(Tensor)], _i),
     "accel_int4_matmul": ([_i, _vp, _P(Tensor), _P(Int4Desc), _P(Tensor)], _i),
+    "accel_int4_linear": ([_i, _vp, _P(Tensor), _P(Int4Desc), _P(Tensor), _P(Tensor)], _i),
     "accel_segment_offsets": ([_i, _vp, _P(Tensor), _P(Tensor)], _i),
     "accel_grouped_matvec": ([_i, _vp, _P(Tensor), _P(Tensor), _P(Tensor), _P(Tensor)], _i),
     "accel_grouped_matmul": ([_i, _vp, _P(Tensor), _P(Tensor), _P(Tensor), _P(Tensor)], _i),
@@ -383,6 +384,15 @@ class Device:
         ta, tw, to = a.tensor(), w.desc(), out.tensor()
         _check(_lib.accel_int4_matmul(self.index, stream, ctypes.byref(ta), ctypes.byref(tw),
                                       ctypes.byref(to)))
+
+    def Int4Linear(self, x: Buffer, w: Int4Weights, bias, out: Buffer, stream=None) -> None:
+        """The int4 analogue of tensor.Linear (tensor/matmul.go:184-225): the
+        product plus a per-column f32 bias (or None) in one kernel; out is f32
+        or bf16."""
+        tx, tw, to = x.tensor(), w.desc(), out.tensor()
+        tb = ctypes.byref(bias.tensor()) if bias is not None else None
+        _check(_lib.accel_int4_linear(self.index, stream, ctypes.byref(tx), ctypes.byref(tw),
+                                      tb, ctypes.byref(to)))
 
     def SegmentOffsets(self, counts: Buffer, offsets: Buffer, stream=None) -> None:
         tc, to = counts.tensor(), offsets.tensor()

@@ -98,8 +98,8 @@ template <int M, int TILE, int CPL>
 __global__ __launch_bounds__(kDecThreads) void int4_decode_f32_kernel(
     const float* __restrict__ a, const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
-    float* __restrict__ out, float* partial, uint32_t* tickets, int ticket_stride, int K, int N,
-    int rows_per_slice, int slices) {
+    void* __restrict__ out, float* partial, uint32_t* tickets, int ticket_stride, int K, int N,
+    int rows_per_slice, int slices, Epilogue ep) {
     constexpr int LPR = TILE / CPL;        // lanes per row
     constexpr int RP = kDecThreads / LPR;  // row phases
     constexpr int RPW = 64 / LPR;          // row phases per wave
@@ -203,14 +203,14 @@ __global__ __launch_bounds__(kDecThreads) void int4_decode_f32_kernel(
             if (split)
                 store_device(&partial[((size_t)slice * M + m) * N + col], sum);
             else
-                out[(size_t)m * N + col] = sum;
+                store_out(out, (size_t)m * N + col, col, sum, ep);
         }
         __syncthreads();
     }
     if (!split) return;
 
     split_k_finish(partial, tickets + (size_t)tile * ticket_stride, out, tile * TILE, TILE, M, N,
-                   slices, &last_flag);
+                   slices, &last_flag, ep);
 }
 
 // Slices: one batch (kBatch rows a lane) per workgroup, so every workgroup
@@ -219,7 +219,7 @@ __global__ __launch_bounds__(kDecThreads) void int4_decode_f32_kernel(
 // hand-off's reads.
 template <int M, int TILE, int CPL>
 hipError_t launch_decode(Device* d, hipStream_t st, const float* a, Int4Planes w,
-                         float* out, int K, int N, int* status) {
+                         void* out, int K, int N, int* status, Epilogue ep) {
     constexpr int LPR = TILE / CPL;
     constexpr int RP = kDecThreads / LPR;
     constexpr int kRowsPerBatch = kBatch * RP;
@@ -245,17 +245,17 @@ hipError_t launch_decode(Device* d, hipStream_t st, const float* a, Int4Planes w
     }
     hipLaunchKernelGGL((int4_decode_f32_kernel<M, TILE, CPL>), dim3(tiles * slices),
                        dim3(kDecThreads), 0, st, a, w.codes, w.scales, w.zeros, out, partial,
-                       tickets, stride, K, N, rows, slices);
+                       tickets, stride, K, N, rows, slices, ep);
     return hipGetLastError();
 }
 
 // Columns per lane by row count: the accumulators (M * CPL) stay near 64.
 template <int M>
 hipError_t launch_decode_m(Device* d, hipStream_t st, const float* a, Int4Planes w,
-                           float* out, int K, int N, int* status) {
+                           void* out, int K, int N, int* status, Epilogue ep) {
     constexpr int CPL = M <= 2 ? 32 : (M <= 4 ? 16 : 8);
-    if (N % 256 == 0) return launch_decode<M, 256, CPL>(d, st, a, w, out, K, N, status);
-    return launch_decode<M, 128, CPL>(d, st, a, w, out, K, N, status);
+    if (N % 256 == 0) return launch_decode<M, 256, CPL>(d, st, a, w, out, K, N, status, ep);
+    return launch_decode<M, 128, CPL>(d, st, a, w, out, K, N, status, ep);
 }
 
 // ---- MatVecF32F16: f32 activations against f16 weights --------------------
@@ -345,7 +345,7 @@ __global__ __launch_bounds__(kDecThreads) void matvec_f16_kernel(
     }
     if (!split) return;
     split_k_finish(partial, tickets + (size_t)tile * ticket_stride, out, tile * TILE, TILE, 1, N,
-                   slices, &last_flag);
+                   slices, &last_flag, Epilogue{});
 }
 
 // Any shape: one lane per column, the reference's 16-phase order.
@@ -400,7 +400,8 @@ __global__ void int4_generic_f32_kernel(const float* __restrict__ a,
                                         const uint32_t* __restrict__ codes,
                                         const uint16_t* __restrict__ scales,
                                         const uint16_t* __restrict__ zeros,
-                                        float* __restrict__ out, int M, int K, int N) {
+                                        void* __restrict__ out, int M, int K, int N,
+                                        Epilogue ep) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (int64_t)M * N) return;
     const int m = (int)(i / N), n = (int)(i % N);
@@ -413,23 +414,19 @@ __global__ void int4_generic_f32_kernel(const float* __restrict__ a,
         const float wv = s == 0.0f ? z : ((float)code - z) * s;
         acc = __builtin_fmaf(a[(size_t)m * K + k], wv, acc);
     }
-    out[i] = acc;
+    store_out(out, (size_t)i, n, acc, ep);
 }
 
 __device__ __forceinline__ float bf16_bits_to_float(uint16_t h) {
     return __uint_as_float((uint32_t)h << 16);
-}
-__device__ __forceinline__ uint16_t float_to_bf16_bits(float f) {
-    const uint32_t b = __float_as_uint(f);
-    if ((b & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
-    return (uint16_t)((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
 }
 
 __global__ void int4_generic_bf16_kernel(const uint16_t* __restrict__ a,
                                          const uint32_t* __restrict__ codes,
                                          const uint16_t* __restrict__ scales,
                                          const uint16_t* __restrict__ zeros,
-                                         uint16_t* __restrict__ out, int M, int K, int N) {
+                                         uint16_t* __restrict__ out, int M, int K, int N,
+                                         const float* __restrict__ bias) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (int64_t)M * N) return;
     const int m = (int)(i / N), n = (int)(i % N);
@@ -442,6 +439,7 @@ __global__ void int4_generic_bf16_kernel(const uint16_t* __restrict__ a,
         const float wv = s == 0.0f ? z : ((float)code - z) * s;
         acc = __builtin_fmaf(bf16_bits_to_float(a[(size_t)m * K + k]), wv, acc);
     }
+    if (bias) acc = acc + bias[n];
     out[i] = float_to_bf16_bits(acc);
 }
 
@@ -627,8 +625,8 @@ template <int G, int NW>
 __global__ __launch_bounds__(64 * NW) void int4_decode_mfma_kernel(
     const float* __restrict__ a, const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
-    float* __restrict__ out, float* partial, uint32_t* tickets, int ticket_stride, int M, int K,
-    int N, int rows_per_slice, int slices) {
+    void* __restrict__ out, float* partial, uint32_t* tickets, int ticket_stride, int M, int K,
+    int N, int rows_per_slice, int slices, Epilogue ep) {
     using T = MfTile<G, NW>;
     constexpr int D = T::kDepth;
     constexpr int V = T::kVmemPerStep;
@@ -881,6 +879,18 @@ __global__ __launch_bounds__(64 * NW) void int4_decode_mfma_kernel(
     }
 
     // ---- epilogue: the waves' sums meet in LDS --------------------------
+    constexpr int C4 = T::kCols / 4;
+    // the fused bias of this lane's output items, fetched now so that its
+    // latency overlaps the reduction
+    f32x4 ebias[T::kItems];
+#pragma unroll
+    for (int u = 0; u < T::kItems; u++) {
+        const int it = tid + T::kThreads * u;
+        const int c = n0 + 4 * (it % C4);
+        ebias[u] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        if (ep.bias && it / C4 < M)
+            ebias[u] = (f32x4){ep.bias[c], ep.bias[c + 1], ep.bias[c + 2], ep.bias[c + 3]};
+    }
     __syncthreads();
     // rows padded by four floats: the four kg rows a store instruction
     // writes land in different banks
@@ -904,7 +914,6 @@ __global__ __launch_bounds__(64 * NW) void int4_decode_mfma_kernel(
     }
     __syncthreads();
 
-    constexpr int C4 = T::kCols / 4;
     f32x4 val[T::kItems];
     int item_m[T::kItems], item_c[T::kItems];
 #pragma unroll
@@ -930,8 +939,12 @@ __global__ __launch_bounds__(64 * NW) void int4_decode_mfma_kernel(
 #pragma unroll
         for (int u = 0; u < T::kItems; u++) {
             if (item_m[u] >= M) continue;
-            float* o = out + (size_t)item_m[u] * N + n0 + item_c[u];
-            o[0] = val[u].x; o[1] = val[u].y; o[2] = val[u].z; o[3] = val[u].w;
+            const size_t o = (size_t)item_m[u] * N + n0 + item_c[u];
+            const f32x4 v = ep.bias ? val[u] + ebias[u] : val[u];
+            store_value(out, o, v.x, ep.bf16);
+            store_value(out, o + 1, v.y, ep.bf16);
+            store_value(out, o + 2, v.z, ep.bf16);
+            store_value(out, o + 3, v.w, ep.bf16);
         }
         return;
     }
@@ -1016,8 +1029,12 @@ __global__ __launch_bounds__(64 * NW) void int4_decode_mfma_kernel(
 #pragma unroll
     for (int u = 0; u < T::kItems; u++) {
         if (item_m[u] >= M) continue;
-        float* o = out + (size_t)item_m[u] * N + n0 + item_c[u];
-        o[0] = sum[u].x; o[1] = sum[u].y; o[2] = sum[u].z; o[3] = sum[u].w;
+        const size_t o = (size_t)item_m[u] * N + n0 + item_c[u];
+        const f32x4 v = ep.bias ? sum[u] + ebias[u] : sum[u];
+        store_value(out, o, v.x, ep.bf16);
+        store_value(out, o + 1, v.y, ep.bf16);
+        store_value(out, o + 2, v.z, ep.bf16);
+        store_value(out, o + 3, v.w, ep.bf16);
     }
     if (tid == 0) {
         __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1059,8 +1076,8 @@ MfPlan plan_decode_mfma(const Device* d, int M, int K, int N, bool planes_4b) {
 }
 
 template <int G, int NW>
-hipError_t launch_mfma(Device* d, hipStream_t st, const float* a, Int4Planes w, float* out,
-                       int M, int K, int N, const MfPlan& p, int* status) {
+hipError_t launch_mfma(Device* d, hipStream_t st, const float* a, Int4Planes w, void* out,
+                       int M, int K, int N, const MfPlan& p, int* status, Epilogue ep) {
     const int tiles = N / (128 * G);
     float* partial = nullptr;
     uint32_t* tickets = nullptr;
@@ -1079,17 +1096,17 @@ hipError_t launch_mfma(Device* d, hipStream_t st, const float* a, Int4Planes w, 
     }
     hipLaunchKernelGGL((int4_decode_mfma_kernel<G, NW>), dim3(tiles * p.slices), dim3(64 * NW),
                        0, st, a, w.codes, w.scales, w.zeros, out, partial, tickets, stride, M, K,
-                       N, p.rows, p.slices);
+                       N, p.rows, p.slices, ep);
     return hipGetLastError();
 }
 
 hipError_t launch_decode_mfma(Device* d, hipStream_t st, const float* a, Int4Planes w,
-                              float* out, int M, int K, int N, int* status) {
+                              void* out, int M, int K, int N, int* status, Epilogue ep) {
     const bool planes_4b = ((reinterpret_cast<uintptr_t>(w.scales) |
                              reinterpret_cast<uintptr_t>(w.zeros)) & 3) == 0;
     const MfPlan p = plan_decode_mfma(d, M, K, N, planes_4b);
-    if (p.groups == 2) return launch_mfma<2, 8>(d, st, a, w, out, M, K, N, p, status);
-    return launch_mfma<1, 8>(d, st, a, w, out, M, K, N, p, status);
+    if (p.groups == 2) return launch_mfma<2, 8>(d, st, a, w, out, M, K, N, p, status, ep);
+    return launch_mfma<1, 8>(d, st, a, w, out, M, K, N, p, status, ep);
 }
 
 }  // namespace
@@ -1114,49 +1131,49 @@ bool int4_decode_f32_supported(int M, int K, int N, const void* codes) {
 }
 
 hipError_t launch_int4_decode_f32(Device* d, hipStream_t st, const float* a, Int4Planes w,
-                                  float* out, int M, int K, int N, int* status) {
+                                  void* out, int M, int K, int N, int* status, Epilogue ep) {
     *status = ACCEL_OK;
     // Three or more rows: the matrix-core kernel, where its shape holds (its
     // per-lane code offsets within a 32-row step are 32-bit).
     if (M >= 3 && K % 32 == 0 && N < (1 << 27) && (reinterpret_cast<uintptr_t>(a) & 15) == 0)
-        return launch_decode_mfma(d, st, a, w, out, M, K, N, status);
+        return launch_decode_mfma(d, st, a, w, out, M, K, N, status, ep);
     switch (M) {
-        case 1: return launch_decode_m<1>(d, st, a, w, out, K, N, status);
-        case 2: return launch_decode_m<2>(d, st, a, w, out, K, N, status);
-        case 3: return launch_decode_m<3>(d, st, a, w, out, K, N, status);
-        case 4: return launch_decode_m<4>(d, st, a, w, out, K, N, status);
-        case 5: return launch_decode_m<5>(d, st, a, w, out, K, N, status);
-        case 6: return launch_decode_m<6>(d, st, a, w, out, K, N, status);
-        case 7: return launch_decode_m<7>(d, st, a, w, out, K, N, status);
-        case 8: return launch_decode_m<8>(d, st, a, w, out, K, N, status);
+        case 1: return launch_decode_m<1>(d, st, a, w, out, K, N, status, ep);
+        case 2: return launch_decode_m<2>(d, st, a, w, out, K, N, status, ep);
+        case 3: return launch_decode_m<3>(d, st, a, w, out, K, N, status, ep);
+        case 4: return launch_decode_m<4>(d, st, a, w, out, K, N, status, ep);
+        case 5: return launch_decode_m<5>(d, st, a, w, out, K, N, status, ep);
+        case 6: return launch_decode_m<6>(d, st, a, w, out, K, N, status, ep);
+        case 7: return launch_decode_m<7>(d, st, a, w, out, K, N, status, ep);
+        case 8: return launch_decode_m<8>(d, st, a, w, out, K, N, status, ep);
         default: break;
     }
     // 9..16 rows: eight, then the rest.
-    hipError_t e = launch_decode_m<8>(d, st, a, w, out, K, N, status);
+    hipError_t e = launch_decode_m<8>(d, st, a, w, out, K, N, status, ep);
     if (e != hipSuccess || *status != ACCEL_OK) return e;
-    return launch_int4_decode_f32(d, st, a + (size_t)8 * K, w, out + (size_t)8 * N, M - 8, K,
-                                  N, status);
+    char* rest = static_cast<char*>(out) + (size_t)8 * N * (ep.bf16 ? 2 : 4);
+    return launch_int4_decode_f32(d, st, a + (size_t)8 * K, w, rest, M - 8, K, N, status, ep);
 }
 
-hipError_t launch_int4_generic_f32(hipStream_t st, const float* a, Int4Planes w, float* out,
-                                   int M, int K, int N) {
+hipError_t launch_int4_generic_f32(hipStream_t st, const float* a, Int4Planes w, void* out,
+                                   int M, int K, int N, Epilogue ep) {
     const int64_t total = (int64_t)M * N;
     if (total == 0) return hipSuccess;
     const int threads = 256;
     const int64_t blocks = (total + threads - 1) / threads;
     hipLaunchKernelGGL(int4_generic_f32_kernel, dim3((unsigned)blocks), dim3(threads), 0, st,
-                       a, w.codes, w.scales, w.zeros, out, M, K, N);
+                       a, w.codes, w.scales, w.zeros, out, M, K, N, ep);
     return hipGetLastError();
 }
 
 hipError_t launch_int4_generic_bf16(hipStream_t st, const uint16_t* a, Int4Planes w,
-                                    uint16_t* out, int M, int K, int N) {
+                                    uint16_t* out, int M, int K, int N, const float* bias) {
     const int64_t total = (int64_t)M * N;
     if (total == 0) return hipSuccess;
     const int threads = 256;
     const int64_t blocks = (total + threads - 1) / threads;
     hipLaunchKernelGGL(int4_generic_bf16_kernel, dim3((unsigned)blocks), dim3(threads), 0,
-                       st, a, w.codes, w.scales, w.zeros, out, M, K, N);
+                       st, a, w.codes, w.scales, w.zeros, out, M, K, N, bias);
     return hipGetLastError();
 }
 

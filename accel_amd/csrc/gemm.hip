@@ -42,6 +42,7 @@
 #include <type_traits>
 
 #include "internal.hpp"
+#include "splitk.hpp"
 
 namespace accel {
 namespace {
@@ -59,12 +60,6 @@ constexpr int BM = 128, BN = 256, BK = 64;
 constexpr int kThreads = 256;        // four waves, one per SIMD
 constexpr int kARowBytes = BK * 2;   // one LDS activation row: 64 bf16
 constexpr int kBQuadWords = BN / 2;  // u32 words per row quad: one per code byte
-
-__device__ __forceinline__ float half_bits_to_float(uint16_t h) {
-    _Float16 v;
-    __builtin_memcpy(&v, &h, 2);
-    return (float)v;
-}
 
 // Byte offset of 16-byte chunk `c` of activation row `r` under the swizzle:
 // LDS has 64 banks (256 bytes), two rows wide; each row pair puts a chunk
@@ -146,12 +141,14 @@ struct SubstepRegs {
 // earlier) into the other buffer and issues the global loads of stage
 // kt+3; the stage's one barrier, before its second substep, makes stage
 // kt+1 visible before that substep reads the next stage's operands.
+template <bool BIAS>
 __device__ __forceinline__ void gemm_tile_bf16(GemmLds& lds, const uint16_t* __restrict__ a,
                                                const uint32_t* __restrict__ codes,
                                                const uint16_t* __restrict__ scales,
                                                const uint16_t* __restrict__ zeros,
                                                uint16_t* __restrict__ out, int m0, int m_end,
-                                               int n0, int K, int N) {
+                                               int n0, int K, int N,
+                                               const float* __restrict__ bias) {
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int ch = wave & 1;     // column half
@@ -332,6 +329,17 @@ __device__ __forceinline__ void gemm_tile_bf16(GemmLds& lds, const uint16_t* __r
     }
     if (kt < ktiles) stage(kt, I0{});
 
+    // The fused bias of this lane's four columns, fetched now so that its
+    // latency overlaps the hand-over below.
+    float bj[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (BIAS) {
+        const int bcol = n0 + 128 * ch + 4 * c32;
+        if (kp == 0 && bcol < N) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) bj[j] = bias[bcol + j];
+        }
+    }
+
     // The odd-parity waves hand their accumulators to the even ones through
     // LDS, one pair of n-tiles at a time.
     __syncthreads();
@@ -374,6 +382,7 @@ __device__ __forceinline__ void gemm_tile_bf16(GemmLds& lds, const uint16_t* __r
     // columns.
     const int col = n0 + 128 * ch + 4 * c32;
     if (col >= N) return;
+    // the fused bias: one f32 value per column, added before the one rounding
 #pragma unroll
     for (int t = 0; t < 4; t++) {
 #pragma unroll
@@ -381,20 +390,24 @@ __device__ __forceinline__ void gemm_tile_bf16(GemmLds& lds, const uint16_t* __r
             const int row = m0 + t * 32 + 8 * (r >> 2) + 4 * kg + (r & 3);
             if (row < m_end) {
                 bf16x4 v;
-                v[0] = (__bf16)acc[t][0][r];
-                v[1] = (__bf16)acc[t][1][r];
-                v[2] = (__bf16)acc[t][2][r];
-                v[3] = (__bf16)acc[t][3][r];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    if constexpr (BIAS)
+                        v[j] = (__bf16)(acc[t][j][r] + bj[j]);
+                    else
+                        v[j] = (__bf16)acc[t][j][r];
+                }
                 *reinterpret_cast<bf16x4*>(out + (size_t)row * N + col) = v;
             }
         }
     }
 }
 
+template <bool BIAS>
 __global__ __launch_bounds__(kThreads, 1) void int4_gemm_bf16_kernel(
     const uint16_t* __restrict__ a, const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
-    uint16_t* __restrict__ out, int M, int K, int N) {
+    uint16_t* __restrict__ out, int M, int K, int N, const float* __restrict__ bias) {
     __shared__ GemmLds lds;
     const int tiles_n = (N + BN - 1) / BN;
     const int grid = gridDim.x;
@@ -402,7 +415,7 @@ __global__ __launch_bounds__(kThreads, 1) void int4_gemm_bf16_kernel(
     if ((grid & 7) == 0) b = (b & 7) * (grid >> 3) + (b >> 3);
     const int m0 = (b / tiles_n) * BM;
     const int n0 = (b % tiles_n) * BN;
-    gemm_tile_bf16(lds, a, codes, scales, zeros, out, m0, M, n0, K, N);
+    gemm_tile_bf16<BIAS>(lds, a, codes, scales, zeros, out, m0, M, n0, K, N, bias);
 }
 
 // Ragged grouped form: blockIdx.x is the column tile, blockIdx.y the
@@ -434,8 +447,9 @@ __global__ __launch_bounds__(kThreads, 1) void int4_grouped_bf16_kernel(
     }
     if (!found) return;
     const size_t per_expert = (size_t)K * N;
-    gemm_tile_bf16(lds, x, codes + e * (per_expert >> 3), scales + e * (per_expert >> 7),
-                   zeros + e * (per_expert >> 7), out, m0, m_end, blockIdx.x * BN, K, N);
+    gemm_tile_bf16<false>(lds, x, codes + e * (per_expert >> 3), scales + e * (per_expert >> 7),
+                   zeros + e * (per_expert >> 7), out, m0, m_end, blockIdx.x * BN, K, N,
+                   nullptr);
 }
 
 // ---- f32 activations, fp32 VALU tiles -------------------------------------
@@ -445,7 +459,7 @@ constexpr int FM = 64, FN = 64, FK = 32;
 __global__ __launch_bounds__(256) void int4_gemm_f32_kernel(
     const float* __restrict__ a, const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
-    float* __restrict__ out, int M, int K, int N) {
+    void* __restrict__ out, int M, int K, int N, Epilogue ep) {
     __shared__ float As[FK][FM + 4];   // k-major so a lane's 4 rows are adjacent
     __shared__ float Bs[FK][FN + 4];
     const int tid = threadIdx.x;
@@ -507,7 +521,7 @@ __global__ __launch_bounds__(256) void int4_gemm_f32_kernel(
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int col = n0 + tx * 4 + j;
-            if (col < N) out[(size_t)row * N + col] = acc[i][j];
+            if (col < N) store_out(out, (size_t)row * N + col, col, acc[i][j], ep);
         }
     }
 }
@@ -520,10 +534,14 @@ bool int4_gemm_bf16_supported(int M, int K, int N) {
 }
 
 hipError_t launch_int4_gemm_bf16(Device*, hipStream_t st, const uint16_t* a, Int4Planes w,
-                                 uint16_t* out, int M, int K, int N) {
+                                 uint16_t* out, int M, int K, int N, const float* bias) {
     const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-    hipLaunchKernelGGL(int4_gemm_bf16_kernel, dim3(tiles), dim3(kThreads), 0, st, a, w.codes,
-                       w.scales, w.zeros, out, M, K, N);
+    if (bias)
+        hipLaunchKernelGGL(int4_gemm_bf16_kernel<true>, dim3(tiles), dim3(kThreads), 0, st, a,
+                           w.codes, w.scales, w.zeros, out, M, K, N, bias);
+    else
+        hipLaunchKernelGGL(int4_gemm_bf16_kernel<false>, dim3(tiles), dim3(kThreads), 0, st, a,
+                           w.codes, w.scales, w.zeros, out, M, K, N, bias);
     return hipGetLastError();
 }
 
@@ -541,10 +559,10 @@ hipError_t launch_int4_grouped_bf16(Device*, hipStream_t st, const uint16_t* x,
 }
 
 hipError_t launch_int4_gemm_f32(Device*, hipStream_t st, const float* a, Int4Planes w,
-                                float* out, int M, int K, int N) {
+                                void* out, int M, int K, int N, Epilogue ep) {
     dim3 grid((N + FN - 1) / FN, (M + FM - 1) / FM);
     hipLaunchKernelGGL(int4_gemm_f32_kernel, grid, dim3(256), 0, st, a, w.codes, w.scales,
-                       w.zeros, out, M, K, N);
+                       w.zeros, out, M, K, N, ep);
     return hipGetLastError();
 }
 

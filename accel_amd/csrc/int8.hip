@@ -151,7 +151,7 @@ __global__ __launch_bounds__(kDecThreads) void int8_decode_kernel(
     }
     if (!split) return;
     split_k_finish(partial, tickets + (size_t)tile * ticket_stride, out, tile * TILE, TILE, M, N,
-                   slices, &last_flag);
+                   slices, &last_flag, Epilogue{});
 }
 
 constexpr int QM = 64, QN = 64, QK = 32;

@@ -59,23 +59,37 @@ struct Int4Planes {
     const uint16_t* zeros;
 };
 
-// Decode product, M <= 16 rows of f32 activations -> f32 out.
+// What the last store of a product does: add bias[col] (f32, one value per
+// output column, broadcast over rows) when `bias` is set, then write f32 or,
+// with `bf16`, the sum rounded once to bf16 (nearest, ties to even).  The
+// default stores the plain f32 sum.
+struct Epilogue {
+    const float* bias = nullptr;
+    bool bf16 = false;
+};
+
+// Decode product, M <= 16 rows of f32 activations -> out (f32, or bf16 with
+// ep.bf16).
 hipError_t launch_int4_decode_f32(Device* d, hipStream_t st, const float* a,
-                                  Int4Planes w, float* out, int M, int K, int N,
-                                  int* status);
-// Any shape, f32: one thread per output element (small or ragged shapes).
+                                  Int4Planes w, void* out, int M, int K, int N,
+                                  int* status, Epilogue ep = Epilogue{});
+// Any shape, f32 activations: one thread per output element (small or ragged
+// shapes).
 hipError_t launch_int4_generic_f32(hipStream_t st, const float* a, Int4Planes w,
-                                   float* out, int M, int K, int N);
-// Any shape, bf16 activations and output.
+                                   void* out, int M, int K, int N, Epilogue ep = Epilogue{});
+// Any shape, bf16 activations and output (ep.bf16 is implied).
 hipError_t launch_int4_generic_bf16(hipStream_t st, const uint16_t* a, Int4Planes w,
-                                    uint16_t* out, int M, int K, int N);
+                                    uint16_t* out, int M, int K, int N,
+                                    const float* bias = nullptr);
 // Prefill product on MFMA: bf16 activations [M,K] -> bf16 out [M,N].
 hipError_t launch_int4_gemm_bf16(Device* d, hipStream_t st, const uint16_t* a,
-                                 Int4Planes w, uint16_t* out, int M, int K, int N);
+                                 Int4Planes w, uint16_t* out, int M, int K, int N,
+                                 const float* bias = nullptr);
 bool int4_gemm_bf16_supported(int M, int K, int N);
 // f32 activations with M > 16, fp32 arithmetic.
 hipError_t launch_int4_gemm_f32(Device* d, hipStream_t st, const float* a,
-                                Int4Planes w, float* out, int M, int K, int N);
+                                Int4Planes w, void* out, int M, int K, int N,
+                                Epilogue ep = Epilogue{});
 bool int4_decode_f32_supported(int M, int K, int N, const void* codes);
 
 // Grouped products over offsets [E+1] already on the device.

@@ -133,9 +133,12 @@ int check_out(const char* op, const accel_tensor_t* out, int32_t dtype, int64_t 
     return ACCEL_OK;
 }
 
-// The shared core of Int4MatVec and Int4MatMul once validated.
+// The shared core of Int4MatVec, Int4MatMul and Int4Linear once validated.
+// `ep` is the fused epilogue (bias, bf16 result); bf16 activations always
+// give a bf16 result.
 int run_int4_product(Device* d, hipStream_t st, const void* a, int32_t dtype,
-                     const accel_int4_t* w, void* out, int M, int K, int N) {
+                     const accel_int4_t* w, void* out, int M, int K, int N,
+                     Epilogue ep = Epilogue{}) {
     int status = begin_submission(d);
     if (status != ACCEL_OK) return status;
     if (M == 0 || N == 0) return ACCEL_OK;
@@ -144,20 +147,19 @@ int run_int4_product(Device* d, hipStream_t st, const void* a, int32_t dtype,
     hipError_t e = hipSuccess;
     if (dtype == ACCEL_F32) {
         const float* af = static_cast<const float*>(a);
-        float* of = static_cast<float*>(out);
         if (int4_decode_f32_supported(M, K, N, w->codes))
-            e = launch_int4_decode_f32(d, st, af, p, of, M, K, N, &status);
+            e = launch_int4_decode_f32(d, st, af, p, out, M, K, N, &status, ep);
         else if (M > 16 && aligned128)
-            e = launch_int4_gemm_f32(d, st, af, p, of, M, K, N);
+            e = launch_int4_gemm_f32(d, st, af, p, out, M, K, N, ep);
         else
-            e = launch_int4_generic_f32(st, af, p, of, M, K, N);
+            e = launch_int4_generic_f32(st, af, p, out, M, K, N, ep);
     } else {
         const uint16_t* ab = static_cast<const uint16_t*>(a);
         uint16_t* ob = static_cast<uint16_t*>(out);
         if (int4_gemm_bf16_supported(M, K, N) && (reinterpret_cast<uintptr_t>(a) & 15) == 0)
-            e = launch_int4_gemm_bf16(d, st, ab, p, ob, M, K, N);
+            e = launch_int4_gemm_bf16(d, st, ab, p, ob, M, K, N, ep.bias);
         else
-            e = launch_int4_generic_bf16(st, ab, p, ob, M, K, N);
+            e = launch_int4_generic_bf16(st, ab, p, ob, M, K, N, ep.bias);
     }
     return finish(d, e, status, "int4 product launch");
 }
@@ -242,6 +244,82 @@ ACCEL_API int accel_int4_matmul(int dev, void* stream, const accel_tensor_t* a,
     if (!d) return ACCEL_E_NO_DEVICE;
     return run_int4_product(d, (hipStream_t)stream, a->data, a->dtype, w, out->data, (int)m,
                             (int)k, (int)n);
+}
+
+// The int4 analogue of tensor.Linear (tensor/matmul.go:184-225): the
+// product and a per-column f32 bias in one kernel, the bias added while the
+// sums are still in registers, and, for f32 activations, an f32 or bf16
+// result.  The composed form (Int4MatMul, then an add and a cast) is the
+// reference the fused one is checked against.
+ACCEL_API int accel_int4_linear(int dev, void* stream, const accel_tensor_t* x,
+                                const accel_int4_t* w, const accel_tensor_t* bias,
+                                accel_tensor_t* out) {
+    clear_error();
+    const char* op = "Int4Linear";
+    std::string why = check_int4(w, "the weight matrix");
+    if (!why.empty()) return refuse(op, why);
+    if (!valid_tensor(x) || !x->data) return refuse(op, "the activations are missing");
+    char buf[512];
+    if (x->dtype != ACCEL_F32 && x->dtype != ACCEL_BF16) {
+        snprintf(buf, sizeof buf, "activations are %s and this kernel reads f32 (or bf16)",
+                 dtype_name(x->dtype));
+        return refuse(op, buf);
+    }
+    if (x->rank != 1 && x->rank != 2) {
+        snprintf(buf, sizeof buf,
+                 "activations are %s; the fused product takes one vector [K] or rows [M, K]",
+                 shape_str(x).c_str());
+        return refuse(op, buf);
+    }
+    const bool vector = x->rank == 1;
+    const int64_t m = vector ? 1 : x->shape[0], k = x->shape[x->rank - 1];
+    if (k == 0 || w->weights % k != 0) {
+        snprintf(buf, sizeof buf,
+                 "activations are %lld wide and the matrix holds %lld weights; the matrix is "
+                 "[K, N] with K the activation width, so the second is a multiple of the "
+                 "first",
+                 (long long)k, (long long)w->weights);
+        return refuse(op, buf);
+    }
+    const int64_t n = w->weights / k;
+    if (m > INT32_MAX || k > INT32_MAX || n > INT32_MAX)
+        return refuse(op, "the product is larger than this backend's 32-bit extents");
+    // the bias (matmul.go:211-218); no bias tensor at all is a product whose
+    // epilogue only narrows
+    if (bias) {
+        if (!valid_tensor(bias) || !bias->data)
+            return refuse(op, "the bias tensor has no data; a product without a bias passes "
+                              "no bias tensor");
+        if (bias->dtype != ACCEL_F32) {
+            snprintf(buf, sizeof buf, "the bias is %s and the epilogue adds in f32",
+                     dtype_name(bias->dtype));
+            return refuse(op, buf);
+        }
+        if (bias->rank != 1 || bias->shape[0] != n) {
+            snprintf(buf, sizeof buf,
+                     "the bias is %s and the output is %lld wide; a bias is one value per "
+                     "output column",
+                     shape_str(bias).c_str(), (long long)n);
+            return refuse(op, buf);
+        }
+    }
+    if (!valid_tensor(out) || !out->data) return refuse(op, "the output tensor is missing");
+    if (out->dtype != ACCEL_F32 && out->dtype != ACCEL_BF16) {
+        snprintf(buf, sizeof buf, "the output is %s and the epilogue writes f32 or bf16",
+                 dtype_name(out->dtype));
+        return refuse(op, buf);
+    }
+    if (x->dtype == ACCEL_BF16 && out->dtype != ACCEL_BF16)
+        return refuse(op, "the output is f32 and bf16 activations give a bf16 result");
+    int rc = check_out(op, out, out->dtype, m, n, vector);
+    if (rc != ACCEL_OK) return rc;
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    Epilogue ep;
+    ep.bias = bias ? static_cast<const float*>(bias->data) : nullptr;
+    ep.bf16 = out->dtype == ACCEL_BF16;
+    return run_int4_product(d, (hipStream_t)stream, x->data, x->dtype, w, out->data, (int)m,
+                            (int)k, (int)n, ep);
 }
 
 ACCEL_API int accel_segment_offsets(int dev, void* stream, const accel_tensor_t* counts,

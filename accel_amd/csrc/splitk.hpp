@@ -24,6 +24,28 @@ __device__ __forceinline__ float half_bits_to_float(uint16_t h) {
     return (float)v;
 }
 
+// f32 -> bf16 bits, round to nearest even; NaN -> the quiet NaN 0x7fc0.
+__device__ __forceinline__ uint16_t float_to_bf16_bits(float f) {
+    const uint32_t b = __float_as_uint(f);
+    if ((b & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
+    return (uint16_t)((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
+}
+
+// The store of a finished value: f32, or bf16 rounded once.
+__device__ __forceinline__ void store_value(void* out, size_t idx, float v, bool bf16) {
+    if (bf16)
+        static_cast<uint16_t*>(out)[idx] = float_to_bf16_bits(v);
+    else
+        static_cast<float*>(out)[idx] = v;
+}
+
+// The product's last store of element idx (column col) under `ep`.
+__device__ __forceinline__ void store_out(void* out, size_t idx, int col, float v,
+                                          const Epilogue& ep) {
+    if (ep.bias) v = v + ep.bias[col];
+    store_value(out, idx, v, ep.bf16);
+}
+
 __device__ __forceinline__ void store_device(float* p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -38,11 +60,11 @@ __device__ __forceinline__ float load_device(float* p) {
 // where the workspace allows, so the atomics of different tiles do not queue
 // behind each other), and the workgroup drawing the last ticket reads all
 // slices' sums with device-scope loads, adds them in slice order (so the
-// result does not depend on scheduling), writes `out` and returns the ticket
-// to zero for the next launch.
-__device__ __forceinline__ void split_k_finish(float* partial, uint32_t* ticket, float* out,
+// result does not depend on scheduling), writes `out` through the epilogue
+// and returns the ticket to zero for the next launch.
+__device__ __forceinline__ void split_k_finish(float* partial, uint32_t* ticket, void* out,
                                                int col0, int cols, int M, int N, int slices,
-                                               int* last_flag) {
+                                               int* last_flag, const Epilogue& ep) {
     const int tid = threadIdx.x;
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(0);
@@ -79,7 +101,7 @@ __device__ __forceinline__ void split_k_finish(float* partial, uint32_t* ticket,
             for (int u = 0; u < 16; u++)
                 if (sl + u < slices) sum += v[u];
         }
-        out[(size_t)m * N + col] = sum;
+        store_out(out, (size_t)m * N + col, col, sum, ep);
     }
     if (tid == 0)
         __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -43,7 +43,7 @@ METRIC = ("int4 linear: HBM GB/s (% peak) at M=1; TFLOP/s (% MFMA peak) at M=204
 ROTATE_BYTES = 544 << 20       # weight copies in rotation, > 2x the Infinity Cache
 TRAFFIC_FILE = os.path.join(HERE, "profiles", "traffic.json")
 GEMV_KERNEL = "int4_decode_f32_kernel<1, 256, 32>"
-GEMM_KERNEL = "int4_gemm_bf16_kernel"
+GEMM_KERNEL = "int4_gemm_bf16_kernel<false>"
 
 
 def parse():
@@ -320,6 +320,52 @@ def bench_int8(dev, stream, M=1, K=4096, N=4096, steps=200):
                 copies=copies)
 
 
+def bench_linear(dev, stream, name, out_bf16, steps=200):
+    """The fused int4 Linear on a config's shape (an f32 [N] bias added in the
+    product's epilogue; f32 or bf16 result) over rotated weights, beside the
+    plain product timed the same way on the same inputs."""
+    from accel_amd import BF16, F32, workloads
+    L = workloads.linear(**workloads.CONFIGS[name])
+    ws = rotated_weights(dev, stream, L)
+    rng = np.random.Generator(np.random.PCG64(9))
+    bias = dev.upload(rng.standard_normal(L.N).astype(np.float32))
+    shape = (L.M, L.N) if L.M > 1 else (L.N,)
+    if L.bf16:
+        a = dev.upload(workloads.bf16_bits(L.x), BF16)
+    else:
+        a = dev.upload(L.x if L.M > 1 else L.x[0])
+    out = dev.alloc(shape, BF16 if (out_bf16 or L.bf16) else F32)
+    plain = dev.alloc(shape, BF16 if L.bf16 else F32)
+
+    def prod(w, o):
+        if L.M == 1:
+            dev.Int4MatVec(a, w, o, stream)
+        else:
+            dev.Int4MatMul(a, w, o, stream)
+
+    for w in ws:
+        dev.Int4Linear(a, w, bias, out, stream)
+        prod(w, plain)
+    dev.sync(stream)
+    res = {}
+    # each timed twice, alternating, the second kept: the first graphs of a
+    # run also pay the clock ramp
+    for _ in range(2):
+        for key, fn in (("product_us", lambda i: prod(ws[i % len(ws)], plain)),
+                        ("fused_us",
+                         lambda i: dev.Int4Linear(a, ws[i % len(ws)], bias, out, stream))):
+            t = Timed(dev, stream, fn, steps)
+            res[key] = round(median_replay(t) / steps * 1e3, 3)
+            t.close()
+    for b in (bias, a, out, plain):
+        b.free()
+    for w in ws:
+        w.free()
+    res.update(M=L.M, K=L.K, N=L.N, x="bf16" if L.bf16 else "f32",
+               out="bf16" if (out_bf16 or L.bf16) else "f32")
+    return res
+
+
 def bench_decode_step(dev, stream, batch, steps=100):
     """Config 5's layer as a whole decode step with its on-device neighbours:
     h = RMSNorm(x); q,k,v <- h; o <- q; h2 = RMSNorm(o); gate,up <- h2;
@@ -471,6 +517,11 @@ def main():
             extra["int8_gemv_4096"] = bench_int8(dev, stream, 1)
             extra["int8_m8_4096"] = bench_int8(dev, stream, 8)
             extra["int8_m1_4096x14336"] = bench_int8(dev, stream, 1, 4096, 14336)
+            extra["linear_gemv_f32"] = bench_linear(dev, stream, "gemv_m1", False)
+            extra["linear_gemv_bf16out"] = bench_linear(dev, stream, "gemv_m1", True)
+            extra["linear_m16_f32"] = bench_linear(dev, stream, "decode_m16", False)
+            extra["linear_prefill_bf16"] = bench_linear(dev, stream, "prefill_m2048", True,
+                                                        steps=40)
             extra["decode_step_b1"] = bench_decode_step(dev, stream, 1)
             extra["decode_step_b8"] = bench_decode_step(dev, stream, 8)
         line["extra"] = extra

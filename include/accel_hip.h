@@ -213,6 +213,18 @@ int accel_int4_matvec(int dev, void* stream, const accel_tensor_t* a,
 int accel_int4_matmul(int dev, void* stream, const accel_tensor_t* a,
                       const accel_int4_t* w, accel_tensor_t* out);
 
+/* The int4 analogue of tensor.Linear (tensor/matmul.go:184-225, kernel
+ * LinearTiled, internal/kernels/matvec.go:232-293): x [K] or [M,K] times the
+ * int4 matrix, plus bias[n] (f32 [N], broadcast over rows) added once to each
+ * f32 sum in the product's own epilogue, in place of Int4MatMul followed by
+ * an Add (and a cast) node.  x is f32 or bf16; out is f32 or bf16 for f32 x
+ * (a bf16 out is the f32 sum plus bias rounded once), bf16 for bf16 x.  bias
+ * may be NULL: the epilogue then only narrows.  Refusals follow Linear's:
+ * a non-f32 bias, or one that is not [N]. */
+int accel_int4_linear(int dev, void* stream, const accel_tensor_t* x,
+                      const accel_int4_t* w, const accel_tensor_t* bias,
+                      accel_tensor_t* out);
+
 /* The SegmentOffsets node (tensor/segment.go:31-50;
  * internal/kernels/segment.go:40-50): offsets[r] = sum of counts[<r],
  * offsets[rows] = total.  counts u32 [rows], offsets u32 [rows+1]. */

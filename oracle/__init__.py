@@ -84,6 +84,7 @@ def lib():
     L.orc_int4_grouped_matmul.argtypes = [_u32, _u32, _u32, _u32, _f32p, _u32p, _u16p,
                                           _u16p, _u32p, _f32p, ctypes.c_int]
     L.orc_swiglu.argtypes = [_f32p, _f32p, _f32p, _i64]
+    L.orc_add_rows.argtypes = [_u32, _u32, _f32p, _f32p, _f32p]
     L.orc_rmsnorm.argtypes = [_u32, _u32, ctypes.c_float, _f32p, _f32p, _f32p]
     L.orc_matvec_f32_f16.argtypes = [_u32, _u32, _f32p, _u16p, _f32p]
     L.orc_quant_matvec_i8.argtypes = [_u32, _u32, _f32p, _i8p, _u16p, _f32p]
@@ -264,6 +265,36 @@ def matmul_f64(a, wdq, M: int, K: int, N: int) -> np.ndarray:
 
 
 # ---- decode-step neighbours -------------------------------------------------
+
+def add_rows(x, v) -> np.ndarray:
+    """ElemAdd (internal/kernels/elementwise.go:19-27) of x [rows, cols] and
+    v [cols] broadcast over rows."""
+    x = _f32(x)
+    v = _f32(v).reshape(-1)
+    cols = v.size
+    rows = x.size // max(cols, 1)
+    assert x.size == rows * cols
+    out = np.empty_like(x)
+    lib().orc_add_rows(rows, cols, x.reshape(-1), v, out.reshape(-1))
+    return out
+
+
+def int4_linear(x, packed, scales, zeros, bias, M: int, K: int, N: int,
+                bf16_out: bool = False) -> np.ndarray:
+    """The composed form of an int4 Linear, which the reference keeps as the
+    fused kernel's reference (tensor/matmul.go:184-188): the int4 product in
+    reference order (QuantMatVecInt4 at M = 1, QuantMatMulInt4 otherwise),
+    then ElemAdd of the bias broadcast over rows when there is one, then one
+    narrowing to bf16 bits (ToBFloat16) for a bf16 result.  Returns [M, N]
+    f32, or u16 bf16 bits."""
+    if M == 1:
+        y = quant_matvec_int4(x, packed, scales, zeros, K, N).reshape(1, N)
+    else:
+        y = quant_matmul_int4(x, packed, scales, zeros, M, K, N)
+    if bias is not None:
+        y = add_rows(y, bias)
+    return to_bf16(y).reshape(M, N) if bf16_out else y
+
 
 def swiglu(a, b) -> np.ndarray:
     """SwiGLU (internal/kernels/elementwise.go:85-91), f32 in reference order."""

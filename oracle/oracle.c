@@ -46,6 +46,12 @@
  *                       a row of ones equals w / sqrt(1 + eps) exactly
  *   orc_matvec_f32_f16  f64 brute force within the f32 reduction bound, and
  *                       exact sums where every partial is an exact integer
+ *   orc_add_rows        IEEE f32 addition against numpy's, signed zeros,
+ *                       infinities and NaN; a -0.0 vector returns x bit for
+ *                       bit (the int4 Linear's composed form is this after
+ *                       the int4 product; its tests check the composition's
+ *                       special cases: a -0.0 bias gives the product, zero
+ *                       weights give the bias on every row)
  *   orc_quant_matvec_i8 / orc_quant_matmul_i8  the reference's exact-input
  *                       cases (prefill_test.go:934-978, differential_cases_
  *                       test.go:950-1010: a = i%7-3, q = i%201-100, dyadic
@@ -625,6 +631,15 @@ void orc_swiglu(const float* a, const float* b, float* out, int64_t n) {
         const float q = x / d;
         out[i] = q * b[i];
     }
+}
+
+/* ElemAdd (internal/kernels/elementwise.go:19-27) of a [rows, cols] matrix
+ * and a [cols] vector under the tensor layer's broadcasting
+ * (tensor/elementwise.go:60-90): out[r][c] = x[r][c] + v[c], one f32 add. */
+void orc_add_rows(uint32_t rows, uint32_t cols, const float* x, const float* v, float* out) {
+    for (uint32_t r = 0; r < rows; r++)
+        for (uint32_t c = 0; c < cols; c++)
+            out[(size_t)r * cols + c] = x[(size_t)r * cols + c] + v[c];
 }
 
 /* RMSNorm (internal/kernels/norm.go:47-80), one 128-invocation workgroup a

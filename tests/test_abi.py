@@ -235,6 +235,46 @@ def test_matvec_f32_f16_refusals():   # tensor/matmul.go:45-121
     assert rc == accel_amd.E_UNSUPPORTED and "M = 1" in msg, msg
 
 
+def test_int4_linear_refusals():   # tensor/matmul.go:189-225's checks on an int4 product
+    lib = accel_amd.lib()
+
+    def lin(x, w, b, o):
+        rc = lib.accel_int4_linear(0, None, ctypes.byref(x), ctypes.byref(w),
+                                   ctypes.byref(b) if b is not None else None, ctypes.byref(o))
+        return rc, accel_amd.last_error()
+
+    K, N = 256, 128
+    w = w4(K * N)
+    x, b, o = t([2, K], F32), t([N], F32), t([2, N], F32)
+    rc, msg = lin(x, w, t([N], F16), o)
+    assert rc == accel_amd.E_INVALID and "the bias is f16 and the epilogue adds in f32" in msg
+    rc, msg = lin(x, w, t([N + 1], F32), o)
+    assert rc == accel_amd.E_INVALID and "the bias is [129] and the output is 128 wide" in msg
+    rc, msg = lin(x, w, t([1, N], F32), o)
+    assert rc == accel_amd.E_INVALID and "a bias is one value per output column" in msg
+    rc, msg = lin(x, w, t([N], F32, data=0), o)
+    assert rc == accel_amd.E_INVALID and "passes no bias tensor" in msg
+    rc, msg = lin(x, w, b, t([2, N], F16))
+    assert rc == accel_amd.E_INVALID and "the epilogue writes f32 or bf16" in msg
+    rc, msg = lin(t([2, K], BF16), w, b, o)
+    assert rc == accel_amd.E_INVALID and "bf16 activations give a bf16 result" in msg
+    rc, msg = lin(t([2, K], F16), w, b, o)
+    assert rc == accel_amd.E_INVALID and "activations are f16" in msg
+    rc, msg = lin(t([1, 2, K], F32), w, b, o)
+    assert rc == accel_amd.E_INVALID and "one vector [K] or rows [M, K]" in msg
+    rc, msg = lin(t([2, K + 1], F32), w, b, o)
+    assert rc == accel_amd.E_INVALID and "a multiple of the first" in msg
+    rc, msg = lin(t([K], F32), w, b, o)
+    assert rc == accel_amd.E_INVALID and "the output is [2 128] and the product is [128]" in msg
+    rc, msg = lin(x, w4(K * N, zeros=0), b, o)
+    assert rc == accel_amd.E_INVALID and "256 groups of 128, and 0 zeros" in msg, msg
+    # valid: f32 -> bf16 with a bias, vector form, and no bias at all
+    assert lin(x, w, b, t([2, N], BF16))[0] == accel_amd.E_NO_DEVICE
+    assert lin(t([K], F32), w, b, t([N], F32))[0] == accel_amd.E_NO_DEVICE
+    assert lin(x, w, None, t([2, N], BF16))[0] == accel_amd.E_NO_DEVICE
+    assert lin(t([2, K], BF16), w, b, t([2, N], BF16))[0] == accel_amd.E_NO_DEVICE
+
+
 def test_quant_matmul_refusals():   # tensor/quantized.go:32-110
     I8 = accel_amd.I8
     lib = accel_amd.lib()
