@@ -77,6 +77,17 @@ class Int4Desc(ctypes.Structure):
                 ("weights", ctypes.c_int64)]
 
 
+QFMT_AWQ, QFMT_GPTQ, QFMT_GPTQ_V2 = 1, 2, 3
+
+
+class ForeignDesc(ctypes.Structure):
+    """accel_foreign_int4_t: a published AWQ / GPTQ layer's planes."""
+    _fields_ = [("format", ctypes.c_int32), ("group_size", ctypes.c_int32),
+                ("K", ctypes.c_int64), ("N", ctypes.c_int64), ("groups", ctypes.c_int64),
+                ("qweight", ctypes.c_void_p), ("qzeros", ctypes.c_void_p),
+                ("scales", ctypes.c_void_p), ("g_idx", ctypes.c_void_p)]
+
+
 _vp = ctypes.c_void_p
 _i = ctypes.c_int
 _sz = ctypes.c_size_t
@@ -131,6 +142,8 @@ SIGNATURES = {
     "accel_int8_dequantize": ([_vp, _vp, ctypes.c_int64, _vp], _i),
     "accel_int4_quantize": ([_vp, ctypes.c_int64, _vp, _vp, _vp], _i),
     "accel_int4_dequantize": ([_vp, _vp, _vp, ctypes.c_int64, _vp], _i),
+    "accel_int4_repack_host": ([_P(ForeignDesc), _vp, _vp, _vp], _i),
+    "accel_int4_repack": ([_i, _vp, _P(ForeignDesc), _P(Int4Desc)], _i),
     "accel_int4_quantize_device": ([_i, _vp, _vp, ctypes.c_int64, _vp, _vp, _vp], _i),
 }
 
@@ -200,6 +213,57 @@ def int8_dequantize(quants, scales) -> np.ndarray:
     out = np.empty(q.size, np.float32)
     _check(_lib.accel_int8_dequantize(_ptr(q), _ptr(s), q.size, _ptr(out)))
     return out
+
+
+@dataclass
+class ForeignInt4:
+    """A published 4-bit layer (AWQ or GPTQ) as host arrays: qweight and qzeros
+    u32 words, scales f16 bits [groups, N], g_idx int32 [K] or None."""
+    format: int
+    group_size: int
+    K: int
+    N: int
+    qweight: np.ndarray
+    qzeros: np.ndarray
+    scales: np.ndarray
+    g_idx: np.ndarray = None
+
+    def __post_init__(self):
+        self.qweight = np.ascontiguousarray(self.qweight).view(np.uint32)
+        self.qzeros = np.ascontiguousarray(self.qzeros).view(np.uint32)
+        self.scales = np.ascontiguousarray(self.scales).view(np.uint16)
+        if self.g_idx is not None:
+            self.g_idx = np.ascontiguousarray(self.g_idx, np.int32)
+
+    @property
+    def groups(self) -> int:
+        return self.scales.size // self.N if self.N else 0
+
+    def desc(self, qweight=None, qzeros=None, scales=None, g_idx=None) -> ForeignDesc:
+        """The C descriptor over the host arrays, or over the given pointers."""
+        d = ForeignDesc()
+        d.format, d.group_size = self.format, self.group_size
+        d.K, d.N, d.groups = self.K, self.N, self.groups
+        d.qweight = qweight if qweight is not None else self.qweight.ctypes.data
+        d.qzeros = qzeros if qzeros is not None else self.qzeros.ctypes.data
+        d.scales = scales if scales is not None else self.scales.ctypes.data
+        if g_idx is not None:
+            d.g_idx = g_idx
+        elif self.g_idx is not None:
+            d.g_idx = self.g_idx.ctypes.data
+        return d
+
+
+def int4_repack_host(layer: ForeignInt4):
+    """A published layer in the reference int4 format, on the host: (codes,
+    scales, zeros) over its K*N weights."""
+    n = layer.K * layer.N
+    codes = np.zeros((n + 7) // 8, np.uint32)
+    scales = np.zeros((n + 127) // 128, np.uint16)
+    zeros = np.zeros((n + 127) // 128, np.uint16)
+    d = layer.desc()
+    _check(_lib.accel_int4_repack_host(ctypes.byref(d), _ptr(codes), _ptr(scales), _ptr(zeros)))
+    return codes, scales, zeros
 
 
 def int4_dequantize(packed, scales, zeros, n: int) -> np.ndarray:
@@ -393,6 +457,27 @@ class Device:
         tb = ctypes.byref(bias.tensor()) if bias is not None else None
         _check(_lib.accel_int4_linear(self.index, stream, ctypes.byref(tx), ctypes.byref(tw),
                                       tb, ctypes.byref(to)))
+
+    def Int4Repack(self, layer: ForeignInt4, stream=None) -> Int4Weights:
+        """A published AWQ / GPTQ layer, uploaded and repacked on the device into
+        the reference int4 format; the published planes are freed after."""
+        n = layer.K * layer.N
+        up = [self.upload(layer.qweight, U32), self.upload(layer.qzeros, U32),
+              self.upload(layer.scales, F16)]
+        gi = self.upload(layer.g_idx.view(np.uint32), U32) if layer.g_idx is not None else None
+        w = Int4Weights(self.alloc(((n + 7) // 8,), U32), self.alloc(((n + 127) // 128,), F16),
+                        self.alloc(((n + 127) // 128,), F16), n)
+        d = layer.desc(up[0].ptr, up[1].ptr, up[2].ptr, gi.ptr if gi is not None else None)
+        tw = w.desc()
+        try:
+            _check(_lib.accel_int4_repack(self.index, stream, ctypes.byref(d), ctypes.byref(tw)))
+        except Exception:
+            w.free()
+            raise
+        finally:
+            for b in up + ([gi] if gi is not None else []):
+                b.free()
+        return w
 
     def SegmentOffsets(self, counts: Buffer, offsets: Buffer, stream=None) -> None:
         tc, to = counts.tensor(), offsets.tensor()

@@ -67,6 +67,8 @@ float widen_f16(uint16_t h) {
 
 }  // namespace
 
+float widen_f16_host(uint16_t h) { return widen_f16(h); }
+
 void int4_quantize_host(const float* w, int64_t n, uint32_t* packed, uint16_t* scales,
                         uint16_t* zeros) {
     const int64_t kGroup = 128;

@@ -16,6 +16,8 @@
 namespace accel {
 namespace {
 
+typedef uint32_t u32x4_q __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ uint32_t rne_shift(uint32_t v, uint32_t n) {
     if (n == 0) return v;
     if (n > 31) return 0;
@@ -78,19 +80,13 @@ __device__ Cand wave_pick(Cand c, bool want_min) {
     return c;
 }
 
-__global__ __launch_bounds__(256) void int4_quantize_kernel(const float* __restrict__ w,
-                                                            int64_t n, uint32_t* packed,
-                                                            uint16_t* scales, uint16_t* zeros,
-                                                            int64_t groups) {
-    const int lane = threadIdx.x & 63;
-    const int64_t g = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (g >= groups) return;
+// Int4Quantize of group g (flat weights lo = 128 g .. lo + 127 of n) by one
+// wave: lane l holds weights lo + l (v0) and lo + 64 + l (v1).
+__device__ __forceinline__ void quantize_group(float v0, float v1, int lane, int64_t g,
+                                               int64_t n, uint32_t* packed, uint16_t* scales,
+                                               uint16_t* zeros) {
     const int64_t lo = g * 128;
-    const int64_t i0 = lo + lane, i1 = lo + 64 + lane;
-    const bool in0 = i0 < n, in1 = i1 < n;
-    const float v0 = in0 ? w[i0] : 0.0f;
-    const float v1 = in1 ? w[i1] : 0.0f;
-
+    const bool in0 = lo + lane < n, in1 = lo + 64 + lane < n;
     const float first = __shfl(v0, 0, 64);  // the scan's starting value
     float least, most;
     if (first != first) {
@@ -150,6 +146,206 @@ __global__ __launch_bounds__(256) void int4_quantize_kernel(const float* __restr
     }
 }
 
+__global__ __launch_bounds__(256) void int4_quantize_kernel(const float* __restrict__ w,
+                                                            int64_t n, uint32_t* packed,
+                                                            uint16_t* scales, uint16_t* zeros,
+                                                            int64_t groups) {
+    const int lane = threadIdx.x & 63;
+    const int64_t g = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (g >= groups) return;
+    const int64_t i0 = g * 128 + lane, i1 = i0 + 64;
+    const float v0 = i0 < n ? w[i0] : 0.0f;
+    const float v1 = i1 < n ? w[i1] : 0.0f;
+    quantize_group(v0, v1, lane, g, n, packed, scales, zeros);
+}
+
+// ---- repacking a published AWQ / GPTQ layer --------------------------------
+//
+// One wave per reference group of 128 flat weights: each lane dequantizes its
+// two weights from the published planes, w = (q - z) * s exactly in f32, and
+// the group is quantized as above.  The packings are the published ones (AWQ:
+// column 8j + c of a word in nibble {0,4,1,5,2,6,3,7}[c]; GPTQ: eight input
+// rows a word, zeros stored z - 1 in its first checkpoint format).  A g_idx
+// entry outside the layer's groups is read as group 0 and reported in *bad.
+
+// The published group of input row k (k < 2^31: 32-bit arithmetic).
+__device__ __forceinline__ int64_t foreign_group(const accel_foreign_int4_t& f, int64_t k,
+                                                 uint32_t* bad) {
+    if (f.g_idx) {
+        const int64_t g = f.g_idx[k];
+        if (g < 0 || g >= f.groups) {
+            *bad = 1u;
+            return 0;
+        }
+        return g;
+    }
+    return (int64_t)((uint32_t)k / (uint32_t)f.group_size);
+}
+
+// w(k, n) of the published layer, dequantized exactly; g is row k's group.
+__device__ __forceinline__ float foreign_weight(const accel_foreign_int4_t& f, int64_t k,
+                                                int64_t n, int64_t g) {
+    const int64_t wpr = f.N >> 3;
+    uint32_t q, z;
+    if (f.format == ACCEL_QFMT_AWQ) {
+        // column c of a word sits in nibble c / 2 (c even) or 4 + c / 2 (c odd)
+        const int c = (int)(n & 7);
+        const int sh = 4 * ((c >> 1) + ((c & 1) << 2));
+        q = (f.qweight[k * wpr + (n >> 3)] >> sh) & 15u;
+        z = (f.qzeros[g * wpr + (n >> 3)] >> sh) & 15u;
+    } else {
+        q = (f.qweight[(k >> 3) * f.N + n] >> (4 * (k & 7))) & 15u;
+        z = ((f.qzeros[g * wpr + (n >> 3)] >> (4 * (n & 7))) & 15u) +
+            (f.format == ACCEL_QFMT_GPTQ ? 1u : 0u);
+    }
+    return (float)((int)q - (int)z) * widen_f16(f.scales[g * f.N + n]);
+}
+
+__global__ __launch_bounds__(256) void int4_repack_kernel(accel_foreign_int4_t f, int64_t n,
+                                                          int64_t groups, int groups_per_row,
+                                                          uint32_t* packed,
+                                                          uint16_t* scales, uint16_t* zeros,
+                                                          uint32_t* bad) {
+    const int lane = threadIdx.x & 63;
+    const int64_t g = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (g >= groups) return;
+    const int64_t i0 = g * 128 + lane, i1 = i0 + 64;
+    float v0 = 0.0f, v1 = 0.0f;
+    if (groups_per_row) {
+        // N % 128 == 0: the group lies in one row, found with one 32-bit
+        // division a wave (the row count and groups a row are below 2^31)
+        const uint32_t gi = (uint32_t)g;
+        const uint32_t k = gi / (uint32_t)groups_per_row;
+        const int64_t n0 = (int64_t)(gi - k * (uint32_t)groups_per_row) * 128 + lane;
+        const int64_t pg = foreign_group(f, k, bad);
+        v0 = foreign_weight(f, k, n0, pg);
+        v1 = foreign_weight(f, k, n0 + 64, pg);
+    } else {
+        if (i0 < n) {
+            const int64_t k = i0 / f.N;
+            v0 = foreign_weight(f, k, i0 - k * f.N, foreign_group(f, k, bad));
+        }
+        if (i1 < n) {
+            const int64_t k = i1 / f.N;
+            v1 = foreign_weight(f, k, i1 - k * f.N, foreign_group(f, k, bad));
+        }
+    }
+    quantize_group(v0, v1, lane, g, n, packed, scales, zeros);
+}
+
+// Rows that hold whole groups (N % 128 == 0): one lane per reference group.
+// The lane walks its 128 weights in order twice, recomputing each from the
+// published planes -- first the reference's sequential scan for the range,
+// then the codes -- so the group's range needs no cross-lane reduction and
+// its scale and zero are worked out once per lane, 64 groups to a wave.
+// Eight weights at a time: one code word (AWQ; eight for GPTQ, which packs
+// rows), one zero word and sixteen bytes of scales.
+template <int FMT>
+__device__ __forceinline__ void foreign_eight(const accel_foreign_int4_t& f, uint32_t k,
+                                              int64_t n, int64_t pg, float* w) {
+    const int64_t wpr = f.N >> 3;
+    const uint32_t zw = f.qzeros[pg * wpr + (n >> 3)];
+    typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+    const u16x8 sc = *reinterpret_cast<const u16x8*>(f.scales + pg * f.N + n);
+    if constexpr (FMT == ACCEL_QFMT_AWQ) {
+        const uint32_t qw = f.qweight[(int64_t)k * wpr + (n >> 3)];
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const int sh = 4 * ((c >> 1) + ((c & 1) << 2));
+            const int q = (int)((qw >> sh) & 15u), z = (int)((zw >> sh) & 15u);
+            w[c] = (float)(q - z) * widen_f16(sc[c]);
+        }
+    } else {
+        const uint32_t* row = f.qweight + (int64_t)(k >> 3) * f.N + n;
+        const int rs = 4 * (int)(k & 7);
+        const int plus = FMT == ACCEL_QFMT_GPTQ ? 1 : 0;
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const int q = (int)((row[c] >> rs) & 15u);
+            const int z = (int)((zw >> (4 * c)) & 15u) + plus;
+            w[c] = (float)(q - z) * widen_f16(sc[c]);
+        }
+    }
+}
+
+// Lanes walk the groups down a column of groups (lane i takes row k0 + i of
+// the same 128 columns): rows of one published group share its scales and
+// zeros, which are most of the bytes read, and in GPTQ eight consecutive rows
+// share each code word.
+template <int FMT>
+__global__ __launch_bounds__(256) void int4_repack_rows_kernel(accel_foreign_int4_t f,
+                                                               int64_t groups, int gpr,
+                                                               uint32_t* packed,
+                                                               uint16_t* scales,
+                                                               uint16_t* zeros, uint32_t* bad) {
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= groups) return;
+    const uint32_t ti = (uint32_t)t;
+    const uint32_t cb = ti / (uint32_t)f.K;
+    const uint32_t k = ti - cb * (uint32_t)f.K;
+    const int64_t g = (int64_t)k * gpr + cb;
+    const int64_t n0 = (int64_t)cb * 128;
+    const int64_t pg = foreign_group(f, k, bad);
+
+    // the reference's scan: from the first weight, replacing on a strict
+    // comparison (a NaN first weight sticks, later NaNs are skipped)
+    float w[8];
+    foreign_eight<FMT>(f, k, n0, pg, w);
+    float least = w[0], most = w[0];
+#pragma unroll 1
+    for (int j = 0; j < 16; j++) {
+        if (j) foreign_eight<FMT>(f, k, n0 + 8 * j, pg, w);
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            if (w[c] < least) least = w[c];
+            if (w[c] > most) most = w[c];
+        }
+    }
+    uint16_t s_bits, z_bits;
+    float s16 = 0.0f, z16 = 0.0f;
+    bool coded = false;
+    if (most == least) {
+        s_bits = narrow_f16(0.0f);
+        z_bits = narrow_f16(least);
+    } else {
+        s_bits = narrow_f16(__fdiv_rn(most - least, 15.0f));
+        s16 = widen_f16(s_bits);
+        if (s16 == 0.0f) {
+            z_bits = narrow_f16(least);
+        } else {
+            z_bits = narrow_f16(__fdiv_rn(-least, s16));
+            z16 = widen_f16(z_bits);
+            coded = true;
+        }
+    }
+    scales[g] = s_bits;
+    zeros[g] = z_bits;
+    uint32_t* out = packed + g * 16;
+    if (!coded) {
+#pragma unroll
+        for (int j = 0; j < 16; j += 4) *reinterpret_cast<u32x4_q*>(out + j) = (u32x4_q){0, 0, 0, 0};
+        return;
+    }
+    const double sd = (double)s16, zd = (double)z16;
+#pragma unroll 1
+    for (int j = 0; j < 16; j += 4) {
+        u32x4_q words;
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) {
+            foreign_eight<FMT>(f, k, n0 + 8 * (j + jj), pg, w);
+            uint32_t word = 0;
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                const double q = rint(__ddiv_rn((double)w[c], sd) + zd);
+                const uint32_t code = q != q ? 0u : (q > 15.0 ? 15u : (q < 0.0 ? 0u : (uint32_t)q));
+                word |= code << (4 * c);
+            }
+            words[jj] = word;
+        }
+        *reinterpret_cast<u32x4_q*>(out + j) = words;
+    }
+}
+
 }  // namespace
 
 hipError_t launch_int4_quantize(hipStream_t st, const float* w, int64_t n, uint32_t* packed,
@@ -158,6 +354,36 @@ hipError_t launch_int4_quantize(hipStream_t st, const float* w, int64_t n, uint3
     const int64_t blocks = (groups + 3) / 4;
     hipLaunchKernelGGL(int4_quantize_kernel, dim3((unsigned)blocks), dim3(256), 0, st, w, n,
                        packed, scales, zeros, groups);
+    return hipGetLastError();
+}
+
+hipError_t launch_int4_repack(hipStream_t st, const accel_foreign_int4_t& f, uint32_t* codes,
+                              uint16_t* scales, uint16_t* zeros, uint32_t* bad) {
+    const int64_t n = f.K * f.N;
+    const int64_t groups = (n + 127) / 128;
+    const int64_t blocks = (groups + 3) / 4;
+    if (blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
+    // one 32-bit division a wave finds a group's row where rows hold whole
+    // groups and the group index fits 32 bits
+    const int gpr = (f.N % 128 == 0 && groups < (int64_t(1) << 32)) ? (int)(f.N / 128) : 0;
+    const bool aligned = ((reinterpret_cast<uintptr_t>(f.scales) |
+                           reinterpret_cast<uintptr_t>(codes)) & 15) == 0;
+    if (gpr && aligned) {
+        const int64_t lane_blocks = (groups + 255) / 256;
+        const dim3 grid((unsigned)lane_blocks), block(256);
+        if (f.format == ACCEL_QFMT_AWQ)
+            hipLaunchKernelGGL(int4_repack_rows_kernel<ACCEL_QFMT_AWQ>, grid, block, 0, st, f,
+                               groups, gpr, codes, scales, zeros, bad);
+        else if (f.format == ACCEL_QFMT_GPTQ)
+            hipLaunchKernelGGL(int4_repack_rows_kernel<ACCEL_QFMT_GPTQ>, grid, block, 0, st, f,
+                               groups, gpr, codes, scales, zeros, bad);
+        else
+            hipLaunchKernelGGL(int4_repack_rows_kernel<ACCEL_QFMT_GPTQ_V2>, grid, block, 0, st,
+                               f, groups, gpr, codes, scales, zeros, bad);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL(int4_repack_kernel, dim3((unsigned)blocks), dim3(256), 0, st, f, n,
+                       groups, gpr, codes, scales, zeros, bad);
     return hipGetLastError();
 }
 

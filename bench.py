@@ -366,6 +366,63 @@ def bench_linear(dev, stream, name, out_bf16, steps=200):
     return res
 
 
+def bench_repack(dev, stream, fmt=1, K=4096, N=14336, G=128, calls=20):
+    """Repacking one published 4-bit layer (AWQ by default) into the reference
+    int4 format on the device, planes already resident: per call, the HIP-event
+    time of the whole call on its stream (flag clear, repack kernel, flag
+    read-back) and the wall time including the call's own synchronization;
+    the host repack of the same layer beside it."""
+    import ctypes
+    import time
+    import accel_amd
+    from accel_amd import F16, U32
+    rng = np.random.Generator(np.random.PCG64(12))
+    groups = K // G
+    qweight = rng.integers(0, 2**32, (K, N // 8) if fmt == 1 else (K // 8, N), dtype=np.uint32)
+    qzeros = rng.integers(0, 2**32, (groups, N // 8), dtype=np.uint32)
+    scales = (rng.random((groups, N), dtype=np.float32) * 0.02 + 1e-3).astype(np.float16)
+    lay = accel_amd.ForeignInt4(fmt, G, K, N, qweight, qzeros, scales.view(np.uint16))
+    up = [dev.upload(lay.qweight, U32), dev.upload(lay.qzeros, U32), dev.upload(lay.scales, F16)]
+    n = K * N
+    w = accel_amd.Int4Weights(dev.alloc(((n + 7) // 8,), U32), dev.alloc(((n + 127) // 128,), F16),
+                              dev.alloc(((n + 127) // 128,), F16), n)
+    d = lay.desc(up[0].ptr, up[1].ptr, up[2].ptr)
+    tw = w.desc()
+    lib = accel_amd.lib()
+
+    def call():
+        accel_amd._check(lib.accel_int4_repack(dev.index, stream, ctypes.byref(d),
+                                               ctypes.byref(tw)))
+
+    for _ in range(3):
+        call()
+    e0, e1 = dev.event(), dev.event()
+    gpu_ms = []
+    t0 = time.perf_counter()
+    for _ in range(calls):
+        dev.record(e0, stream)
+        call()
+        dev.record(e1, stream)
+        dev.wait(e1)
+        gpu_ms.append(dev.elapsed_ms(e0, e1))
+    wall_us = (time.perf_counter() - t0) / calls * 1e6
+    dev.destroy_event(e0)
+    dev.destroy_event(e1)
+    t0 = time.perf_counter()
+    accel_amd.int4_repack_host(lay)
+    host_ms = (time.perf_counter() - t0) * 1e3
+    for b in up:
+        b.free()
+    w.free()
+    read = qweight.nbytes + qzeros.nbytes + scales.nbytes
+    written = n // 2 + (n // 128) * 4
+    us = float(np.median(gpu_ms)) * 1e3
+    return dict(format={1: "awq", 2: "gptq", 3: "gptq_v2"}[fmt], K=K, N=N, group=G,
+                us=round(us, 2), wall_us=round(wall_us, 2),
+                gbs=round((read + written) / (us * 1e-6) / 1e9, 1), host_ms=round(host_ms, 1),
+                bytes=read + written)
+
+
 def bench_decode_step(dev, stream, batch, steps=100):
     """Config 5's layer as a whole decode step with its on-device neighbours:
     h = RMSNorm(x); q,k,v <- h; o <- q; h2 = RMSNorm(o); gate,up <- h2;
@@ -522,6 +579,8 @@ def main():
             extra["linear_m16_f32"] = bench_linear(dev, stream, "decode_m16", False)
             extra["linear_prefill_bf16"] = bench_linear(dev, stream, "prefill_m2048", True,
                                                         steps=40)
+            extra["repack_awq_4096x14336"] = bench_repack(dev, stream, 1)
+            extra["repack_gptq_4096x14336"] = bench_repack(dev, stream, 2)
             extra["decode_step_b1"] = bench_decode_step(dev, stream, 1)
             extra["decode_step_b8"] = bench_decode_step(dev, stream, 8)
         line["extra"] = extra

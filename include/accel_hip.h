@@ -200,6 +200,59 @@ typedef struct accel_int4 {
     int64_t weights;
 } accel_int4_t;
 
+/* A published 4-bit checkpoint layer (specs/048-int4.md:126-131,167 name
+ * reading these files as the unbuilt next step of the int4 format).  Both
+ * families keep one f16 scale and one 4-bit zero per output column per group
+ * of `group_size` input rows, w(k,n) = (q(k,n) - z(g,n)) * s(g,n), where the
+ * reference format keeps one scale and zero per 128 consecutive weights of the
+ * flat [K,N] array; a repack therefore re-quantizes.
+ *   ACCEL_QFMT_AWQ      AutoAWQ "gemm" packing: qweight u32 [K, N/8], eight
+ *                       columns a word with column 8j+c in nibble
+ *                       {0,4,1,5,2,6,3,7}[c]; qzeros u32 [groups, N/8] packed
+ *                       the same way; scales f16 [groups, N]; g = k / group.
+ *   ACCEL_QFMT_GPTQ     GPTQ ("gptq" checkpoint format): qweight u32 [K/8, N],
+ *                       row 8i+j in nibble j of word (i, n); qzeros u32
+ *                       [groups, N/8], column 8j+c in nibble c, holding z - 1;
+ *                       scales f16 [groups, N]; g = g_idx[k] when g_idx is
+ *                       given (act-order), else k / group.
+ *   ACCEL_QFMT_GPTQ_V2  as GPTQ, with qzeros holding z itself ("gptq_v2"). */
+#define ACCEL_QFMT_AWQ 1
+#define ACCEL_QFMT_GPTQ 2
+#define ACCEL_QFMT_GPTQ_V2 3
+typedef struct {
+    int32_t format;
+    int32_t group_size;      /* input rows a group spans; K for a single group */
+    int64_t K, N;            /* in_features, out_features */
+    int64_t groups;          /* rows of scales and qzeros */
+    const uint32_t* qweight;
+    const uint32_t* qzeros;
+    const uint16_t* scales;
+    const int32_t* g_idx;    /* GPTQ only: [K] group of each input row, or NULL */
+} accel_foreign_int4_t;
+
+/* Repacks a published 4-bit layer into the reference int4 format
+ * (quant/int4.go:71-138 applied to the layer's dequantized [K,N] weights):
+ * every weight is dequantized exactly in f32, (q - z) * s, and each group of
+ * 128 consecutive flat weights is quantized by the reference's Int4Quantize.
+ * Where a reference group's weights share one published (scale, zero) and use
+ * the full code range the repack is lossless (codes, scale and zero come back
+ * exactly); elsewhere the second rounding is bounded by Int4ErrorBound.
+ * Host memory: codes [ceil(K*N/8)], scales and zeros [ceil(K*N/128)].
+ * Refused: an unknown format, N % 8 != 0, GPTQ with K % 8 != 0, AWQ with K
+ * not a multiple of group_size, groups that do not cover K, or a g_idx entry
+ * outside [0, groups). */
+int accel_int4_repack_host(const accel_foreign_int4_t* src, uint32_t* codes,
+                           uint16_t* scales, uint16_t* zeros);
+
+/* The same repack on the device, bit-identical to the host's: src's planes
+ * and dst's (weights = K*N) are device memory.  One wave per reference group,
+ * dequantizing its 128 weights from the published planes in registers and
+ * quantizing them with the device Int4Quantize.  A g_idx entry outside
+ * [0, groups) is reported as ACCEL_E_INVALID after the stream is synchronized
+ * (the call waits for the repack, a load-time operation). */
+int accel_int4_repack(int dev, void* stream, const accel_foreign_int4_t* src,
+                      accel_int4_t* dst);
+
 /* tensor.Int4MatVec (tensor/int4.go:99-147): out[n] = sum_k a[k] * w(k,n),
  * w = s==0 ? z : (code-z)*s.  a is f32 [K]; out is f32 [N], N = weights/K. */
 int accel_int4_matvec(int dev, void* stream, const accel_tensor_t* a,

@@ -85,6 +85,8 @@ def lib():
                                           _u16p, _u32p, _f32p, ctypes.c_int]
     L.orc_swiglu.argtypes = [_f32p, _f32p, _f32p, _i64]
     L.orc_add_rows.argtypes = [_u32, _u32, _f32p, _f32p, _f32p]
+    L.orc_foreign_dequant.argtypes = [ctypes.c_int32, _i64, _i64, _i64, _u32p, _u32p, _u16p,
+                                      ctypes.c_void_p, _f32p]
     L.orc_rmsnorm.argtypes = [_u32, _u32, ctypes.c_float, _f32p, _f32p, _f32p]
     L.orc_matvec_f32_f16.argtypes = [_u32, _u32, _f32p, _u16p, _f32p]
     L.orc_quant_matvec_i8.argtypes = [_u32, _u32, _f32p, _i8p, _u16p, _f32p]
@@ -265,6 +267,30 @@ def matmul_f64(a, wdq, M: int, K: int, N: int) -> np.ndarray:
 
 
 # ---- decode-step neighbours -------------------------------------------------
+
+def foreign_dequant(fmt: int, K: int, N: int, group_size: int, qweight, qzeros, scales,
+                    g_idx=None) -> np.ndarray:
+    """A published AWQ (fmt 1) / GPTQ (2) / GPTQ v2 (3) layer's weights,
+    dequantized exactly, [K, N] f32."""
+    qw = np.ascontiguousarray(qweight).view(np.uint32).reshape(-1)
+    qz = np.ascontiguousarray(qzeros).view(np.uint32).reshape(-1)
+    sc = np.ascontiguousarray(scales).view(np.uint16).reshape(-1)
+    gi = None if g_idx is None else np.ascontiguousarray(g_idx, np.int32)
+    if gi is not None:
+        assert gi.size == K and gi.min() >= 0 and gi.max() < sc.size // N
+    w = np.empty(K * N, np.float32)
+    lib().orc_foreign_dequant(fmt, K, N, group_size, qw, qz, sc,
+                              None if gi is None else gi.ctypes.data, w)
+    return w.reshape(K, N)
+
+
+def int4_repack(fmt: int, K: int, N: int, group_size: int, qweight, qzeros, scales,
+                g_idx=None):
+    """A published layer in the reference int4 format: the reference's
+    Int4Quantize (quant/int4.go:71-138) of its exactly dequantized weights."""
+    w = foreign_dequant(fmt, K, N, group_size, qweight, qzeros, scales, g_idx)
+    return int4_quantize(w.reshape(-1))
+
 
 def add_rows(x, v) -> np.ndarray:
     """ElemAdd (internal/kernels/elementwise.go:19-27) of x [rows, cols] and

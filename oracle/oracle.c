@@ -46,6 +46,14 @@
  *                       a row of ones equals w / sqrt(1 + eps) exactly
  *   orc_matvec_f32_f16  f64 brute force within the f32 reduction bound, and
  *                       exact sums where every partial is an exact integer
+ *   orc_foreign_dequant round trips with independent numpy restatements of
+ *                       the published packers (AutoAWQ's column order, GPTQ's
+ *                       row packing and its z - 1 zeros, act-order g_idx);
+ *                       the repack it feeds (with orc_int4_quantize) returns
+ *                       codes, scales and zeros exactly where a reference
+ *                       group shares one published (scale, zero) and spans
+ *                       the full code range, a closed form a wrong nibble
+ *                       order or column permutation fails
  *   orc_add_rows        IEEE f32 addition against numpy's, signed zeros,
  *                       infinities and NaN; a -0.0 vector returns x bit for
  *                       bit (the int4 Linear's composed form is this after
@@ -630,6 +638,50 @@ void orc_swiglu(const float* a, const float* b, float* out, int64_t n) {
         const float d = 1.0f + e;
         const float q = x / d;
         out[i] = q * b[i];
+    }
+}
+
+/* Published 4-bit layers, dequantized (the unpack side of the published
+ * formats; the reference names reading them as unbuilt,
+ * specs/048-int4.md:126-131,167).  fmt 1 = AWQ (AutoAWQ 0.2 "gemm"): the
+ * unpacker takes nibble i of word (k, j) in packing order, position 8j + i,
+ * then reverses the packer's column order {0,2,4,6,1,3,5,7}: column 8j + c is
+ * packing position 8j + {0,4,1,5,2,6,3,7}[c]; zeros likewise; g = k / G.
+ * fmt 2 = GPTQ (AutoGPTQ 0.7): row 8i + j is nibble j of word (i, n); zero
+ * column 8j + c is nibble c of word (g, j), plus one; g = g_idx[k] or k / G.
+ * fmt 3 = GPTQ v2: as 2 without the plus one.  w = (q - z) * s in f32, which
+ * is exact.  w is [K, N]. */
+void orc_foreign_dequant(int32_t fmt, int64_t K, int64_t N, int64_t G, const uint32_t* qweight,
+                         const uint32_t* qzeros, const uint16_t* scales, const int32_t* g_idx,
+                         float* w) {
+    static const int reverse_order[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+    const int64_t wpr = N / 8;
+    for (int64_t k = 0; k < K; k++) {
+        const int64_t g = g_idx ? (int64_t)g_idx[k] : k / G;
+        for (int64_t j = 0; j < wpr; j++) {
+            uint32_t q[8], z[8];
+            if (fmt == 1) {
+                uint32_t qp[8], zp[8];   /* packing order */
+                for (int i = 0; i < 8; i++) {
+                    qp[i] = (qweight[k * wpr + j] >> (4 * i)) & 15u;
+                    zp[i] = (qzeros[g * wpr + j] >> (4 * i)) & 15u;
+                }
+                for (int c = 0; c < 8; c++) {
+                    q[c] = qp[reverse_order[c]];
+                    z[c] = zp[reverse_order[c]];
+                }
+            } else {
+                for (int c = 0; c < 8; c++) {
+                    q[c] = (qweight[(k / 8) * N + 8 * j + c] >> (4 * (k % 8))) & 15u;
+                    z[c] = ((qzeros[g * wpr + j] >> (4 * c)) & 15u) + (fmt == 2 ? 1u : 0u);
+                }
+            }
+            for (int c = 0; c < 8; c++) {
+                const int64_t n = 8 * j + c;
+                const float s = orc_f16_to_f32(scales[g * N + n]);
+                w[k * N + n] = (float)((int32_t)q[c] - (int32_t)z[c]) * s;
+            }
+        }
     }
 }
 
