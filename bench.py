@@ -503,6 +503,64 @@ def cpu_baseline(L, seconds):
                        f"reference evaluation order, {threads} threads)")
 
 
+def _time_calls(fn, seconds):
+    fn()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            return el / n, n
+
+
+def cpu_baseline_extras(seconds=1.5):
+    """The oracle's single-threaded C ports of the widened rows (the reference
+    CPU algorithms in reference order), each timed on a bounded sample on the
+    host cores, to sit beside the `extra` GPU figures."""
+    import oracle
+    rng = np.random.Generator(np.random.PCG64(21))
+    K = N = 4096
+    out = {}
+    x = rng.standard_normal(K).astype(np.float32)
+    q = rng.integers(-127, 128, K * N, dtype=np.int8)
+    sc = np.full((K * N) // 32, 0x1c00, np.uint16)
+    per, n = _time_calls(lambda: oracle.quant_matvec_i8(x, q, sc, K, N), seconds)
+    nbytes = K * N + K * N // 16 + 4 * K + 4 * N
+    out["int8_gemv_4096"] = dict(us=round(per * 1e6, 1), gbs=round(nbytes / per / 1e9, 3),
+                                 calls=n, what="QuantMatVecF32, M=1 K=N=4096")
+    wb = (rng.standard_normal(K * N, dtype=np.float32) * 0.02).astype(np.float16).view(np.uint16)
+    per, n = _time_calls(lambda: oracle.matvec_f32_f16(x, wb, K, N), seconds)
+    nbytes = 2 * K * N + 4 * K + 4 * N
+    out["matvec_f32_f16"] = dict(us=round(per * 1e6, 1), gbs=round(nbytes / per / 1e9, 3),
+                                 calls=n, what="MatVecF32F16, K=N=4096")
+    from accel_amd import workloads
+    L = workloads.linear(**workloads.CONFIGS["gemv_m1"])
+    bias = rng.standard_normal(N).astype(np.float32)
+    per, n = _time_calls(lambda: oracle.int4_linear(L.x[0], L.packed, L.scales, L.zeros, bias,
+                                                    1, K, N), seconds)
+    out["linear_gemv_f32"] = dict(us=round(per * 1e6, 1), calls=n,
+                                  what="composed int4 Linear (QuantMatVecInt4 + ElemAdd), M=1 "
+                                       "K=N=4096")
+    a = rng.standard_normal(14336).astype(np.float32)
+    b = rng.standard_normal(14336).astype(np.float32)
+    per, n = _time_calls(lambda: oracle.swiglu(a, b), seconds / 3)
+    out["swiglu_14336"] = dict(us=round(per * 1e6, 1), calls=n, what="SwiGLU over 14336")
+    xr = rng.standard_normal((1, 4096)).astype(np.float32)
+    g = rng.standard_normal(4096).astype(np.float32)
+    per, n = _time_calls(lambda: oracle.rmsnorm(xr, g, 1e-5), seconds / 3)
+    out["rmsnorm_4096"] = dict(us=round(per * 1e6, 1), calls=n, what="RMSNorm, one 4096 row")
+    Kr, Nr, G = 4096, 14336, 128
+    qw = rng.integers(0, 2**32, (Kr, Nr // 8), dtype=np.uint32)
+    qz = rng.integers(0, 2**32, (Kr // G, Nr // 8), dtype=np.uint32)
+    ss = (rng.random((Kr // G, Nr), dtype=np.float32) * 0.02 + 1e-3).astype(np.float16)
+    per, n = _time_calls(lambda: oracle.int4_repack(1, Kr, Nr, G, qw, qz, ss.view(np.uint16)),
+                         seconds)
+    out["repack_awq_4096x14336"] = dict(ms=round(per * 1e3, 1), calls=n,
+                                        what="AWQ unpack + Int4Quantize, one 4096x14336 layer")
+    return dict(kind="port", cores=1, rows=out)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -586,6 +644,8 @@ def main():
         line["extra"] = extra
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(L, args.cpu_seconds)
+        if args.configs and not args.no_extra:
+            line["extra"]["cpu_baselines"] = cpu_baseline_extras()
     dev.destroy_stream(stream)
     print(json.dumps(line), flush=True)
 
