@@ -15,9 +15,9 @@
 // bytes for a 256-column tile).  A lane issues all its loads -- codes, then
 // the scale, zero and activations of each of its rows -- before it uses
 // any, branch free, so a workgroup waits for one memory latency; the slice
-// count grows with K instead of a loop (only past 32 slices does a workgroup
-// loop over batches, the next batch's loads issued before the current one is
-// computed).  Per (row, group) the dequantisation folds
+// count grows with K instead of a loop (only past 64 slices at one row, 32 at
+// more, does a workgroup loop over batches, the next batch's loads then
+// issued before the current one is computed).  Per (row, group) the dequantisation folds
 // into two scalars,
 //     x*w = (x*s)*code + b,   b = -(x*s)*z   (or x*z for a zero scale),
 // so the inner loop is one conversion per two weights and one FMA per
@@ -95,7 +95,7 @@ __device__ __forceinline__ void load_words(const uint32_t* p, uint32_t* w) {
 // given a zero factor), so the workgroup waits for one memory latency.
 // Matrices longer than the slices the launch can take loop over such
 // batches.
-template <int M, int TILE, int CPL>
+template <int M, int TILE, int CPL, bool PIPE>
 __global__ __launch_bounds__(kDecThreads) void int4_decode_f32_kernel(
     const float* __restrict__ a, const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
@@ -138,8 +138,6 @@ __global__ __launch_bounds__(kDecThreads) void int4_decode_f32_kernel(
         for (int j = 0; j < CPL; j++) acc[m][j] = 0.0f;
     }
 
-    // Software-pipelined over batches: the next batch's loads are issued
-    // before the current batch is computed.
     uint32_t q[kBatch][WPL];
     uint16_t sb[kBatch], zb[kBatch];
     float xv[kBatch][M];
@@ -159,13 +157,7 @@ __global__ __launch_bounds__(kDecThreads) void int4_decode_f32_kernel(
             for (int m = 0; m < M; m++) xx[i][m] = a[(size_t)m * K + row];
         }
     };
-    if (k_begin < k_end) fetch(k_begin, q, sb, zb, xv);
-    for (int kb = k_begin; kb < k_end; kb += kBatch * RP) {
-        uint32_t qn[kBatch][WPL];
-        uint16_t sn[kBatch], zn[kBatch];
-        float xn[kBatch][M];
-        const bool more = kb + kBatch * RP < k_end;
-        if (more) fetch(kb + kBatch * RP, qn, sn, zn, xn);
+    auto compute = [&](int kb) {
 #pragma unroll
         for (int i = 0; i < kBatch; i++) {
             const bool valid = kb + rp + i * RP < k_end;
@@ -190,16 +182,34 @@ __global__ __launch_bounds__(kDecThreads) void int4_decode_f32_kernel(
                         acc[m][wi * 8 + j] = __builtin_fmaf(c[m], f[j], acc[m][wi * 8 + j]);
             }
         }
-        if (more) {
+    };
+    if constexpr (PIPE) {
+        // Several batches a workgroup: the next batch's loads are issued
+        // before the current batch is computed.
+        if (k_begin < k_end) fetch(k_begin, q, sb, zb, xv);
+        for (int kb = k_begin; kb < k_end; kb += kBatch * RP) {
+            uint32_t qn[kBatch][WPL];
+            uint16_t sn[kBatch], zn[kBatch];
+            float xn[kBatch][M];
+            const bool more = kb + kBatch * RP < k_end;
+            if (more) fetch(kb + kBatch * RP, qn, sn, zn, xn);
+            compute(kb);
+            if (more) {
 #pragma unroll
-            for (int i = 0; i < kBatch; i++) {
+                for (int i = 0; i < kBatch; i++) {
 #pragma unroll
-                for (int w = 0; w < WPL; w++) q[i][w] = qn[i][w];
-                sb[i] = sn[i];
-                zb[i] = zn[i];
+                    for (int w = 0; w < WPL; w++) q[i][w] = qn[i][w];
+                    sb[i] = sn[i];
+                    zb[i] = zn[i];
 #pragma unroll
-                for (int m = 0; m < M; m++) xv[i][m] = xn[i][m];
+                    for (int m = 0; m < M; m++) xv[i][m] = xn[i][m];
+                }
             }
+        }
+    } else {
+        for (int kb = k_begin; kb < k_end; kb += kBatch * RP) {
+            fetch(kb, q, sb, zb, xv);
+            compute(kb);
         }
     }
 
@@ -237,7 +247,7 @@ __global__ __launch_bounds__(kDecThreads) void int4_decode_f32_kernel(
 }
 
 // Slices: one batch (kBatch rows a lane) per workgroup, so every workgroup
-// waits for one memory latency; past 32 slices a workgroup loops over
+// waits for one memory latency; past the slice cap a workgroup loops over
 // several batches instead (pipelined), which bounds the partial sums and the
 // hand-off's reads.
 template <int M, int TILE, int CPL>
@@ -248,12 +258,15 @@ hipError_t launch_decode(Device* d, hipStream_t st, const float* a, Int4Planes w
     constexpr int kRowsPerBatch = kBatch * RP;
     const int tiles = N / TILE;
     const int batches = (K + kRowsPerBatch - 1) / kRowsPerBatch;
-    // At most 32 slices: past that a workgroup takes two or more batches,
-    // whose loads overlap the previous batch's arithmetic, and the hand-off
-    // reads fewer partial sums (measured: K = 14336, N = 4096, 28 slices of
-    // two batches 12.9 us against 56 of one 13.8 us).
-    constexpr int kMaxInt4Slices = 32;
-    const int per_slice = (batches + kMaxInt4Slices - 1) / kMaxInt4Slices;
+    // One row: up to 64 slices of one batch each.  More rows: up to 32
+    // slices, past which a workgroup takes several batches, pipelined (the
+    // next batch's loads before the current one's arithmetic).  Measured at
+    // K = 14336, N = 4096: M = 1 56 single-batch slices 12.7 us against 28
+    // pipelined pairs 13.0; M = 2 19.8 against 18.9; M = 8 55.6 against
+    // 42.3.  The pipelined kernel holds more registers, so it is used only
+    // where a workgroup has more than one batch.
+    const int max_slices = M == 1 ? kMaxSlices : 32;
+    const int per_slice = (batches + max_slices - 1) / max_slices;
     const int rows = per_slice * kRowsPerBatch;
     const int slices = (K + rows - 1) / rows;
     float* partial = nullptr;
@@ -271,9 +284,14 @@ hipError_t launch_decode(Device* d, hipStream_t st, const float* a, Int4Planes w
         tickets = static_cast<uint32_t*>(ws);
         partial = reinterpret_cast<float*>(static_cast<char*>(ws) + kWorkspaceCounterBytes);
     }
-    hipLaunchKernelGGL((int4_decode_f32_kernel<M, TILE, CPL>), dim3(tiles * slices),
-                       dim3(kDecThreads), 0, st, a, w.codes, w.scales, w.zeros, out, partial,
-                       tickets, stride, K, N, rows, slices, ep);
+    if (per_slice > 1)
+        hipLaunchKernelGGL((int4_decode_f32_kernel<M, TILE, CPL, true>), dim3(tiles * slices),
+                           dim3(kDecThreads), 0, st, a, w.codes, w.scales, w.zeros, out, partial,
+                           tickets, stride, K, N, rows, slices, ep);
+    else
+        hipLaunchKernelGGL((int4_decode_f32_kernel<M, TILE, CPL, false>), dim3(tiles * slices),
+                           dim3(kDecThreads), 0, st, a, w.codes, w.scales, w.zeros, out, partial,
+                           tickets, stride, K, N, rows, slices, ep);
     return hipGetLastError();
 }
 

@@ -42,7 +42,7 @@ BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, vendor figure
 METRIC = ("int4 linear: HBM GB/s (% peak) at M=1; TFLOP/s (% MFMA peak) at M=2048")
 ROTATE_BYTES = 544 << 20       # weight copies in rotation, > 2x the Infinity Cache
 TRAFFIC_FILE = os.path.join(HERE, "profiles", "traffic.json")
-GEMV_KERNEL = "int4_decode_f32_kernel<1, 256, 32>"
+GEMV_KERNEL = "int4_decode_f32_kernel<1, 256, 32, false>"
 GEMM_KERNEL = "int4_gemm_bf16_kernel<false>"
 
 
