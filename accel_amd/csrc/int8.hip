@@ -56,7 +56,8 @@ __global__ __launch_bounds__(kDecThreads) void int8_decode_kernel(
     constexpr int RPW = 64 / LPR;
     constexpr int WPL = CPL / 4;   // quant words per lane per row
     constexpr int NWAVE = kDecThreads / 64;
-    __shared__ __attribute__((aligned(16))) float red[NWAVE][TILE];
+    // every row's per-wave column sums at once: one barrier for all M rows
+    __shared__ __attribute__((aligned(16))) float red[NWAVE][M][TILE];
     __shared__ int last_flag;
 
     const int tiles = N / TILE;
@@ -135,19 +136,19 @@ __global__ __launch_bounds__(kDecThreads) void int8_decode_kernel(
         transpose_reduce<CPL, 64 / 2, LPR>(v, l64);
         const int c0 = lane * CPL + reduced_offset<CPL, 64 / 2, LPR>(l64);
 #pragma unroll
-        for (int e = 0; e < NV; e++) red[wave][c0 + e] = v[e];
-        __syncthreads();
-        for (int cc = tid; cc < TILE; cc += kDecThreads) {
-            float sum = 0.0f;
+        for (int e = 0; e < NV; e++) red[wave][m][c0 + e] = v[e];
+    }
+    __syncthreads();
+    for (int idx = tid; idx < M * TILE; idx += kDecThreads) {
+        const int m = idx / TILE, cc = idx - m * TILE;
+        float sum = 0.0f;
 #pragma unroll
-            for (int w = 0; w < NWAVE; w++) sum += red[w][cc];
-            const int col = tile * TILE + cc;
-            if (split)
-                store_device(&partial[((size_t)slice * M + m) * N + col], sum);
-            else
-                out[(size_t)m * N + col] = sum;
-        }
-        __syncthreads();
+        for (int w = 0; w < NWAVE; w++) sum += red[w][m][cc];
+        const int col = tile * TILE + cc;
+        if (split)
+            store_device(&partial[((size_t)slice * M + m) * N + col], sum);
+        else
+            out[(size_t)m * N + col] = sum;
     }
     if (!split) return;
     split_k_finish(partial, tickets + (size_t)tile * ticket_stride, out, tile * TILE, TILE, M, N,
