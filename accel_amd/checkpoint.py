@@ -53,15 +53,25 @@ def read_safetensors(path: str) -> dict:
     data_bytes = size - 8 - n
     mm = np.memmap(path, np.uint8, mode="r", offset=8 + n, shape=(data_bytes,)) \
         if data_bytes else np.zeros(0, np.uint8)
+    if not isinstance(header, dict):
+        raise CheckpointError(f"{path}: header is not a JSON object")
     out = {}
     for name, info in header.items():
         if name == "__metadata__":
             continue
+        if not isinstance(info, dict):
+            raise CheckpointError(f"{path}: tensor {name} has a malformed header entry")
         dt = _DTYPES.get(info.get("dtype"))
         if dt is None:
             raise CheckpointError(f"{path}: tensor {name} has dtype {info.get('dtype')!r}")
-        shape = tuple(int(d) for d in info["shape"])
-        b, e = (int(v) for v in info["data_offsets"])
+        try:
+            shape = tuple(int(d) for d in info["shape"])
+            b, e = (int(v) for v in info["data_offsets"])
+        except (KeyError, TypeError, ValueError):
+            raise CheckpointError(f"{path}: tensor {name} has a malformed shape or "
+                                  "data_offsets") from None
+        if any(d < 0 for d in shape):
+            raise CheckpointError(f"{path}: tensor {name} has shape {shape}")
         count = int(np.prod(shape, dtype=np.int64)) if shape else 1
         if not 0 <= b <= e <= data_bytes or e - b != count * np.dtype(dt).itemsize:
             raise CheckpointError(f"{path}: tensor {name} spans [{b}, {e}) for {count} "

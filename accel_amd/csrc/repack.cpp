@@ -202,9 +202,11 @@ ACCEL_API int accel_int4_repack(int dev, void* stream, const accel_foreign_int4_
         e = launch_int4_repack(st, *src, const_cast<uint32_t*>(dst->codes),
                                const_cast<uint16_t*>(dst->scales),
                                const_cast<uint16_t*>(dst->zeros), bad);
+    // the repack is done before the flag is read, with a blocking copy: no
+    // transfer into this frame can outlive the call
     uint32_t flag = 0;
-    if (e == hipSuccess) e = hipMemcpyAsync(&flag, bad, sizeof flag, hipMemcpyDeviceToHost, st);
     if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e == hipSuccess) e = hipMemcpy(&flag, bad, sizeof flag, hipMemcpyDeviceToHost);
     status = classify(d, e, "Int4Repack");
     if (status != ACCEL_OK) return status;
     if (flag)

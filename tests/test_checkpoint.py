@@ -48,6 +48,15 @@ def test_read_safetensors_refuses_a_broken_file(tmp_path):
     p.write_bytes(struct.pack("<Q", len(header)) + header + b"\0")
     with pytest.raises(checkpoint.CheckpointError, match="dtype"):
         checkpoint.read_safetensors(str(p))
+    for bad, text in ((b"[1, 2]", "not a JSON object"),
+                      (json.dumps({"x": 3}).encode(), "malformed header entry"),
+                      (json.dumps({"x": {"dtype": "F32", "shape": [1]}}).encode(),
+                       "malformed shape"),
+                      (json.dumps({"x": {"dtype": "F32", "shape": [-1],
+                                         "data_offsets": [0, 0]}}).encode(), "shape")):
+        p.write_bytes(struct.pack("<Q", len(bad)) + bad + b"\0" * 4)
+        with pytest.raises(checkpoint.CheckpointError, match=text):
+            checkpoint.read_safetensors(str(p))
 
 
 @pytest.mark.parametrize("cfg,fmt,group", [
