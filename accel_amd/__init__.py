@@ -127,6 +127,7 @@ SIGNATURES = {
     "accel_int4_matvec": ([_i, _vp, _P(Tensor), _P(Int4Desc), _P(Tensor)], _i),
     "accel_int4_matmul": ([_i, _vp, _P(Tensor), _P(Int4Desc), _P(Tensor)], _i),
     "accel_int4_linear": ([_i, _vp, _P(Tensor), _P(Int4Desc), _P(Tensor), _P(Tensor)], _i),
+    "accel_int4_matvec_set": ([_i, _vp, _P(Tensor), _P(Int4Desc), _P(Tensor), _i], _i),
     "accel_segment_offsets": ([_i, _vp, _P(Tensor), _P(Tensor)], _i),
     "accel_grouped_matvec": ([_i, _vp, _P(Tensor), _P(Tensor), _P(Tensor), _P(Tensor)], _i),
     "accel_grouped_matmul": ([_i, _vp, _P(Tensor), _P(Tensor), _P(Tensor), _P(Tensor)], _i),
@@ -448,6 +449,15 @@ class Device:
         ta, tw, to = a.tensor(), w.desc(), out.tensor()
         _check(_lib.accel_int4_matmul(self.index, stream, ctypes.byref(ta), ctypes.byref(tw),
                                       ctypes.byref(to)))
+
+    def Int4MatVecSet(self, a: Buffer, ws, outs, stream=None) -> None:
+        """Int4MatVec of each of ws (1..4 matrices sharing the input vector a)
+        into outs, in one launch where the decode kernel takes them all."""
+        n = len(ws)
+        descs = (Int4Desc * max(n, 1))(*[w.desc() for w in ws])
+        outt = (Tensor * max(n, 1))(*[o.tensor() for o in outs])
+        ta = a.tensor()
+        _check(_lib.accel_int4_matvec_set(self.index, stream, ctypes.byref(ta), descs, outt, n))
 
     def Int4Linear(self, x: Buffer, w: Int4Weights, bias, out: Buffer, stream=None) -> None:
         """The int4 analogue of tensor.Linear (tensor/matmul.go:184-225): the

@@ -95,12 +95,14 @@ __device__ __forceinline__ void load_words(const uint32_t* p, uint32_t* w) {
 // given a zero factor), so the workgroup waits for one memory latency.
 // Matrices longer than the slices the launch can take loop over such
 // batches.
+// One workgroup's share: column tile `tile` of the matrix, K slice `slice`;
+// `ticket` is this tile's split-K ticket.
 template <int M, int TILE, int CPL, bool PIPE>
-__global__ __launch_bounds__(kDecThreads) void int4_decode_f32_kernel(
+__device__ __forceinline__ void decode_tile(
     const float* __restrict__ a, const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
-    void* __restrict__ out, float* partial, uint32_t* tickets, int ticket_stride, int K, int N,
-    int rows_per_slice, int slices, Epilogue ep) {
+    void* __restrict__ out, float* partial, uint32_t* ticket, int K, int N, int tile, int slice,
+    int rows_per_slice, int slices, const Epilogue& ep) {
     constexpr int LPR = TILE / CPL;        // lanes per row
     constexpr int RP = kDecThreads / LPR;  // row phases
     constexpr int RPW = 64 / LPR;          // row phases per wave
@@ -108,13 +110,6 @@ __global__ __launch_bounds__(kDecThreads) void int4_decode_f32_kernel(
     constexpr int NWAVE = kDecThreads / 64;
     __shared__ __attribute__((aligned(16))) float red[NWAVE][TILE];
     __shared__ int last_flag;
-
-    const int tiles = N / TILE;
-    const int grid = tiles * slices;
-    int b = blockIdx.x;
-    if ((grid & 7) == 0) b = (b & 7) * (grid >> 3) + (b >> 3);
-    const int tile = b % tiles;
-    const int slice = b / tiles;
 
     const int tid = threadIdx.x;
     const int l64 = tid & 63;
@@ -242,8 +237,60 @@ __global__ __launch_bounds__(kDecThreads) void int4_decode_f32_kernel(
     }
     if (!split) return;
 
-    split_k_finish(partial, tickets + (size_t)tile * ticket_stride, out, tile * TILE, TILE, M, N,
-                   slices, &last_flag, ep);
+    split_k_finish(partial, ticket, out, tile * TILE, TILE, M, N, slices, &last_flag, ep);
+}
+
+template <int M, int TILE, int CPL, bool PIPE>
+__global__ __launch_bounds__(kDecThreads) void int4_decode_f32_kernel(
+    const float* __restrict__ a, const uint32_t* __restrict__ codes,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
+    void* __restrict__ out, float* partial, uint32_t* tickets, int ticket_stride, int K, int N,
+    int rows_per_slice, int slices, Epilogue ep) {
+    const int tiles = N / TILE;
+    const int grid = tiles * slices;
+    int b = blockIdx.x;
+    if ((grid & 7) == 0) b = (b & 7) * (grid >> 3) + (b >> 3);
+    const int tile = b % tiles;
+    const int slice = b / tiles;
+    decode_tile<M, TILE, CPL, PIPE>(a, codes, scales, zeros, out, partial,
+                                    tickets + (size_t)tile * ticket_stride, K, N, tile, slice,
+                                    rows_per_slice, slices, ep);
+}
+
+// Several matrices against one input in one launch (the q, k, v or gate, up
+// products of a decode step): the grid is the matrices' column tiles side by
+// side, times the K slices; a workgroup finds its matrix from its global
+// tile.  Each matrix's results are those of its own launch, bit for bit.
+constexpr int kMaxSet = 4;
+struct DecodeSet {
+    const uint32_t* codes[kMaxSet];
+    const uint16_t* scales[kMaxSet];
+    const uint16_t* zeros[kMaxSet];
+    void* out[kMaxSet];
+    float* partial[kMaxSet];
+    int n[kMaxSet];
+    int tile0[kMaxSet + 1];   // first global tile of each matrix; tile0[count] = all
+    int count;
+};
+
+template <int M, int TILE, int CPL, bool PIPE>
+__global__ __launch_bounds__(kDecThreads) void int4_decode_set_kernel(
+    const float* __restrict__ a, DecodeSet set, uint32_t* tickets, int ticket_stride, int K,
+    int rows_per_slice, int slices) {
+    const int tiles = set.tile0[set.count];
+    const int grid = tiles * slices;
+    int b = blockIdx.x;
+    if ((grid & 7) == 0) b = (b & 7) * (grid >> 3) + (b >> 3);
+    const int tg = b % tiles;
+    const int slice = b / tiles;
+    int i = 0;
+#pragma unroll
+    for (int j = 1; j < kMaxSet; j++)
+        if (j < set.count && tg >= set.tile0[j]) i = j;
+    decode_tile<M, TILE, CPL, PIPE>(a, set.codes[i], set.scales[i], set.zeros[i], set.out[i],
+                                    set.partial[i], tickets + (size_t)tg * ticket_stride, K,
+                                    set.n[i], tg - set.tile0[i], slice, rows_per_slice, slices,
+                                    Epilogue{});
 }
 
 // Slices: one batch (kBatch rows a lane) per workgroup, so every workgroup
@@ -1155,6 +1202,60 @@ hipError_t launch_decode_mfma(Device* d, hipStream_t st, const float* a, Int4Pla
     return launch_mfma<1, 8>(d, st, a, w, out, M, K, N, p, status, ep);
 }
 
+template <int TILE>
+hipError_t launch_matvec_set(Device* d, hipStream_t st, const float* a, const Int4Planes* w,
+                             float* const* out, const int* N, int count, int K, int* status) {
+    constexpr int CPL = 32;
+    constexpr int LPR = TILE / CPL;
+    constexpr int RP = kDecThreads / LPR;
+    constexpr int kRowsPerBatch = kBatch * RP;
+    const int batches = (K + kRowsPerBatch - 1) / kRowsPerBatch;
+    const int per_slice = (batches + kMaxSlices - 1) / kMaxSlices;   // as a lone M = 1 launch
+    const int rows = per_slice * kRowsPerBatch;
+    const int slices = (K + rows - 1) / rows;
+    DecodeSet set{};
+    set.count = count;
+    int tiles = 0;
+    size_t partial_floats = 0;
+    for (int i = 0; i < count; i++) {
+        set.codes[i] = w[i].codes;
+        set.scales[i] = w[i].scales;
+        set.zeros[i] = w[i].zeros;
+        set.out[i] = out[i];
+        set.n[i] = N[i];
+        set.tile0[i] = tiles;
+        tiles += N[i] / TILE;
+        partial_floats += (size_t)slices * N[i];
+    }
+    set.tile0[count] = tiles;
+    uint32_t* tickets = nullptr;
+    int stride = 0;
+    if (slices > 1) {
+        stride = ticket_stride(tiles);
+        if (stride == 0) {
+            *status = fail(ACCEL_E_INVALID,
+                           "decode product: %d tiles need more tickets than the workspace holds",
+                           tiles);
+            return hipSuccess;
+        }
+        void* ws = workspace(d, partial_floats * sizeof(float), status);
+        if (!ws) return hipSuccess;
+        tickets = static_cast<uint32_t*>(ws);
+        float* p = reinterpret_cast<float*>(static_cast<char*>(ws) + kWorkspaceCounterBytes);
+        for (int i = 0; i < count; i++) {
+            set.partial[i] = p;
+            p += (size_t)slices * N[i];
+        }
+    }
+    if (per_slice > 1)
+        hipLaunchKernelGGL((int4_decode_set_kernel<1, TILE, CPL, true>), dim3(tiles * slices),
+                           dim3(kDecThreads), 0, st, a, set, tickets, stride, K, rows, slices);
+    else
+        hipLaunchKernelGGL((int4_decode_set_kernel<1, TILE, CPL, false>), dim3(tiles * slices),
+                           dim3(kDecThreads), 0, st, a, set, tickets, stride, K, rows, slices);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_matvec_f32_f16(Device* d, hipStream_t st, const float* a, const uint16_t* w,
@@ -1169,6 +1270,36 @@ hipError_t launch_matvec_f32_f16(Device* d, hipStream_t st, const float* a, cons
     hipLaunchKernelGGL(matvec_f16_generic_kernel, dim3((N + 255) / 256), dim3(256), 0, st, a, w,
                        out, K, N);
     return hipGetLastError();
+}
+
+bool int4_matvec_set_supported(const Int4Planes* w, const int* N, int count, int K) {
+    if (count < 1 || count > kMaxSet) return false;
+    for (int i = 0; i < count; i++)
+        if (!int4_decode_f32_supported(1, K, N[i], w[i].codes)) return false;
+    return true;
+}
+
+hipError_t launch_int4_matvec_set(Device* d, hipStream_t st, const float* a, const Int4Planes* w,
+                                  float* const* out, const int* N, int count, int K,
+                                  int* status) {
+    *status = ACCEL_OK;
+    // Each matrix keeps the tile width its own launch would take (256 columns
+    // where N allows, else 128), so its sums are added in the same order and
+    // its result is its own Int4MatVec's: one launch per width present.
+    Int4Planes wg[2][kMaxSet];
+    float* og[2][kMaxSet];
+    int ng[2][kMaxSet], cnt[2] = {0, 0};
+    for (int i = 0; i < count; i++) {
+        const int g = N[i] % 256 == 0 ? 0 : 1;
+        wg[g][cnt[g]] = w[i];
+        og[g][cnt[g]] = out[i];
+        ng[g][cnt[g]++] = N[i];
+    }
+    hipError_t e = hipSuccess;
+    if (cnt[0]) e = launch_matvec_set<256>(d, st, a, wg[0], og[0], ng[0], cnt[0], K, status);
+    if (e != hipSuccess || *status != ACCEL_OK) return e;
+    if (cnt[1]) e = launch_matvec_set<128>(d, st, a, wg[1], og[1], ng[1], cnt[1], K, status);
+    return e;
 }
 
 bool int4_decode_f32_supported(int M, int K, int N, const void* codes) {

@@ -91,6 +91,12 @@ hipError_t launch_int4_gemm_f32(Device* d, hipStream_t st, const float* a,
                                 Int4Planes w, void* out, int M, int K, int N,
                                 Epilogue ep = Epilogue{});
 bool int4_decode_f32_supported(int M, int K, int N, const void* codes);
+// Int4MatVec of up to four matrices against one f32 vector [K] in one launch
+// (all must take the decode kernel: int4_matvec_set_supported).
+bool int4_matvec_set_supported(const Int4Planes* w, const int* N, int count, int K);
+hipError_t launch_int4_matvec_set(Device* d, hipStream_t st, const float* a, const Int4Planes* w,
+                                  float* const* out, const int* N, int count, int K,
+                                  int* status);
 
 // Grouped products over offsets [E+1] already on the device.
 hipError_t launch_segment_offsets(hipStream_t st, const uint32_t* counts,

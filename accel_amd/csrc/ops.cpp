@@ -166,10 +166,67 @@ int run_int4_product(Device* d, hipStream_t st, const void* a, int32_t dtype,
 
 }  // namespace
 
+// Int4MatVec's checks (tensor/int4.go:99-147); on success fills K and N.
+static int check_matvec(const char* op, const accel_tensor_t* a, const accel_int4_t* w,
+                        const accel_tensor_t* out, int64_t* K, int64_t* N);
+
 ACCEL_API int accel_int4_matvec(int dev, void* stream, const accel_tensor_t* a,
                                 const accel_int4_t* w, accel_tensor_t* out) {
     clear_error();
-    const char* op = "Int4MatVec";
+    int64_t k = 0, n = 0;
+    const int rc = check_matvec("Int4MatVec", a, w, out, &k, &n);
+    if (rc != ACCEL_OK) return rc;
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    return run_int4_product(d, (hipStream_t)stream, a->data, ACCEL_F32, w, out->data, 1,
+                            (int)k, (int)n);
+}
+
+// Int4MatVec over several matrices that share one input vector, in one
+// launch where they all take the decode kernel (the q, k, v or gate, up
+// products of a decode step); each result is its own Int4MatVec's.
+ACCEL_API int accel_int4_matvec_set(int dev, void* stream, const accel_tensor_t* a,
+                                    const accel_int4_t* w, accel_tensor_t* out, int count) {
+    clear_error();
+    const char* op = "Int4MatVecSet";
+    if (count < 1 || count > 4 || !w || !out) {
+        char buf[160];
+        snprintf(buf, sizeof buf, "%d matrices; a set holds one to four", count);
+        return refuse(op, buf);
+    }
+    int64_t K = 0;
+    int N[4];
+    Int4Planes p[4];
+    float* o[4];
+    for (int i = 0; i < count; i++) {
+        int64_t k = 0, n = 0;
+        const int rc = check_matvec(op, a, &w[i], &out[i], &k, &n);
+        if (rc != ACCEL_OK) return rc;
+        K = k;
+        N[i] = (int)n;
+        p[i] = planes(&w[i]);
+        o[i] = static_cast<float*>(out[i].data);
+    }
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    hipStream_t st = (hipStream_t)stream;
+    if (!int4_matvec_set_supported(p, N, count, (int)K)) {
+        for (int i = 0; i < count; i++) {
+            const int rc = run_int4_product(d, st, a->data, ACCEL_F32, &w[i], out[i].data, 1,
+                                            (int)K, N[i]);
+            if (rc != ACCEL_OK) return rc;
+        }
+        return ACCEL_OK;
+    }
+    int status = begin_submission(d);
+    if (status != ACCEL_OK) return status;
+    hipError_t e = launch_int4_matvec_set(d, st, static_cast<const float*>(a->data), p, o, N,
+                                          count, (int)K, &status);
+    return finish(d, e, status, "Int4MatVecSet launch");
+}
+
+static int check_matvec(const char* op, const accel_tensor_t* a, const accel_int4_t* w,
+                        const accel_tensor_t* out, int64_t* K, int64_t* N) {
     std::string why = check_int4(w, "the weight matrix");
     if (!why.empty()) return refuse(op, why);
     if (!valid_tensor(a) || !a->data) return refuse(op, "the activations are missing");
@@ -198,12 +255,11 @@ ACCEL_API int accel_int4_matvec(int dev, void* stream, const accel_tensor_t* a,
     const int64_t n = w->weights / k;
     if (k > INT32_MAX || n > INT32_MAX)
         return refuse(op, "the matrix is larger than this backend's 32-bit extents");
-    int rc = check_out(op, out, ACCEL_F32, 1, n, true);
+    const int rc = check_out(op, out, ACCEL_F32, 1, n, true);
     if (rc != ACCEL_OK) return rc;
-    Device* d = device(dev);
-    if (!d) return ACCEL_E_NO_DEVICE;
-    return run_int4_product(d, (hipStream_t)stream, a->data, ACCEL_F32, w, out->data, 1,
-                            (int)k, (int)n);
+    *K = k;
+    *N = n;
+    return ACCEL_OK;
 }
 
 ACCEL_API int accel_int4_matmul(int dev, void* stream, const accel_tensor_t* a,

@@ -423,10 +423,11 @@ def bench_repack(dev, stream, fmt=1, K=4096, N=14336, G=128, calls=20):
                 bytes=read + written)
 
 
-def bench_decode_step(dev, stream, batch, steps=100):
+def bench_decode_step(dev, stream, batch, steps=100, merged=True):
     """Config 5's layer as a whole decode step with its on-device neighbours:
     h = RMSNorm(x); q,k,v <- h; o <- q; h2 = RMSNorm(o); gate,up <- h2;
-    a = SwiGLU(gate, up); down <- a.  Ten launches a step, captured in one
+    a = SwiGLU(gate, up); down <- a.  Ten launches a step (seven at batch 1,
+    where q, k, v and gate, up each run as one launch), captured in one
     HIP graph and replayed (attention itself is outside the int4 path)."""
     from accel_amd import F32, workloads
     shapes = workloads.LAYER_SHAPES
@@ -456,15 +457,20 @@ def bench_decode_step(dev, stream, batch, steps=100):
         else:
             dev.Int4MatVec(a, w, o, stream)
 
+    def ops(a, names):
+        # at batch 1 the products that share an input run as one launch
+        if batch == 1 and merged:
+            dev.Int4MatVecSet(a, [ws[n] for n in names], [bufs[n] for n in names], stream)
+        else:
+            for n in names:
+                op(a, ws[n], bufs[n])
+
     def step(i):
         dev.RMSNorm(xin, gb1, 1e-5, h1, stream)
-        op(h1, ws["q"], bufs["q"])
-        op(h1, ws["k"], bufs["k"])
-        op(h1, ws["v"], bufs["v"])
+        ops(h1, ("q", "k", "v"))
         op(bufs["q"], ws["o"], bufs["o"])
         dev.RMSNorm(bufs["o"], gb2, 1e-5, h2, stream)
-        op(h2, ws["gate"], bufs["gate"])
-        op(h2, ws["up"], bufs["up"])
+        ops(h2, ("gate", "up"))
         dev.SwiGLU(bufs["gate"], bufs["up"], act, stream)
         op(act, ws["down"], bufs["down"])
 
@@ -479,7 +485,8 @@ def bench_decode_step(dev, stream, batch, steps=100):
         b.free()
     return dict(us_per_step=round(ms * 1e3, 2),
                 gbs=round(total_bytes / (ms * 1e-3) / 1e9, 1),
-                weight_bytes=total_bytes, batch=batch, launches=10)
+                weight_bytes=total_bytes, batch=batch,
+                launches=7 if (batch == 1 and merged) else 10)
 
 
 def cpu_baseline(L, seconds):
@@ -640,6 +647,7 @@ def main():
             extra["repack_awq_4096x14336"] = bench_repack(dev, stream, 1)
             extra["repack_gptq_4096x14336"] = bench_repack(dev, stream, 2)
             extra["decode_step_b1"] = bench_decode_step(dev, stream, 1)
+            extra["decode_step_b1_unmerged"] = bench_decode_step(dev, stream, 1, merged=False)
             extra["decode_step_b8"] = bench_decode_step(dev, stream, 8)
         line["extra"] = extra
     if not args.no_cpu:

@@ -258,6 +258,17 @@ int accel_int4_repack(int dev, void* stream, const accel_foreign_int4_t* src,
 int accel_int4_matvec(int dev, void* stream, const accel_tensor_t* a,
                       const accel_int4_t* w, accel_tensor_t* out);
 
+/* Int4MatVec over `count` (1..4) matrices w[i] that share one f32 vector a
+ * [K], out[i] f32 [N_i], in one launch per tile width (N_i a multiple of 256,
+ * or of 128 only) where every matrix takes the decode kernel (N_i a multiple
+ * of 128, 16-byte aligned codes), else one launch each.
+ * Each out[i] is exactly Int4MatVec(a, w[i]).  No reference counterpart as
+ * one call: it is the plan-level merge of the reference's separate
+ * Int4MatVec dispatches that read the same activations (a decode step's q, k,
+ * v and gate, up), with Int4MatVec's checks and wording per matrix. */
+int accel_int4_matvec_set(int dev, void* stream, const accel_tensor_t* a,
+                          const accel_int4_t* w, accel_tensor_t* out, int count);
+
 /* tensor.Int4MatMul (tensor/int4.go:168-212): a [M,K] -> out [M,N].  The
  * reference takes f32 a and gives f32 out; this also accepts bf16 a with bf16
  * out (fp32 accumulation), the additive dtype selection QuantMatMul makes by

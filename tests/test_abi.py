@@ -275,6 +275,29 @@ def test_int4_linear_refusals():   # tensor/matmul.go:189-225's checks on an int
     assert lin(t([2, K], BF16), w, b, t([2, N], BF16))[0] == accel_amd.E_NO_DEVICE
 
 
+def test_int4_matvec_set_refusals():
+    lib = accel_amd.lib()
+    K, N = 256, 128
+
+    def call(a, ws, outs, count):
+        wd = (accel_amd.Int4Desc * max(len(ws), 1))(*ws)
+        od = (accel_amd.Tensor * max(len(outs), 1))(*outs)
+        rc = lib.accel_int4_matvec_set(0, None, ctypes.byref(a), wd, od, count)
+        return rc, accel_amd.last_error()
+
+    a = t([K], F32)
+    rc, msg = call(a, [w4(K * N)], [t([N], F32)], 0)
+    assert rc == accel_amd.E_INVALID and "a set holds one to four" in msg
+    rc, msg = call(a, [w4(K * N)] * 5, [t([N], F32)] * 5, 5)
+    assert rc == accel_amd.E_INVALID and "a set holds one to four" in msg
+    rc, msg = call(a, [w4(K * N), w4(K * N + 8)], [t([N], F32)] * 2, 2)
+    assert rc == accel_amd.E_INVALID and "Int4MatVecSet" in msg and "multiple of the first" in msg
+    rc, msg = call(a, [w4(K * N), w4(K * 64)], [t([N], F32), t([N], F32)], 2)
+    assert rc == accel_amd.E_INVALID and "the output is [128] and the product is [64]" in msg
+    rc, msg = call(a, [w4(K * N), w4(K * 64)], [t([N], F32), t([64], F32)], 2)
+    assert rc == accel_amd.E_NO_DEVICE
+
+
 def test_quant_matmul_refusals():   # tensor/quantized.go:32-110
     I8 = accel_amd.I8
     lib = accel_amd.lib()

@@ -1,0 +1,50 @@
+"""Several Int4MatVec products that share one input vector in one launch
+(accel_int4_matvec_set): every result equals its own Int4MatVec bit for bit,
+on the decode kernel's 256- and 128-column tiles, its pipelined multi-batch
+form (long K), and the per-matrix fallback for shapes the decode kernel does
+not take."""
+import numpy as np
+import pytest
+
+import oracle
+from accel_amd import F32, workloads
+from conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def _weights(dev, K, N, rng):
+    p, s, z = workloads.fast_int4(K, N, rng)
+    return dev.upload_int4(p, s, z, K * N), (p, s, z)
+
+
+@pytest.mark.parametrize("K,Ns", [
+    (4096, [4096, 1024, 1024]),       # q, k, v of a Llama-3-8B layer
+    (4096, [14336, 14336]),           # gate, up
+    (1024, [384, 256, 128, 512]),     # 128-column tiles (384 is not a multiple of 256)
+    (20000, [256, 512]),              # more batches than slices: the pipelined kernel
+    (300, [40, 256]),                 # 40 columns: one launch per matrix
+    (512, [256]),
+])
+def test_set_equals_separate_matvecs(dev, K, Ns):
+    rng = np.random.Generator(np.random.PCG64(K + sum(Ns)))
+    x = rng.standard_normal(K).astype(np.float32)
+    xb = dev.upload(x)
+    ws, planes = zip(*[_weights(dev, K, N, rng) for N in Ns])
+    singles, outs = [], [dev.alloc((N,), F32) for N in Ns]
+    for w, N in zip(ws, Ns):
+        ob = dev.alloc((N,), F32)
+        dev.Int4MatVec(xb, w, ob)
+        singles.append(ob.numpy().copy())
+        ob.free()
+    for rep in range(2):   # the second call reuses the hand-off's tickets
+        dev.Int4MatVecSet(xb, list(ws), outs)
+        for o, want in zip(outs, singles):
+            assert np.array_equal(o.numpy().view(np.uint32), want.view(np.uint32))
+    # and against the oracle, for one matrix
+    p, s, z = planes[0]
+    assert rel_l2(outs[0].numpy(), oracle.quant_matvec_int4(x, p, s, z, K, Ns[0])) <= 1e-5
+    for b in list(outs) + [xb]:
+        b.free()
+    for w in ws:
+        w.free()
