@@ -128,6 +128,7 @@ SIGNATURES = {
     "accel_int4_matmul": ([_i, _vp, _P(Tensor), _P(Int4Desc), _P(Tensor)], _i),
     "accel_int4_linear": ([_i, _vp, _P(Tensor), _P(Int4Desc), _P(Tensor), _P(Tensor)], _i),
     "accel_int4_matvec_set": ([_i, _vp, _P(Tensor), _P(Int4Desc), _P(Tensor), _i], _i),
+    "accel_int4_matmul_set": ([_i, _vp, _P(Tensor), _P(Int4Desc), _P(Tensor), _i], _i),
     "accel_segment_offsets": ([_i, _vp, _P(Tensor), _P(Tensor)], _i),
     "accel_grouped_matvec": ([_i, _vp, _P(Tensor), _P(Tensor), _P(Tensor), _P(Tensor)], _i),
     "accel_grouped_matmul": ([_i, _vp, _P(Tensor), _P(Tensor), _P(Tensor), _P(Tensor)], _i),
@@ -458,6 +459,15 @@ class Device:
         outt = (Tensor * max(n, 1))(*[o.tensor() for o in outs])
         ta = a.tensor()
         _check(_lib.accel_int4_matvec_set(self.index, stream, ctypes.byref(ta), descs, outt, n))
+
+    def Int4MatMulSet(self, a: Buffer, ws, outs, stream=None) -> None:
+        """Int4MatMul of f32 rows a [M, K] against each of ws (1..4 matrices)
+        into outs, one launch per tile width where the decode kernels take them."""
+        n = len(ws)
+        descs = (Int4Desc * max(n, 1))(*[w.desc() for w in ws])
+        outt = (Tensor * max(n, 1))(*[o.tensor() for o in outs])
+        ta = a.tensor()
+        _check(_lib.accel_int4_matmul_set(self.index, stream, ctypes.byref(ta), descs, outt, n))
 
     def Int4Linear(self, x: Buffer, w: Int4Weights, bias, out: Buffer, stream=None) -> None:
         """The int4 analogue of tensor.Linear (tensor/matmul.go:184-225): the

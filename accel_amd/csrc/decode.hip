@@ -714,24 +714,20 @@ __device__ __forceinline__ void codes_to_b(const uint32_t (&w)[8], bf16x8 (&b)[8
         b[j] = __builtin_bit_cast(bf16x8, (u32x4){bw[j][0], bw[j][1], bw[j][2], bw[j][3]});
 }
 
+// One workgroup's share: column tile `tile`, K slice `slice`; `ticket` is
+// the tile's pair of hand-off counters.
 template <int G, int NW>
-__global__ __launch_bounds__(64 * NW) void int4_decode_mfma_kernel(
+__device__ __forceinline__ void decode_mfma_tile(
     const float* __restrict__ a, const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
-    void* __restrict__ out, float* partial, uint32_t* tickets, int ticket_stride, int M, int K,
-    int N, int rows_per_slice, int slices, Epilogue ep) {
+    void* __restrict__ out, float* partial, uint32_t* ticket, int M, int K, int N, int tile,
+    int slice, int rows_per_slice, int slices, const Epilogue& ep) {
     using T = MfTile<G, NW>;
     constexpr int D = T::kDepth;
     constexpr int V = T::kVmemPerStep;
     __shared__ __attribute__((aligned(16))) uint8_t lds[kMfLdsBytes];
     __shared__ int last_flag;
 
-    const int tiles = N / T::kCols;
-    const int grid = tiles * slices;
-    int b = blockIdx.x;
-    if ((grid & 7) == 0) b = (b & 7) * (grid >> 3) + (b >> 3);
-    const int tile = b % tiles;
-    const int slice = b / tiles;
     const int n0 = tile * T::kCols;
     const int g0 = tile * G;
     const size_t gpr = (size_t)(N >> 7);           // groups per row
@@ -1051,7 +1047,7 @@ __global__ __launch_bounds__(64 * NW) void int4_decode_mfma_kernel(
     // none waits on anything -- are done, and adds the slices in slice order.
     // This takes the last arriver's store round trip off the critical path.
     const size_t slice_stride = (size_t)M * N;
-    uint32_t* arrive = tickets + (size_t)tile * ticket_stride;
+    uint32_t* arrive = ticket;
     uint32_t* done = arrive + 1;
     if (tid == 0) {
         const uint32_t prev = __hip_atomic_fetch_add(arrive, 1u, __ATOMIC_RELAXED,
@@ -1135,6 +1131,63 @@ __global__ __launch_bounds__(64 * NW) void int4_decode_mfma_kernel(
     }
 }
 
+template <int G, int NW>
+__global__ __launch_bounds__(64 * NW) void int4_decode_mfma_kernel(
+    const float* __restrict__ a, const uint32_t* __restrict__ codes,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
+    void* __restrict__ out, float* partial, uint32_t* tickets, int ticket_stride, int M, int K,
+    int N, int rows_per_slice, int slices, Epilogue ep) {
+    using T = MfTile<G, NW>;
+    const int tiles = N / T::kCols;
+    const int grid = tiles * slices;
+    int b = blockIdx.x;
+    if ((grid & 7) == 0) b = (b & 7) * (grid >> 3) + (b >> 3);
+    const int tile = b % tiles;
+    const int slice = b / tiles;
+    decode_mfma_tile<G, NW>(a, codes, scales, zeros, out, partial,
+                            tickets + (size_t)tile * ticket_stride, M, K, N, tile, slice,
+                            rows_per_slice, slices, ep);
+}
+
+// Several matrices against one activation block in one launch, each with the
+// plan (slices, rows) its own launch would take, so each result is its own
+// launch's bit for bit: the grid is the matrices' workgroups side by side.
+// The hand-off waits only on workgroups that already hold tickets, so a set
+// larger than the chip drains like consecutive launches.
+struct MfSet {
+    const uint32_t* codes[kMaxSet];
+    const uint16_t* scales[kMaxSet];
+    const uint16_t* zeros[kMaxSet];
+    void* out[kMaxSet];
+    float* partial[kMaxSet];
+    int n[kMaxSet];
+    int rows[kMaxSet];
+    int slices[kMaxSet];
+    int wg0[kMaxSet + 1];    // first workgroup of each matrix; wg0[count] = grid
+    int tick0[kMaxSet];      // first ticket pair of each matrix
+    int count;
+};
+
+template <int G, int NW>
+__global__ __launch_bounds__(64 * NW) void int4_decode_mfma_set_kernel(
+    const float* __restrict__ a, MfSet set, uint32_t* tickets, int ticket_stride, int M, int K) {
+    using T = MfTile<G, NW>;
+    const int grid = set.wg0[set.count];
+    int b = blockIdx.x;
+    if ((grid & 7) == 0) b = (b & 7) * (grid >> 3) + (b >> 3);
+    int i = 0;
+#pragma unroll
+    for (int j = 1; j < kMaxSet; j++)
+        if (j < set.count && b >= set.wg0[j]) i = j;
+    const int bl = b - set.wg0[i];
+    const int tiles = set.n[i] / T::kCols;
+    const int tile = bl % tiles;
+    const int slice = bl / tiles;
+    decode_mfma_tile<G, NW>(a, set.codes[i], set.scales[i], set.zeros[i], set.out[i],
+                            set.partial[i], tickets + (size_t)(set.tick0[i] + tile) * ticket_stride,
+                            M, K, set.n[i], tile, slice, set.rows[i], set.slices[i], Epilogue{});
+}
+
 struct MfPlan {
     int groups;   // G
     int slices;
@@ -1190,6 +1243,57 @@ hipError_t launch_mfma(Device* d, hipStream_t st, const float* a, Int4Planes w, 
     hipLaunchKernelGGL((int4_decode_mfma_kernel<G, NW>), dim3(tiles * p.slices), dim3(64 * NW),
                        0, st, a, w.codes, w.scales, w.zeros, out, partial, tickets, stride, M, K,
                        N, p.rows, p.slices, ep);
+    return hipGetLastError();
+}
+
+// Matrices of one tile width G in one launch, each with its own plan.
+template <int G>
+hipError_t launch_mfma_set(Device* d, hipStream_t st, const float* a, const Int4Planes* w,
+                           float* const* out, const int* N, const MfPlan* plan, int count, int M,
+                           int K, int* status) {
+    MfSet set{};
+    set.count = count;
+    int wgs = 0, tiles_all = 0;
+    size_t partial_floats = 0;
+    bool split = false;
+    for (int i = 0; i < count; i++) {
+        const int tiles = N[i] / (128 * G);
+        set.codes[i] = w[i].codes;
+        set.scales[i] = w[i].scales;
+        set.zeros[i] = w[i].zeros;
+        set.out[i] = out[i];
+        set.n[i] = N[i];
+        set.rows[i] = plan[i].rows;
+        set.slices[i] = plan[i].slices;
+        set.wg0[i] = wgs;
+        set.tick0[i] = tiles_all;
+        wgs += tiles * plan[i].slices;
+        tiles_all += tiles;
+        partial_floats += (size_t)plan[i].slices * M * N[i];
+        split = split || plan[i].slices > 1;
+    }
+    set.wg0[count] = wgs;
+    uint32_t* tickets = nullptr;
+    int stride = 0;
+    if (split) {
+        stride = ticket_stride(tiles_all);
+        if (stride < 2) {
+            *status = fail(ACCEL_E_INVALID,
+                           "decode product: %d tiles need more tickets than the workspace holds",
+                           tiles_all);
+            return hipSuccess;
+        }
+        void* ws = workspace(d, partial_floats * sizeof(float), status);
+        if (!ws) return hipSuccess;
+        tickets = static_cast<uint32_t*>(ws);
+        float* p = reinterpret_cast<float*>(static_cast<char*>(ws) + kWorkspaceCounterBytes);
+        for (int i = 0; i < count; i++) {
+            set.partial[i] = p;
+            p += (size_t)plan[i].slices * M * N[i];
+        }
+    }
+    hipLaunchKernelGGL((int4_decode_mfma_set_kernel<G, 8>), dim3(wgs), dim3(64 * 8), 0, st, a,
+                       set, tickets, stride, M, K);
     return hipGetLastError();
 }
 
@@ -1270,6 +1374,43 @@ hipError_t launch_matvec_f32_f16(Device* d, hipStream_t st, const float* a, cons
     hipLaunchKernelGGL(matvec_f16_generic_kernel, dim3((N + 255) / 256), dim3(256), 0, st, a, w,
                        out, K, N);
     return hipGetLastError();
+}
+
+bool int4_matmul_set_supported(const float* a, const Int4Planes* w, const int* N, int count,
+                               int M, int K) {
+    if (count < 1 || count > kMaxSet || M < 3 || M > 16 || K % 32 != 0 ||
+        (reinterpret_cast<uintptr_t>(a) & 15) != 0)
+        return false;
+    for (int i = 0; i < count; i++)
+        if (!int4_decode_f32_supported(M, K, N[i], w[i].codes) || N[i] >= (1 << 27))
+            return false;
+    return true;
+}
+
+hipError_t launch_int4_matmul_set(Device* d, hipStream_t st, const float* a, const Int4Planes* w,
+                                  float* const* out, const int* N, int count, int M, int K,
+                                  int* status) {
+    *status = ACCEL_OK;
+    // each matrix with the plan its own launch would take; one launch per G
+    Int4Planes wg[2][kMaxSet];
+    float* og[2][kMaxSet];
+    int ng[2][kMaxSet], cnt[2] = {0, 0};
+    MfPlan pg[2][kMaxSet];
+    for (int i = 0; i < count; i++) {
+        const bool planes_4b = ((reinterpret_cast<uintptr_t>(w[i].scales) |
+                                 reinterpret_cast<uintptr_t>(w[i].zeros)) & 3) == 0;
+        const MfPlan p = plan_decode_mfma(d, M, K, N[i], planes_4b);
+        const int g = p.groups == 2 ? 0 : 1;
+        wg[g][cnt[g]] = w[i];
+        og[g][cnt[g]] = out[i];
+        pg[g][cnt[g]] = p;
+        ng[g][cnt[g]++] = N[i];
+    }
+    hipError_t e = hipSuccess;
+    if (cnt[0]) e = launch_mfma_set<2>(d, st, a, wg[0], og[0], ng[0], pg[0], cnt[0], M, K, status);
+    if (e != hipSuccess || *status != ACCEL_OK) return e;
+    if (cnt[1]) e = launch_mfma_set<1>(d, st, a, wg[1], og[1], ng[1], pg[1], cnt[1], M, K, status);
+    return e;
 }
 
 bool int4_matvec_set_supported(const Int4Planes* w, const int* N, int count, int K) {

@@ -225,6 +225,73 @@ ACCEL_API int accel_int4_matvec_set(int dev, void* stream, const accel_tensor_t*
     return finish(d, e, status, "Int4MatVecSet launch");
 }
 
+// Int4MatMul over several matrices that share one f32 activation block
+// [M, K]: one launch per tile width where they all take the matrix-core
+// decode kernel (3 <= M <= 16), each with its own launch's plan, so each
+// result is its own Int4MatMul's; else one Int4MatMul each.
+ACCEL_API int accel_int4_matmul_set(int dev, void* stream, const accel_tensor_t* a,
+                                    const accel_int4_t* w, accel_tensor_t* out, int count) {
+    clear_error();
+    const char* op = "Int4MatMulSet";
+    char buf[320];
+    if (count < 1 || count > 4 || !w || !out) {
+        snprintf(buf, sizeof buf, "%d matrices; a set holds one to four", count);
+        return refuse(op, buf);
+    }
+    if (!valid_tensor(a) || !a->data) return refuse(op, "the activations are missing");
+    if (a->dtype != ACCEL_F32 || a->rank != 2) {
+        snprintf(buf, sizeof buf, "activations are %s %s; a set takes f32 rows [M, K]",
+                 dtype_name(a->dtype), shape_str(a).c_str());
+        return refuse(op, buf);
+    }
+    const int64_t m = a->shape[0], k = a->shape[1];
+    int N[4];
+    Int4Planes p[4];
+    float* o[4];
+    for (int i = 0; i < count; i++) {
+        std::string why = check_int4(&w[i], "the weight matrix");
+        if (!why.empty()) return refuse(op, why);
+        if (k == 0 || w[i].weights % k != 0) {
+            snprintf(buf, sizeof buf,
+                     "activations are %lld wide and matrix %d holds %lld weights; the matrix is "
+                     "[K, N] with K the activation width, so the second is a multiple of the "
+                     "first",
+                     (long long)k, i, (long long)w[i].weights);
+            return refuse(op, buf);
+        }
+        const int64_t n = w[i].weights / k;
+        if (m > INT32_MAX || k > INT32_MAX || n > INT32_MAX)
+            return refuse(op, "the product is larger than this backend's 32-bit extents");
+        const int rc = check_out(op, &out[i], ACCEL_F32, m, n, false);
+        if (rc != ACCEL_OK) return rc;
+        N[i] = (int)n;
+        p[i] = planes(&w[i]);
+        o[i] = static_cast<float*>(out[i].data);
+    }
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    hipStream_t st = (hipStream_t)stream;
+    const float* af = static_cast<const float*>(a->data);
+    if (m == 1 && int4_matvec_set_supported(p, N, count, (int)k)) {
+        int status = begin_submission(d);
+        if (status != ACCEL_OK) return status;
+        hipError_t e = launch_int4_matvec_set(d, st, af, p, o, N, count, (int)k, &status);
+        return finish(d, e, status, "Int4MatMulSet launch");
+    }
+    if (int4_matmul_set_supported(af, p, N, count, (int)m, (int)k)) {
+        int status = begin_submission(d);
+        if (status != ACCEL_OK) return status;
+        hipError_t e = launch_int4_matmul_set(d, st, af, p, o, N, count, (int)m, (int)k, &status);
+        return finish(d, e, status, "Int4MatMulSet launch");
+    }
+    for (int i = 0; i < count; i++) {
+        const int rc = run_int4_product(d, st, a->data, ACCEL_F32, &w[i], out[i].data, (int)m,
+                                        (int)k, N[i]);
+        if (rc != ACCEL_OK) return rc;
+    }
+    return ACCEL_OK;
+}
+
 static int check_matvec(const char* op, const accel_tensor_t* a, const accel_int4_t* w,
                         const accel_tensor_t* out, int64_t* K, int64_t* N) {
     std::string why = check_int4(w, "the weight matrix");

@@ -211,11 +211,12 @@ def bench_moe(dev, stream, steps=20):
 _LAYER_PLANES = {}
 
 
-def bench_layer_chain(dev, stream, batch, steps=100):
+def bench_layer_chain(dev, stream, batch, steps=100, merged=False):
     """Config 5: one Llama-3-8B-shaped decoder layer's seven int4 products
     as a decode step: q,k,v <- x; o <- q; gate,up <- o; down <- gate*up
     (the gate*up product is the caller's; the step times the seven
-    products, chained on one stream)."""
+    products, chained on one stream).  merged: q, k, v and gate, up each as
+    one set (four launches, the same results bit for bit)."""
     import accel_amd
     from accel_amd import F32, workloads
     shapes = workloads.LAYER_SHAPES  # name -> (K, N)
@@ -242,13 +243,18 @@ def bench_layer_chain(dev, stream, batch, steps=100):
         else:
             dev.Int4MatVec(a, w, o, stream)
 
+    def ops(a, names):
+        if merged:
+            fn = dev.Int4MatVecSet if batch == 1 else dev.Int4MatMulSet
+            fn(a, [ws[n] for n in names], [bufs[n] for n in names], stream)
+        else:
+            for n in names:
+                op(a, ws[n], bufs[n])
+
     def step(i):
-        op(xin, ws["q"], bufs["q"])
-        op(xin, ws["k"], bufs["k"])
-        op(xin, ws["v"], bufs["v"])
+        ops(xin, ("q", "k", "v"))
         op(bufs["q"], ws["o"], bufs["o"])
-        op(bufs["o"], ws["gate"], bufs["gate"])
-        op(bufs["o"], ws["up"], bufs["up"])
+        ops(bufs["o"], ("gate", "up"))
         op(inter, ws["down"], bufs["down"])
 
     step(0)
@@ -262,7 +268,7 @@ def bench_layer_chain(dev, stream, batch, steps=100):
         b.free()
     return dict(us_per_step=round(ms * 1e3, 2),
                 gbs=round(total_bytes / (ms * 1e-3) / 1e9, 1),
-                weight_bytes=total_bytes, batch=batch)
+                weight_bytes=total_bytes, batch=batch, launches=4 if merged else 7)
 
 
 def bench_matvec_f16(dev, stream, K=4096, N=4096, steps=200):
@@ -426,8 +432,8 @@ def bench_repack(dev, stream, fmt=1, K=4096, N=14336, G=128, calls=20):
 def bench_decode_step(dev, stream, batch, steps=100, merged=True):
     """Config 5's layer as a whole decode step with its on-device neighbours:
     h = RMSNorm(x); q,k,v <- h; o <- q; h2 = RMSNorm(o); gate,up <- h2;
-    a = SwiGLU(gate, up); down <- a.  Ten launches a step (seven at batch 1,
-    where q, k, v and gate, up each run as one launch), captured in one
+    a = SwiGLU(gate, up); down <- a.  Seven launches a step (q, k, v and
+    gate, up each run as one set; ten with merged=False), captured in one
     HIP graph and replayed (attention itself is outside the int4 path)."""
     from accel_amd import F32, workloads
     shapes = workloads.LAYER_SHAPES
@@ -458,9 +464,11 @@ def bench_decode_step(dev, stream, batch, steps=100, merged=True):
             dev.Int4MatVec(a, w, o, stream)
 
     def ops(a, names):
-        # at batch 1 the products that share an input run as one launch
-        if batch == 1 and merged:
+        # products that share an input run as one launch per tile width
+        if merged and batch == 1:
             dev.Int4MatVecSet(a, [ws[n] for n in names], [bufs[n] for n in names], stream)
+        elif merged:
+            dev.Int4MatMulSet(a, [ws[n] for n in names], [bufs[n] for n in names], stream)
         else:
             for n in names:
                 op(a, ws[n], bufs[n])
@@ -486,7 +494,7 @@ def bench_decode_step(dev, stream, batch, steps=100, merged=True):
     return dict(us_per_step=round(ms * 1e3, 2),
                 gbs=round(total_bytes / (ms * 1e-3) / 1e9, 1),
                 weight_bytes=total_bytes, batch=batch,
-                launches=7 if (batch == 1 and merged) else 10)
+                launches=7 if merged else 10)
 
 
 def cpu_baseline(L, seconds):
@@ -635,6 +643,8 @@ def main():
             extra["moe_grouped_bf16"] = bench_moe(dev, stream)
             extra["layer_chain_b1"] = bench_layer_chain(dev, stream, 1)
             extra["layer_chain_b8"] = bench_layer_chain(dev, stream, 8)
+            extra["layer_chain_b1_sets"] = bench_layer_chain(dev, stream, 1, merged=True)
+            extra["layer_chain_b8_sets"] = bench_layer_chain(dev, stream, 8, merged=True)
             extra["matvec_f32_f16"] = bench_matvec_f16(dev, stream)
             extra["int8_gemv_4096"] = bench_int8(dev, stream, 1)
             extra["int8_m8_4096"] = bench_int8(dev, stream, 8)
@@ -649,6 +659,7 @@ def main():
             extra["decode_step_b1"] = bench_decode_step(dev, stream, 1)
             extra["decode_step_b1_unmerged"] = bench_decode_step(dev, stream, 1, merged=False)
             extra["decode_step_b8"] = bench_decode_step(dev, stream, 8)
+            extra["decode_step_b8_unmerged"] = bench_decode_step(dev, stream, 8, merged=False)
         line["extra"] = extra
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(L, args.cpu_seconds)

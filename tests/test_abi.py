@@ -298,6 +298,31 @@ def test_int4_matvec_set_refusals():
     assert rc == accel_amd.E_NO_DEVICE
 
 
+def test_int4_matmul_set_refusals():
+    lib = accel_amd.lib()
+    K, N = 256, 128
+
+    def call(a, ws, outs, count):
+        wd = (accel_amd.Int4Desc * max(len(ws), 1))(*ws)
+        od = (accel_amd.Tensor * max(len(outs), 1))(*outs)
+        rc = lib.accel_int4_matmul_set(0, None, ctypes.byref(a), wd, od, count)
+        return rc, accel_amd.last_error()
+
+    a = t([8, K], F32)
+    rc, msg = call(a, [w4(K * N)], [t([8, N], F32)], 5)
+    assert rc == accel_amd.E_INVALID and "a set holds one to four" in msg
+    rc, msg = call(t([8, K], BF16), [w4(K * N)], [t([8, N], F32)], 1)
+    assert rc == accel_amd.E_INVALID and "a set takes f32 rows [M, K]" in msg
+    rc, msg = call(t([K], F32), [w4(K * N)], [t([N], F32)], 1)
+    assert rc == accel_amd.E_INVALID and "a set takes f32 rows [M, K]" in msg
+    rc, msg = call(a, [w4(K * N), w4(K * N + 8)], [t([8, N], F32)] * 2, 2)
+    assert rc == accel_amd.E_INVALID and "matrix 1 holds" in msg
+    rc, msg = call(a, [w4(K * N)], [t([8, N + 1], F32)], 1)
+    assert rc == accel_amd.E_INVALID and "the product is [8 128]" in msg
+    rc, msg = call(a, [w4(K * N), w4(K * 64)], [t([8, N], F32), t([8, 64], F32)], 2)
+    assert rc == accel_amd.E_NO_DEVICE
+
+
 def test_quant_matmul_refusals():   # tensor/quantized.go:32-110
     I8 = accel_amd.I8
     lib = accel_amd.lib()

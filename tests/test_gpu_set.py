@@ -48,3 +48,37 @@ def test_set_equals_separate_matvecs(dev, K, Ns):
         b.free()
     for w in ws:
         w.free()
+
+
+@pytest.mark.parametrize("M,K,Ns", [
+    (8, 4096, [4096, 1024, 1024]),    # q, k, v at batch 8: matrix-core decode
+    (8, 4096, [14336, 14336]),        # gate, up
+    (5, 1024, [384, 256, 512]),       # one- and two-group tiles: two launches
+    (16, 2048, [1024, 2048]),
+    (3, 512, [128]),
+    (2, 1024, [256, 512]),            # two rows: one Int4MatMul each
+    (1, 4096, [4096, 1024]),          # one row: the vector set
+    (4, 100, [256, 128]),             # K % 32 != 0: one Int4MatMul each
+])
+def test_matmul_set_equals_separate_matmuls(dev, M, K, Ns):
+    rng = np.random.Generator(np.random.PCG64(M * 1000 + K + sum(Ns)))
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    xb = dev.upload(x)
+    ws, planes = zip(*[_weights(dev, K, N, rng) for N in Ns])
+    singles, outs = [], [dev.alloc((M, N), F32) for N in Ns]
+    for w, N in zip(ws, Ns):
+        ob = dev.alloc((M, N), F32)
+        dev.Int4MatMul(xb, w, ob)
+        singles.append(ob.numpy().copy())
+        ob.free()
+    for rep in range(2):
+        dev.Int4MatMulSet(xb, list(ws), outs)
+        for o, want in zip(outs, singles):
+            assert np.array_equal(o.numpy().view(np.uint32), want.view(np.uint32))
+    p, s, z = planes[-1]
+    assert rel_l2(outs[-1].numpy(),
+                  oracle.quant_matmul_int4(x, p, s, z, M, K, Ns[-1])) <= 1e-5
+    for b in list(outs) + [xb]:
+        b.free()
+    for w in ws:
+        w.free()
