@@ -262,3 +262,21 @@ def test_info_reports_gfx950(dev):
     info = dev.info()
     assert info.arch.decode().startswith("gfx950")
     assert info.compute_units >= 200 and info.wavefront == 64
+
+
+@pytest.mark.parametrize("M,K,N", [(5, 200, 20), (5, 4096, 4096), (12, 1024, 384)])
+def test_matmul_equals_matvec_row_for_row(dev, M, K, N):
+    # TestAnInt4MatMulEqualsTheMatVecRowForRow (tensor/int4_test.go:275-354):
+    # w uniform in [-1, 1), a[i] = sin(0.23 i); the batched product and the
+    # row product sum in different orders (here on different kernels at the
+    # larger shapes), so the bound is the reduction budget mag * 1e-6
+    rng = np.random.default_rng(53)
+    w = (rng.random(K * N) * 2 - 1).astype(np.float32)
+    a = np.sin(np.arange(M * K, dtype=np.float64) * 0.23).astype(np.float32)
+    p, s, z = oracle.int4_quantize(w)
+    batched = run_matmul(dev, a, p, s, z, M, K, N)
+    wabs = np.abs(w.astype(np.float64)).reshape(K, N)
+    for m in range(M):
+        row = run_matvec(dev, a[m * K:(m + 1) * K], p, s, z, K, N)
+        mag = np.abs(a[m * K:(m + 1) * K].astype(np.float64)) @ wabs
+        assert np.all(np.abs(batched[m].astype(np.float64) - row) <= mag * 1e-6), m
