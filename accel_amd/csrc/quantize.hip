@@ -51,6 +51,41 @@ __device__ float widen_f16(uint16_t h) {
     return __uint_as_float(sign | ((uint32_t)(113 - shift) << 23) | (m << 13));
 }
 
+// The code of one weight: RoundToEven(f64(v) / f64(s) + f64(z)) clamped to
+// [0, 15], a NaN giving 0 (quant/int4.go:121-129).  Most weights are settled
+// in f32: e = fma(v, rs, z) with rs = 1/s correctly rounded is within
+// 2^-23 (|v/s| + |z|) of the exact sum, and the f64 result within
+// 2^-52 (|v/s| + |z|), so when e lies farther than `slack` (a group-wide
+// bound 4x that) from every half-integer, both round to the same integer.
+// The rest -- near a tie, or with a NaN, an infinity or a slack of 1/2 or
+// more, all of which fail the comparison -- take the f64 division.
+struct CodeRule {
+    float s, z, rs, slack;
+};
+
+__device__ __forceinline__ CodeRule code_rule(float s16, float z16, float least, float most) {
+    CodeRule r;
+    r.s = s16;
+    r.z = z16;
+    r.rs = __fdiv_rn(1.0f, s16);
+    r.slack = fmaf(fmaxf(fabsf(least), fabsf(most)), r.rs, fabsf(z16)) * 0x1p-20f;
+    if (least != least || most != most) r.slack = __uint_as_float(0x7fc00000u);
+    return r;
+}
+
+__device__ __forceinline__ uint32_t code_of_weight(float v, const CodeRule& r) {
+    const float e = fmaf(v, r.rs, r.z);
+    const float m = rintf(e);
+    double q;
+    if (fabsf(e - m) < 0.5f - r.slack) {
+        q = (double)m;
+    } else {
+        q = rint(__ddiv_rn((double)v, (double)r.s) + (double)r.z);
+        if (q != q) return 0u;
+    }
+    return q > 15.0 ? 15u : (q < 0.0 ? 0u : (uint32_t)q);
+}
+
 // (value, index) candidates; `ok` is false for a NaN that cannot win.
 struct Cand {
     float v;
@@ -118,11 +153,10 @@ __device__ __forceinline__ void quantize_group(float v0, float v1, int lane, int
             coded = true;
         }
     }
+    const CodeRule rule = code_rule(s16, z16, least, most);
     auto code_of = [&](float v, bool in) -> uint32_t {
         if (!coded || !in) return 0u;
-        const double q = rint(__ddiv_rn((double)v, (double)s16) + (double)z16);
-        if (q != q) return 0u;
-        return q > 15.0 ? 15u : (q < 0.0 ? 0u : (uint32_t)q);
+        return code_of_weight(v, rule);
     };
     // Pack: lane's weight lo+lane is nibble lane%8 of word lane/8; OR across
     // each run of eight lanes.
@@ -326,7 +360,7 @@ __global__ __launch_bounds__(256) void int4_repack_rows_kernel(accel_foreign_int
         for (int j = 0; j < 16; j += 4) *reinterpret_cast<u32x4_q*>(out + j) = (u32x4_q){0, 0, 0, 0};
         return;
     }
-    const double sd = (double)s16, zd = (double)z16;
+    const CodeRule rule = code_rule(s16, z16, least, most);
 #pragma unroll 1
     for (int j = 0; j < 16; j += 4) {
         u32x4_q words;
@@ -335,11 +369,7 @@ __global__ __launch_bounds__(256) void int4_repack_rows_kernel(accel_foreign_int
             foreign_eight<FMT>(f, k, n0 + 8 * (j + jj), pg, w);
             uint32_t word = 0;
 #pragma unroll
-            for (int c = 0; c < 8; c++) {
-                const double q = rint(__ddiv_rn((double)w[c], sd) + zd);
-                const uint32_t code = q != q ? 0u : (q > 15.0 ? 15u : (q < 0.0 ? 0u : (uint32_t)q));
-                word |= code << (4 * c);
-            }
+            for (int c = 0; c < 8; c++) word |= code_of_weight(w[c], rule) << (4 * c);
             words[jj] = word;
         }
         *reinterpret_cast<u32x4_q*>(out + j) = words;

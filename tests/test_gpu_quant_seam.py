@@ -26,7 +26,8 @@ def device_quantize(dev, w):
 
 
 @pytest.mark.parametrize("kind", ["normal", "far", "tiny", "denorm", "huge", "ties",
-                                  "signed_zero", "nan_inf", "nan_first"])
+                                  "signed_zero", "nan_inf", "nan_first", "halves",
+                                  "near_halves"])
 @pytest.mark.parametrize("n", [1, 9, 128, 129, 1000, 8192 + 5])
 def test_device_packer_is_bit_exact(dev, kind, n):
     rng = np.random.default_rng(n + len(kind))
@@ -42,6 +43,12 @@ def test_device_packer_is_bit_exact(dev, kind, n):
                                     np.where(rng.random(n) < 0.03, np.inf,
                                              rng.standard_normal(n))),
         "nan_first": lambda: np.where(np.arange(n) % 128 == 0, np.nan, rng.standard_normal(n)),
+        # groups spanning 0..15 quantize with s = 1, z = 0: every weight an
+        # exact tie of the round-half-to-even rule
+        "halves": lambda: rng.integers(0, 31, n) / 2.0,
+        # and weights a few ulps to 2^-10 off those ties
+        "near_halves": lambda: (rng.integers(0, 31, n) / 2.0) *
+        (1 + rng.choice([-1.0, 1.0], n) * 2.0 ** -rng.integers(10, 24, n)),
     }
     w = np.asarray(gens[kind](), np.float32)
     got = device_quantize(dev, w)
