@@ -73,17 +73,58 @@ __device__ __forceinline__ CodeRule code_rule(float s16, float z16, float least,
     return r;
 }
 
-__device__ __forceinline__ uint32_t code_of_weight(float v, const CodeRule& r) {
+__device__ __forceinline__ uint32_t code_exact(float v, const CodeRule& r) {
+    const double q = rint(__ddiv_rn((double)v, (double)r.s) + (double)r.z);
+    if (q != q) return 0u;
+    return q > 15.0 ? 15u : (q < 0.0 ? 0u : (uint32_t)q);
+}
+
+// Sets bit 0 of *open when the f32 estimate leaves the code to the f64 rule.
+__device__ __forceinline__ uint32_t code_estimate(float v, const CodeRule& r, uint32_t* open) {
     const float e = fmaf(v, r.rs, r.z);
     const float m = rintf(e);
-    double q;
-    if (fabsf(e - m) < 0.5f - r.slack) {
-        q = (double)m;
-    } else {
-        q = rint(__ddiv_rn((double)v, (double)r.s) + (double)r.z);
-        if (q != q) return 0u;
+    *open = fabsf(e - m) < 0.5f - r.slack ? 0u : 1u;
+    return (uint32_t)fminf(fmaxf(m, 0.0f), 15.0f);
+}
+
+__device__ __forceinline__ uint32_t code_of_weight(float v, const CodeRule& r) {
+    uint32_t open;
+    const uint32_t code = code_estimate(v, r, &open);
+    return open ? code_exact(v, r) : code;
+}
+
+// Eight codes estimated in f32 as one word, nibble c for w[c]; bit 8 jj + c
+// of *open set for each code left to the f64 rule.
+__device__ __forceinline__ uint32_t code_word_estimate(const float* w, const CodeRule& r,
+                                                       uint32_t* open, int jj = 0) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+        uint32_t o;
+        word |= code_estimate(w[c], r, &o) << (4 * c);
+        *open |= o << (8 * jj + c);
     }
-    return q > 15.0 ? 15u : (q < 0.0 ? 0u : (uint32_t)q);
+    return word;
+}
+
+// Eight codes as one word, nibble c for w[c]: all estimated in f32, then the
+// f64 rule for the open ones behind one branch that waves skip when no lane
+// has any.
+__device__ __forceinline__ uint32_t code_word(const float* w, const CodeRule& r) {
+    uint32_t word = 0, open = 0;
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+        uint32_t o;
+        word |= code_estimate(w[c], r, &o) << (4 * c);
+        open |= o << c;
+    }
+    if (open) {
+#pragma unroll
+        for (int c = 0; c < 8; c++)
+            if ((open >> c) & 1u)
+                word = (word & ~(15u << (4 * c))) | (code_exact(w[c], r) << (4 * c));
+    }
+    return word;
 }
 
 // (value, index) candidates; `ok` is false for a NaN that cannot win.
@@ -267,13 +308,43 @@ __global__ __launch_bounds__(256) void int4_repack_kernel(accel_foreign_int4_t f
     quantize_group(v0, v1, lane, g, n, packed, scales, zeros);
 }
 
-// Rows that hold whole groups (N % 128 == 0): one lane per reference group.
-// The lane walks its 128 weights in order twice, recomputing each from the
-// published planes -- first the reference's sequential scan for the range,
-// then the codes -- so the group's range needs no cross-lane reduction and
-// its scale and zero are worked out once per lane, 64 groups to a wave.
-// Eight weights at a time: one code word (AWQ; eight for GPTQ, which packs
-// rows), one zero word and sixteen bytes of scales.
+// Rows that hold whole groups (N % 128 == 0): one lane per reference group,
+// 64 groups to a wave, each lane running the reference's two walks over its
+// 128 weights -- the sequential scan for the range, then the codes -- so the
+// range needs no cross-lane reduction and the scale and zero are worked out
+// once per lane.  AWQ: the lane loads its group's planes at once with 16-byte
+// loads (sixteen code words, sixteen zero words, 256 bytes of scales) and
+// dequantizes the 128 weights into registers; lanes run along a row of
+// groups, so a wave's loads and its 64-byte stores of codes are contiguous.
+// Every row offset is a multiple of sixteen bytes when N % 128 == 0 and the
+// planes start 16-byte aligned.
+typedef uint16_t u16x8_q __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ void awq_group_weights(const accel_foreign_int4_t& f, uint32_t k,
+                                                  int64_t n0, int64_t pg, float* w) {
+    const int64_t wpr = f.N >> 3;
+    const u32x4_q* zrow = reinterpret_cast<const u32x4_q*>(f.qzeros + pg * wpr + (n0 >> 3));
+    const u16x8_q* srow = reinterpret_cast<const u16x8_q*>(f.scales + pg * f.N + n0);
+    const u32x4_q* qrow = reinterpret_cast<const u32x4_q*>(f.qweight + (int64_t)k * wpr + (n0 >> 3));
+#pragma unroll
+    for (int j4 = 0; j4 < 4; j4++) {
+        const u32x4_q zv = zrow[j4], qv = qrow[j4];
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) {
+            const u16x8_q sc = srow[4 * j4 + jj];
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                // column c of a word sits in nibble {0,4,1,5,2,6,3,7}[c]
+                const int sh = 4 * ((c >> 1) + ((c & 1) << 2));
+                const int q = (int)((qv[jj] >> sh) & 15u), z = (int)((zv[jj] >> sh) & 15u);
+                w[8 * (4 * j4 + jj) + c] = (float)(q - z) * widen_f16(sc[c]);
+            }
+        }
+    }
+}
+
+// GPTQ packs eight input rows a word, so a group's 128 codes are spread over
+// 128 words: too many to hold, they are walked eight weights at a time, twice.
 template <int FMT>
 __device__ __forceinline__ void foreign_eight(const accel_foreign_int4_t& f, uint32_t k,
                                               int64_t n, int64_t pg, float* w) {
@@ -302,10 +373,9 @@ __device__ __forceinline__ void foreign_eight(const accel_foreign_int4_t& f, uin
     }
 }
 
-// Lanes walk the groups down a column of groups (lane i takes row k0 + i of
-// the same 128 columns): rows of one published group share its scales and
-// zeros, which are most of the bytes read, and in GPTQ eight consecutive rows
-// share each code word.
+// GPTQ lanes walk the groups down a column of groups (lane i takes row k0 + i
+// of the same 128 columns): rows of one published group share its scales and
+// zeros, and eight rows share a code word, so a wave's loads coincide.
 template <int FMT>
 __global__ __launch_bounds__(256) void int4_repack_rows_kernel(accel_foreign_int4_t f,
                                                                int64_t groups, int gpr,
@@ -315,24 +385,36 @@ __global__ __launch_bounds__(256) void int4_repack_rows_kernel(accel_foreign_int
     const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (t >= groups) return;
     const uint32_t ti = (uint32_t)t;
-    const uint32_t cb = ti / (uint32_t)f.K;
-    const uint32_t k = ti - cb * (uint32_t)f.K;
+    constexpr bool kAwq = FMT == ACCEL_QFMT_AWQ;
+    const uint32_t cb = kAwq ? ti % (uint32_t)gpr : ti / (uint32_t)f.K;
+    const uint32_t k = kAwq ? ti / (uint32_t)gpr : ti - cb * (uint32_t)f.K;
     const int64_t g = (int64_t)k * gpr + cb;
     const int64_t n0 = (int64_t)cb * 128;
     const int64_t pg = foreign_group(f, k, bad);
 
     // the reference's scan: from the first weight, replacing on a strict
     // comparison (a NaN first weight sticks, later NaNs are skipped)
-    float w[8];
-    foreign_eight<FMT>(f, k, n0, pg, w);
-    float least = w[0], most = w[0];
-#pragma unroll 1
-    for (int j = 0; j < 16; j++) {
-        if (j) foreign_eight<FMT>(f, k, n0 + 8 * j, pg, w);
+    float w[kAwq ? 128 : 8];
+    float least, most;
+    if constexpr (kAwq) {
+        awq_group_weights(f, k, n0, pg, w);
+        least = most = w[0];
 #pragma unroll
-        for (int c = 0; c < 8; c++) {
-            if (w[c] < least) least = w[c];
-            if (w[c] > most) most = w[c];
+        for (int i = 1; i < 128; i++) {
+            if (w[i] < least) least = w[i];
+            if (w[i] > most) most = w[i];
+        }
+    } else {
+        foreign_eight<FMT>(f, k, n0, pg, w);
+        least = most = w[0];
+#pragma unroll 1
+        for (int j = 0; j < 16; j++) {
+            if (j) foreign_eight<FMT>(f, k, n0 + 8 * j, pg, w);
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                if (w[c] < least) least = w[c];
+                if (w[c] > most) most = w[c];
+            }
         }
     }
     uint16_t s_bits, z_bits;
@@ -354,25 +436,44 @@ __global__ __launch_bounds__(256) void int4_repack_rows_kernel(accel_foreign_int
     }
     scales[g] = s_bits;
     zeros[g] = z_bits;
-    uint32_t* out = packed + g * 16;
+    u32x4_q* out = reinterpret_cast<u32x4_q*>(packed + g * 16);
     if (!coded) {
 #pragma unroll
-        for (int j = 0; j < 16; j += 4) *reinterpret_cast<u32x4_q*>(out + j) = (u32x4_q){0, 0, 0, 0};
+        for (int j4 = 0; j4 < 4; j4++) out[j4] = (u32x4_q){0, 0, 0, 0};
         return;
     }
     const CodeRule rule = code_rule(s16, z16, least, most);
-#pragma unroll 1
-    for (int j = 0; j < 16; j += 4) {
-        u32x4_q words;
+    if constexpr (kAwq) {
 #pragma unroll
-        for (int jj = 0; jj < 4; jj++) {
-            foreign_eight<FMT>(f, k, n0 + 8 * (j + jj), pg, w);
-            uint32_t word = 0;
+        for (int j4 = 0; j4 < 4; j4++) {
+            u32x4_q words;
+            uint32_t open = 0;
 #pragma unroll
-            for (int c = 0; c < 8; c++) word |= code_of_weight(w[c], rule) << (4 * c);
-            words[jj] = word;
+            for (int jj = 0; jj < 4; jj++) words[jj] = code_word_estimate(w + 32 * j4 + 8 * jj,
+                                                                      rule, &open, jj);
+            // the f64 rule for the weights the estimate left open, each
+            // dequantized again from the planes: one short loop, not 128
+            // inlined divisions
+            while (open) {
+                const int b = __builtin_ctz(open);
+                open &= open - 1u;
+                const int i = 32 * j4 + b, sh = 4 * (b & 7);
+                const uint32_t code = code_exact(foreign_weight(f, k, n0 + i, pg), rule);
+                words[b >> 3] = (words[b >> 3] & ~(15u << sh)) | (code << sh);
+            }
+            out[j4] = words;
         }
-        *reinterpret_cast<u32x4_q*>(out + j) = words;
+    } else {
+#pragma unroll 1
+        for (int j4 = 0; j4 < 4; j4++) {
+            u32x4_q words;
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) {
+                foreign_eight<FMT>(f, k, n0 + 8 * (4 * j4 + jj), pg, w);
+                words[jj] = code_word(w, rule);
+            }
+            out[j4] = words;
+        }
     }
 }
 
@@ -397,6 +498,8 @@ hipError_t launch_int4_repack(hipStream_t st, const accel_foreign_int4_t& f, uin
     // groups and the group index fits 32 bits
     const int gpr = (f.N % 128 == 0 && groups < (int64_t(1) << 32)) ? (int)(f.N / 128) : 0;
     const bool aligned = ((reinterpret_cast<uintptr_t>(f.scales) |
+                           reinterpret_cast<uintptr_t>(f.qweight) |
+                           reinterpret_cast<uintptr_t>(f.qzeros) |
                            reinterpret_cast<uintptr_t>(codes)) & 15) == 0;
     if (gpr && aligned) {
         const int64_t lane_blocks = (groups + 255) / 256;

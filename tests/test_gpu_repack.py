@@ -53,6 +53,28 @@ def test_device_repack_is_the_host_repack(dev, fmt, K, N, G, act):
     w.free()
 
 
+@pytest.mark.parametrize("fmt", [AWQ, GPTQ2])
+def test_device_repack_at_rounding_ties(dev, fmt):
+    """Published scales alternating 1 and 1/2 by column with zero points 0 and
+    every row of 128 columns spanning codes 0..15: each reference group comes
+    out with scale 1 and zero 0, so its odd codes in the half-scale columns
+    sit exactly on a tie of the round-half-to-even rule."""
+    K, N, G = 256, 1024, 128
+    rng = np.random.default_rng(fmt)
+    q = rng.integers(0, 16, (K, N), dtype=np.int64)
+    q[:, 0::128], q[:, 2::128] = 15, 0
+    z = np.zeros((K // G, N), np.int64)
+    s = oracle.to_f16(np.tile(np.float32([1.0, 0.5]), (K // G, N // 2))).reshape(K // G, N)
+    qw, qz = foreign_np.pack_awq(q, z) if fmt == AWQ else foreign_np.pack_gptq(q, z, True)
+    lay = accel_amd.ForeignInt4(fmt, G, K, N, qw, qz, s, None)
+    want = accel_amd.int4_repack_host(lay)
+    assert np.all(want[1] == 0x3C00)   # every reference scale is 1
+    w = dev.Int4Repack(lay)
+    for a, b in zip((w.codes.numpy(), w.scales.numpy(), w.zeros.numpy()), want):
+        assert np.array_equal(a.reshape(-1), b)
+    w.free()
+
+
 @pytest.mark.parametrize("fmt,M,K,N,G", [(AWQ, 1, 4096, 4096, 128), (GPTQ, 4, 1024, 512, 32)])
 def test_repacked_weights_multiply_like_the_oracles(dev, fmt, M, K, N, G):
     lay = _layer(fmt, K, N, G, seed=M + K)
