@@ -121,6 +121,9 @@ SIGNATURES = {
     "accel_hip_capture_end": ([_i, _vp, _P(_vp)], _i),
     "accel_hip_exec_launch": ([_i, _vp, _vp], _i),
     "accel_hip_exec_destroy": ([_i, _vp], _i),
+    "accel_hip_set_wait_limit": ([_i, ctypes.c_int32], _i),
+    "accel_hip_set_xcd_local": ([_i, _i], _i),
+    "accel_hip_workspace_generation": ([_i, _P(ctypes.c_uint64), _P(ctypes.c_int32)], _i),
     "accel_hip_supports_kernel": ([ctypes.c_char_p], _i),
     "accel_hip_dispatch": ([_i, _vp, ctypes.c_char_p, _P(_vp), _P(ctypes.c_uint64),
                             ctypes.c_int32, _vp, _sz, _P(ctypes.c_uint32)], _i),
@@ -237,6 +240,26 @@ class ForeignInt4:
         if self.g_idx is not None:
             self.g_idx = np.ascontiguousarray(self.g_idx, np.int32)
 
+    def check_lengths(self) -> None:
+        """Raises ValueError unless the planes hold what a K x N layer with
+        this group size needs.  The repack (host and device) indexes the planes
+        from K, N and the group count alone, so this runs before any pointer
+        to them crosses the ABI."""
+        K, N, G = int(self.K), int(self.N), int(self.group_size)
+        if K <= 0 or N <= 0 or G <= 0:
+            raise ValueError(f"layer dims K={K} N={N} group_size={G} must be positive")
+        if N % 8 or (self.format != QFMT_AWQ and K % 8):
+            raise ValueError(f"layer dims K={K} N={N} do not pack eight codes a word")
+        groups = -(-K // G)
+        want = {"qweight": K * N // 8, "qzeros": groups * N // 8, "scales": groups * N}
+        for name, n in want.items():
+            got = getattr(self, name).size
+            if got != n:
+                raise ValueError(f"{name} holds {got} elements; a {K}x{N} layer with "
+                                 f"{G}-row groups needs {n}")
+        if self.g_idx is not None and self.g_idx.size != K:
+            raise ValueError(f"g_idx holds {self.g_idx.size} entries; the layer has {K} rows")
+
     @property
     def groups(self) -> int:
         return self.scales.size // self.N if self.N else 0
@@ -259,6 +282,7 @@ class ForeignInt4:
 def int4_repack_host(layer: ForeignInt4):
     """A published layer in the reference int4 format, on the host: (codes,
     scales, zeros) over its K*N weights."""
+    layer.check_lengths()
     n = layer.K * layer.N
     codes = np.zeros((n + 7) // 8, np.uint32)
     scales = np.zeros((n + 127) // 128, np.uint16)
@@ -367,6 +391,23 @@ class Device:
 
     def inject_loss(self, at_submission: int) -> None:
         _check(_lib.accel_hip_inject_loss(self.index, at_submission))
+
+    def set_wait_limit(self, spins: int) -> None:
+        """Spins a split-K hand-off's bounded wait may take before it gives up
+        and reports the fault (a test hook)."""
+        _check(_lib.accel_hip_set_wait_limit(self.index, spins))
+
+    def set_xcd_local(self, enable: bool) -> None:
+        """Whether the decode products keep their split-K hand-off inside one
+        XCD (the same results either way)."""
+        _check(_lib.accel_hip_set_xcd_local(self.index, 1 if enable else 0))
+
+    def workspace_generation(self):
+        """(allocations of the workspace so far, replaced workspaces still held
+        by live executables)."""
+        g, r = ctypes.c_uint64(), ctypes.c_int32()
+        _check(_lib.accel_hip_workspace_generation(self.index, ctypes.byref(g), ctypes.byref(r)))
+        return g.value, r.value
 
     # memory
     def alloc(self, shape, dtype: int) -> Buffer:
@@ -481,6 +522,7 @@ class Device:
     def Int4Repack(self, layer: ForeignInt4, stream=None) -> Int4Weights:
         """A published AWQ / GPTQ layer, uploaded and repacked on the device into
         the reference int4 format; the published planes are freed after."""
+        layer.check_lengths()
         n = layer.K * layer.N
         up = [self.upload(layer.qweight, U32), self.upload(layer.qzeros, U32),
               self.upload(layer.scales, F16)]

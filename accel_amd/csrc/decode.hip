@@ -97,7 +97,7 @@ __device__ __forceinline__ void load_words(const uint32_t* p, uint32_t* w) {
 // batches.
 // One workgroup's share: column tile `tile` of the matrix, K slice `slice`;
 // `ticket` is this tile's split-K ticket.
-template <int M, int TILE, int CPL, bool PIPE>
+template <int M, int TILE, int CPL, bool PIPE, bool XL>
 __device__ __forceinline__ void decode_tile(
     const float* __restrict__ a, const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
@@ -228,33 +228,52 @@ __device__ __forceinline__ void decode_tile(
 #pragma unroll
             for (int w = 0; w < NWAVE; w++) sum += red[w][c];
             const int col = tile * TILE + c;
-            if (split)
-                store_device(&partial[((size_t)slice * M + m) * N + col], sum);
-            else
+            if (!split)
                 store_out(out, (size_t)m * N + col, col, sum, ep);
+            else if (XL)
+                partial[((size_t)slice * M + m) * N + col] = sum;
+            else
+                store_device(&partial[((size_t)slice * M + m) * N + col], sum);
         }
         __syncthreads();
     }
     if (!split) return;
 
-    split_k_finish(partial, ticket, out, tile * TILE, TILE, M, N, slices, &last_flag, ep);
+    split_k_finish<XL>(partial, ticket, out, tile * TILE, TILE, M, N, slices, &last_flag, ep);
 }
 
-template <int M, int TILE, int CPL, bool PIPE>
+// Workgroup b's (tile, K slice).  XL: the slices of tile t all run on XCD
+// t % n_xcc (workgroup b runs on XCD b % n_xcc; tiles % n_xcc == 0), so the
+// split-K hand-off stays in that XCD's L2.  Otherwise consecutive workgroups
+// -- the tiles of one K slice, which share scale and zero rows, activations
+// and 128-byte code lines -- are placed on one XCD.
+template <bool XL>
+__device__ __forceinline__ void place(int b, int tiles, int slices, int n_xcc, uint32_t* fault,
+                                      int& tile, int& slice) {
+    if constexpr (XL) {
+        const int x = b % n_xcc, j = b / n_xcc;
+        tile = x + n_xcc * (j / slices);
+        slice = j % slices;
+        check_placement(x, fault);
+    } else {
+        const int grid = tiles * slices;
+        if ((grid & 7) == 0) b = (b & 7) * (grid >> 3) + (b >> 3);
+        tile = b % tiles;
+        slice = b / tiles;
+    }
+}
+
+template <int M, int TILE, int CPL, bool PIPE, bool XL>
 __global__ __launch_bounds__(kDecThreads) void int4_decode_f32_kernel(
     const float* __restrict__ a, const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
     void* __restrict__ out, float* partial, uint32_t* tickets, int ticket_stride, int K, int N,
-    int rows_per_slice, int slices, Epilogue ep) {
-    const int tiles = N / TILE;
-    const int grid = tiles * slices;
-    int b = blockIdx.x;
-    if ((grid & 7) == 0) b = (b & 7) * (grid >> 3) + (b >> 3);
-    const int tile = b % tiles;
-    const int slice = b / tiles;
-    decode_tile<M, TILE, CPL, PIPE>(a, codes, scales, zeros, out, partial,
-                                    tickets + (size_t)tile * ticket_stride, K, N, tile, slice,
-                                    rows_per_slice, slices, ep);
+    int rows_per_slice, int slices, Epilogue ep, uint32_t* fault, int n_xcc) {
+    int tile, slice;
+    place<XL>(blockIdx.x, N / TILE, slices, n_xcc, fault, tile, slice);
+    decode_tile<M, TILE, CPL, PIPE, XL>(a, codes, scales, zeros, out, partial,
+                                        tickets + (size_t)tile * ticket_stride, K, N, tile,
+                                        slice, rows_per_slice, slices, ep);
 }
 
 // Several matrices against one input in one launch (the q, k, v or gate, up
@@ -273,21 +292,17 @@ struct DecodeSet {
     int count;
 };
 
-template <int M, int TILE, int CPL, bool PIPE>
+template <int M, int TILE, int CPL, bool PIPE, bool XL>
 __global__ __launch_bounds__(kDecThreads) void int4_decode_set_kernel(
     const float* __restrict__ a, DecodeSet set, uint32_t* tickets, int ticket_stride, int K,
-    int rows_per_slice, int slices) {
-    const int tiles = set.tile0[set.count];
-    const int grid = tiles * slices;
-    int b = blockIdx.x;
-    if ((grid & 7) == 0) b = (b & 7) * (grid >> 3) + (b >> 3);
-    const int tg = b % tiles;
-    const int slice = b / tiles;
+    int rows_per_slice, int slices, uint32_t* fault, int n_xcc) {
+    int tg, slice;
+    place<XL>(blockIdx.x, set.tile0[set.count], slices, n_xcc, fault, tg, slice);
     int i = 0;
 #pragma unroll
     for (int j = 1; j < kMaxSet; j++)
         if (j < set.count && tg >= set.tile0[j]) i = j;
-    decode_tile<M, TILE, CPL, PIPE>(a, set.codes[i], set.scales[i], set.zeros[i], set.out[i],
+    decode_tile<M, TILE, CPL, PIPE, XL>(a, set.codes[i], set.scales[i], set.zeros[i], set.out[i],
                                     set.partial[i], tickets + (size_t)tg * ticket_stride, K,
                                     set.n[i], tg - set.tile0[i], slice, rows_per_slice, slices,
                                     Epilogue{});
@@ -326,19 +341,24 @@ hipError_t launch_decode(Device* d, hipStream_t st, const float* a, Int4Planes w
                            "decode product: N=%d needs more tickets than the workspace holds", N);
             return hipSuccess;
         }
-        void* ws = workspace(d, (size_t)slices * M * N * sizeof(float), status);
+        void* ws = workspace(d, st, (size_t)slices * M * N * sizeof(float), status);
         if (!ws) return hipSuccess;
         tickets = static_cast<uint32_t*>(ws);
         partial = reinterpret_cast<float*>(static_cast<char*>(ws) + kWorkspaceCounterBytes);
     }
-    if (per_slice > 1)
-        hipLaunchKernelGGL((int4_decode_f32_kernel<M, TILE, CPL, true>), dim3(tiles * slices),
-                           dim3(kDecThreads), 0, st, a, w.codes, w.scales, w.zeros, out, partial,
-                           tickets, stride, K, N, rows, slices, ep);
-    else
-        hipLaunchKernelGGL((int4_decode_f32_kernel<M, TILE, CPL, false>), dim3(tiles * slices),
-                           dim3(kDecThreads), 0, st, a, w.codes, w.scales, w.zeros, out, partial,
-                           tickets, stride, K, N, rows, slices, ep);
+    const bool xl = slices > 1 && d->xcd_local && tiles % d->n_xcc == 0;
+#define ACCEL_DECODE_LAUNCH(P, X)                                                            \
+    hipLaunchKernelGGL((int4_decode_f32_kernel<M, TILE, CPL, P, X>), dim3(tiles * slices),   \
+                       dim3(kDecThreads), 0, st, a, w.codes, w.scales, w.zeros, out, partial, \
+                       tickets, stride, K, N, rows, slices, ep, d->fault_dev, d->n_xcc)
+    if (per_slice > 1) {
+        if (xl) ACCEL_DECODE_LAUNCH(true, true);
+        else ACCEL_DECODE_LAUNCH(true, false);
+    } else {
+        if (xl) ACCEL_DECODE_LAUNCH(false, true);
+        else ACCEL_DECODE_LAUNCH(false, false);
+    }
+#undef ACCEL_DECODE_LAUNCH
     return hipGetLastError();
 }
 
@@ -478,7 +498,7 @@ hipError_t launch_matvec_f16_tiled(Device* d, hipStream_t st, const float* a, co
                            "matvec: N=%d needs more tickets than the workspace holds", N);
             return hipSuccess;
         }
-        void* ws = workspace(d, (size_t)slices * N * sizeof(float), status);
+        void* ws = workspace(d, st, (size_t)slices * N * sizeof(float), status);
         if (!ws) return hipSuccess;
         tickets = static_cast<uint32_t*>(ws);
         partial = reinterpret_cast<float*>(static_cast<char*>(ws) + kWorkspaceCounterBytes);
@@ -721,12 +741,14 @@ __device__ __forceinline__ void decode_mfma_tile(
     const float* __restrict__ a, const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
     void* __restrict__ out, float* partial, uint32_t* ticket, int M, int K, int N, int tile,
-    int slice, int rows_per_slice, int slices, const Epilogue& ep) {
+    int slice, int rows_per_slice, int slices, const Epilogue& ep, uint32_t* fault,
+    int wait_limit) {
     using T = MfTile<G, NW>;
     constexpr int D = T::kDepth;
     constexpr int V = T::kVmemPerStep;
     __shared__ __attribute__((aligned(16))) uint8_t lds[kMfLdsBytes];
     __shared__ int last_flag;
+    __shared__ int waited;
 
     const int n0 = tile * T::kCols;
     const int g0 = tile * G;
@@ -1075,15 +1097,27 @@ __device__ __forceinline__ void decode_mfma_tile(
         return;
     }
     if (tid == 0) {
-        // bounded: every workgroup counted in `arrive` is running toward `done`
-        for (int spin = 0; spin < (1 << 22); spin++) {
+        // Bounded: every workgroup counted in `arrive` is running toward
+        // `done`.  Should the bound run out all the same, the workgroup
+        // reports it in the fault word and leaves the output and the
+        // counters alone (a late workgroup may still count itself done; the
+        // host clears the counters when it reads the fault).
+        int ok = 0;
+        for (int spin = 0; spin < wait_limit; spin++) {
             if (__hip_atomic_load(done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                (uint32_t)(slices - 1))
+                (uint32_t)(slices - 1)) {
+                ok = 1;
                 break;
+            }
             __builtin_amdgcn_s_sleep(1);
         }
+        if (!ok)
+            __hip_atomic_fetch_or(fault, kFaultWaitGaveUp, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_SYSTEM);
+        waited = ok;
     }
     __syncthreads();
+    if (!waited) return;
     // every slice's sums in slice order, eight slices' loads in flight at a
     // time; this workgroup's own come from registers
     f32x4 sum[T::kItems];
@@ -1136,7 +1170,7 @@ __global__ __launch_bounds__(64 * NW) void int4_decode_mfma_kernel(
     const float* __restrict__ a, const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
     void* __restrict__ out, float* partial, uint32_t* tickets, int ticket_stride, int M, int K,
-    int N, int rows_per_slice, int slices, Epilogue ep) {
+    int N, int rows_per_slice, int slices, Epilogue ep, uint32_t* fault, int wait_limit) {
     using T = MfTile<G, NW>;
     const int tiles = N / T::kCols;
     const int grid = tiles * slices;
@@ -1146,7 +1180,7 @@ __global__ __launch_bounds__(64 * NW) void int4_decode_mfma_kernel(
     const int slice = b / tiles;
     decode_mfma_tile<G, NW>(a, codes, scales, zeros, out, partial,
                             tickets + (size_t)tile * ticket_stride, M, K, N, tile, slice,
-                            rows_per_slice, slices, ep);
+                            rows_per_slice, slices, ep, fault, wait_limit);
 }
 
 // Several matrices against one activation block in one launch, each with the
@@ -1170,7 +1204,8 @@ struct MfSet {
 
 template <int G, int NW>
 __global__ __launch_bounds__(64 * NW) void int4_decode_mfma_set_kernel(
-    const float* __restrict__ a, MfSet set, uint32_t* tickets, int ticket_stride, int M, int K) {
+    const float* __restrict__ a, MfSet set, uint32_t* tickets, int ticket_stride, int M, int K,
+    uint32_t* fault, int wait_limit) {
     using T = MfTile<G, NW>;
     const int grid = set.wg0[set.count];
     int b = blockIdx.x;
@@ -1185,7 +1220,8 @@ __global__ __launch_bounds__(64 * NW) void int4_decode_mfma_set_kernel(
     const int slice = bl / tiles;
     decode_mfma_tile<G, NW>(a, set.codes[i], set.scales[i], set.zeros[i], set.out[i],
                             set.partial[i], tickets + (size_t)(set.tick0[i] + tile) * ticket_stride,
-                            M, K, set.n[i], tile, slice, set.rows[i], set.slices[i], Epilogue{});
+                            M, K, set.n[i], tile, slice, set.rows[i], set.slices[i], Epilogue{},
+                            fault, wait_limit);
 }
 
 struct MfPlan {
@@ -1235,14 +1271,14 @@ hipError_t launch_mfma(Device* d, hipStream_t st, const float* a, Int4Planes w, 
                            "decode product: N=%d needs more tickets than the workspace holds", N);
             return hipSuccess;
         }
-        void* ws = workspace(d, (size_t)p.slices * M * N * sizeof(float), status);
+        void* ws = workspace(d, st, (size_t)p.slices * M * N * sizeof(float), status);
         if (!ws) return hipSuccess;
         tickets = static_cast<uint32_t*>(ws);
         partial = reinterpret_cast<float*>(static_cast<char*>(ws) + kWorkspaceCounterBytes);
     }
     hipLaunchKernelGGL((int4_decode_mfma_kernel<G, NW>), dim3(tiles * p.slices), dim3(64 * NW),
                        0, st, a, w.codes, w.scales, w.zeros, out, partial, tickets, stride, M, K,
-                       N, p.rows, p.slices, ep);
+                       N, p.rows, p.slices, ep, d->fault_dev, d->wait_limit);
     return hipGetLastError();
 }
 
@@ -1283,7 +1319,7 @@ hipError_t launch_mfma_set(Device* d, hipStream_t st, const float* a, const Int4
                            tiles_all);
             return hipSuccess;
         }
-        void* ws = workspace(d, partial_floats * sizeof(float), status);
+        void* ws = workspace(d, st, partial_floats * sizeof(float), status);
         if (!ws) return hipSuccess;
         tickets = static_cast<uint32_t*>(ws);
         float* p = reinterpret_cast<float*>(static_cast<char*>(ws) + kWorkspaceCounterBytes);
@@ -1293,7 +1329,7 @@ hipError_t launch_mfma_set(Device* d, hipStream_t st, const float* a, const Int4
         }
     }
     hipLaunchKernelGGL((int4_decode_mfma_set_kernel<G, 8>), dim3(wgs), dim3(64 * 8), 0, st, a,
-                       set, tickets, stride, M, K);
+                       set, tickets, stride, M, K, d->fault_dev, d->wait_limit);
     return hipGetLastError();
 }
 
@@ -1342,7 +1378,7 @@ hipError_t launch_matvec_set(Device* d, hipStream_t st, const float* a, const In
                            tiles);
             return hipSuccess;
         }
-        void* ws = workspace(d, partial_floats * sizeof(float), status);
+        void* ws = workspace(d, st, partial_floats * sizeof(float), status);
         if (!ws) return hipSuccess;
         tickets = static_cast<uint32_t*>(ws);
         float* p = reinterpret_cast<float*>(static_cast<char*>(ws) + kWorkspaceCounterBytes);
@@ -1351,12 +1387,19 @@ hipError_t launch_matvec_set(Device* d, hipStream_t st, const float* a, const In
             p += (size_t)slices * N[i];
         }
     }
-    if (per_slice > 1)
-        hipLaunchKernelGGL((int4_decode_set_kernel<1, TILE, CPL, true>), dim3(tiles * slices),
-                           dim3(kDecThreads), 0, st, a, set, tickets, stride, K, rows, slices);
-    else
-        hipLaunchKernelGGL((int4_decode_set_kernel<1, TILE, CPL, false>), dim3(tiles * slices),
-                           dim3(kDecThreads), 0, st, a, set, tickets, stride, K, rows, slices);
+    const bool xl = slices > 1 && d->xcd_local && tiles % d->n_xcc == 0;
+#define ACCEL_SET_LAUNCH(P, X)                                                               \
+    hipLaunchKernelGGL((int4_decode_set_kernel<1, TILE, CPL, P, X>), dim3(tiles * slices),   \
+                       dim3(kDecThreads), 0, st, a, set, tickets, stride, K, rows, slices,    \
+                       d->fault_dev, d->n_xcc)
+    if (per_slice > 1) {
+        if (xl) ACCEL_SET_LAUNCH(true, true);
+        else ACCEL_SET_LAUNCH(true, false);
+    } else {
+        if (xl) ACCEL_SET_LAUNCH(false, true);
+        else ACCEL_SET_LAUNCH(false, false);
+    }
+#undef ACCEL_SET_LAUNCH
     return hipGetLastError();
 }
 

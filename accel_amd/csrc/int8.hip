@@ -244,7 +244,7 @@ hipError_t launch_int8_decode(Device* d, hipStream_t st, const ACT* a, const int
                            "int8 product: N=%d needs more tickets than the workspace holds", N);
             return hipSuccess;
         }
-        void* ws = workspace(d, (size_t)slices * M * N * sizeof(float), status);
+        void* ws = workspace(d, st, (size_t)slices * M * N * sizeof(float), status);
         if (!ws) return hipSuccess;
         tickets = static_cast<uint32_t*>(ws);
         partial = reinterpret_cast<float*>(static_cast<char*>(ws) + kWorkspaceCounterBytes);

@@ -8,6 +8,8 @@
 #include <cstddef>
 #include <cstdint>
 #include <mutex>
+#include <unordered_map>
+#include <vector>
 
 #include "../../include/accel_hip.h"
 
@@ -17,8 +19,13 @@ namespace accel {
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 void clear_error();
 
-// Per-device state: the open flag, sticky loss, fault injection and the
-// library-owned workspace.
+// Bits of the device fault word: what a kernel reports when it gives up
+// instead of producing its result.
+constexpr uint32_t kFaultWaitGaveUp = 1u;     // a split-K hand-off's bounded wait ran out
+constexpr uint32_t kFaultPlacement = 2u;      // a workgroup ran on an XCD its plan did not assume
+
+// Per-device state: the open flag, sticky loss, fault injection, the
+// library-owned workspace and the fault word.
 struct Device {
     int ordinal = -1;
     bool open = false;
@@ -28,6 +35,24 @@ struct Device {
     int64_t lose_at = 0;
     void* ws = nullptr;        // workspace (device memory)
     size_t ws_bytes = 0;
+    uint64_t ws_gen = 0;       // bumped each time the workspace is reallocated
+    // Workspaces replaced by a larger one while a live executable still
+    // names them (its kernels carry the old addresses): freed when the last
+    // such executable is destroyed, or at close.
+    struct Retired {
+        void* ptr;
+        uint64_t gen;
+    };
+    std::vector<Retired> retired;
+    std::unordered_map<void*, uint64_t> exec_gen;   // live executable -> workspace generation
+    // Fault word: host memory the kernels write (system scope) when a bounded
+    // wait gives up or a placement check fails; read after every wait.
+    uint32_t* fault_host = nullptr;
+    uint32_t* fault_dev = nullptr;
+    int32_t wait_limit = 1 << 22;   // spins of a hand-off's bounded wait
+    int n_xcc = 1;                  // XCDs (accelerator complexes) of the device
+    bool xcd_mapped = false;        // workgroup b runs on XCD b % n_xcc (probed at open)
+    bool xcd_local = false;         // hand-offs may stay inside one XCD's L2
     int cu_count = 256;
     size_t lds_per_block = 65536;
 };
@@ -45,11 +70,19 @@ int begin_submission(Device* d);
 // does not.  Returns the ACCEL_* code.
 int classify(Device* d, hipError_t e, const char* what);
 
-// The workspace, at least `bytes` long.  The first kWorkspaceCounterBytes are
-// kept zero between launches by the kernels that use them (a counter is reset
-// by the workgroup that consumes it).
+// The workspace, at least `bytes` long beyond its counters.  The first
+// kWorkspaceCounterBytes are kept zero between launches by the kernels that
+// use them (a counter is reset by the workgroup that consumes it).  It grows
+// only outside graph capture: a call that needs more on a capturing stream
+// is refused (ACCEL_E_INVALID).  A workspace that a live executable names is
+// retired, not freed, when it grows.
 constexpr size_t kWorkspaceCounterBytes = 1 << 16;
-void* workspace(Device* d, size_t bytes, int* status);
+void* workspace(Device* d, hipStream_t st, size_t bytes, int* status);
+
+// After a wait on the device: ACCEL_OK, or ACCEL_E_HIP with the message
+// naming what a kernel reported in the fault word (which is then cleared,
+// together with the workspaces' counters, so later calls start clean).
+int take_fault(Device* d);
 
 // ---- kernel launchers (defined in the .hip files) ------------------------
 

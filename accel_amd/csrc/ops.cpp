@@ -526,7 +526,7 @@ int check_grouped(const char* op, const accel_tensor_t* x, const accel_tensor_t*
 // pointer or nullptr with status set.
 uint32_t* offsets_in_workspace(Device* d, hipStream_t st, const uint32_t* counts,
                                int64_t experts, int* status) {
-    void* ws = workspace(d, (size_t)(experts + 1) * sizeof(uint32_t), status);
+    void* ws = workspace(d, st, (size_t)(experts + 1) * sizeof(uint32_t), status);
     if (!ws) return nullptr;
     uint32_t* off =
         reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + kWorkspaceCounterBytes);

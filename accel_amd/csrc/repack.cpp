@@ -193,10 +193,10 @@ ACCEL_API int accel_int4_repack(int dev, void* stream, const accel_foreign_int4_
     if (!d) return ACCEL_E_NO_DEVICE;
     int status = begin_submission(d);
     if (status != ACCEL_OK) return status;
-    void* ws = workspace(d, sizeof(uint32_t), &status);
+    hipStream_t st = (hipStream_t)stream;
+    void* ws = workspace(d, st, sizeof(uint32_t), &status);
     if (!ws) return status;
     uint32_t* bad = reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + kWorkspaceCounterBytes);
-    hipStream_t st = (hipStream_t)stream;
     hipError_t e = hipMemsetAsync(bad, 0, sizeof(uint32_t), st);
     if (e == hipSuccess)
         e = launch_int4_repack(st, *src, const_cast<uint32_t*>(dst->codes),

@@ -78,19 +78,69 @@ int classify(Device* d, hipError_t e, const char* what) {
     }
 }
 
-void* workspace(Device* d, size_t bytes, int* status) {
+namespace {
+
+// Frees the retired workspaces that no live executable names any more.  The
+// caller holds d->mu.
+void free_unreferenced(Device* d) {
+    bool waited = false;
+    for (size_t i = 0; i < d->retired.size();) {
+        bool named = false;
+        for (const auto& kv : d->exec_gen)
+            if (kv.second == d->retired[i].gen) named = true;
+        if (named) {
+            i++;
+            continue;
+        }
+        if (!waited) {
+            (void)hipDeviceSynchronize();
+            waited = true;
+        }
+        (void)hipFree(d->retired[i].ptr);
+        d->retired.erase(d->retired.begin() + (ptrdiff_t)i);
+    }
+}
+
+bool capturing(hipStream_t st) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+
+}  // namespace
+
+void* workspace(Device* d, hipStream_t st, size_t bytes, int* status) {
     *status = ACCEL_OK;
-    size_t need = kWorkspaceCounterBytes + bytes;
+    const size_t need = kWorkspaceCounterBytes + bytes;
     std::lock_guard<std::mutex> lk(d->mu);
     if (d->ws && d->ws_bytes >= need) return d->ws;
-    // Growing: nothing queued may still use the old allocation.
+    if (capturing(st)) {
+        *status = fail(ACCEL_E_INVALID,
+                       "accel_hip: this call needs a workspace of %zu bytes and the device has "
+                       "%zu; a workspace cannot grow inside a graph capture: issue the call "
+                       "once outside the capture first",
+                       need, d->ws_bytes);
+        return nullptr;
+    }
+    // Growing.  Queued eager work may still use the old buffer, so wait for
+    // it; an executable captured against it keeps its address, so a named
+    // buffer is retired rather than freed.
     if (d->ws) {
-        (void)hipDeviceSynchronize();
-        (void)hipFree(d->ws);
+        hipError_t e = hipDeviceSynchronize();
+        if (e != hipSuccess) {
+            *status = classify(d, e, "workspace growth");
+            return nullptr;
+        }
+        bool named = false;
+        for (const auto& kv : d->exec_gen)
+            if (kv.second == d->ws_gen) named = true;
+        if (named)
+            d->retired.push_back({d->ws, d->ws_gen});
+        else
+            (void)hipFree(d->ws);
         d->ws = nullptr;
         d->ws_bytes = 0;
     }
-    size_t sz = need < (size_t(8) << 20) ? (size_t(8) << 20) : need;
+    const size_t sz = need < (size_t(8) << 20) ? (size_t(8) << 20) : need;
     hipError_t e = hipMalloc(&d->ws, sz);
     if (e != hipSuccess) {
         d->ws = nullptr;
@@ -99,12 +149,76 @@ void* workspace(Device* d, size_t bytes, int* status) {
     }
     e = hipMemset(d->ws, 0, kWorkspaceCounterBytes);
     if (e != hipSuccess) {
+        (void)hipFree(d->ws);
+        d->ws = nullptr;
         *status = classify(d, e, "workspace clear");
         return nullptr;
     }
     d->ws_bytes = sz;
+    d->ws_gen++;
     return d->ws;
 }
+
+int take_fault(Device* d) {
+    if (!d->fault_host) return ACCEL_OK;
+    const uint32_t f = __atomic_exchange_n(d->fault_host, 0u, __ATOMIC_ACQ_REL);
+    if (!f) return ACCEL_OK;
+    // A kernel that gave up left its hand-off counters mid-way: wait for the
+    // device, then clear the counters of every workspace.
+    (void)hipDeviceSynchronize();
+    {
+        std::lock_guard<std::mutex> lk(d->mu);
+        if (d->ws) (void)hipMemset(d->ws, 0, kWorkspaceCounterBytes);
+        for (const auto& r : d->retired) (void)hipMemset(r.ptr, 0, kWorkspaceCounterBytes);
+    }
+    std::string what;
+    if (f & kFaultWaitGaveUp) what += "a split-K hand-off's bounded wait gave up";
+    if (f & kFaultPlacement) {
+        if (!what.empty()) what += "; ";
+        what += "a workgroup ran on an XCD its launch plan did not assume";
+    }
+    if (f & ~(kFaultWaitGaveUp | kFaultPlacement)) {
+        if (!what.empty()) what += "; ";
+        what += "unknown fault bits";
+    }
+    return fail(ACCEL_E_HIP,
+                "accel_hip: device fault word 0x%x (%s): the results of the work waited on "
+                "are undefined",
+                f, what.c_str());
+}
+
+// XCD of each workgroup of a one-wave-per-workgroup probe grid.
+__global__ void xcc_probe_kernel(uint32_t* out) {
+    uint32_t x;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+    if (threadIdx.x == 0) out[blockIdx.x] = x;
+}
+
+namespace {
+
+// Whether workgroup b of a launch runs on XCD b % n_xcc, which the XCD-local
+// hand-offs rely on (the hardware deals workgroups to XCDs round robin).
+// Checked once per open on a probe grid; every launch that relies on it
+// checks its own workgroups again and reports kFaultPlacement otherwise.
+bool probe_xcd_mapping(int n_xcc) {
+    constexpr int kBlocks = 256;
+    uint32_t* buf = nullptr;
+    if (hipMalloc(&buf, kBlocks * sizeof(uint32_t)) != hipSuccess) return false;
+    bool ok = hipMemset(buf, 0xff, kBlocks * sizeof(uint32_t)) == hipSuccess;
+    if (ok) {
+        hipLaunchKernelGGL(xcc_probe_kernel, dim3(kBlocks), dim3(64), 0, nullptr, buf);
+        ok = hipGetLastError() == hipSuccess && hipDeviceSynchronize() == hipSuccess;
+    }
+    uint32_t host[kBlocks];
+    if (ok) ok = hipMemcpy(host, buf, sizeof host, hipMemcpyDeviceToHost) == hipSuccess;
+    (void)hipFree(buf);
+    if (!ok) return false;
+    for (int b = 0; b < kBlocks; b++)
+        if (host[b] != (uint32_t)(b % n_xcc)) return false;
+    return true;
+}
+
+}  // namespace
 
 }  // namespace accel
 
@@ -170,6 +284,28 @@ ACCEL_API int accel_hip_open(int dev) {
         return fail(ACCEL_E_UNSUPPORTED,
                     "accel_hip_open: device %d is %s; this library carries gfx950 code only",
                     dev, p.gcnArchName);
+    if (!d->fault_host) {
+        void* h = nullptr;
+        e = hipHostMalloc(&h, 64, hipHostMallocDefault);
+        if (e != hipSuccess) return classify(nullptr, e, "fault word allocation");
+        void* dp = nullptr;
+        e = hipHostGetDevicePointer(&dp, h, 0);
+        if (e != hipSuccess) {
+            (void)hipHostFree(h);
+            return classify(nullptr, e, "fault word mapping");
+        }
+        d->fault_host = static_cast<uint32_t*>(h);
+        d->fault_dev = static_cast<uint32_t*>(dp);
+    }
+    *d->fault_host = 0;
+    int n_xcc = 1;
+    if (hipDeviceGetAttribute(&n_xcc, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess ||
+        n_xcc < 1)
+        n_xcc = 1;
+    d->n_xcc = n_xcc;
+    d->xcd_mapped = n_xcc > 1 && probe_xcd_mapping(n_xcc);
+    d->xcd_local = d->xcd_mapped;
+    d->wait_limit = 1 << 22;
     d->ordinal = dev;
     d->cu_count = p.multiProcessorCount;
     d->lds_per_block = p.sharedMemPerBlock;
@@ -187,12 +323,14 @@ ACCEL_API int accel_hip_close(int dev) {
     Device* d = &g_devices[dev];
     if (!d->open) return ACCEL_OK;
     (void)hipSetDevice(dev);
-    if (d->ws) {
-        (void)hipDeviceSynchronize();
-        (void)hipFree(d->ws);
-    }
+    (void)hipDeviceSynchronize();
+    if (d->ws) (void)hipFree(d->ws);
+    for (const auto& r : d->retired) (void)hipFree(r.ptr);
+    d->retired.clear();
+    d->exec_gen.clear();
     d->ws = nullptr;
     d->ws_bytes = 0;
+    if (d->fault_host) *d->fault_host = 0;
     d->open = false;
     return ACCEL_OK;
 }
@@ -295,7 +433,8 @@ ACCEL_API int accel_hip_stream_sync(int dev, void* stream) {
     Device* d = device(dev);
     if (!d) return ACCEL_E_NO_DEVICE;
     if (d->lost.load()) return fail(ACCEL_E_DEVICE_LOST, "accel: device lost");
-    return classify(d, hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
+    const int rc = classify(d, hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
+    return rc != ACCEL_OK ? rc : take_fault(d);
 }
 
 ACCEL_API int accel_hip_event_create(int dev, void** event) {
@@ -332,7 +471,10 @@ ACCEL_API int accel_hip_event_query(int dev, void* event) {
     if (!d) return ACCEL_E_NO_DEVICE;
     if (d->lost.load()) return 1;  // a lost device is done (plan.go:380-382)
     hipError_t e = hipEventQuery((hipEvent_t)event);
-    if (e == hipSuccess) return 1;
+    if (e == hipSuccess) {
+        const int rc = take_fault(d);
+        return rc != ACCEL_OK ? rc : 1;
+    }
     if (e == hipErrorNotReady) return 0;
     return classify(d, e, "hipEventQuery");
 }
@@ -342,7 +484,8 @@ ACCEL_API int accel_hip_event_sync(int dev, void* event) {
     Device* d = device(dev);
     if (!d) return ACCEL_E_NO_DEVICE;
     if (d->lost.load()) return fail(ACCEL_E_DEVICE_LOST, "accel: device lost");
-    return classify(d, hipEventSynchronize((hipEvent_t)event), "hipEventSynchronize");
+    const int rc = classify(d, hipEventSynchronize((hipEvent_t)event), "hipEventSynchronize");
+    return rc != ACCEL_OK ? rc : take_fault(d);
 }
 
 ACCEL_API int accel_hip_event_elapsed(int dev, void* start, void* end, float* ms) {
@@ -379,6 +522,11 @@ ACCEL_API int accel_hip_capture_end(int dev, void* stream, void** exec) {
     rc = classify(d, hipGraphInstantiate(&ge, g, nullptr, nullptr, 0), "hipGraphInstantiate");
     (void)hipGraphDestroy(g);
     if (rc != ACCEL_OK) return rc;
+    {
+        // the executable's kernels carry this workspace's addresses
+        std::lock_guard<std::mutex> lk(d->mu);
+        d->exec_gen[ge] = d->ws_gen;
+    }
     *exec = ge;
     return ACCEL_OK;
 }
@@ -399,5 +547,43 @@ ACCEL_API int accel_hip_exec_destroy(int dev, void* exec) {
     Device* d = device(dev);
     if (!d) return ACCEL_E_NO_DEVICE;
     if (!exec) return ACCEL_OK;
-    return classify(d, hipGraphExecDestroy((hipGraphExec_t)exec), "hipGraphExecDestroy");
+    const int rc = classify(d, hipGraphExecDestroy((hipGraphExec_t)exec), "hipGraphExecDestroy");
+    std::lock_guard<std::mutex> lk(d->mu);
+    d->exec_gen.erase(exec);
+    free_unreferenced(d);
+    return rc;
+}
+
+ACCEL_API int accel_hip_set_wait_limit(int dev, int32_t spins) {
+    clear_error();
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    if (spins < 0) return fail(ACCEL_E_INVALID, "accel_hip_set_wait_limit: %d spins", spins);
+    std::lock_guard<std::mutex> lk(d->mu);
+    d->wait_limit = spins;
+    return ACCEL_OK;
+}
+
+ACCEL_API int accel_hip_set_xcd_local(int dev, int enable) {
+    clear_error();
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    std::lock_guard<std::mutex> lk(d->mu);
+    if (enable && !d->xcd_mapped)
+        return fail(ACCEL_E_UNSUPPORTED,
+                    "accel_hip_set_xcd_local: workgroups of device %d are not dealt to its %d "
+                    "XCDs round robin, so no hand-off can stay inside one XCD",
+                    dev, d->n_xcc);
+    d->xcd_local = enable != 0;
+    return ACCEL_OK;
+}
+
+ACCEL_API int accel_hip_workspace_generation(int dev, uint64_t* gen, int32_t* retired) {
+    clear_error();
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    std::lock_guard<std::mutex> lk(d->mu);
+    if (gen) *gen = d->ws_gen;
+    if (retired) *retired = (int32_t)d->retired.size();
+    return ACCEL_OK;
 }

@@ -31,7 +31,19 @@
  * K split) and the grouped products (segment offsets, tile lists) use a
  * per-device workspace owned by the library.  Two operator calls that run
  * concurrently on different streams of one device race on it; serialize
- * them or use one stream per device.
+ * them or use one stream per device.  The workspace grows on demand outside
+ * graph capture; a call that would need it to grow on a capturing stream is
+ * refused (ACCEL_E_INVALID).  When it grows, a workspace that a live
+ * executable still names is kept until that executable is destroyed, so an
+ * executable stays valid across later, larger eager calls.
+ *
+ * Faults.  A kernel that gives up instead of producing its result (a
+ * split-K hand-off whose bounded wait runs out, a workgroup placed on an XCD
+ * its plan did not assume) records it in the device's fault word; the next
+ * stream_sync, event_sync or event_query that completes reports it as
+ * ACCEL_E_HIP with a message, and clears it (the analogue of the
+ * reference's per-node fault words read back by Fence.Wait,
+ * internal/metal/exec_darwin.go:46-53,822-826).
  */
 #ifndef ACCEL_HIP_H
 #define ACCEL_HIP_H
@@ -125,7 +137,8 @@ int accel_hip_stream_sync(int dev, void* stream);
 int accel_hip_event_create(int dev, void** event);
 int accel_hip_event_destroy(int dev, void* event);
 int accel_hip_event_record(int dev, void* event, void* stream);
-/* 1 = done (a lost device is done), 0 = pending, <0 = error. */
+/* 1 = done (a lost device is done), 0 = pending, <0 = error (including a
+ * fault a kernel reported; see Faults above). */
 int accel_hip_event_query(int dev, void* event);
 int accel_hip_event_sync(int dev, void* event);
 int accel_hip_event_elapsed(int dev, void* start, void* end, float* ms);
@@ -135,11 +148,30 @@ int accel_hip_event_elapsed(int dev, void* start, void* end, float* ms);
  * recorded, not run; exec_launch replays them as one submission (the
  * reference's resubmittable compiled plan, GraphCompiler.Compile,
  * plan.go:398-400).  Issue every captured call once eagerly before capturing,
- * so the workspace it needs is already allocated. */
+ * so the workspace it needs is already allocated (a call that would grow it
+ * inside the capture is refused).  An executable records the workspace it
+ * was captured against; that workspace lives until the executable is
+ * destroyed. */
 int accel_hip_capture_begin(int dev, void* stream);
 int accel_hip_capture_end(int dev, void* stream, void** exec);
 int accel_hip_exec_launch(int dev, void* exec, void* stream);
 int accel_hip_exec_destroy(int dev, void* exec);
+
+/* Test and diagnostic hooks; no reference counterpart.
+ *  set_wait_limit: the spins a split-K hand-off's bounded wait may take
+ *    before it gives up and reports kFault "wait gave up" (default 1 << 22;
+ *    0 makes every such wait give up at once, so a test can force the fault
+ *    from the host while every kernel still exits normally).
+ *  set_xcd_local: whether the decode products may keep their split-K
+ *    hand-off inside one XCD's L2 (the default where open found workgroups
+ *    dealt to XCDs round robin); 0 selects the device-scope hand-off, which
+ *    gives the same results bit for bit.  ACCEL_E_UNSUPPORTED when enabling it
+ *    on a device whose placement open could not confirm.
+ *  workspace_generation: how many times the workspace has been allocated,
+ *    and how many replaced workspaces live executables still hold. */
+int accel_hip_set_wait_limit(int dev, int32_t spins);
+int accel_hip_set_xcd_local(int dev, int enable);
+int accel_hip_workspace_generation(int dev, uint64_t* gen, int32_t* retired);
 
 /* KernelSupport.SupportsKernel (plan.go:424-428): 1 if the named reference
  * kernel record has a gfx950 implementation here, else 0.  Records without

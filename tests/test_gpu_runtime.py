@@ -1,0 +1,222 @@
+"""The runtime's own guarantees, on the GPU, through the C ABI.
+
+* An executable stays valid when a later eager call grows the workspace: the
+  workspace it was captured against is kept (retired) while it lives, and
+  freed when it is destroyed.
+* A call that would grow the workspace inside a graph capture is refused.
+* A split-K hand-off whose bounded wait gives up reports it through the
+  device's fault word at the next wait (forced from the host with a zero wait
+  limit, so every kernel still exits normally), and products are correct
+  again afterwards.
+"""
+import numpy as np
+import pytest
+
+import accel_amd
+import oracle
+from accel_amd import F32, U32, F16, workloads
+from conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def _reopen(dev):
+    """A fresh workspace: close frees it, open starts without one."""
+    dev.close()
+    accel_amd.Device(dev.index)
+
+
+def _big_matvec_args(dev):
+    """An Int4MatVec whose split-K partial sums need 16 MiB (64 slices x 65536
+    columns x 4 bytes), twice the workspace's first allocation.  Its weights
+    are left uninitialised: only the workspace it asks for matters here."""
+    K, N = 16384, 65536
+    n = K * N
+    w = accel_amd.Int4Weights(dev.alloc((n // 8,), U32), dev.alloc((n // 128,), F16),
+                              dev.alloc((n // 128,), F16), n)
+    a = dev.upload(np.zeros(K, np.float32))
+    out = dev.alloc((N,), F32)
+    return a, w, out
+
+
+def test_executable_survives_workspace_growth(dev):
+    _reopen(dev)
+    rng = np.random.Generator(np.random.PCG64(31))
+    K, N = 4096, 4096
+    p, s, z = workloads.fast_int4(K, N, rng)
+    x = rng.standard_normal(K).astype(np.float32)
+    w = dev.upload_int4(p, s, z, K * N)
+    a = dev.upload(x)
+    eager = dev.alloc((N,), F32)
+    dev.Int4MatVec(a, w, eager)           # allocates the first workspace
+    dev.sync()
+    gen0, retired0 = dev.workspace_generation()
+    assert gen0 >= 1 and retired0 == 0
+
+    stream = dev.stream()
+    replayed = dev.alloc((N,), F32)
+    dev.capture_begin(stream)
+    dev.Int4MatVec(a, w, replayed, stream)
+    ex = dev.capture_end(stream)
+
+    ba, bw, bo = _big_matvec_args(dev)
+    dev.Int4MatVec(ba, bw, bo, stream)     # grows the workspace
+    dev.sync(stream)
+    gen1, retired1 = dev.workspace_generation()
+    assert gen1 == gen0 + 1 and retired1 == 1   # the executable's workspace is kept
+
+    for _ in range(3):
+        dev.launch(ex, stream)
+        dev.sync(stream)
+        assert np.array_equal(replayed.numpy().view(np.uint32), eager.numpy().view(np.uint32))
+    assert rel_l2(replayed.numpy(), oracle.quant_matvec_int4(x, p, s, z, K, N)) <= 1e-5
+
+    dev.destroy_exec(ex)
+    assert dev.workspace_generation() == (gen1, 0)   # freed with its last executable
+    # eager calls after the growth still agree
+    dev.Int4MatVec(a, w, replayed, stream)
+    dev.sync(stream)
+    assert np.array_equal(replayed.numpy().view(np.uint32), eager.numpy().view(np.uint32))
+    for b in (a, eager, replayed, ba, bo):
+        b.free()
+    w.free()
+    bw.free()
+    dev.destroy_stream(stream)
+
+
+def test_growth_inside_a_capture_is_refused(dev):
+    _reopen(dev)
+    rng = np.random.Generator(np.random.PCG64(32))
+    K, N = 1024, 1024
+    p, s, z = workloads.fast_int4(K, N, rng)
+    w = dev.upload_int4(p, s, z, K * N)
+    a = dev.upload(rng.standard_normal(K).astype(np.float32))
+    out = dev.alloc((N,), F32)
+    dev.Int4MatVec(a, w, out)
+    dev.sync()
+    gen0, _ = dev.workspace_generation()
+    ba, bw, bo = _big_matvec_args(dev)
+    stream = dev.stream()
+    dev.capture_begin(stream)
+    with pytest.raises(accel_amd.Refused, match="cannot grow inside a graph capture"):
+        dev.Int4MatVec(ba, bw, bo, stream)
+    ex = dev.capture_end(stream)
+    dev.destroy_exec(ex)
+    assert dev.workspace_generation()[0] == gen0
+    # outside the capture the same call grows the workspace and runs
+    dev.Int4MatVec(ba, bw, bo, stream)
+    dev.sync(stream)
+    assert dev.workspace_generation()[0] == gen0 + 1
+    for b in (a, out, ba, bo):
+        b.free()
+    w.free()
+    bw.free()
+    dev.destroy_stream(stream)
+
+
+def test_bounded_wait_that_gives_up_is_reported(dev):
+    # The matrix-core decode product (3..16 rows) hands its K slices to the
+    # last arriver, which waits (bounded) for the others' stores.
+    rng = np.random.Generator(np.random.PCG64(33))
+    M, K, N = 8, 4096, 4096
+    p, s, z = workloads.fast_int4(K, N, rng)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = dev.upload_int4(p, s, z, K * N)
+    a = dev.upload(x)
+    out = dev.alloc((M, N), F32)
+    want = oracle.quant_matmul_int4(x, p, s, z, M, K, N, threads=8)
+    dev.Int4MatMul(a, w, out)
+    dev.sync()
+    assert rel_l2(out.numpy(), want) <= 1e-5
+    try:
+        dev.set_wait_limit(0)             # every such wait gives up at once
+        dev.Int4MatMul(a, w, out)
+        with pytest.raises(accel_amd.AccelError, match="bounded wait gave up") as ei:
+            dev.sync()
+        assert ei.value.code == accel_amd.E_HIP
+        assert not dev.lost
+    finally:
+        dev.set_wait_limit(1 << 22)
+    dev.sync()                            # reported once, then cleared
+    for _ in range(2):
+        dev.Int4MatMul(a, w, out)
+        dev.sync()
+        assert rel_l2(out.numpy(), want) <= 1e-5
+    for b in (a, out):
+        b.free()
+    w.free()
+
+
+@pytest.mark.parametrize("M,K,N", [
+    (1, 4096, 4096), (1, 4096, 14336), (1, 14336, 4096), (1, 20000, 2048),
+    (2, 4096, 4096), (1, 4096, 1024), (1, 1024, 384),
+])
+def test_xcd_local_hand_off_equals_device_scope(dev, M, K, N):
+    """The decode product's split-K hand-off inside one XCD's L2 and through
+    the device's coherence point add the same values in the same order."""
+    rng = np.random.Generator(np.random.PCG64(M * 7 + K + N))
+    p, s, z = workloads.fast_int4(K, N, rng)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = dev.upload_int4(p, s, z, K * N)
+    a = dev.upload(x if M > 1 else x[0])
+    out = dev.alloc((M, N) if M > 1 else (N,), F32)
+    got = {}
+    try:
+        for local in (False, True, False, True):
+            try:
+                dev.set_xcd_local(local)
+            except accel_amd.AccelError as e:
+                assert e.code == accel_amd.E_UNSUPPORTED and local
+                continue
+            (dev.Int4MatMul if M > 1 else dev.Int4MatVec)(a, w, out)
+            dev.sync()
+            r = out.numpy().copy()
+            if local in got:
+                assert np.array_equal(got[local].view(np.uint32), r.view(np.uint32))
+            got[local] = r
+    finally:
+        try:
+            dev.set_xcd_local(True)
+        except accel_amd.AccelError:
+            pass
+    if True in got:
+        assert np.array_equal(got[True].view(np.uint32), got[False].view(np.uint32))
+    want = oracle.quant_matmul_int4(x, p, s, z, M, K, N, threads=8) if M > 1 else \
+        oracle.quant_matvec_int4(x[0], p, s, z, K, N)
+    assert rel_l2(got[False], want) <= 1e-5
+    for b in (a, out):
+        b.free()
+    w.free()
+
+
+def test_xcd_local_sets_equal_device_scope(dev):
+    rng = np.random.Generator(np.random.PCG64(77))
+    K, Ns = 4096, [4096, 1024, 1024]
+    x = rng.standard_normal(K).astype(np.float32)
+    xb = dev.upload(x)
+    planes = [workloads.fast_int4(K, N, rng) for N in Ns]
+    ws = [dev.upload_int4(p, s, z, K * N) for (p, s, z), N in zip(planes, Ns)]
+    outs = [dev.alloc((N,), F32) for N in Ns]
+    res = {}
+    try:
+        for local in (False, True):
+            try:
+                dev.set_xcd_local(local)
+            except accel_amd.AccelError:
+                continue
+            dev.Int4MatVecSet(xb, ws, outs)
+            dev.sync()
+            res[local] = [o.numpy().copy() for o in outs]
+    finally:
+        try:
+            dev.set_xcd_local(True)
+        except accel_amd.AccelError:
+            pass
+    for i, ((p, s, z), N) in enumerate(zip(planes, Ns)):
+        assert rel_l2(res[False][i], oracle.quant_matvec_int4(x, p, s, z, K, N)) <= 1e-5
+        if True in res:
+            assert np.array_equal(res[True][i].view(np.uint32), res[False][i].view(np.uint32))
+    for b in outs + [xb]:
+        b.free()
+    for w in ws:
+        w.free()
