@@ -122,7 +122,6 @@ SIGNATURES = {
     "accel_hip_exec_launch": ([_i, _vp, _vp], _i),
     "accel_hip_exec_destroy": ([_i, _vp], _i),
     "accel_hip_set_wait_limit": ([_i, ctypes.c_int32], _i),
-    "accel_hip_set_xcd_local": ([_i, _i], _i),
     "accel_hip_workspace_generation": ([_i, _P(ctypes.c_uint64), _P(ctypes.c_int32)], _i),
     "accel_hip_supports_kernel": ([ctypes.c_char_p], _i),
     "accel_hip_dispatch": ([_i, _vp, ctypes.c_char_p, _P(_vp), _P(ctypes.c_uint64),
@@ -396,11 +395,6 @@ class Device:
         """Spins a split-K hand-off's bounded wait may take before it gives up
         and reports the fault (a test hook)."""
         _check(_lib.accel_hip_set_wait_limit(self.index, spins))
-
-    def set_xcd_local(self, enable: bool) -> None:
-        """Whether the decode products keep their split-K hand-off inside one
-        XCD (the same results either way)."""
-        _check(_lib.accel_hip_set_xcd_local(self.index, 1 if enable else 0))
 
     def workspace_generation(self):
         """(allocations of the workspace so far, replaced workspaces still held

@@ -97,7 +97,7 @@ __device__ __forceinline__ void load_words(const uint32_t* p, uint32_t* w) {
 // batches.
 // One workgroup's share: column tile `tile` of the matrix, K slice `slice`;
 // `ticket` is this tile's split-K ticket.
-template <int M, int TILE, int CPL, bool PIPE, bool XL>
+template <int M, int TILE, int CPL, bool PIPE>
 __device__ __forceinline__ void decode_tile(
     const float* __restrict__ a, const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
@@ -228,52 +228,40 @@ __device__ __forceinline__ void decode_tile(
 #pragma unroll
             for (int w = 0; w < NWAVE; w++) sum += red[w][c];
             const int col = tile * TILE + c;
-            if (!split)
-                store_out(out, (size_t)m * N + col, col, sum, ep);
-            else if (XL)
-                partial[((size_t)slice * M + m) * N + col] = sum;
-            else
+            if (split)
                 store_device(&partial[((size_t)slice * M + m) * N + col], sum);
+            else
+                store_out(out, (size_t)m * N + col, col, sum, ep);
         }
         __syncthreads();
     }
     if (!split) return;
 
-    split_k_finish<XL>(partial, ticket, out, tile * TILE, TILE, M, N, slices, &last_flag, ep);
+    split_k_finish(partial, ticket, out, tile * TILE, TILE, M, N, slices, &last_flag, ep);
 }
 
-// Workgroup b's (tile, K slice).  XL: the slices of tile t all run on XCD
-// t % n_xcc (workgroup b runs on XCD b % n_xcc; tiles % n_xcc == 0), so the
-// split-K hand-off stays in that XCD's L2.  Otherwise consecutive workgroups
-// -- the tiles of one K slice, which share scale and zero rows, activations
-// and 128-byte code lines -- are placed on one XCD.
-template <bool XL>
-__device__ __forceinline__ void place(int b, int tiles, int slices, int n_xcc, uint32_t* fault,
-                                      int& tile, int& slice) {
-    if constexpr (XL) {
-        const int x = b % n_xcc, j = b / n_xcc;
-        tile = x + n_xcc * (j / slices);
-        slice = j % slices;
-        check_placement(x, fault);
-    } else {
-        const int grid = tiles * slices;
-        if ((grid & 7) == 0) b = (b & 7) * (grid >> 3) + (b >> 3);
-        tile = b % tiles;
-        slice = b / tiles;
-    }
+// Workgroup b's (tile, K slice): consecutive workgroups -- the tiles of one
+// K slice, which share scale and zero rows, activations and 128-byte code
+// lines -- are placed on one XCD (workgroups are dealt to the XCDs round
+// robin); the placement matters for speed only.
+__device__ __forceinline__ void place(int b, int tiles, int slices, int& tile, int& slice) {
+    const int grid = tiles * slices;
+    if ((grid & 7) == 0) b = (b & 7) * (grid >> 3) + (b >> 3);
+    tile = b % tiles;
+    slice = b / tiles;
 }
 
-template <int M, int TILE, int CPL, bool PIPE, bool XL>
+template <int M, int TILE, int CPL, bool PIPE>
 __global__ __launch_bounds__(kDecThreads) void int4_decode_f32_kernel(
     const float* __restrict__ a, const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
     void* __restrict__ out, float* partial, uint32_t* tickets, int ticket_stride, int K, int N,
-    int rows_per_slice, int slices, Epilogue ep, uint32_t* fault, int n_xcc) {
+    int rows_per_slice, int slices, Epilogue ep) {
     int tile, slice;
-    place<XL>(blockIdx.x, N / TILE, slices, n_xcc, fault, tile, slice);
-    decode_tile<M, TILE, CPL, PIPE, XL>(a, codes, scales, zeros, out, partial,
-                                        tickets + (size_t)tile * ticket_stride, K, N, tile,
-                                        slice, rows_per_slice, slices, ep);
+    place(blockIdx.x, N / TILE, slices, tile, slice);
+    decode_tile<M, TILE, CPL, PIPE>(a, codes, scales, zeros, out, partial,
+                                    tickets + (size_t)tile * ticket_stride, K, N, tile, slice,
+                                    rows_per_slice, slices, ep);
 }
 
 // Several matrices against one input in one launch (the q, k, v or gate, up
@@ -292,17 +280,17 @@ struct DecodeSet {
     int count;
 };
 
-template <int M, int TILE, int CPL, bool PIPE, bool XL>
+template <int M, int TILE, int CPL, bool PIPE>
 __global__ __launch_bounds__(kDecThreads) void int4_decode_set_kernel(
     const float* __restrict__ a, DecodeSet set, uint32_t* tickets, int ticket_stride, int K,
-    int rows_per_slice, int slices, uint32_t* fault, int n_xcc) {
+    int rows_per_slice, int slices) {
     int tg, slice;
-    place<XL>(blockIdx.x, set.tile0[set.count], slices, n_xcc, fault, tg, slice);
+    place(blockIdx.x, set.tile0[set.count], slices, tg, slice);
     int i = 0;
 #pragma unroll
     for (int j = 1; j < kMaxSet; j++)
         if (j < set.count && tg >= set.tile0[j]) i = j;
-    decode_tile<M, TILE, CPL, PIPE, XL>(a, set.codes[i], set.scales[i], set.zeros[i], set.out[i],
+    decode_tile<M, TILE, CPL, PIPE>(a, set.codes[i], set.scales[i], set.zeros[i], set.out[i],
                                     set.partial[i], tickets + (size_t)tg * ticket_stride, K,
                                     set.n[i], tg - set.tile0[i], slice, rows_per_slice, slices,
                                     Epilogue{});
@@ -346,19 +334,14 @@ hipError_t launch_decode(Device* d, hipStream_t st, const float* a, Int4Planes w
         tickets = static_cast<uint32_t*>(ws);
         partial = reinterpret_cast<float*>(static_cast<char*>(ws) + kWorkspaceCounterBytes);
     }
-    const bool xl = slices > 1 && d->xcd_local && tiles % d->n_xcc == 0;
-#define ACCEL_DECODE_LAUNCH(P, X)                                                            \
-    hipLaunchKernelGGL((int4_decode_f32_kernel<M, TILE, CPL, P, X>), dim3(tiles * slices),   \
-                       dim3(kDecThreads), 0, st, a, w.codes, w.scales, w.zeros, out, partial, \
-                       tickets, stride, K, N, rows, slices, ep, d->fault_dev, d->n_xcc)
-    if (per_slice > 1) {
-        if (xl) ACCEL_DECODE_LAUNCH(true, true);
-        else ACCEL_DECODE_LAUNCH(true, false);
-    } else {
-        if (xl) ACCEL_DECODE_LAUNCH(false, true);
-        else ACCEL_DECODE_LAUNCH(false, false);
-    }
-#undef ACCEL_DECODE_LAUNCH
+    if (per_slice > 1)
+        hipLaunchKernelGGL((int4_decode_f32_kernel<M, TILE, CPL, true>), dim3(tiles * slices),
+                           dim3(kDecThreads), 0, st, a, w.codes, w.scales, w.zeros, out, partial,
+                           tickets, stride, K, N, rows, slices, ep);
+    else
+        hipLaunchKernelGGL((int4_decode_f32_kernel<M, TILE, CPL, false>), dim3(tiles * slices),
+                           dim3(kDecThreads), 0, st, a, w.codes, w.scales, w.zeros, out, partial,
+                           tickets, stride, K, N, rows, slices, ep);
     return hipGetLastError();
 }
 
@@ -1387,19 +1370,12 @@ hipError_t launch_matvec_set(Device* d, hipStream_t st, const float* a, const In
             p += (size_t)slices * N[i];
         }
     }
-    const bool xl = slices > 1 && d->xcd_local && tiles % d->n_xcc == 0;
-#define ACCEL_SET_LAUNCH(P, X)                                                               \
-    hipLaunchKernelGGL((int4_decode_set_kernel<1, TILE, CPL, P, X>), dim3(tiles * slices),   \
-                       dim3(kDecThreads), 0, st, a, set, tickets, stride, K, rows, slices,    \
-                       d->fault_dev, d->n_xcc)
-    if (per_slice > 1) {
-        if (xl) ACCEL_SET_LAUNCH(true, true);
-        else ACCEL_SET_LAUNCH(true, false);
-    } else {
-        if (xl) ACCEL_SET_LAUNCH(false, true);
-        else ACCEL_SET_LAUNCH(false, false);
-    }
-#undef ACCEL_SET_LAUNCH
+    if (per_slice > 1)
+        hipLaunchKernelGGL((int4_decode_set_kernel<1, TILE, CPL, true>), dim3(tiles * slices),
+                           dim3(kDecThreads), 0, st, a, set, tickets, stride, K, rows, slices);
+    else
+        hipLaunchKernelGGL((int4_decode_set_kernel<1, TILE, CPL, false>), dim3(tiles * slices),
+                           dim3(kDecThreads), 0, st, a, set, tickets, stride, K, rows, slices);
     return hipGetLastError();
 }
 

@@ -22,7 +22,6 @@ void clear_error();
 // Bits of the device fault word: what a kernel reports when it gives up
 // instead of producing its result.
 constexpr uint32_t kFaultWaitGaveUp = 1u;     // a split-K hand-off's bounded wait ran out
-constexpr uint32_t kFaultPlacement = 2u;      // a workgroup ran on an XCD its plan did not assume
 
 // Per-device state: the open flag, sticky loss, fault injection, the
 // library-owned workspace and the fault word.
@@ -46,13 +45,10 @@ struct Device {
     std::vector<Retired> retired;
     std::unordered_map<void*, uint64_t> exec_gen;   // live executable -> workspace generation
     // Fault word: host memory the kernels write (system scope) when a bounded
-    // wait gives up or a placement check fails; read after every wait.
+    // wait gives up; read after every wait.
     uint32_t* fault_host = nullptr;
     uint32_t* fault_dev = nullptr;
     int32_t wait_limit = 1 << 22;   // spins of a hand-off's bounded wait
-    int n_xcc = 1;                  // XCDs (accelerator complexes) of the device
-    bool xcd_mapped = false;        // workgroup b runs on XCD b % n_xcc (probed at open)
-    bool xcd_local = false;         // hand-offs may stay inside one XCD's L2
     int cu_count = 256;
     size_t lds_per_block = 65536;
 };

@@ -13,23 +13,23 @@
 namespace accel {
 
 namespace {
-thread_local std::string g_last_error;
+// The calling thread's last message.  A fixed buffer: recording an error
+// allocates nothing.
+thread_local char g_last_error[1024];
 constexpr int kMaxDevices = 64;
 Device g_devices[kMaxDevices];
 std::mutex g_open_mu;
 }  // namespace
 
 int fail(int code, const char* fmt, ...) {
-    char buf[1024];
     va_list ap;
     va_start(ap, fmt);
-    vsnprintf(buf, sizeof buf, fmt, ap);
+    vsnprintf(g_last_error, sizeof g_last_error, fmt, ap);
     va_end(ap);
-    g_last_error = buf;
     return code;
 }
 
-void clear_error() { g_last_error.clear(); }
+void clear_error() { g_last_error[0] = '\0'; }
 
 Device* device(int dev) {
     if (dev < 0 || dev >= kMaxDevices) {
@@ -171,54 +171,13 @@ int take_fault(Device* d) {
         if (d->ws) (void)hipMemset(d->ws, 0, kWorkspaceCounterBytes);
         for (const auto& r : d->retired) (void)hipMemset(r.ptr, 0, kWorkspaceCounterBytes);
     }
-    std::string what;
-    if (f & kFaultWaitGaveUp) what += "a split-K hand-off's bounded wait gave up";
-    if (f & kFaultPlacement) {
-        if (!what.empty()) what += "; ";
-        what += "a workgroup ran on an XCD its launch plan did not assume";
-    }
-    if (f & ~(kFaultWaitGaveUp | kFaultPlacement)) {
-        if (!what.empty()) what += "; ";
-        what += "unknown fault bits";
-    }
+    const char* what = f == kFaultWaitGaveUp ? "a split-K hand-off's bounded wait gave up"
+                                              : "unknown fault bits";
     return fail(ACCEL_E_HIP,
                 "accel_hip: device fault word 0x%x (%s): the results of the work waited on "
                 "are undefined",
-                f, what.c_str());
+                f, what);
 }
-
-// XCD of each workgroup of a one-wave-per-workgroup probe grid.
-__global__ void xcc_probe_kernel(uint32_t* out) {
-    uint32_t x;
-    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
-    if (threadIdx.x == 0) out[blockIdx.x] = x;
-}
-
-namespace {
-
-// Whether workgroup b of a launch runs on XCD b % n_xcc, which the XCD-local
-// hand-offs rely on (the hardware deals workgroups to XCDs round robin).
-// Checked once per open on a probe grid; every launch that relies on it
-// checks its own workgroups again and reports kFaultPlacement otherwise.
-bool probe_xcd_mapping(int n_xcc) {
-    constexpr int kBlocks = 256;
-    uint32_t* buf = nullptr;
-    if (hipMalloc(&buf, kBlocks * sizeof(uint32_t)) != hipSuccess) return false;
-    bool ok = hipMemset(buf, 0xff, kBlocks * sizeof(uint32_t)) == hipSuccess;
-    if (ok) {
-        hipLaunchKernelGGL(xcc_probe_kernel, dim3(kBlocks), dim3(64), 0, nullptr, buf);
-        ok = hipGetLastError() == hipSuccess && hipDeviceSynchronize() == hipSuccess;
-    }
-    uint32_t host[kBlocks];
-    if (ok) ok = hipMemcpy(host, buf, sizeof host, hipMemcpyDeviceToHost) == hipSuccess;
-    (void)hipFree(buf);
-    if (!ok) return false;
-    for (int b = 0; b < kBlocks; b++)
-        if (host[b] != (uint32_t)(b % n_xcc)) return false;
-    return true;
-}
-
-}  // namespace
 
 }  // namespace accel
 
@@ -226,7 +185,7 @@ using namespace accel;
 
 #define ACCEL_API extern "C" __attribute__((visibility("default")))
 
-ACCEL_API const char* accel_hip_last_error(void) { return g_last_error.c_str(); }
+ACCEL_API const char* accel_hip_last_error(void) { return g_last_error; }
 
 ACCEL_API int accel_hip_abi_version(void) { return 1; }
 
@@ -298,13 +257,6 @@ ACCEL_API int accel_hip_open(int dev) {
         d->fault_dev = static_cast<uint32_t*>(dp);
     }
     *d->fault_host = 0;
-    int n_xcc = 1;
-    if (hipDeviceGetAttribute(&n_xcc, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess ||
-        n_xcc < 1)
-        n_xcc = 1;
-    d->n_xcc = n_xcc;
-    d->xcd_mapped = n_xcc > 1 && probe_xcd_mapping(n_xcc);
-    d->xcd_local = d->xcd_mapped;
     d->wait_limit = 1 << 22;
     d->ordinal = dev;
     d->cu_count = p.multiProcessorCount;
@@ -561,20 +513,6 @@ ACCEL_API int accel_hip_set_wait_limit(int dev, int32_t spins) {
     if (spins < 0) return fail(ACCEL_E_INVALID, "accel_hip_set_wait_limit: %d spins", spins);
     std::lock_guard<std::mutex> lk(d->mu);
     d->wait_limit = spins;
-    return ACCEL_OK;
-}
-
-ACCEL_API int accel_hip_set_xcd_local(int dev, int enable) {
-    clear_error();
-    Device* d = device(dev);
-    if (!d) return ACCEL_E_NO_DEVICE;
-    std::lock_guard<std::mutex> lk(d->mu);
-    if (enable && !d->xcd_mapped)
-        return fail(ACCEL_E_UNSUPPORTED,
-                    "accel_hip_set_xcd_local: workgroups of device %d are not dealt to its %d "
-                    "XCDs round robin, so no hand-off can stay inside one XCD",
-                    dev, d->n_xcc);
-    d->xcd_local = enable != 0;
     return ACCEL_OK;
 }
 

@@ -53,23 +53,14 @@ __device__ __forceinline__ float load_device(float* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // Split-K hand-off, called by every lane of a workgroup after it stored its
-// sums for columns [col0, col0 + cols) of slice `slice`: the stores are
-// acknowledged before the tile's ticket is drawn (each tile's ticket has a
-// 128-byte line of its own where the workspace allows, so the atomics of
-// different tiles do not queue behind each other), and the workgroup drawing
-// the last ticket reads all slices' sums, adds them in slice order (so the
+// sums for columns [col0, col0 + cols) of slice `slice` with store_device:
+// the stores are acknowledged by the device's coherence point before the
+// tile's ticket is drawn (each tile's ticket has a 128-byte line of its own
+// where the workspace allows, so the atomics of different tiles do not queue
+// behind each other), and the workgroup drawing the last ticket reads all
+// slices' sums with device-scope loads, adds them in slice order (so the
 // result does not depend on scheduling), writes `out` through the epilogue
 // and returns the ticket to zero for the next launch.
-//
-// Two forms of the same exchange.  Device scope (XL false): the sums were
-// stored with store_device and are read with device-scope loads, which go
-// through the device's coherence point, so the slices of a tile may run on
-// any XCDs.  XCD-local (XL true): every slice of the tile runs on one XCD, so
-// plain stores (the L1 writes through to that XCD's L2) and plain loads (the
-// reader's L1 has never held these lines in this launch) meet in that L2,
-// which is cheaper by about two device round trips.  Both add the same values
-// in the same order: the results are identical.
-template <bool XL = false>
 __device__ __forceinline__ void split_k_finish(float* partial, uint32_t* ticket, void* out,
                                                int col0, int cols, int M, int N, int slices,
                                                int* last_flag, const Epilogue& ep) {
@@ -97,8 +88,7 @@ __device__ __forceinline__ void split_k_finish(float* partial, uint32_t* ticket,
             float v[16];
 #pragma unroll
             for (int u = 0; u < 16; u++)
-                v[u] = XL ? p[(size_t)(sl + u) * slice_stride]
-                          : load_device(p + (size_t)(sl + u) * slice_stride);
+                v[u] = load_device(p + (size_t)(sl + u) * slice_stride);
 #pragma unroll
             for (int u = 0; u < 16; u++) sum += v[u];
         }
@@ -106,9 +96,7 @@ __device__ __forceinline__ void split_k_finish(float* partial, uint32_t* ticket,
             float v[16];
 #pragma unroll
             for (int u = 0; u < 16; u++)
-                v[u] = sl + u >= slices ? 0.0f
-                       : XL           ? p[(size_t)(sl + u) * slice_stride]
-                                      : load_device(p + (size_t)(sl + u) * slice_stride);
+                v[u] = sl + u < slices ? load_device(p + (size_t)(sl + u) * slice_stride) : 0.0f;
 #pragma unroll
             for (int u = 0; u < 16; u++)
                 if (sl + u < slices) sum += v[u];
@@ -117,20 +105,6 @@ __device__ __forceinline__ void split_k_finish(float* partial, uint32_t* ticket,
     }
     if (tid == 0)
         __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// The split-K slices of a tile share XCD `xcd` when workgroup b runs on XCD
-// b % n_xcc, which the host confirmed when it opened the device; each
-// workgroup checks its own placement again and reports a mismatch in the
-// fault word (its tile's sum is then undefined).
-__device__ __forceinline__ void check_placement(int xcd, uint32_t* fault) {
-    if (threadIdx.x == 0) {
-        uint32_t x;
-        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
-        if (x != (uint32_t)xcd)
-            __hip_atomic_fetch_or(fault, kFaultPlacement, __ATOMIC_RELAXED,
-                                  __HIP_MEMORY_SCOPE_SYSTEM);
-    }
 }
 
 // Cross-lane sums over the row phases of a wave.  A wave holds 64 / LPR row

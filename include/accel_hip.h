@@ -38,8 +38,8 @@
  * executable stays valid across later, larger eager calls.
  *
  * Faults.  A kernel that gives up instead of producing its result (a
- * split-K hand-off whose bounded wait runs out, a workgroup placed on an XCD
- * its plan did not assume) records it in the device's fault word; the next
+ * split-K hand-off whose bounded wait runs out) records it in the device's
+ * fault word; the next
  * stream_sync, event_sync or event_query that completes reports it as
  * ACCEL_E_HIP with a message, and clears it (the analogue of the
  * reference's per-node fault words read back by Fence.Wait,
@@ -162,15 +162,9 @@ int accel_hip_exec_destroy(int dev, void* exec);
  *    before it gives up and reports kFault "wait gave up" (default 1 << 22;
  *    0 makes every such wait give up at once, so a test can force the fault
  *    from the host while every kernel still exits normally).
- *  set_xcd_local: whether the decode products may keep their split-K
- *    hand-off inside one XCD's L2 (the default where open found workgroups
- *    dealt to XCDs round robin); 0 selects the device-scope hand-off, which
- *    gives the same results bit for bit.  ACCEL_E_UNSUPPORTED when enabling it
- *    on a device whose placement open could not confirm.
  *  workspace_generation: how many times the workspace has been allocated,
  *    and how many replaced workspaces live executables still hold. */
 int accel_hip_set_wait_limit(int dev, int32_t spins);
-int accel_hip_set_xcd_local(int dev, int enable);
 int accel_hip_workspace_generation(int dev, uint64_t* gen, int32_t* retired);
 
 /* KernelSupport.SupportsKernel (plan.go:424-428): 1 if the named reference

@@ -145,78 +145,3 @@ def test_bounded_wait_that_gives_up_is_reported(dev):
     for b in (a, out):
         b.free()
     w.free()
-
-
-@pytest.mark.parametrize("M,K,N", [
-    (1, 4096, 4096), (1, 4096, 14336), (1, 14336, 4096), (1, 20000, 2048),
-    (2, 4096, 4096), (1, 4096, 1024), (1, 1024, 384),
-])
-def test_xcd_local_hand_off_equals_device_scope(dev, M, K, N):
-    """The decode product's split-K hand-off inside one XCD's L2 and through
-    the device's coherence point add the same values in the same order."""
-    rng = np.random.Generator(np.random.PCG64(M * 7 + K + N))
-    p, s, z = workloads.fast_int4(K, N, rng)
-    x = rng.standard_normal((M, K)).astype(np.float32)
-    w = dev.upload_int4(p, s, z, K * N)
-    a = dev.upload(x if M > 1 else x[0])
-    out = dev.alloc((M, N) if M > 1 else (N,), F32)
-    got = {}
-    try:
-        for local in (False, True, False, True):
-            try:
-                dev.set_xcd_local(local)
-            except accel_amd.AccelError as e:
-                assert e.code == accel_amd.E_UNSUPPORTED and local
-                continue
-            (dev.Int4MatMul if M > 1 else dev.Int4MatVec)(a, w, out)
-            dev.sync()
-            r = out.numpy().copy()
-            if local in got:
-                assert np.array_equal(got[local].view(np.uint32), r.view(np.uint32))
-            got[local] = r
-    finally:
-        try:
-            dev.set_xcd_local(True)
-        except accel_amd.AccelError:
-            pass
-    if True in got:
-        assert np.array_equal(got[True].view(np.uint32), got[False].view(np.uint32))
-    want = oracle.quant_matmul_int4(x, p, s, z, M, K, N, threads=8) if M > 1 else \
-        oracle.quant_matvec_int4(x[0], p, s, z, K, N)
-    assert rel_l2(got[False], want) <= 1e-5
-    for b in (a, out):
-        b.free()
-    w.free()
-
-
-def test_xcd_local_sets_equal_device_scope(dev):
-    rng = np.random.Generator(np.random.PCG64(77))
-    K, Ns = 4096, [4096, 1024, 1024]
-    x = rng.standard_normal(K).astype(np.float32)
-    xb = dev.upload(x)
-    planes = [workloads.fast_int4(K, N, rng) for N in Ns]
-    ws = [dev.upload_int4(p, s, z, K * N) for (p, s, z), N in zip(planes, Ns)]
-    outs = [dev.alloc((N,), F32) for N in Ns]
-    res = {}
-    try:
-        for local in (False, True):
-            try:
-                dev.set_xcd_local(local)
-            except accel_amd.AccelError:
-                continue
-            dev.Int4MatVecSet(xb, ws, outs)
-            dev.sync()
-            res[local] = [o.numpy().copy() for o in outs]
-    finally:
-        try:
-            dev.set_xcd_local(True)
-        except accel_amd.AccelError:
-            pass
-    for i, ((p, s, z), N) in enumerate(zip(planes, Ns)):
-        assert rel_l2(res[False][i], oracle.quant_matvec_int4(x, p, s, z, K, N)) <= 1e-5
-        if True in res:
-            assert np.array_equal(res[True][i].view(np.uint32), res[False][i].view(np.uint32))
-    for b in outs + [xb]:
-        b.free()
-    for w in ws:
-        w.free()
