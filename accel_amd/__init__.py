@@ -128,6 +128,7 @@ SIGNATURES = {
                             ctypes.c_int32, _vp, _sz, _P(ctypes.c_uint32)], _i),
     "accel_int4_matvec": ([_i, _vp, _P(Tensor), _P(Int4Desc), _P(Tensor)], _i),
     "accel_int4_matmul": ([_i, _vp, _P(Tensor), _P(Int4Desc), _P(Tensor)], _i),
+    "accel_int4_matvec_noalloc": ([_i, _vp, _P(Tensor), _P(Int4Desc), _P(Tensor)], _i),
     "accel_int4_linear": ([_i, _vp, _P(Tensor), _P(Int4Desc), _P(Tensor), _P(Tensor)], _i),
     "accel_int4_matvec_set": ([_i, _vp, _P(Tensor), _P(Int4Desc), _P(Tensor), _i], _i),
     "accel_int4_matmul_set": ([_i, _vp, _P(Tensor), _P(Int4Desc), _P(Tensor), _i], _i),
@@ -480,6 +481,13 @@ class Device:
         ta, tw, to = a.tensor(), w.desc(), out.tensor()
         _check(_lib.accel_int4_matvec(self.index, stream, ctypes.byref(ta), ctypes.byref(tw),
                                       ctypes.byref(to)))
+
+    def Int4MatVecNoAlloc(self, a: Buffer, w: Int4Weights, out: Buffer, stream=None) -> None:
+        """Int4MatVec with its split-K buffers in the library's static scratch
+        (allocates nothing; calls that overlap on one GPU race)."""
+        ta, tw, to = a.tensor(), w.desc(), out.tensor()
+        _check(_lib.accel_int4_matvec_noalloc(self.index, stream, ctypes.byref(ta),
+                                              ctypes.byref(tw), ctypes.byref(to)))
 
     def Int4MatMul(self, a: Buffer, w: Int4Weights, out: Buffer, stream=None) -> None:
         ta, tw, to = a.tensor(), w.desc(), out.tensor()

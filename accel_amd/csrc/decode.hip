@@ -302,7 +302,8 @@ __global__ __launch_bounds__(kDecThreads) void int4_decode_set_kernel(
 // hand-off's reads.
 template <int M, int TILE, int CPL>
 hipError_t launch_decode(Device* d, hipStream_t st, const float* a, Int4Planes w,
-                         void* out, int K, int N, int* status, Epilogue ep) {
+                         void* out, int K, int N, int* status, Epilogue ep,
+                         void* fixed_scratch = nullptr) {
     constexpr int LPR = TILE / CPL;
     constexpr int RP = kDecThreads / LPR;
     constexpr int kRowsPerBatch = kBatch * RP;
@@ -329,8 +330,21 @@ hipError_t launch_decode(Device* d, hipStream_t st, const float* a, Int4Planes w
                            "decode product: N=%d needs more tickets than the workspace holds", N);
             return hipSuccess;
         }
-        void* ws = workspace(d, st, (size_t)slices * M * N * sizeof(float), status);
-        if (!ws) return hipSuccess;
+        const size_t bytes = (size_t)slices * M * N * sizeof(float);
+        void* ws = nullptr;
+        if (fixed_scratch) {
+            if (kWorkspaceCounterBytes + bytes > kScratchBytes) {
+                *status = fail(ACCEL_E_INVALID,
+                               "Int4MatVecNoAlloc: K=%d, N=%d needs %zu bytes of split-K sums "
+                               "and the static scratch holds %zu",
+                               K, N, bytes, kScratchBytes - kWorkspaceCounterBytes);
+                return hipSuccess;
+            }
+            ws = fixed_scratch;
+        } else {
+            ws = workspace(d, st, bytes, status);
+            if (!ws) return hipSuccess;
+        }
         tickets = static_cast<uint32_t*>(ws);
         partial = reinterpret_cast<float*>(static_cast<char*>(ws) + kWorkspaceCounterBytes);
     }
@@ -1490,6 +1504,46 @@ hipError_t launch_int4_decode_f32(Device* d, hipStream_t st, const float* a, Int
     if (e != hipSuccess || *status != ACCEL_OK) return e;
     char* rest = static_cast<char*>(out) + (size_t)8 * N * (ep.bf16 ? 2 : 4);
     return launch_int4_decode_f32(d, st, a + (size_t)8 * K, w, rest, M - 8, K, N, status, ep);
+}
+
+// ---- the no-allocation Int4MatVec -----------------------------------------
+//
+// A caller that cannot allocate (code under graph capture, a serving loop
+// that must not call hipMalloc) gets Int4MatVec with its split-K tickets and
+// partial sums in this file-scope array instead of the library's workspace.
+// Each GPU holds its own copy until the process ends.  In host code the name
+// `scratch` is only a stand-in; the device address of this GPU's copy comes
+// from hipGetSymbolAddress (init_scratch, at open) and is what every launch
+// receives.  Every call on one GPU shares the array: calls that overlap on a
+// GPU race.  The tickets start at zero (cleared at open) and each launch's
+// consumer returns its own to zero.
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+int init_scratch(Device* d) {
+    void* ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return classify(d, e, "hipGetSymbolAddress(scratch)");
+    e = hipMemset(ptr, 0, kWorkspaceCounterBytes);
+    if (e != hipSuccess) return classify(d, e, "scratch ticket clear");
+    e = hipDeviceSynchronize();
+    if (e != hipSuccess) return classify(d, e, "scratch ticket clear");
+    d->scratch = ptr;
+    return ACCEL_OK;
+}
+
+hipError_t launch_int4_matvec_noalloc(Device* d, hipStream_t st, const float* a, Int4Planes w,
+                                      float* out, int K, int N, int* status) {
+    *status = ACCEL_OK;
+    if (!d->scratch) {
+        *status = fail(ACCEL_E_HIP, "Int4MatVecNoAlloc: the device's static scratch was not "
+                                    "resolved when it was opened");
+        return hipSuccess;
+    }
+    if (!int4_decode_f32_supported(1, K, N, w.codes))
+        return launch_int4_generic_f32(st, a, w, out, 1, K, N, Epilogue{});   // no scratch
+    if (N % 256 == 0)
+        return launch_decode<1, 256, 32>(d, st, a, w, out, K, N, status, Epilogue{}, d->scratch);
+    return launch_decode<1, 128, 32>(d, st, a, w, out, K, N, status, Epilogue{}, d->scratch);
 }
 
 hipError_t launch_int4_generic_f32(hipStream_t st, const float* a, Int4Planes w, void* out,

@@ -49,6 +49,9 @@ struct Device {
     uint32_t* fault_host = nullptr;
     uint32_t* fault_dev = nullptr;
     int32_t wait_limit = 1 << 22;   // spins of a hand-off's bounded wait
+    // This device's copy of the no-allocation entry point's static scratch
+    // (its device address, from hipGetSymbolAddress at open).
+    void* scratch = nullptr;
     int cu_count = 256;
     size_t lds_per_block = 65536;
 };
@@ -96,6 +99,17 @@ struct Epilogue {
     const float* bias = nullptr;
     bool bf16 = false;
 };
+
+// The no-allocation Int4MatVec's static scratch: split-K tickets (the first
+// kWorkspaceCounterBytes), then partial sums.  init_scratch resolves this
+// device's copy (call with the device current, once per open).
+constexpr size_t kScratchBytes = kWorkspaceCounterBytes + (size_t(4) << 20);
+int init_scratch(Device* d);
+// Int4MatVec (a f32 [K] -> out f32 [N]) with any cross-workgroup buffer
+// taken from the static scratch instead of the workspace; refuses
+// (ACCEL_E_INVALID) a shape whose split-K sums exceed it.  Allocates nothing.
+hipError_t launch_int4_matvec_noalloc(Device* d, hipStream_t st, const float* a, Int4Planes w,
+                                      float* out, int K, int N, int* status);
 
 // Decode product, M <= 16 rows of f32 activations -> out (f32, or bf16 with
 // ep.bf16).

@@ -182,6 +182,25 @@ ACCEL_API int accel_int4_matvec(int dev, void* stream, const accel_tensor_t* a,
                             (int)k, (int)n);
 }
 
+// Int4MatVec without allocating: the same checks and kernels, with the
+// split-K buffers in the library's static scratch.
+ACCEL_API int accel_int4_matvec_noalloc(int dev, void* stream, const accel_tensor_t* a,
+                                        const accel_int4_t* w, accel_tensor_t* out) {
+    clear_error();
+    int64_t k = 0, n = 0;
+    const int rc = check_matvec("Int4MatVecNoAlloc", a, w, out, &k, &n);
+    if (rc != ACCEL_OK) return rc;
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    int status = begin_submission(d);
+    if (status != ACCEL_OK) return status;
+    if (n == 0) return ACCEL_OK;
+    const hipError_t e = launch_int4_matvec_noalloc(
+        d, (hipStream_t)stream, static_cast<const float*>(a->data), planes(w),
+        static_cast<float*>(out->data), (int)k, (int)n, &status);
+    return finish(d, e, status, "Int4MatVecNoAlloc launch");
+}
+
 // Int4MatVec over several matrices that share one input vector, in one
 // launch where they all take the decode kernel (the q, k, v or gate, up
 // products of a decode step); each result is its own Int4MatVec's.

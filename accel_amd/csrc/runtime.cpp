@@ -170,6 +170,7 @@ int take_fault(Device* d) {
         std::lock_guard<std::mutex> lk(d->mu);
         if (d->ws) (void)hipMemset(d->ws, 0, kWorkspaceCounterBytes);
         for (const auto& r : d->retired) (void)hipMemset(r.ptr, 0, kWorkspaceCounterBytes);
+        if (d->scratch) (void)hipMemset(d->scratch, 0, kWorkspaceCounterBytes);
     }
     const char* what = f == kFaultWaitGaveUp ? "a split-K hand-off's bounded wait gave up"
                                               : "unknown fault bits";
@@ -257,6 +258,10 @@ ACCEL_API int accel_hip_open(int dev) {
         d->fault_dev = static_cast<uint32_t*>(dp);
     }
     *d->fault_host = 0;
+    if (!d->scratch) {
+        const int rc = init_scratch(d);
+        if (rc != ACCEL_OK) return rc;
+    }
     d->wait_limit = 1 << 22;
     d->ordinal = dev;
     d->cu_count = p.multiProcessorCount;

@@ -284,6 +284,18 @@ int accel_int4_repack(int dev, void* stream, const accel_foreign_int4_t* src,
 int accel_int4_matvec(int dev, void* stream, const accel_tensor_t* a,
                       const accel_int4_t* w, accel_tensor_t* out);
 
+/* Int4MatVec that allocates nothing: the same checks, kernels and results
+ * (bit for bit) as accel_int4_matvec, with the K-split's tickets and partial
+ * sums in a static device array of 4 MiB + 64 KiB that every GPU the library
+ * runs on holds until the process ends, instead of the workspace (which may
+ * call hipMalloc to grow).  No counterpart in the reference: it is for
+ * callers that cannot allocate (code under graph capture, serving loops,
+ * harnesses that forbid hipMalloc).  Refused (ACCEL_E_INVALID) when the
+ * shape's split-K sums exceed 4 MiB (e.g. N > 16384 at K >= 16384).  Calls
+ * that overlap on one GPU share the array and race; serialize them. */
+int accel_int4_matvec_noalloc(int dev, void* stream, const accel_tensor_t* a,
+                              const accel_int4_t* w, accel_tensor_t* out);
+
 /* Int4MatVec over `count` (1..4) matrices w[i] that share one f32 vector a
  * [K], out[i] f32 [N_i], in one launch per tile width (N_i a multiple of 256,
  * or of 128 only) where every matrix takes the decode kernel (N_i a multiple
