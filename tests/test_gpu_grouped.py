@@ -170,7 +170,13 @@ def test_int4_grouped_matches_the_oracle(dev, bf16, form, E, K, N, counts, pad):
         assert np.all(got[covered:] == 7.0)
 
 
-def test_config4_moe_full_size_sampled(dev):
+def test_config4_moe_full_size(dev):
+    """Config 4 at full size (1024 routed rows, 8 experts of [4096, 14336]):
+    every row through two per-expert f64 checksums of the output columns, the
+    plain column sum and one weighted by the row's position in its segment
+    (which a dropped, duplicated or misplaced row changes), plus the first and
+    last row of every expert and 64 seeded rows against the oracle row for
+    row."""
     m = workloads.moe()
     R = int(m.counts.sum())
     assert R == 1024
@@ -179,20 +185,30 @@ def test_config4_moe_full_size_sampled(dev):
     cb = dev.upload(m.counts, U32)
     ob = dev.alloc((R, m.N), BF16)
     dev.Int4GroupedMatMul(xb, w, m.E, cb, ob)
-    got = workloads.bf16_to_f32(ob.numpy())
+    got = workloads.bf16_to_f32(ob.numpy()).astype(np.float64)
     off = oracle.segment_offsets(m.counts)
-    # the first and last rows of every expert's segment, against the oracle
+    rng = np.random.Generator(np.random.PCG64(44))
+    sampled = set(rng.choice(R, 64, replace=False).tolist())
     for e in range(m.E):
-        if off[e] == off[e + 1]:
+        lo, hi = int(off[e]), int(off[e + 1])
+        if lo == hi:
             continue
-        rows = np.unique([off[e], off[e + 1] - 1])
         base = e * m.K * m.N
         pe = m.packed[base // 8:(base + m.K * m.N) // 8]
         se = m.scales[base // 128:(base + m.K * m.N) // 128]
         ze = m.zeros[base // 128:(base + m.K * m.N) // 128]
+        wdq = oracle.dequantized(pe, se, ze, m.K * m.N).reshape(m.K, m.N).astype(np.float64)
+        xs = m.x[lo:hi].astype(np.float64)
+        pos = np.arange(1, hi - lo + 1, dtype=np.float64)[:, None]
+        for weights in (np.ones_like(pos), pos):
+            want = (weights * xs).sum(axis=0) @ wdq
+            have = (weights * got[lo:hi]).sum(axis=0)
+            assert rel_l2(have, want) <= 2e-2, (e, rel_l2(have, want))
+        rows = sorted({lo, hi - 1} | {r for r in sampled if lo <= r < hi})
         want = oracle.quant_matmul_int4(np.ascontiguousarray(m.x[rows]), pe, se, ze,
-                                        len(rows), m.K, m.N, threads=8)
+                                        len(rows), m.K, m.N, threads=16)
         assert rel_l2(got[rows], oracle.round_bf16(want)) <= 2e-2
+        del wdq
     for b in (xb, cb, ob):
         b.free()
     w.free()

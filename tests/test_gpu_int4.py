@@ -110,6 +110,8 @@ SHAPES_F32 = [
     # steps, several slices, the layer chain's down projection
     (4, 4096, 4096), (9, 1024, 384), (11, 2048, 768), (15, 14336, 4096), (16, 96, 256),
     (6, 32, 128), (10, 4096, 1024),
+    # config 5 at batch 8: q/o [4096,4096] and down [14336,4096] at their own size
+    (8, 4096, 4096), (8, 14336, 4096),
 ]
 
 

@@ -41,9 +41,9 @@ def test_set_equals_separate_matvecs(dev, K, Ns):
         dev.Int4MatVecSet(xb, list(ws), outs)
         for o, want in zip(outs, singles):
             assert np.array_equal(o.numpy().view(np.uint32), want.view(np.uint32))
-    # and against the oracle, for one matrix
-    p, s, z = planes[0]
-    assert rel_l2(outs[0].numpy(), oracle.quant_matvec_int4(x, p, s, z, K, Ns[0])) <= 1e-5
+    # and every matrix against the oracle
+    for o, (p, s, z), N in zip(outs, planes, Ns):
+        assert rel_l2(o.numpy(), oracle.quant_matvec_int4(x, p, s, z, K, N)) <= 1e-5
     for b in list(outs) + [xb]:
         b.free()
     for w in ws:
@@ -75,9 +75,8 @@ def test_matmul_set_equals_separate_matmuls(dev, M, K, Ns):
         dev.Int4MatMulSet(xb, list(ws), outs)
         for o, want in zip(outs, singles):
             assert np.array_equal(o.numpy().view(np.uint32), want.view(np.uint32))
-    p, s, z = planes[-1]
-    assert rel_l2(outs[-1].numpy(),
-                  oracle.quant_matmul_int4(x, p, s, z, M, K, Ns[-1])) <= 1e-5
+    for o, (p, s, z), N in zip(outs, planes, Ns):
+        assert rel_l2(o.numpy(), oracle.quant_matmul_int4(x, p, s, z, M, K, N, threads=8)) <= 1e-5
     for b in list(outs) + [xb]:
         b.free()
     for w in ws:
