@@ -2,29 +2,38 @@
 """Benchmark of the int4 weight-only linear path on one MI355X.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-extra]
-                    [--configs]
+                    [--configs] [--eager]
 
 Headline (the M=1 leg of BASELINE.json's metric): the decode product
 Int4MatVec at M=1, K=N=4096, in the reference's int4 format (128-weight
 groups, f16 scale and zero), f32 activations and output.  One step is one
-product.  The weights rotate over enough device copies (> 512 MB in all)
-that the 256 MB Infinity Cache cannot hold them, so each step reads its
-weights from HBM.  K steps are captured into one HIP graph and replayed,
+product.  The weights rotate over device copies totalling more than 512 MB,
+and the device's 256 MB Infinity Cache is flushed (a 512 MiB device copy,
+untimed) before every timed replay, so each step reads its weights from HBM
+at any --steps.  K steps are captured into one HIP graph and replayed,
 bracketed by HIP events on the stream they run on; ``value`` is algorithmic
 bytes per step over the per-step time, and ``roofline`` prices the same
-kernel against the HBM peak.  ``roofline.traffic`` is the HBM bytes a
-launch of that kernel moves, from the rocprofv3 FETCH_SIZE / WRITE_SIZE
-summary committed under profiles/ (null when absent).
+kernel against the HBM peak.  ``roofline.traffic`` is the HBM bytes a launch
+of that kernel moves, from the rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+committed under profiles/ (null when absent).
 
-The M=2048 leg of the metric (bf16 prefill product on the matrix cores,
-TFLOP/s against the dense bf16 peak) is reported under ``extra`` with a
-roofline object of its own.  ``--configs`` adds the other BASELINE shapes
-(M=16 decode, the ragged MoE product, the layer chain) to ``extra``.
-``cpu_baseline`` is the oracle's restatement of the reference CPU
-backend's algorithm (``oracle/``), timed on this host's cores on a bounded
-sample of the headline workload.
+``extra`` holds every other BASELINE config, each with a roofline object of
+its own and CPU baselines beside it: the M=2048 leg of the metric (config 3,
+bf16 prefill on the matrix cores, TFLOP/s against the dense bf16 peak),
+config 2 (M=16 decode), config 4 (the ragged MoE product), config 5 (the
+seven-product layer chain at batch 1 and 8, weights rotated over five sets),
+and the reference's own published workload (Int4MatVec 2048 x 2048, one
+submission waited for per step), which ``vs_baseline`` compares with the
+published 0.76 ms.  ``--configs`` adds the widened rows (int8, the f16
+matvec, the fused Linear, the repack, whole decode steps).  ``--eager``
+times plain stream launches instead of graph replays (for profiler runs).
 
-Prints one JSON line.
+``cpu_baseline`` is the oracle's restatement of the reference CPU backend's
+algorithm (``oracle/``), timed on this host's cores on a bounded sample of
+the headline workload; ``extra.cpu_baselines`` does the same for configs 2-5
+at 16 threads and at one thread.
+
+Prints one JSON line on stdout; progress goes to stderr.
 """
 from __future__ import annotations
 
@@ -44,6 +53,15 @@ ROTATE_BYTES = 544 << 20       # weight copies in rotation, > 2x the Infinity Ca
 TRAFFIC_FILE = os.path.join(HERE, "profiles", "traffic.json")
 GEMV_KERNEL = "int4_decode_f32_kernel<1, 256, 32, false>"
 GEMM_KERNEL = "int4_gemm_bf16_kernel<false>"
+DECODE_MFMA_KERNEL = "int4_decode_mfma_kernel<2, 8>"
+GROUPED_KERNEL = "int4_grouped_bf16_kernel"
+FLUSH_BYTES = 512 << 20        # device copy that evicts the Infinity Cache
+PUBLISHED_US = 760.0           # Int4MatVec [2048] x [2048,2048] on an M2, one plan a step
+PUBLISHED_SRC = "specs/010-kernel-corpus.md:593-602 (tensor/decodebench_darwin_test.go:148-189)"
+
+
+def progress(msg: str) -> None:
+    print(f"bench: {msg}", file=sys.stderr, flush=True)
 
 
 def parse():
@@ -56,6 +74,8 @@ def parse():
     ap.add_argument("--configs", action="store_true",
                     help="also time BASELINE configs 2, 4 and 5 (slower)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--eager", action="store_true",
+                    help="time plain stream launches, not graph replays (profiler runs)")
     return ap.parse_args()
 
 
@@ -75,37 +95,81 @@ def traffic_of(kernel: str):
         return None
 
 
+class Flusher:
+    """Evicts the Infinity Cache with an untimed 512 MiB device-to-device copy,
+    so that the replay timed after it reads its weights from HBM."""
+
+    def __init__(self, dev):
+        import accel_amd
+        self.dev = dev
+        self.src = dev.alloc((FLUSH_BYTES // 4,), accel_amd.U32)
+        self.dst = dev.alloc((FLUSH_BYTES // 4,), accel_amd.U32)
+
+    def __call__(self, stream):
+        import accel_amd
+        accel_amd._check(accel_amd.lib().accel_hip_copy(self.dev.index, stream, self.dst.ptr,
+                                                        self.src.ptr, FLUSH_BYTES))
+
+    def free(self):
+        self.src.free()
+        self.dst.free()
+
+
+_FLUSH = None
+EAGER = False
+
+
+def flush(dev, stream):
+    global _FLUSH
+    if _FLUSH is None:
+        _FLUSH = Flusher(dev)
+    _FLUSH(stream)
+
+
 class Timed:
     """Captures `count` calls of `issue(i)` into a graph and times replays
-    with HIP events on the stream the graph runs on."""
+    with HIP events on the stream the graph runs on (or, with EAGER, issues
+    the calls as plain launches between the events).  The Infinity Cache is
+    flushed before every timed run."""
 
     def __init__(self, dev, stream, issue, count):
-        self.dev, self.stream = dev, stream
-        dev.capture_begin(stream)
-        for i in range(count):
-            issue(i)
-        self.exec = dev.capture_end(stream)
+        self.dev, self.stream, self.issue, self.count = dev, stream, issue, count
+        self.exec = None
+        if not EAGER:
+            dev.capture_begin(stream)
+            for i in range(count):
+                issue(i)
+            self.exec = dev.capture_end(stream)
         self.e0, self.e1 = dev.event(), dev.event()
         self.warm = False
 
+    def _once(self):
+        if self.exec is not None:
+            self.dev.launch(self.exec, self.stream)
+        else:
+            for i in range(self.count):
+                self.issue(i)
+
     def run(self, replays: int = 1) -> float:
-        """Milliseconds for `replays` replays of the graph, timed after one
-        untimed replay (the first launch of a graph also uploads it)."""
+        """Milliseconds for `replays` runs of the K calls, timed after one
+        untimed run (the first launch of a graph also uploads it)."""
         d = self.dev
         if not self.warm:
-            d.launch(self.exec, self.stream)
+            self._once()
             self.warm = True
+        flush(d, self.stream)
         d.sync(self.stream)
         d.record(self.e0, self.stream)
         for _ in range(replays):
-            d.launch(self.exec, self.stream)
+            self._once()
         d.record(self.e1, self.stream)
         d.wait(self.e1)
         d.sync(self.stream)
         return d.elapsed_ms(self.e0, self.e1)
 
     def close(self):
-        self.dev.destroy_exec(self.exec)
+        if self.exec is not None:
+            self.dev.destroy_exec(self.exec)
         self.dev.destroy_event(self.e0)
         self.dev.destroy_event(self.e1)
 
@@ -186,52 +250,83 @@ def bench_gemm(dev, stream, name, steps=40, warmup=4):
 
 
 def bench_moe(dev, stream, steps=20):
-    """Config 4: Int4GroupedMatMul over 1024 routed bf16 rows, 8 experts."""
+    """Config 4: Int4GroupedMatMul over 1024 routed bf16 rows, 8 experts.  The
+    experts' weights (250 MB) rotate over three copies (750 MB), so with the
+    cache flushed before the timed replay every call reads them from HBM."""
     from accel_amd import BF16, U32, workloads
+    progress("config 4: routing and quantizing eight experts")
     m = workloads.moe_fast()
     R = int(m.counts.sum())
-    w = dev.upload_int4(m.packed, m.scales, m.zeros, m.E * m.K * m.N)
+    copies = 3
+    ws = [dev.upload_int4(m.packed, m.scales, m.zeros, m.E * m.K * m.N) for _ in range(copies)]
     xb = dev.upload(workloads.bf16_bits(m.x), BF16)
     cb = dev.upload(m.counts, U32)
     ob = dev.alloc((R, m.N), BF16)
-    dev.Int4GroupedMatMul(xb, w, m.E, cb, ob, stream=stream)
+    for w in ws:
+        dev.Int4GroupedMatMul(xb, w, m.E, cb, ob, stream=stream)
     dev.sync(stream)
-    t = Timed(dev, stream, lambda i: dev.Int4GroupedMatMul(xb, w, m.E, cb, ob, stream=stream),
+    t = Timed(dev, stream,
+              lambda i: dev.Int4GroupedMatMul(xb, ws[i % copies], m.E, cb, ob, stream=stream),
               steps)
     ms = median_replay(t) / steps
     t.close()
     flops = 2.0 * R * m.K * m.N
+    wbytes = m.packed.nbytes + m.scales.nbytes + m.zeros.nbytes
+    nbytes = wbytes + R * m.K * 2 + R * m.N * 2
     for b in (xb, cb, ob):
         b.free()
-    w.free()
-    return dict(us=round(ms * 1e3, 2), tflops=round(flops / (ms * 1e-3) / 1e12, 1),
-                rows=R, experts=m.E)
+    for w in ws:
+        w.free()
+    tflops = flops / (ms * 1e-3) / 1e12
+    return dict(workload=f"Int4GroupedMatMul: {R} routed bf16 rows (512 tokens, top-2 of 8 "
+                         f"experts, seed 3), K={m.K}, N={m.N}, bf16 out; expert weights "
+                         f"rotated over {copies} copies",
+                us=round(ms * 1e3, 2), rows=R, experts=m.E,
+                counts=[int(c) for c in m.counts],
+                roofline={"bound": "mfma", "achieved": round(tflops, 1),
+                          "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                          "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                          "traffic": traffic_of(GROUPED_KERNEL), "kernel": GROUPED_KERNEL,
+                          "flops_per_launch": int(flops), "bytes_per_launch": int(nbytes),
+                          "hbm_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)})
 
 
 _LAYER_PLANES = {}
 
 
-def bench_layer_chain(dev, stream, batch, steps=100, merged=False):
+def layer_planes(rng):
+    """Config 5's seven weights (seed 4's stream, after x and the gains)."""
+    from accel_amd import workloads
+    if not _LAYER_PLANES:
+        for name, (K, N) in workloads.LAYER_SHAPES.items():
+            _LAYER_PLANES[name] = workloads.fast_int4(K, N, rng)
+    return _LAYER_PLANES
+
+
+def bench_layer_chain(dev, stream, batch, steps=100, merged=True, sets=5):
     """Config 5: one Llama-3-8B-shaped decoder layer's seven int4 products
     as a decode step: q,k,v <- x; o <- q; gate,up <- o; down <- gate*up
     (the gate*up product is the caller's; the step times the seven
     products, chained on one stream).  merged: q, k, v and gate, up each as
-    one set (four launches, the same results bit for bit)."""
-    import accel_amd
+    one set (four launches, the same results bit for bit).  The layer's
+    115.9 MB of weights rotate over `sets` copies (580 MB), so with the cache
+    flushed before the timed replay each step reads its weights from HBM."""
     from accel_amd import F32, workloads
     shapes = workloads.LAYER_SHAPES  # name -> (K, N)
     rng = np.random.Generator(np.random.PCG64(4))
     x = rng.standard_normal((batch, 4096)).astype(np.float32)
-    if not _LAYER_PLANES:
-        for name, (K, N) in shapes.items():
-            _LAYER_PLANES[name] = workloads.fast_int4(K, N, rng)
-    ws, bufs = {}, {}
+    rng.standard_normal(4096)   # the two RMSNorm gains of the decode step
+    rng.standard_normal(4096)
+    planes = layer_planes(rng)
+    wsets, bufs = [], {}
     total_bytes = 0
     for name, (K, N) in shapes.items():
-        packed, scales, zeros = _LAYER_PLANES[name]
-        ws[name] = dev.upload_int4(packed, scales, zeros, K * N)
+        packed, scales, zeros = planes[name]
         total_bytes += packed.nbytes + scales.nbytes + zeros.nbytes
         bufs[name] = dev.alloc((batch, N) if batch > 1 else (N,), F32)
+    for _ in range(sets):
+        wsets.append({name: dev.upload_int4(*planes[name], K * N)
+                      for name, (K, N) in shapes.items()})
     xin = dev.upload(x if batch > 1 else x[0])
     # the down projection's input (the caller's gate*up), as activations
     hmid = rng.standard_normal((batch, 14336)).astype(np.float32)
@@ -243,7 +338,7 @@ def bench_layer_chain(dev, stream, batch, steps=100, merged=False):
         else:
             dev.Int4MatVec(a, w, o, stream)
 
-    def ops(a, names):
+    def ops(a, ws, names):
         if merged:
             fn = dev.Int4MatVecSet if batch == 1 else dev.Int4MatMulSet
             fn(a, [ws[n] for n in names], [bufs[n] for n in names], stream)
@@ -252,23 +347,83 @@ def bench_layer_chain(dev, stream, batch, steps=100, merged=False):
                 op(a, ws[n], bufs[n])
 
     def step(i):
-        ops(xin, ("q", "k", "v"))
+        ws = wsets[i % sets]
+        ops(xin, ws, ("q", "k", "v"))
         op(bufs["q"], ws["o"], bufs["o"])
-        ops(bufs["o"], ("gate", "up"))
+        ops(bufs["o"], ws, ("gate", "up"))
         op(inter, ws["down"], bufs["down"])
 
-    step(0)
+    for i in range(sets):
+        step(i)
     dev.sync(stream)
     t = Timed(dev, stream, step, steps)
     ms = median_replay(t) / steps
     t.close()
-    for w in ws.values():
-        w.free()
+    for ws in wsets:
+        for w in ws.values():
+            w.free()
     for b in list(bufs.values()) + [xin, inter]:
         b.free()
-    return dict(us_per_step=round(ms * 1e3, 2),
-                gbs=round(total_bytes / (ms * 1e-3) / 1e9, 1),
-                weight_bytes=total_bytes, batch=batch, launches=4 if merged else 7)
+    act = 4 * batch * (4096 + 4096 + 4096 + 14336) + 4 * batch * (4096 + 1024 + 1024 + 4096
+                                                                   + 14336 + 14336 + 4096)
+    gbs = (total_bytes + act) / (ms * 1e-3) / 1e9
+    kernels = ("int4_decode_set_kernel + int4_decode_f32_kernel (VALU decode)" if batch == 1
+               else "int4_decode_mfma_set_kernel + int4_decode_mfma_kernel (matrix-core decode)")
+    return dict(workload=f"config 5: seven Llama-3-8B layer products as one decode step at "
+                         f"batch {batch} (q/k/v and gate/up as sets, {4 if merged else 7} "
+                         f"launches), f32 x, weights rotated over {sets} sets",
+                us_per_step=round(ms * 1e3, 2), batch=batch, launches=4 if merged else 7,
+                weight_bytes=total_bytes,
+                roofline={"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                          "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                          "traffic": None, "kernel": kernels,
+                          "bytes_per_step": int(total_bytes + act)})
+
+
+def bench_published(dev, stream, steps=200):
+    """The reference's published decode benchmark, BenchmarkDecodeInt4MatMulOnMetal
+    (tensor/decodebench_darwin_test.go:148-189): Int4MatVec of x[i] = (i%7)*0.25
+    against a [2048, 2048] weight w[i] = (i%13)*0.125 - 0.75 packed by
+    Int4Quantize, one submission waited for per step, so the host's part is
+    in the figure (0.76 ms on an M2, specs/010-kernel-corpus.md:593-602).
+    Timed the same way here: one Int4MatVec call and one stream wait per step,
+    by the host's clock; the device time of the same calls beside it."""
+    import accel_amd
+    from accel_amd import F32
+    K = N = 2048
+    wv = (np.arange(K * N) % 13).astype(np.float32) * np.float32(0.125) - np.float32(0.75)
+    packed, scales, zeros = accel_amd.int4_quantize(wv)
+    xs = (np.arange(K) % 7).astype(np.float32) * np.float32(0.25)
+    w = dev.upload_int4(packed, scales, zeros, K * N)
+    a = dev.upload(xs)
+    out = dev.alloc((N,), F32)
+    for _ in range(20):
+        dev.Int4MatVec(a, w, out, stream)
+        dev.sync(stream)
+    e0, e1 = dev.event(), dev.event()
+    walls, gpu = [], []
+    for _ in range(steps):
+        t0 = time.perf_counter()
+        dev.record(e0, stream)
+        dev.Int4MatVec(a, w, out, stream)
+        dev.record(e1, stream)
+        dev.sync(stream)
+        walls.append(time.perf_counter() - t0)
+        gpu.append(dev.elapsed_ms(e0, e1))
+    dev.destroy_event(e0)
+    dev.destroy_event(e1)
+    for b in (a, out):
+        b.free()
+    w.free()
+    us = float(np.median(walls)) * 1e6
+    nbytes = K * N // 2 + 4 * (K * N // 128) + 4 * K + 4 * N
+    return dict(workload="the reference's published decode benchmark: Int4MatVec [2048] x "
+                         "[2048,2048], w[i] = (i%13)*0.125-0.75, x[i] = (i%7)*0.25, one "
+                         "submission waited for per step (host time included)",
+                us_per_step=round(us, 2), device_us=round(float(np.median(gpu)) * 1e3, 2),
+                gbs_effective=round(nbytes / (us * 1e-6) / 1e9, 2),
+                published_us=PUBLISHED_US, published_hw="Apple M2 (Metal backend)",
+                published_src=PUBLISHED_SRC, speedup_vs_published=round(PUBLISHED_US / us, 1))
 
 
 def bench_matvec_f16(dev, stream, K=4096, N=4096, steps=200):
@@ -441,9 +596,7 @@ def bench_decode_step(dev, stream, batch, steps=100, merged=True):
     x = rng.standard_normal((batch, 4096)).astype(np.float32)
     g1 = (rng.standard_normal(4096) * 0.1 + 1).astype(np.float32)
     g2 = (rng.standard_normal(4096) * 0.1 + 1).astype(np.float32)
-    if not _LAYER_PLANES:
-        for name, (K, N) in shapes.items():
-            _LAYER_PLANES[name] = workloads.fast_int4(K, N, rng)
+    layer_planes(rng)
     ws, bufs = {}, {}
     total_bytes = 0
     shape = (lambda n: (batch, n)) if batch > 1 else (lambda n: (n,))
@@ -518,6 +671,93 @@ def cpu_baseline(L, seconds):
                        f"reference evaluation order, {threads} threads)")
 
 
+def _timed_once(fn, min_seconds):
+    """Seconds per call of fn, repeated until min_seconds have passed (at least once)."""
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= min_seconds:
+            return el / n, n
+
+
+def cpu_baselines_configs(min_seconds=0.3):
+    """The reference CPU algorithm restated in C (oracle/oracle.c, reference
+    evaluation order: QuantMatVecInt4's 32 x 16 workgroups, QuantMatMulInt4's
+    16 x 8 tiles, the grouped tiles) on bounded samples of configs 2-5, at the
+    host's thread count and at one thread, reported in each config's unit."""
+    import oracle
+    from accel_amd import workloads
+    out = {}
+    hi = cpu_threads()
+    rng = np.random.Generator(np.random.PCG64(21))
+    K, N = 4096, 14336
+    p2, s2, z2 = workloads.fast_int4(K, N, rng)
+    x16 = rng.standard_normal((16, K)).astype(np.float32)
+    rows = []
+    for th, M in ((hi, 16), (1, 8)):
+        per, n = _timed_once(lambda: oracle.quant_matmul_int4(x16[:M], p2, s2, z2, M, K, N,
+                                                              threads=th), min_seconds)
+        nbytes = workloads.algorithmic_bytes(M, K, N)
+        rows.append(dict(cores=th, value=round(nbytes / per / 1e9, 3), unit="GB/s",
+                         us_per_call=round(per * 1e6, 1),
+                         sample=f"{n} calls of QuantMatMulInt4 on {M} of config 2's 16 rows"))
+    out["decode_m16_f32"] = rows
+    # config 3: bf16-rounded rows through the f32 oracle, a row sample
+    K3 = N3 = 4096
+    p3, s3, z3 = workloads.fast_int4(K3, N3, rng)
+    x3 = workloads.bf16_to_f32(workloads.bf16_bits(
+        rng.standard_normal((256, K3)).astype(np.float32)))
+    rows = []
+    for th, M in ((hi, 256), (1, 32)):
+        per, n = _timed_once(lambda: oracle.quant_matmul_int4(x3[:M], p3, s3, z3, M, K3, N3,
+                                                              threads=th), min_seconds)
+        rows.append(dict(cores=th, value=round(2.0 * M * K3 * N3 / per / 1e12, 5),
+                         unit="TFLOP/s", sample=f"{n} calls of QuantMatMulInt4 on {M} of "
+                                                f"config 3's 2048 rows"))
+    out["prefill_m2048_bf16"] = rows
+    # config 4: one expert's segment through the grouped oracle
+    E = 2
+    pe = np.concatenate([p2, p2])
+    se = np.concatenate([s2, s2])
+    ze = np.concatenate([z2, z2])
+    rows = []
+    for th, R in ((hi, 128), (1, 16)):
+        xr = workloads.bf16_to_f32(workloads.bf16_bits(
+            rng.standard_normal((R, K)).astype(np.float32)))
+        off = np.array([0, R, R], np.uint32)
+        per, n = _timed_once(lambda: oracle.int4_grouped_matmul(xr, pe, se, ze, off, E, R, K, N,
+                                                                threads=th), min_seconds)
+        rows.append(dict(cores=th, value=round(2.0 * R * K * N / per / 1e12, 5),
+                         unit="TFLOP/s", sample=f"{n} calls of GroupedMatMul (int4) over one "
+                                                f"expert's {R} routed rows"))
+    out["moe_grouped_bf16"] = rows
+    # config 5: the seven products of a step in the oracle
+    planes = layer_planes(np.random.Generator(np.random.PCG64(4)))
+    wbytes = sum(p.nbytes + s.nbytes + z.nbytes for p, s, z in planes.values())
+    for batch in (1, 8):
+        xs = rng.standard_normal((batch, 14336)).astype(np.float32)
+        rows = []
+        for th in (hi, 1):
+            def step():
+                for name, (Kc, Nc) in workloads.LAYER_SHAPES.items():
+                    p, s, z = planes[name]
+                    if batch == 1:
+                        oracle.quant_matvec_int4(xs[0, :Kc], p, s, z, Kc, Nc, threads=th)
+                    else:
+                        oracle.quant_matmul_int4(np.ascontiguousarray(xs[:, :Kc]), p, s, z,
+                                                 batch, Kc, Nc, threads=th)
+            per, n = _timed_once(step, min_seconds)
+            rows.append(dict(cores=th, us_per_step=round(per * 1e6, 1),
+                             value=round(wbytes / per / 1e9, 3), unit="GB/s",
+                             sample=f"{n} steps of the seven products at batch {batch}"))
+        out[f"layer_chain_b{batch}"] = rows
+    return dict(kind="port", what="the reference CPU algorithm restated in C "
+                                  "(oracle/oracle.c), not the Go backend (no Go toolchain)",
+                rows=out)
+
+
 def _time_calls(fn, seconds):
     fn()
     n, t0 = 0, time.perf_counter()
@@ -576,13 +816,27 @@ def cpu_baseline_extras(seconds=1.5):
     return dict(kind="port", cores=1, rows=out)
 
 
+def gemm_line(p, workload, kernel, bound, flops, bytes_per):
+    if bound == "mfma":
+        rl = {"bound": "mfma", "achieved": round(p["tflops"], 1), "peak": BF16_PEAK_TFLOPS,
+              "unit": "TFLOP/s", "frac": round(p["tflops"] / BF16_PEAK_TFLOPS, 4),
+              "traffic": traffic_of(kernel), "kernel": kernel, "flops_per_launch": int(flops)}
+    else:
+        rl = {"bound": "hbm", "achieved": round(p["gbs"], 1), "peak": HBM_PEAK_GBS,
+              "unit": "GB/s", "frac": round(p["gbs"] / HBM_PEAK_GBS, 4),
+              "traffic": traffic_of(kernel), "kernel": kernel, "bytes_per_launch": int(bytes_per)}
+    return {"workload": workload, "us": round(p["us"], 2), "roofline": rl}
+
+
 def main():
+    global EAGER
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (this build "
               "runs on a single MI355X; DESIGN.md describes how the path would shard)",
               file=sys.stderr)
         sys.exit(2)
+    EAGER = args.eager
     import accel_amd
     if accel_amd.device_count() < 1:
         print("no HIP device", file=sys.stderr)
@@ -590,8 +844,10 @@ def main():
     dev = accel_amd.Device(0)
     stream = dev.stream()
     steps = max(1, args.steps)
+    progress("config 1 (headline): Int4MatVec M=1 K=N=4096")
     r = bench_gemv(dev, stream, steps, args.warmup)
     L = r["L"]
+    pub = None
     line = {
         "metric": METRIC,
         "value": round(r["gbs"], 2),
@@ -609,7 +865,8 @@ def main():
             "workload": "Int4MatVec M=1 K=4096 N=4096 (BASELINE config 1's shape and the "
                         "metric's M=1 leg) in the reference int4 format: 128-weight groups, "
                         "f16 scale+zero; f32 activations and output; weights rotated over "
-                        f"{r['copies']} device copies so every step reads HBM",
+                        f"{r['copies']} device copies and the Infinity Cache flushed before "
+                        "the timed replay, so every step reads HBM",
             "seed": 0,
         },
         "roofline": {
@@ -625,26 +882,37 @@ def main():
         },
     }
     if not args.no_extra:
+        extra = {}
+        progress("config 3: prefill M=2048 bf16")
         p = bench_gemm(dev, stream, "prefill_m2048")
-        extra = {"prefill_m2048_bf16": {
-            "workload": "Int4MatMul M=2048 K=4096 N=4096, bf16 x/out, fp32 accumulate "
-                        "(BASELINE config 3, the metric's M=2048 leg)",
-            "us": round(p["us"], 2),
-            "roofline": {"bound": "mfma", "achieved": round(p["tflops"], 1),
-                         "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(p["tflops"] / BF16_PEAK_TFLOPS, 4),
-                         "traffic": traffic_of(GEMM_KERNEL), "kernel": GEMM_KERNEL,
-                         "flops_per_launch": 2 * 2048 * 4096 * 4096},
-        }}
+        extra["prefill_m2048_bf16"] = gemm_line(
+            p, "Int4MatMul M=2048 K=4096 N=4096, bf16 x/out, fp32 accumulate (BASELINE "
+               "config 3, the metric's M=2048 leg)", GEMM_KERNEL, "mfma",
+            2 * 2048 * 4096 * 4096, p["bytes"])
+        progress("config 2: decode M=16 K=4096 N=14336")
+        d = bench_gemm(dev, stream, "decode_m16", steps=200, warmup=10)
+        extra["decode_m16_f32"] = gemm_line(
+            d, "Int4MatMul M=16 K=4096 N=14336, f32 x/out (BASELINE config 2, Llama-3-8B "
+               "MLP up-projection at decode batch 16)", DECODE_MFMA_KERNEL, "hbm",
+            2 * 16 * 4096 * 14336, d["bytes"])
+        progress("config 4: MoE grouped product")
+        extra["moe_grouped_bf16"] = bench_moe(dev, stream)
+        for b in (1, 8):
+            progress(f"config 5: layer chain at batch {b}")
+            extra[f"layer_chain_b{b}"] = bench_layer_chain(dev, stream, b)
+        progress("the reference's published workload (2048 x 2048, one wait a step)")
+        pub = bench_published(dev, stream)
+        extra["published_decode_2048"] = pub
+        line["vs_baseline"] = pub["speedup_vs_published"]
+        extra["vs_baseline_basis"] = (
+            "vs_baseline is the reference's published figure for its own decode benchmark "
+            f"({PUBLISHED_US:.0f} us a step, {PUBLISHED_SRC}) over this build's time for the "
+            "same workload and protocol (extra.published_decode_2048); BASELINE.md publishes "
+            "no figure for config 1 itself")
         if args.configs:
-            d = bench_gemm(dev, stream, "decode_m16", steps=200, warmup=10)
-            extra["decode_m16_f32"] = {"us": round(d["us"], 2), "gbs": round(d["gbs"], 1),
-                                       "frac_of_hbm": round(d["gbs"] / HBM_PEAK_GBS, 4)}
-            extra["moe_grouped_bf16"] = bench_moe(dev, stream)
-            extra["layer_chain_b1"] = bench_layer_chain(dev, stream, 1)
-            extra["layer_chain_b8"] = bench_layer_chain(dev, stream, 8)
-            extra["layer_chain_b1_sets"] = bench_layer_chain(dev, stream, 1, merged=True)
-            extra["layer_chain_b8_sets"] = bench_layer_chain(dev, stream, 8, merged=True)
+            progress("--configs: widened rows")
+            extra["layer_chain_b1_unmerged"] = bench_layer_chain(dev, stream, 1, merged=False)
+            extra["layer_chain_b8_unmerged"] = bench_layer_chain(dev, stream, 8, merged=False)
             extra["matvec_f32_f16"] = bench_matvec_f16(dev, stream)
             extra["int8_gemv_4096"] = bench_int8(dev, stream, 1)
             extra["int8_m8_4096"] = bench_int8(dev, stream, 8)
@@ -662,11 +930,16 @@ def main():
             extra["decode_step_b8_unmerged"] = bench_decode_step(dev, stream, 8, merged=False)
         line["extra"] = extra
     if not args.no_cpu:
+        progress("CPU baseline: config 1")
         line["cpu_baseline"] = cpu_baseline(L, args.cpu_seconds)
-        if args.configs and not args.no_extra:
-            line["extra"]["cpu_baselines"] = cpu_baseline_extras()
+        if not args.no_extra:
+            progress("CPU baselines: configs 2-5")
+            line["extra"]["cpu_baselines"] = cpu_baselines_configs()
+            if args.configs:
+                line["extra"]["cpu_baselines_widened"] = cpu_baseline_extras()
     dev.destroy_stream(stream)
     print(json.dumps(line), flush=True)
+    progress("done")
 
 
 if __name__ == "__main__":
