@@ -123,6 +123,7 @@ SIGNATURES = {
     "accel_hip_exec_destroy": ([_i, _vp], _i),
     "accel_hip_set_wait_limit": ([_i, ctypes.c_int32], _i),
     "accel_hip_workspace_generation": ([_i, _P(ctypes.c_uint64), _P(ctypes.c_int32)], _i),
+    "accel_hip_floor": ([_i, _vp, _i, _vp, _sz, _vp], _i),
     "accel_hip_supports_kernel": ([ctypes.c_char_p], _i),
     "accel_hip_dispatch": ([_i, _vp, ctypes.c_char_p, _P(_vp), _P(ctypes.c_uint64),
                             ctypes.c_int32, _vp, _sz, _P(ctypes.c_uint32)], _i),
@@ -396,6 +397,12 @@ class Device:
         """Spins a split-K hand-off's bounded wait may take before it gives up
         and reports the fault (a test hook)."""
         _check(_lib.accel_hip_set_wait_limit(self.index, spins))
+
+    def floor(self, kind: int, src, nbytes: int, sink, stream=None) -> None:
+        """A launch-floor probe: kind 0 an empty kernel, kind 1 a pure read of
+        nbytes from src, both with the M = 1 decode kernel's launch shape."""
+        _check(_lib.accel_hip_floor(self.index, stream, kind, src.ptr if src else None, nbytes,
+                                    sink.ptr))
 
     def workspace_generation(self):
         """(allocations of the workspace so far, replaced workspaces still held

@@ -521,6 +521,86 @@ ACCEL_API int accel_hip_set_wait_limit(int dev, int32_t spins) {
     return ACCEL_OK;
 }
 
+// ---- launch-floor probes ----------------------------------------------------
+//
+// The ceilings a decode product's roofline sits under, measured with the
+// M = 1 decode kernel's launch shape (256 workgroups of 512 lanes): an empty
+// kernel (what a launch costs before any work), and a pure read of `bytes`
+// with 16-byte loads, every lane's loads issued before any is used (what
+// moving the bytes costs without the product's arithmetic or hand-off).
+// Diagnostics for bench.py; no reference counterpart.
+namespace {
+constexpr int kFloorBlocks = 256, kFloorThreads = 512, kFloorLoads = 8;
+typedef uint32_t floor_u32x4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(kFloorThreads) void floor_empty_kernel(uint32_t* sink) {
+    if (threadIdx.x == 0 && blockIdx.x == 0xffffff) sink[0] = 1;
+}
+
+// L 16-byte loads a lane, issued together (a lane past the end re-reads
+// chunk 0, which the caches serve, and leaves it out).
+template <int L>
+__global__ __launch_bounds__(kFloorThreads) void floor_read_kernel(const floor_u32x4* src,
+                                                                   size_t chunks, uint32_t* sink) {
+    const size_t grid = (size_t)gridDim.x * blockDim.x;
+    const size_t g = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    floor_u32x4 v[L];
+#pragma unroll
+    for (int k = 0; k < L; k++) {
+        const size_t i = g + k * grid;
+        v[k] = __builtin_nontemporal_load(src + (i < chunks ? i : 0));
+    }
+    uint32_t x = 0;
+#pragma unroll
+    for (int k = 0; k < L; k++)
+        if (g + k * grid < chunks) x ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
+    if (x == 0x9e3779b9u) sink[blockIdx.x] = x;   // keeps the loads; almost never stores
+}
+
+template <int L>
+void launch_floor_read(hipStream_t st, const void* src, size_t chunks, void* sink) {
+    hipLaunchKernelGGL(floor_read_kernel<L>, dim3(kFloorBlocks), dim3(kFloorThreads), 0, st,
+                       static_cast<const floor_u32x4*>(src), chunks,
+                       static_cast<uint32_t*>(sink));
+}
+}  // namespace
+
+ACCEL_API int accel_hip_floor(int dev, void* stream, int kind, const void* src, size_t bytes,
+                              void* sink) {
+    clear_error();
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    if (!sink) return fail(ACCEL_E_INVALID, "accel_hip_floor: sink is NULL");
+    hipStream_t st = (hipStream_t)stream;
+    if (kind == 0) {
+        hipLaunchKernelGGL(floor_empty_kernel, dim3(kFloorBlocks), dim3(kFloorThreads), 0, st,
+                           static_cast<uint32_t*>(sink));
+    } else if (kind == 1) {
+        const size_t chunks = bytes / 16;
+        if (!src || bytes % 16 || reinterpret_cast<uintptr_t>(src) % 16 || chunks == 0 ||
+            chunks > (size_t)kFloorBlocks * kFloorThreads * kFloorLoads)
+            return fail(ACCEL_E_INVALID,
+                        "accel_hip_floor: a read of %zu bytes needs a 16-byte aligned source, "
+                        "a multiple of 16 bytes and at most %zu bytes",
+                        bytes, (size_t)kFloorBlocks * kFloorThreads * kFloorLoads * 16);
+        const size_t lanes = (size_t)kFloorBlocks * kFloorThreads;
+        switch ((chunks + lanes - 1) / lanes) {
+            case 1: launch_floor_read<1>(st, src, chunks, sink); break;
+            case 2: launch_floor_read<2>(st, src, chunks, sink); break;
+            case 3: launch_floor_read<3>(st, src, chunks, sink); break;
+            case 4: launch_floor_read<4>(st, src, chunks, sink); break;
+            case 5: launch_floor_read<5>(st, src, chunks, sink); break;
+            case 6: launch_floor_read<6>(st, src, chunks, sink); break;
+            case 7: launch_floor_read<7>(st, src, chunks, sink); break;
+            default: launch_floor_read<8>(st, src, chunks, sink); break;
+        }
+    } else {
+        return fail(ACCEL_E_INVALID, "accel_hip_floor: kind %d is neither 0 (empty) nor 1 (read)",
+                    kind);
+    }
+    return classify(d, hipGetLastError(), "accel_hip_floor launch");
+}
+
 ACCEL_API int accel_hip_workspace_generation(int dev, uint64_t* gen, int32_t* retired) {
     clear_error();
     Device* d = device(dev);

@@ -816,6 +816,36 @@ def cpu_baseline_extras(seconds=1.5):
     return dict(kind="port", cores=1, rows=out)
 
 
+def bench_floors(dev, stream, steps=640):
+    """What a decode product's launch shape costs before its arithmetic: an
+    empty kernel of 256 x 512 lanes, and a pure read of config 1's 8 945 664
+    algorithmic bytes with that shape (16-byte loads, all issued before any is
+    used), over 64 device copies with the cache flushed, timed like the
+    headline (graph replay, HIP events)."""
+    from accel_amd import U32
+    nbytes = 8945664
+    copies = max(1, -(-ROTATE_BYTES // nbytes))
+    bufs = [dev.alloc((nbytes // 4,), U32) for _ in range(copies)]
+    sink = dev.alloc((256,), U32)
+    res = {}
+    for kind, key in ((0, "empty_kernel"), (1, "read_8945664_bytes")):
+        t = Timed(dev, stream,
+                  lambda i: dev.floor(kind, bufs[i % copies], nbytes, sink, stream), steps)
+        t.run()
+        ms = median_replay(t) / steps
+        t.close()
+        res[key] = {"us_per_launch": round(ms * 1e3, 3)}
+        if kind == 1:
+            res[key]["gbs"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+            res[key]["frac_of_hbm_peak"] = round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+    for b in bufs + [sink]:
+        b.free()
+    res["what"] = ("launch floors of the M=1 decode kernel's shape (256 workgroups of 512 "
+                   "lanes): an empty kernel, and a pure read of config 1's algorithmic bytes "
+                   "over rotated copies with the cache flushed; graph replay, HIP events")
+    return res
+
+
 def gemm_line(p, workload, kernel, bound, flops, bytes_per):
     if bound == "mfma":
         rl = {"bound": "mfma", "achieved": round(p["tflops"], 1), "peak": BF16_PEAK_TFLOPS,
@@ -900,6 +930,8 @@ def main():
         for b in (1, 8):
             progress(f"config 5: layer chain at batch {b}")
             extra[f"layer_chain_b{b}"] = bench_layer_chain(dev, stream, b)
+        progress("launch floors of the decode shape")
+        extra["floors"] = bench_floors(dev, stream)
         progress("the reference's published workload (2048 x 2048, one wait a step)")
         pub = bench_published(dev, stream)
         extra["published_decode_2048"] = pub

@@ -165,6 +165,13 @@ int accel_hip_exec_destroy(int dev, void* exec);
  *  workspace_generation: how many times the workspace has been allocated,
  *    and how many replaced workspaces live executables still hold. */
 int accel_hip_set_wait_limit(int dev, int32_t spins);
+/* Launch-floor probes for the roofline's ceiling, with the M = 1 decode
+ * kernel's launch shape (256 workgroups of 512 lanes): kind 0 launches an
+ * empty kernel; kind 1 reads `bytes` (a multiple of 16, at most 16 MiB) from
+ * the 16-byte aligned device pointer `src` with 16-byte loads, all of a
+ * lane's issued before any is used.  `sink` is a device buffer of at least
+ * 1 KiB the read kernel may write.  Diagnostics for the benchmark. */
+int accel_hip_floor(int dev, void* stream, int kind, const void* src, size_t bytes, void* sink);
 int accel_hip_workspace_generation(int dev, uint64_t* gen, int32_t* retired);
 
 /* KernelSupport.SupportsKernel (plan.go:424-428): 1 if the named reference
