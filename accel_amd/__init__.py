@@ -582,7 +582,7 @@ class Device:
                                               ctypes.byref(to)))
 
     def SwiGLU(self, gate: Buffer, value: Buffer, out: Buffer, stream=None) -> None:
-        """tensor.SwiGLU (tensor/elementwise.go:161-189)."""
+        """tensor.SwiGLU (tensor/elementwise.go:161-188)."""
         tg, tv, to = gate.tensor(), value.tensor(), out.tensor()
         _check(_lib.accel_swiglu(self.index, stream, ctypes.byref(tg), ctypes.byref(tv),
                                  ctypes.byref(to)))

@@ -1,5 +1,5 @@
 // Prefill-shape int4 products: the counterpart of the reference's tiled
-// QuantMatMulInt4 (internal/kernels/int4tiled.go:166-238), rebuilt around
+// QuantMatMulInt4 (internal/kernels/int4tiled.go:66-137), rebuilt around
 // CDNA4's bf16 matrix cores.
 //
 // bf16 path (activations and output bf16, fp32 accumulation).  A workgroup
@@ -421,7 +421,7 @@ __global__ __launch_bounds__(kThreads, 1) void int4_gemm_bf16_kernel(
 // Ragged grouped form: blockIdx.x is the column tile, blockIdx.y the
 // position in the list of (expert, 128-row block) pairs, walked from the
 // offsets; blocks past the list's end exit.  Expert e's rows are
-// [off[e], min(off[e+1], T)) (groupedtiled.go:184-188).
+// [off[e], min(off[e+1], T)) (groupedtiled.go:87-91).
 __global__ __launch_bounds__(kThreads, 1) void int4_grouped_bf16_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,

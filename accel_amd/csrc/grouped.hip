@@ -1,7 +1,7 @@
 // Ragged grouped products and their segment offsets: the counterparts of the
 // reference's SegmentOffsets (internal/kernels/segment.go:40-50),
 // GroupedMatVec (internal/kernels/grouped.go:47-97) and GroupedMatMul
-// (internal/kernels/groupedtiled.go:172-231), for f32 weights [E,K,N] and
+// (internal/kernels/groupedtiled.go:77-134), for f32 weights [E,K,N] and
 // for stacked int4 weights.
 //
 // Token t of x [T,K] belongs to expert e(t) = #{r : off[r+1] <= t}.  The

@@ -720,7 +720,7 @@ bool same_shape(const accel_tensor_t* a, const accel_tensor_t* b) {
 
 }  // namespace
 
-// tensor.SwiGLU (tensor/elementwise.go:161-189) over the registered f32
+// tensor.SwiGLU (tensor/elementwise.go:161-188) over the registered f32
 // kernel: gate, value and out share one shape.
 ACCEL_API int accel_swiglu(int dev, void* stream, const accel_tensor_t* gate,
                            const accel_tensor_t* value, accel_tensor_t* out) {

@@ -367,7 +367,7 @@ int accel_grouped_matmul(int dev, void* stream, const accel_tensor_t* x,
  * (groups never straddle experts when K*N % 128 == 0, which is required).
  * x is f32 or bf16 [T,K]; out matches x's dtype, [T,N].  The matvec form
  * writes 0 past the last segment (grouped.go:66-77); the matmul form leaves
- * such rows unwritten (groupedtiled.go:184-231). */
+ * such rows unwritten (groupedtiled.go:87-132). */
 int accel_int4_grouped_matvec(int dev, void* stream, const accel_tensor_t* x,
                               const accel_int4_t* w, int64_t experts,
                               const accel_tensor_t* counts, accel_tensor_t* out);
@@ -377,7 +377,7 @@ int accel_int4_grouped_matmul(int dev, void* stream, const accel_tensor_t* x,
 
 /* ---- decode-step neighbours of the int4 products ---------------------- */
 
-/* tensor.SwiGLU (tensor/elementwise.go:161-189; kernel
+/* tensor.SwiGLU (tensor/elementwise.go:161-188; kernel
  * internal/kernels/elementwise.go:85-91): out = gate / (1 + Exp(-gate)) *
  * value, f32, one shape for all three; Exp is the f64 exponential rounded to
  * f32 (kmath/kmath.go:55).  Bit-identical to the reference CPU backend. */

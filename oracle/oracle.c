@@ -432,7 +432,7 @@ void orc_quant_matvec_int4(uint32_t K, uint32_t N, const float* a, const uint32_
     run_grid(matvec_int4_wg, &c, (N + 31) / 32, threads, 512);
 }
 
-/* QuantMatMulInt4, one 16(N) x 8(M) workgroup (int4tiled.go:166-238;
+/* QuantMatMulInt4, one 16(N) x 8(M) workgroup (int4tiled.go:66-137;
  * lowering accel_kernels.go:6949-7049).  Each K tile of 16 is staged with
  * zero pads past the edges, then every output accumulates all 16 products of
  * the tile in k order. */
@@ -555,7 +555,7 @@ void orc_int4_grouped_matvec(uint32_t E, uint32_t T, uint32_t K, uint32_t N,
 }
 
 /* GroupedMatMul, one workgroup per (16-column tile, expert)
- * (internal/kernels/groupedtiled.go:172-231): rows [off[e], min(off[e+1], T))
+ * (internal/kernels/groupedtiled.go:77-134): rows [off[e], min(off[e+1], T))
  * in blocks of 8, each block through the K tiles of 16 as the tiled GEMM;
  * rows outside every segment are never written. */
 static void grouped_matmul_wg(void* vctx, int64_t wg, float* scratch) {

@@ -199,7 +199,7 @@ def test_int4_grouped_refuses_straddling_groups():
     assert rc == accel_amd.E_INVALID and "straddles" in accel_amd.last_error()
 
 
-def test_swiglu_refusals():   # tensor/elementwise.go:161-189; ops_test.go:563-569
+def test_swiglu_refusals():   # tensor/elementwise.go:161-188; ops_test.go:563-569
     rc, msg = call("accel_swiglu", t([8], F32), t([8], F16), t([8], F32))
     assert rc == accel_amd.E_INVALID and "operands are f32 and f16" in msg, msg
     rc, msg = call("accel_swiglu", t([8], F32), t([4, 2], F32), t([8], F32))

@@ -1,5 +1,5 @@
 """The int8 weight path on the CPU: the library's host packer against the
-oracle, the reference's quantizer tests (quant/quant_test.go:22-250), and the
+oracle, the reference's quantizer tests (quant/quant_test.go:22-237), and the
 oracle's int8 kernels (QuantMatVecF32, internal/kernels/matvec.go:204-235;
 QuantMatMulTiledF32, internal/kernels/quant.go:195-238) pinned by the
 reference's exact-input cases, f64 brute force within the reduction bound,
@@ -59,7 +59,7 @@ def test_scales_that_underflow_f16():   # quant_test.go:203-225
     assert np.all(oracle.int8_dequantize(q, s) == 0)
 
 
-def test_dequantize_is_the_reference():   # quant_test.go:227-240
+def test_dequantize_is_the_reference():   # quant_test.go:227-237
     q = np.array([1, -2, 127, -127], np.int8)
     s = oracle.to_f16(np.array([0.5], np.float32))
     assert np.array_equal(oracle.int8_dequantize(q, s), np.array([0.5, -1, 63.5, -63.5], np.float32))
