@@ -3,26 +3,28 @@
 // CDNA4's bf16 matrix cores.
 //
 // bf16 path (activations and output bf16, fp32 accumulation).  A workgroup
-// of 256 lanes (four waves, one per SIMD) computes a 128 x 256 output tile.
-// Wave w owns the column half ch = w & 1 (128 columns: one quantisation
-// group) and all 128 rows, as 4 x 4 tiles of v_mfma_f32_32x32x16_bf16,
-// for the 16-k substeps of parity w >> 1 of every 64-k stage; the two
-// parities' accumulators are added through LDS at the end.  Per stage:
-//   * the activation tile (128 rows x 128 bytes) goes to LDS through 16-byte
-//     loads, rows XOR-swizzled in 16-byte chunks so the fragment reads
-//     (32 rows x one chunk) spread over the banks;
-//   * the packed codes (64 rows x 128 bytes) go to LDS as they are, four
+// of 256 lanes (four waves, one per SIMD) computes an output tile of up to
+// 256 rows (MT active 32-row m-tiles) by 128 columns -- one quantisation
+// group.  Wave w owns the column half ch = w & 1 (64 columns) and all MT
+// m-tiles, as MT x 2 tiles of v_mfma_f32_32x32x16_bf16, for the 16-k
+// substeps of parity w >> 1 of every 64-k stage; the two parities'
+// accumulators are added through LDS at the end.  Per stage:
+//   * the activation rows (MT x 32 rows x 128 bytes) go to LDS through
+//     16-byte loads, rows XOR-swizzled in 16-byte chunks so the fragment
+//     reads (32 rows x one chunk) spread over the banks;
+//   * the packed codes (64 rows x 64 bytes) go to LDS as they are, four
 //     bits a weight, transposed in 4 x 4-byte blocks so that each u32 holds
 //     one byte (two adjacent columns) of four consecutive rows;
-//   * per (row, group) the fold (512*s, s == 0 ? z : -z*s) goes to LDS.
-// Each wave dequantises its own B fragments in registers: a lane reads two
-// code bytes of its eight rows, turns the nibbles into exact floats with
-// the fp8 converter (byte 0000qqqq as OCP e4m3 is q*2^-9; a converter pair
-// is the same column of two rows, the pairing the bf16x2 operand wants),
-// applies w = f*(512 s) + add in fp32 and packs to bf16.  The MFMA's
-// n-tile j, column c is the tile column 128 ch + 4c + j, so a lane's four
-// n-tiles are the four nibbles of two adjacent code bytes and its outputs
-// are four adjacent bf16.  Every weight is dequantised once.
+//   * per row the fold (512*s, s == 0 ? z : -z*s) goes to LDS.
+// Each wave dequantises its own B fragments in registers: a lane reads one
+// code byte of its eight rows, turns the nibbles into exact floats with the
+// fp8 converter (byte 0000qqqq as OCP e4m3 is q*2^-9; a converter pair is
+// the same column of two rows, the pairing the bf16x2 operand wants),
+// applies w = f*(512 s) + add in fp32 and packs to bf16.  The MFMA's n-tile
+// j, column c is the tile column 64 ch + 2c + j, so a lane's two n-tiles are
+// the two nibbles of one code byte and its outputs two adjacent bf16.
+// Every weight is dequantised once and feeds MT m-tiles: with all eight,
+// the dequantisation costs about 2.4 VALU instructions per MFMA.
 //
 // Measured on gfx950 (one wave per SIMD, 16 independent 32x32x16 MFMAs a
 // step): the matrix cores sustain about 2.1 PFLOP/s alone; up to ~32 VALU
@@ -30,7 +32,7 @@
 // the VALU the bound; LDS reads and vector-memory loads interleaved with the
 // MFMAs cost more (eight 16-byte LDS reads per 16 MFMAs: -18%; eight
 // L1-hitting global loads: -40%), which is why the activations are shared
-// through LDS and each wave's tile is as wide as a group.
+// through LDS.
 //
 // Placement: consecutive logical tiles (the column tiles of one row band,
 // which share its activations) are dealt to one XCD so its L2 serves them.
@@ -52,11 +54,10 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int BM = 128, BN = 256, BK = 64;
+constexpr int BM = 256, BN = 128, BK = 64;
 constexpr int kThreads = 256;        // four waves, one per SIMD
 constexpr int kARowBytes = BK * 2;   // one LDS activation row: 64 bf16
 constexpr int kBQuadWords = BN / 2;  // u32 words per row quad: one per code byte
@@ -68,9 +69,9 @@ constexpr int kBQuadWords = BN / 2;  // u32 words per row quad: one per code byt
 __device__ __forceinline__ int a_off(int r, int c) {
     return r * kARowBytes + ((c ^ ((r >> 1) & 7)) << 4);
 }
-// Word offset of code byte `bc` of row quad `rq`: odd quad pairs are
-// shifted by half a bank width, so the two k-groups of a fragment read
-// (quads 2h and 2h+1 apart by two) use different banks.
+// Word offset of code byte `bc` of row quad `rq`: a lane reads quads 2p and
+// 2p + 1 (its eight rows); the next pair of quads -- the other k-group of
+// the wave -- is shifted by half the banks.
 __device__ __forceinline__ int b_off(int rq, int bc) {
     return rq * kBQuadWords + (bc ^ (((rq >> 1) & 1) << 5));
 }
@@ -92,56 +93,47 @@ __device__ __forceinline__ u32x4 transpose4(uint32_t r0, uint32_t r1, uint32_t r
 
 // One 64-k stage in LDS.
 struct __attribute__((aligned(16))) GemmStage {
-    char a[BM * kARowBytes];                  // 16 KB, swizzled rows
-    uint32_t b[(BK / 4) * kBQuadWords];       // 8 KB: [row quad][code byte]
-    f32x2 fold[2][BK];                        // (512 s, add) per [group of the tile][row]
+    char a[BM * kARowBytes];                  // 32 KB, swizzled rows
+    uint32_t b[(BK / 4) * kBQuadWords];       // 4 KB: [row quad][code byte]
+    f32x2 fold[BK];                           // (512 s, add) per row of the stage
 };
 struct __attribute__((aligned(16))) GemmLds {
     union {
         GemmStage st[2];
-        // Accumulator hand-off of the k-parity wave pairs, half a tile at a
-        // time: [column half][n-tile pair][row tile][register quad][lane].
-        f32x4 red[2][2][4][4][64];
+        // Accumulator hand-off of the k-parity wave pairs, four m-tiles at a
+        // time: [column half][m-tile][n-tile][register quad][lane].
+        f32x4 red[2][4][2][4][64];
     };
 };
 
 // One stage's global loads, held in registers until written to LDS.
+template <int MT>
 struct StageRegs {
-    u32x4 a[4];       // four 16-byte activation chunks
-    u32x2 b[4];       // 8 bytes of codes of each of four consecutive rows
+    u32x4 a[MT];      // 16-byte activation chunks: 32 rows each across the workgroup
+    uint32_t b[4];    // 4 bytes of codes of each of four consecutive rows
     uint16_t s, z;
 };
 
 // One 16-k substep's LDS operands for a wave.
+template <int MT>
 struct SubstepRegs {
-    bf16x8 af[4];      // A fragments of the four 32-row tiles
-    u32x2 tw[2];       // two code bytes (four columns) of rows 8*kg .. 8*kg+7, two quads
+    bf16x8 af[MT];     // A fragments of the m-tiles
+    uint32_t tw[2];    // one code byte (two columns) of rows 8*kg .. +3 and +4 .. +7
     f32x4 fr[4];       // (mul, add) of those rows, two per vector
 };
 
-// One 128 x 256 output tile.  Rows [m0, m_end) of a/out are valid; rows
-// past m_end are computed from a clamped row and not stored.  Columns
-// [n0, n0 + 256) with n0 + 128 == N allowed (the upper half is computed
-// from clamped columns and not stored).  codes/scales/zeros describe the
-// [K, N] matrix in use.
-//
-// Waves.  Wave w (one per SIMD) owns the column half ch = w & 1 -- 128
-// columns, one quantisation group -- and all 128 rows, as 4 x 4 tiles of
-// v_mfma_f32_32x32x16_bf16, for the 16-k substeps of parity kp = w >> 1 of
-// every 64-k stage; the two parities' accumulators are added at the end.
-// MFMA column c of n-tile j is the column 128 ch + 4c + j, so a lane's four
-// n-tiles are the four nibbles of two adjacent code bytes.  Every weight is
-// dequantised once, and each wave reads the activation tile only for its
-// own substeps.  A wave pipelines its substeps: while the 16 MFMAs of one
-// run, it dequantises the next one's codes, read from LDS at the start of
-// the current one.
+// One output tile: rows [m0, m0 + 32 MT) of which [m0, m_end) are valid
+// (rows past m_end are computed from a clamped row and not stored), columns
+// [n0, n0 + 128).  codes/scales/zeros describe the [K, N] matrix in use.
 //
 // Stages.  Stage kt (64 k) sits in LDS buffer kt % 2.  At its first
 // substep a wave writes its share of stage kt+1 (loaded two stages
 // earlier) into the other buffer and issues the global loads of stage
 // kt+3; the stage's one barrier, before its second substep, makes stage
-// kt+1 visible before that substep reads the next stage's operands.
-template <bool BIAS>
+// kt+1 visible before that substep reads the next stage's operands.  A
+// wave pipelines its substeps: while the MFMAs of one run, it dequantises
+// the next one's codes, read from LDS at the start of the current one.
+template <int MT, bool BIAS>
 __device__ __forceinline__ void gemm_tile_bf16(GemmLds& lds, const uint16_t* __restrict__ a,
                                                const uint32_t* __restrict__ codes,
                                                const uint16_t* __restrict__ scales,
@@ -158,130 +150,110 @@ __device__ __forceinline__ void gemm_tile_bf16(GemmLds& lds, const uint16_t* __r
     const int kg = lane >> 5;    // MFMA k-group (8 consecutive k)
     const size_t groups_per_row = (size_t)(N >> 7);
     const size_t words_per_row = (size_t)(N >> 3);
-    const bool half_tile = n0 + BN > N;   // only the first 128 columns exist
     const int ktiles = K / BK;
 
-    // Activation staging: 1024 chunks of 16 bytes a stage, four per lane.
-    const uint16_t* a_src[4];
-    int a_dst[4];
+    // Activation staging: 32 rows (256 chunks of 16 bytes) per m-tile a
+    // stage, one chunk per lane and m-tile.
+    const uint16_t* a_src[MT];
+    int a_dst[MT];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < MT; i++) {
         const int q = tid + kThreads * i;
         const int r = q >> 3, c = q & 7;
         const int row = min(m0 + r, m_end - 1);
         a_src[i] = a + (size_t)row * K + c * 8;
         a_dst[i] = a_off(r, c);
     }
-    // Code staging: row quad tid / 16 and 8-byte column chunk tid % 16 (16
-    // columns, two words) of each of the quad's four rows.
+    // Code staging: row quad tid / 16 and 4-byte column chunk tid % 16 (eight
+    // columns) of each of the quad's four rows.
     const int b_rq = tid >> 4;
     const int b_cc = tid & 15;
-    const int b_cc_src = (half_tile && b_cc >= 8) ? b_cc - 8 : b_cc;
-    const uint32_t* b_src = codes + (size_t)(4 * b_rq) * words_per_row + (n0 >> 3) + 2 * b_cc_src;
-    const int b_dst = b_off(b_rq, 8 * b_cc);
-    // Fold staging: one (row, group of the tile) per lane, lanes 128..255
-    // repeating lanes 0..127 (the same value to the same place).
-    const int f_row = tid & 63;
-    const int f_grp = (tid >> 6) & 1;
-    const size_t f_g = (size_t)(n0 >> 7) + ((half_tile && f_grp) ? 0 : f_grp);
+    const uint32_t* b_src = codes + (size_t)(4 * b_rq) * words_per_row + (n0 >> 3) + b_cc;
+    const int b_dst = b_off(b_rq, 4 * b_cc);
+    // Fold staging: one row per lane, every wave alike (the same value to the
+    // same place), so the stage code has no branch to cut the schedule.
+    const int f_row = lane;
+    const size_t f_g = (size_t)(n0 >> 7);
     const uint16_t* s_src = scales + (size_t)f_row * groups_per_row + f_g;
     const uint16_t* z_src = zeros + (size_t)f_row * groups_per_row + f_g;
 
     // Stage indices past the end are clamped to the last stage: the loads
     // repeat valid data and land in buffers no later stage reads.
-    auto load_global = [&](StageRegs& g, int kt) {
+    auto load_global = [&](StageRegs<MT>& g, int kt) {
         const int k0 = min(kt, ktiles - 1) * BK;
 #pragma unroll
-        for (int i = 0; i < 4; i++) g.a[i] = *reinterpret_cast<const u32x4*>(a_src[i] + k0);
+        for (int i = 0; i < MT; i++) g.a[i] = *reinterpret_cast<const u32x4*>(a_src[i] + k0);
         const uint32_t* bp = b_src + (size_t)k0 * words_per_row;
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-            g.b[i] = *reinterpret_cast<const u32x2*>(bp + (size_t)i * words_per_row);
+        for (int i = 0; i < 4; i++) g.b[i] = bp[(size_t)i * words_per_row];
         g.s = s_src[(size_t)k0 * groups_per_row];
         g.z = z_src[(size_t)k0 * groups_per_row];
     };
-    auto store_lds = [&](const StageRegs& g, int buf) {
+    auto store_lds = [&](const StageRegs<MT>& g, int buf) {
         GemmStage& S = lds.st[buf];
 #pragma unroll
-        for (int i = 0; i < 4; i++) *reinterpret_cast<u32x4*>(S.a + a_dst[i]) = g.a[i];
-#pragma unroll
-        for (int w = 0; w < 2; w++)
-            *reinterpret_cast<u32x4*>(&S.b[b_dst + 4 * w]) =
-                transpose4(g.b[0][w], g.b[1][w], g.b[2][w], g.b[3][w]);
+        for (int i = 0; i < MT; i++) *reinterpret_cast<u32x4*>(S.a + a_dst[i]) = g.a[i];
+        *reinterpret_cast<u32x4*>(&S.b[b_dst]) = transpose4(g.b[0], g.b[1], g.b[2], g.b[3]);
         const float s = half_bits_to_float(g.s);
         const float z = half_bits_to_float(g.z);
         f32x2 f;
         f.x = s * 512.0f;
         f.y = (s == 0.0f) ? z : -(z * s);
-        S.fold[f_grp][f_row] = f;
+        S.fold[f_row] = f;
     };
-    // This lane's code bytes: 64*ch + 2*c32 and +1 (columns 128ch + 4c32 .. +3).
-    const int my_bc = 64 * ch + 2 * c32;
+    // This lane's code byte: 32*ch + c32 (columns 64ch + 2c32, + 1).
+    const int my_bc = 32 * ch + c32;
 
-    auto read_substep = [&](SubstepRegs& r, int buf, int ks) {
+    auto read_substep = [&](SubstepRegs<MT>& r, int buf, int ks) {
         const GemmStage& S = lds.st[buf];
 #pragma unroll
-        for (int i = 0; i < 2; i++)
-            r.tw[i] = *reinterpret_cast<const u32x2*>(&S.b[b_off(ks * 4 + 2 * kg + i, my_bc)]);
-        const f32x4* fp = reinterpret_cast<const f32x4*>(&S.fold[ch][ks * 16 + 8 * kg]);
+        for (int h = 0; h < 2; h++) r.tw[h] = S.b[b_off(ks * 4 + 2 * kg + h, my_bc)];
+        const f32x4* fp = reinterpret_cast<const f32x4*>(&S.fold[ks * 16 + 8 * kg]);
 #pragma unroll
         for (int i = 0; i < 4; i++) r.fr[i] = fp[i];   // (mul, add) of rows 2i, 2i+1
 #pragma unroll
-        for (int t = 0; t < 4; t++)
+        for (int t = 0; t < MT; t++)
             r.af[t] = *reinterpret_cast<const bf16x8*>(S.a + a_off(t * 32 + c32, ks * 2 + kg));
     };
-    // B fragments of the four n-tiles: code byte e of tw (e = 0, 1) holds
-    // columns 2e (low nibble) and 2e + 1 (high nibble); u32 h of a u32x2
-    // pair is quad h (rows 4h .. 4h+3).
-    auto dequant = [&](const SubstepRegs& r, bf16x8 (&bfr)[4]) {
+    // B fragments of the two n-tiles: the code byte of row i of a quad is
+    // byte i of tw[h]; its low nibble is n-tile 0, its high nibble n-tile 1.
+    auto dequant = [&](const SubstepRegs<MT>& r, bf16x8 (&bfr)[2]) {
 #pragma unroll
-        for (int e = 0; e < 2; e++) {
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const uint32_t t = r.tw[h][e];
-                const uint32_t lo = t & 0x0F0F0F0Fu;          // column 2e of rows 0..3
-                const uint32_t hi = (t >> 4) & 0x0F0F0F0Fu;   // column 2e + 1
-                const f32x2 c0a = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);  // rows 0, 1
-                const f32x2 c0b = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);   // rows 2, 3
-                const f32x2 c1a = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
-                const f32x2 c1b = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
-                const f32x4 f01 = r.fr[2 * h], f23 = r.fr[2 * h + 1];
-                const int p = 4 * h;
-                bfr[2 * e][p + 0] = (__bf16)__builtin_fmaf(c0a.x, f01.x, f01.y);
-                bfr[2 * e][p + 1] = (__bf16)__builtin_fmaf(c0a.y, f01.z, f01.w);
-                bfr[2 * e][p + 2] = (__bf16)__builtin_fmaf(c0b.x, f23.x, f23.y);
-                bfr[2 * e][p + 3] = (__bf16)__builtin_fmaf(c0b.y, f23.z, f23.w);
-                bfr[2 * e + 1][p + 0] = (__bf16)__builtin_fmaf(c1a.x, f01.x, f01.y);
-                bfr[2 * e + 1][p + 1] = (__bf16)__builtin_fmaf(c1a.y, f01.z, f01.w);
-                bfr[2 * e + 1][p + 2] = (__bf16)__builtin_fmaf(c1b.x, f23.x, f23.y);
-                bfr[2 * e + 1][p + 3] = (__bf16)__builtin_fmaf(c1b.y, f23.z, f23.w);
-            }
+        for (int h = 0; h < 2; h++) {
+            const uint32_t t = r.tw[h];
+            const uint32_t lo = t & 0x0F0F0F0Fu;          // n-tile 0, rows 4h .. 4h+3
+            const uint32_t hi = (t >> 4) & 0x0F0F0F0Fu;   // n-tile 1
+            const f32x2 c0a = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);  // rows 0, 1
+            const f32x2 c0b = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);   // rows 2, 3
+            const f32x2 c1a = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
+            const f32x2 c1b = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
+            const f32x4 f01 = r.fr[2 * h], f23 = r.fr[2 * h + 1];
+            const int p = 4 * h;
+            bfr[0][p + 0] = (__bf16)__builtin_fmaf(c0a.x, f01.x, f01.y);
+            bfr[0][p + 1] = (__bf16)__builtin_fmaf(c0a.y, f01.z, f01.w);
+            bfr[0][p + 2] = (__bf16)__builtin_fmaf(c0b.x, f23.x, f23.y);
+            bfr[0][p + 3] = (__bf16)__builtin_fmaf(c0b.y, f23.z, f23.w);
+            bfr[1][p + 0] = (__bf16)__builtin_fmaf(c1a.x, f01.x, f01.y);
+            bfr[1][p + 1] = (__bf16)__builtin_fmaf(c1a.y, f01.z, f01.w);
+            bfr[1][p + 2] = (__bf16)__builtin_fmaf(c1b.x, f23.x, f23.y);
+            bfr[1][p + 3] = (__bf16)__builtin_fmaf(c1b.y, f23.z, f23.w);
         }
     };
 
-    f32x16 acc[4][4];
+    f32x16 acc[MT][2];
 #pragma unroll
-    for (int t = 0; t < 4; t++)
+    for (int t = 0; t < MT; t++)
 #pragma unroll
-        for (int j = 0; j < 4; j++)
+        for (int j = 0; j < 2; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[t][j][r] = 0.0f;
-
-    auto mfmas = [&](const SubstepRegs& r, const bf16x8 (&bfr)[4]) {
-#pragma unroll
-        for (int t = 0; t < 4; t++)
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                acc[t][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(r.af[t], bfr[j], acc[t][j],
-                                                                   0, 0, 0);
-    };
 
     // Prologue: stage 0 in LDS buffer 0, stage 1 in register set 1, stage 2
     // in flight into register set 0, this wave's first substep read and
     // dequantised.
-    StageRegs g[2];
-    SubstepRegs fr[2];
-    bf16x8 bq[2][4];
+    StageRegs<MT> g[2];
+    SubstepRegs<MT> fr[2];
+    bf16x8 bq[2][2];
     load_global(g[0], 0);
     load_global(g[1], 1);
     store_lds(g[0], 0);
@@ -290,30 +262,115 @@ __device__ __forceinline__ void gemm_tile_bf16(GemmLds& lds, const uint16_t* __r
     read_substep(fr[0], 0, kp);
     dequant(fr[0], bq[0]);
 
-    // The wave's substep u (0, 1) of stage kt is ks = 2u + kp.  SET = kt % 2
-    // names the register set that holds stage kt+2 (the other one holds
-    // stage kt+1 until it is written).
+    // Issue order of a substep.  Each of its 2*MT MFMAs is followed by a
+    // share of the other work, in this order: the next substep's code bytes
+    // and folds (R0-R2); at u = 0 the stage's LDS writes of stage kt+1 and
+    // global loads of stage kt+3, A chunk by chunk (W, L), then the codes and
+    // folds; last the next substep's A fragments (RA) with its four
+    // dequantisation pieces (D) spread among them, late enough for the code
+    // and fold reads to have landed.  A scheduling barrier after every MFMA
+    // keeps this order.
+    constexpr int kMfmas = 2 * MT;
+    constexpr int kTail = MT + 4;   // RA and D
+    auto tail_is_d = [](int t) {
+        for (int q = 0; q < 4; q++)
+            if (t == q * kTail / 4 + 1) return q;
+        return -1;
+    };
+    auto tail_ra = [&](int t) {
+        int d = 0;
+        for (int q = 0; q < 4; q++) d += (q * kTail / 4 + 1) < t;
+        return t - d;
+    };
+
     auto substep = [&](int kt, auto U, auto SET) {
         constexpr int u = decltype(U)::value;
         constexpr int set = decltype(SET)::value;
+        constexpr int kItems = u == 0 ? 3 * MT + 15 : MT + 7;
         const int buf = kt & 1;
-        if constexpr (u == 0) {
-            store_lds(g[set ^ 1], buf ^ 1);      // stage kt+1
-            load_global(g[set ^ 1], kt + 3);
-            read_substep(fr[1], buf, 2 + kp);
-        } else {
-            __syncthreads();                      // stage kt+1 visible
-            read_substep(fr[0], buf ^ 1, kp);
-        }
-        mfmas(fr[u], bq[u]);
-        dequant(fr[u ^ 1], bq[u ^ 1]);
-        // The MFMAs in issue order, each followed by a share of the next
-        // substep's LDS reads and dequant VALU.
+        const int rbuf = u == 0 ? buf : buf ^ 1;   // the next substep's buffer
+        const int rks = u == 0 ? 2 + kp : kp;      // and its 16-k step in it
+        SubstepRegs<MT>& nx = fr[u ^ 1];
+        StageRegs<MT>& gs = g[set ^ 1];
+        const GemmStage& RS = lds.st[rbuf];
+        GemmStage& WS = lds.st[buf ^ 1];
+        const int k0n = min(kt + 3, ktiles - 1) * BK;   // the stage loaded now
+        const f32x4* fp = reinterpret_cast<const f32x4*>(&RS.fold[rks * 16 + 8 * kg]);
+
+        auto dq = [&](int q) {
+            const int h = q >> 1, j = q & 1;
+            const uint32_t t = nx.tw[h];
+            const uint32_t nib = (j ? (t >> 4) : t) & 0x0F0F0F0Fu;
+            const f32x2 ca = __builtin_amdgcn_cvt_pk_f32_fp8(nib, false);   // rows 0, 1
+            const f32x2 cb = __builtin_amdgcn_cvt_pk_f32_fp8(nib, true);    // rows 2, 3
+            const f32x4 f01 = nx.fr[2 * h], f23 = nx.fr[2 * h + 1];
+            bf16x8& b = bq[u ^ 1][j];
+            b[4 * h + 0] = (__bf16)__builtin_fmaf(ca.x, f01.x, f01.y);
+            b[4 * h + 1] = (__bf16)__builtin_fmaf(ca.y, f01.z, f01.w);
+            b[4 * h + 2] = (__bf16)__builtin_fmaf(cb.x, f23.x, f23.y);
+            b[4 * h + 3] = (__bf16)__builtin_fmaf(cb.y, f23.z, f23.w);
+        };
+        auto item = [&](int it) {
+            if (it == 0) {
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
-            __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);   // VALU
+                for (int h = 0; h < 2; h++) nx.tw[h] = RS.b[b_off(rks * 4 + 2 * kg + h, my_bc)];
+                return;
+            }
+            if (it == 1) { nx.fr[0] = fp[0]; nx.fr[1] = fp[1]; return; }
+            if (it == 2) { nx.fr[2] = fp[2]; nx.fr[3] = fp[3]; return; }
+            it -= 3;
+            if (u == 0) {
+                if (it < 2 * MT) {
+                    const int p = it >> 1;
+                    if ((it & 1) == 0)
+                        *reinterpret_cast<u32x4*>(WS.a + a_dst[p]) = gs.a[p];
+                    else
+                        gs.a[p] = *reinterpret_cast<const u32x4*>(a_src[p] + k0n);
+                    return;
+                }
+                it -= 2 * MT;
+                if (it == 0) {
+                    *reinterpret_cast<u32x4*>(&WS.b[b_dst]) =
+                        transpose4(gs.b[0], gs.b[1], gs.b[2], gs.b[3]);
+                    return;
+                }
+                if (it <= 4) {
+                    gs.b[it - 1] = b_src[(size_t)(k0n + it - 1) * words_per_row];
+                    return;
+                }
+                if (it == 5) {
+                    const float sv = half_bits_to_float(gs.s);
+                    const float zv = half_bits_to_float(gs.z);
+                    f32x2 f;
+                    f.x = sv * 512.0f;
+                    f.y = (sv == 0.0f) ? zv : -(zv * sv);
+                    WS.fold[f_row] = f;
+                    return;
+                }
+                if (it == 6) { gs.s = s_src[(size_t)k0n * groups_per_row]; return; }
+                if (it == 7) { gs.z = z_src[(size_t)k0n * groups_per_row]; return; }
+                it -= 8;
+            }
+            const int q = tail_is_d(it);
+            if (q >= 0) {
+                dq(q);
+            } else {
+                const int t = tail_ra(it);
+                nx.af[t] = *reinterpret_cast<const bf16x8*>(
+                    RS.a + a_off(t * 32 + c32, rks * 2 + kg));
+            }
+        };
+
+#pragma unroll
+        for (int i = 0; i < kMfmas; i++) {
+            const int t = i >> 1, j = i & 1;
+            acc[t][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fr[u].af[t], bq[u][j], acc[t][j],
+                                                               0, 0, 0);
+            if (u == 1 && i == 0) __syncthreads();   // stage kt+1 visible
+#pragma unroll
+            for (int it = 0; it < kItems; it++)
+                if (it * kMfmas / kItems == i) item(it);
+            __builtin_amdgcn_sched_barrier(0);
         }
     };
     using I0 = std::integral_constant<int, 0>;
@@ -329,99 +386,102 @@ __device__ __forceinline__ void gemm_tile_bf16(GemmLds& lds, const uint16_t* __r
     }
     if (kt < ktiles) stage(kt, I0{});
 
-    // The fused bias of this lane's four columns, fetched now so that its
+    // The fused bias of this lane's two columns, fetched now so that its
     // latency overlaps the hand-over below.
-    float bj[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const int col = n0 + 64 * ch + 2 * c32;
+    float bj[2] = {0.0f, 0.0f};
     if constexpr (BIAS) {
-        const int bcol = n0 + 128 * ch + 4 * c32;
-        if (kp == 0 && bcol < N) {
-#pragma unroll
-            for (int j = 0; j < 4; j++) bj[j] = bias[bcol + j];
+        if (kp == 0) {
+            bj[0] = bias[col];
+            bj[1] = bias[col + 1];
         }
     }
 
     // The odd-parity waves hand their accumulators to the even ones through
-    // LDS, one pair of n-tiles at a time.
+    // LDS, four m-tiles at a time.
     __syncthreads();
 #pragma unroll
-    for (int jp = 0; jp < 2; jp++) {
+    for (int hp = 0; hp < (MT + 3) / 4; hp++) {
         if (kp == 1) {
 #pragma unroll
-            for (int jj = 0; jj < 2; jj++)
+            for (int tt = 0; tt < 4; tt++) {
+                const int t = 4 * hp + tt;
+                if (t >= MT) break;
 #pragma unroll
-                for (int t = 0; t < 4; t++)
+                for (int j = 0; j < 2; j++)
 #pragma unroll
                     for (int q = 0; q < 4; q++) {
-                        const f32x16& v = acc[t][2 * jp + jj];
-                        lds.red[ch][jj][t][q][lane] =
+                        const f32x16& v = acc[t][j];
+                        lds.red[ch][tt][j][q][lane] =
                             (f32x4){v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
                     }
+            }
         }
         __syncthreads();
         if (kp == 0) {
 #pragma unroll
-            for (int jj = 0; jj < 2; jj++)
+            for (int tt = 0; tt < 4; tt++) {
+                const int t = 4 * hp + tt;
+                if (t >= MT) break;
 #pragma unroll
-                for (int t = 0; t < 4; t++)
+                for (int j = 0; j < 2; j++)
 #pragma unroll
                     for (int q = 0; q < 4; q++) {
-                        const f32x4 v = lds.red[ch][jj][t][q][lane];
-                        f32x16& d = acc[t][2 * jp + jj];
+                        const f32x4 v = lds.red[ch][tt][j][q][lane];
+                        f32x16& d = acc[t][j];
                         d[4 * q] += v.x;
                         d[4 * q + 1] += v.y;
                         d[4 * q + 2] += v.z;
                         d[4 * q + 3] += v.w;
                     }
+            }
         }
         __syncthreads();
     }
     if (kp == 1) return;
 
     // D of a 32 x 32 tile: lane holds column lane % 32; register r is row
-    // 8*(r/4) + 4*(lane/32) + r%4.  A lane's four n-tiles are four adjacent
-    // columns.
-    const int col = n0 + 128 * ch + 4 * c32;
-    if (col >= N) return;
-    // the fused bias: one f32 value per column, added before the one rounding
+    // 8*(r/4) + 4*(lane/32) + r%4.  A lane's two n-tiles are two adjacent
+    // columns; the fused bias is one f32 value per column, added before the
+    // one rounding.
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
+    for (int t = 0; t < MT; t++) {
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             const int row = m0 + t * 32 + 8 * (r >> 2) + 4 * kg + (r & 3);
             if (row < m_end) {
-                bf16x4 v;
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    if constexpr (BIAS)
-                        v[j] = (__bf16)(acc[t][j][r] + bj[j]);
-                    else
-                        v[j] = (__bf16)acc[t][j][r];
-                }
-                *reinterpret_cast<bf16x4*>(out + (size_t)row * N + col) = v;
+                bf16x2 v;
+                v[0] = (__bf16)(BIAS ? acc[t][0][r] + bj[0] : acc[t][0][r]);
+                v[1] = (__bf16)(BIAS ? acc[t][1][r] + bj[1] : acc[t][1][r]);
+                *reinterpret_cast<bf16x2*>(out + (size_t)row * N + col) = v;
             }
         }
     }
 }
 
-template <bool BIAS>
+// Row bands of BM rows by column tiles of BN; MT = 8 for the full bands, the
+// last band's own count for a partial one (launched separately).
+template <int MT, bool BIAS>
 __global__ __launch_bounds__(kThreads, 1) void int4_gemm_bf16_kernel(
     const uint16_t* __restrict__ a, const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
-    uint16_t* __restrict__ out, int M, int K, int N, const float* __restrict__ bias) {
+    uint16_t* __restrict__ out, int m_first, int M, int K, int N,
+    const float* __restrict__ bias) {
     __shared__ GemmLds lds;
-    const int tiles_n = (N + BN - 1) / BN;
+    const int tiles_n = N / BN;
     const int grid = gridDim.x;
     int b = blockIdx.x;
     if ((grid & 7) == 0) b = (b & 7) * (grid >> 3) + (b >> 3);
-    const int m0 = (b / tiles_n) * BM;
+    const int m0 = m_first + (b / tiles_n) * BM;
     const int n0 = (b % tiles_n) * BN;
-    gemm_tile_bf16<BIAS>(lds, a, codes, scales, zeros, out, m0, M, n0, K, N, bias);
+    gemm_tile_bf16<MT, BIAS>(lds, a, codes, scales, zeros, out, m0, M, n0, K, N, bias);
 }
 
 // Ragged grouped form: blockIdx.x is the column tile, blockIdx.y the
-// position in the list of (expert, 128-row block) pairs, walked from the
+// position in the list of (expert, row block) pairs, walked from the
 // offsets; blocks past the list's end exit.  Expert e's rows are
-// [off[e], min(off[e+1], T)) (groupedtiled.go:87-91).
+// [off[e], min(off[e+1], T)) (groupedtiled.go:87-91); a block takes up to
+// BM of them, with as many active m-tiles as it has rows.
 __global__ __launch_bounds__(kThreads, 1) void int4_grouped_bf16_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
@@ -447,9 +507,20 @@ __global__ __launch_bounds__(kThreads, 1) void int4_grouped_bf16_kernel(
     }
     if (!found) return;
     const size_t per_expert = (size_t)K * N;
-    gemm_tile_bf16<false>(lds, x, codes + e * (per_expert >> 3), scales + e * (per_expert >> 7),
-                   zeros + e * (per_expert >> 7), out, m0, m_end, blockIdx.x * BN, K, N,
-                   nullptr);
+    const uint32_t* c = codes + e * (per_expert >> 3);
+    const uint16_t* s = scales + e * (per_expert >> 7);
+    const uint16_t* z = zeros + e * (per_expert >> 7);
+    const int n0 = blockIdx.x * BN;
+    switch ((min(m_end - m0, BM) + 31) / 32) {
+        case 1: gemm_tile_bf16<1, false>(lds, x, c, s, z, out, m0, m_end, n0, K, N, nullptr); break;
+        case 2: gemm_tile_bf16<2, false>(lds, x, c, s, z, out, m0, m_end, n0, K, N, nullptr); break;
+        case 3: gemm_tile_bf16<3, false>(lds, x, c, s, z, out, m0, m_end, n0, K, N, nullptr); break;
+        case 4: gemm_tile_bf16<4, false>(lds, x, c, s, z, out, m0, m_end, n0, K, N, nullptr); break;
+        case 5: gemm_tile_bf16<5, false>(lds, x, c, s, z, out, m0, m_end, n0, K, N, nullptr); break;
+        case 6: gemm_tile_bf16<6, false>(lds, x, c, s, z, out, m0, m_end, n0, K, N, nullptr); break;
+        case 7: gemm_tile_bf16<7, false>(lds, x, c, s, z, out, m0, m_end, n0, K, N, nullptr); break;
+        default: gemm_tile_bf16<8, false>(lds, x, c, s, z, out, m0, m_end, n0, K, N, nullptr); break;
+    }
 }
 
 // ---- f32 activations, fp32 VALU tiles -------------------------------------
@@ -529,19 +600,42 @@ __global__ __launch_bounds__(256) void int4_gemm_f32_kernel(
 }  // namespace
 
 bool int4_gemm_bf16_supported(int M, int K, int N) {
-    return M >= 1 && K >= BK && K % BK == 0 && N >= 128 && N % 128 == 0 &&
+    return M >= 1 && K >= BK && K % BK == 0 && N >= BN && N % BN == 0 &&
            K < (1 << 30) && N < (1 << 30);
+}
+
+template <int MT>
+void launch_band(hipStream_t st, const uint16_t* a, Int4Planes w, uint16_t* out, int m_first,
+                 int bands, int M, int K, int N, const float* bias) {
+    const dim3 grid(bands * (N / BN));
+    if (bias)
+        hipLaunchKernelGGL((int4_gemm_bf16_kernel<MT, true>), grid, dim3(kThreads), 0, st, a,
+                           w.codes, w.scales, w.zeros, out, m_first, M, K, N, bias);
+    else
+        hipLaunchKernelGGL((int4_gemm_bf16_kernel<MT, false>), grid, dim3(kThreads), 0, st, a,
+                           w.codes, w.scales, w.zeros, out, m_first, M, K, N, bias);
 }
 
 hipError_t launch_int4_gemm_bf16(Device*, hipStream_t st, const uint16_t* a, Int4Planes w,
                                  uint16_t* out, int M, int K, int N, const float* bias) {
-    const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-    if (bias)
-        hipLaunchKernelGGL(int4_gemm_bf16_kernel<true>, dim3(tiles), dim3(kThreads), 0, st, a,
-                           w.codes, w.scales, w.zeros, out, M, K, N, bias);
-    else
-        hipLaunchKernelGGL(int4_gemm_bf16_kernel<false>, dim3(tiles), dim3(kThreads), 0, st, a,
-                           w.codes, w.scales, w.zeros, out, M, K, N, bias);
+    // full 256-row bands in one launch, a partial last band in another with
+    // only its own m-tiles
+    const int full = M / BM;
+    if (full > 0) launch_band<8>(st, a, w, out, 0, full, M, K, N, bias);
+    const int rest = M - full * BM;
+    if (rest > 0) {
+        const int m_first = full * BM;
+        switch ((rest + 31) / 32) {
+            case 1: launch_band<1>(st, a, w, out, m_first, 1, M, K, N, bias); break;
+            case 2: launch_band<2>(st, a, w, out, m_first, 1, M, K, N, bias); break;
+            case 3: launch_band<3>(st, a, w, out, m_first, 1, M, K, N, bias); break;
+            case 4: launch_band<4>(st, a, w, out, m_first, 1, M, K, N, bias); break;
+            case 5: launch_band<5>(st, a, w, out, m_first, 1, M, K, N, bias); break;
+            case 6: launch_band<6>(st, a, w, out, m_first, 1, M, K, N, bias); break;
+            case 7: launch_band<7>(st, a, w, out, m_first, 1, M, K, N, bias); break;
+            default: launch_band<8>(st, a, w, out, m_first, 1, M, K, N, bias); break;
+        }
+    }
     return hipGetLastError();
 }
 
@@ -552,7 +646,7 @@ hipError_t launch_int4_grouped_bf16(Device*, hipStream_t st, const uint16_t* x,
     // partial block.
     const int max_blocks = (T + BM - 1) / BM + E;
     if (max_blocks > 65535) return hipErrorInvalidConfiguration;
-    dim3 grid((N + BN - 1) / BN, max_blocks);
+    dim3 grid(N / BN, max_blocks);
     hipLaunchKernelGGL(int4_grouped_bf16_kernel, grid, dim3(kThreads), 0, st, x, w.codes,
                        w.scales, w.zeros, off, out, E, T, K, N);
     return hipGetLastError();

@@ -170,7 +170,9 @@ SHAPES_BF16 = [(1, 64, 128), (64, 256, 256), (100, 512, 384), (128, 128, 128),
                (257, 1024, 640), (512, 2048, 1024),
                # the 256-row tiles with one stage, an odd stage count and a
                # ragged last row band
-               (300, 64, 128), (256, 192, 384), (511, 320, 256)]
+               (300, 64, 128), (256, 192, 384), (511, 320, 256),
+               # last bands of 2, 4, 7 and 8 active 32-row m-tiles
+               (832, 128, 256), (97, 64, 256), (200, 256, 128), (480, 128, 128)]
 
 
 def _bf16_oracle(x, p, s, z, M, K, N, rows=None):
