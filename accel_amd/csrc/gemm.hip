@@ -106,13 +106,22 @@ struct __attribute__((aligned(16))) GemmLds {
     };
 };
 
-// One stage's global loads, held in registers until written to LDS.
+// One stage's global loads, held in registers until written to LDS: the
+// activations (two stages ahead) and the codes with their scale and zero
+// (a deeper ring: they come from HBM, the activations from L2).
 template <int MT>
-struct StageRegs {
+struct ARegs {
     u32x4 a[MT];      // 16-byte activation chunks: 32 rows each across the workgroup
+};
+struct CRegs {
     uint32_t b[4];    // 4 bytes of codes of each of four consecutive rows
     uint16_t s, z;
 };
+// Stages of codes in flight: as many as the registers allow.
+template <int MT>
+constexpr int code_depth() {
+    return MT >= 7 ? 2 : 4;
+}
 
 // One 16-k substep's LDS operands for a wave.
 template <int MT>
@@ -179,20 +188,23 @@ __device__ __forceinline__ void gemm_tile_bf16(GemmLds& lds, const uint16_t* __r
 
     // Stage indices past the end are clamped to the last stage: the loads
     // repeat valid data and land in buffers no later stage reads.
-    auto load_global = [&](StageRegs<MT>& g, int kt) {
+    auto load_a = [&](ARegs<MT>& g, int kt) {
         const int k0 = min(kt, ktiles - 1) * BK;
 #pragma unroll
         for (int i = 0; i < MT; i++) g.a[i] = *reinterpret_cast<const u32x4*>(a_src[i] + k0);
+    };
+    auto load_c = [&](CRegs& g, int kt) {
+        const int k0 = min(kt, ktiles - 1) * BK;
         const uint32_t* bp = b_src + (size_t)k0 * words_per_row;
 #pragma unroll
         for (int i = 0; i < 4; i++) g.b[i] = bp[(size_t)i * words_per_row];
         g.s = s_src[(size_t)k0 * groups_per_row];
         g.z = z_src[(size_t)k0 * groups_per_row];
     };
-    auto store_lds = [&](const StageRegs<MT>& g, int buf) {
+    auto store_lds = [&](const ARegs<MT>& ga, const CRegs& g, int buf) {
         GemmStage& S = lds.st[buf];
 #pragma unroll
-        for (int i = 0; i < MT; i++) *reinterpret_cast<u32x4*>(S.a + a_dst[i]) = g.a[i];
+        for (int i = 0; i < MT; i++) *reinterpret_cast<u32x4*>(S.a + a_dst[i]) = ga.a[i];
         *reinterpret_cast<u32x4*>(&S.b[b_dst]) = transpose4(g.b[0], g.b[1], g.b[2], g.b[3]);
         const float s = half_bits_to_float(g.s);
         const float z = half_bits_to_float(g.z);
@@ -248,16 +260,22 @@ __device__ __forceinline__ void gemm_tile_bf16(GemmLds& lds, const uint16_t* __r
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[t][j][r] = 0.0f;
 
-    // Prologue: stage 0 in LDS buffer 0, stage 1 in register set 1, stage 2
-    // in flight into register set 0, this wave's first substep read and
-    // dequantised.
-    StageRegs<MT> g[2];
+    // Prologue: stage 0 in LDS buffer 0; activations of stage 1 in set 1 and
+    // stage 2 in flight into set 0; codes of stages 1 .. PD - 1 in code sets
+    // 1 .. PD - 1 and stage PD in flight into code set 0 (stage s in set
+    // s mod PD); this wave's first substep read and dequantised.
+    constexpr int PD = code_depth<MT>();
+    ARegs<MT> g[2];
+    CRegs cg[PD];
     SubstepRegs<MT> fr[2];
     bf16x8 bq[2][2];
-    load_global(g[0], 0);
-    load_global(g[1], 1);
-    store_lds(g[0], 0);
-    load_global(g[0], 2);
+    load_a(g[0], 0);
+#pragma unroll
+    for (int c = 0; c < PD; c++) load_c(cg[c], c);
+    load_a(g[1], 1);
+    store_lds(g[0], cg[0], 0);
+    load_a(g[0], 2);
+    load_c(cg[0], PD);
     __syncthreads();
     read_substep(fr[0], 0, kp);
     dequant(fr[0], bq[0]);
@@ -265,8 +283,8 @@ __device__ __forceinline__ void gemm_tile_bf16(GemmLds& lds, const uint16_t* __r
     // Issue order of a substep.  Each of its 2*MT MFMAs is followed by a
     // share of the other work, in this order: the next substep's code bytes
     // and folds (R0-R2); at u = 0 the stage's LDS writes of stage kt+1 and
-    // global loads of stage kt+3, A chunk by chunk (W, L), then the codes and
-    // folds; last the next substep's A fragments (RA) with its four
+    // global loads of stage kt+3 (activations) and kt+1+PD (codes, scale and
+    // zero), A chunk by chunk (W, L), then the codes and folds; last the next substep's A fragments (RA) with its four
     // dequantisation pieces (D) spread among them, late enough for the code
     // and fold reads to have landed.  A scheduling barrier after every MFMA
     // keeps this order.
@@ -283,18 +301,21 @@ __device__ __forceinline__ void gemm_tile_bf16(GemmLds& lds, const uint16_t* __r
         return t - d;
     };
 
-    auto substep = [&](int kt, auto U, auto SET) {
+    auto substep = [&](int kt, auto U, auto SET, auto CSET) {
         constexpr int u = decltype(U)::value;
         constexpr int set = decltype(SET)::value;
+        constexpr int cset = decltype(CSET)::value;   // code set of stage kt+1
         constexpr int kItems = u == 0 ? 3 * MT + 15 : MT + 7;
         const int buf = kt & 1;
         const int rbuf = u == 0 ? buf : buf ^ 1;   // the next substep's buffer
         const int rks = u == 0 ? 2 + kp : kp;      // and its 16-k step in it
         SubstepRegs<MT>& nx = fr[u ^ 1];
-        StageRegs<MT>& gs = g[set ^ 1];
+        ARegs<MT>& gs = g[set ^ 1];
+        CRegs& cs = cg[cset];
         const GemmStage& RS = lds.st[rbuf];
         GemmStage& WS = lds.st[buf ^ 1];
-        const int k0n = min(kt + 3, ktiles - 1) * BK;   // the stage loaded now
+        const int k0n = min(kt + 3, ktiles - 1) * BK;        // activations loaded now
+        const int k0c = min(kt + 1 + PD, ktiles - 1) * BK;   // codes loaded now
         const f32x4* fp = reinterpret_cast<const f32x4*>(&RS.fold[rks * 16 + 8 * kg]);
 
         auto dq = [&](int q) {
@@ -331,24 +352,24 @@ __device__ __forceinline__ void gemm_tile_bf16(GemmLds& lds, const uint16_t* __r
                 it -= 2 * MT;
                 if (it == 0) {
                     *reinterpret_cast<u32x4*>(&WS.b[b_dst]) =
-                        transpose4(gs.b[0], gs.b[1], gs.b[2], gs.b[3]);
+                        transpose4(cs.b[0], cs.b[1], cs.b[2], cs.b[3]);
                     return;
                 }
                 if (it <= 4) {
-                    gs.b[it - 1] = b_src[(size_t)(k0n + it - 1) * words_per_row];
+                    cs.b[it - 1] = b_src[(size_t)(k0c + it - 1) * words_per_row];
                     return;
                 }
                 if (it == 5) {
-                    const float sv = half_bits_to_float(gs.s);
-                    const float zv = half_bits_to_float(gs.z);
+                    const float sv = half_bits_to_float(cs.s);
+                    const float zv = half_bits_to_float(cs.z);
                     f32x2 f;
                     f.x = sv * 512.0f;
                     f.y = (sv == 0.0f) ? zv : -(zv * sv);
                     WS.fold[f_row] = f;
                     return;
                 }
-                if (it == 6) { gs.s = s_src[(size_t)k0n * groups_per_row]; return; }
-                if (it == 7) { gs.z = z_src[(size_t)k0n * groups_per_row]; return; }
+                if (it == 6) { cs.s = s_src[(size_t)k0c * groups_per_row]; return; }
+                if (it == 7) { cs.z = z_src[(size_t)k0c * groups_per_row]; return; }
                 it -= 8;
             }
             const int q = tail_is_d(it);
@@ -375,16 +396,30 @@ __device__ __forceinline__ void gemm_tile_bf16(GemmLds& lds, const uint16_t* __r
     };
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
-    auto stage = [&](int kt, auto SET) {
-        substep(kt, I0{}, SET);
-        substep(kt, I1{}, SET);
+    // Stage kt = base + j of a group of SU stages (SU a multiple of 2 and of
+    // PD) uses activation set j % 2 and code set (j + 1) % PD.
+    constexpr int SU = PD == 2 ? 2 : 4;
+    auto stage = [&](int kt, auto J) {
+        constexpr int j = decltype(J)::value;
+        using S = std::integral_constant<int, j % 2>;
+        using C = std::integral_constant<int, (j + 1) % PD>;
+        substep(kt, I0{}, S{}, C{});
+        substep(kt, I1{}, S{}, C{});
     };
     int kt = 0;
-    for (; kt + 2 <= ktiles; kt += 2) {
-        stage(kt, I0{});
-        stage(kt + 1, I1{});
+    for (; kt + SU <= ktiles; kt += SU) {
+        stage(kt, std::integral_constant<int, 0>{});
+        stage(kt + 1, std::integral_constant<int, 1>{});
+        if constexpr (SU == 4) {
+            stage(kt + 2, std::integral_constant<int, 2>{});
+            stage(kt + 3, std::integral_constant<int, 3>{});
+        }
     }
-    if (kt < ktiles) stage(kt, I0{});
+    if (kt < ktiles) stage(kt, std::integral_constant<int, 0>{});
+    if constexpr (SU == 4) {
+        if (kt + 1 < ktiles) stage(kt + 1, std::integral_constant<int, 1>{});
+        if (kt + 2 < ktiles) stage(kt + 2, std::integral_constant<int, 2>{});
+    }
 
     // The fused bias of this lane's two columns, fetched now so that its
     // latency overlaps the hand-over below.
@@ -477,26 +512,46 @@ __global__ __launch_bounds__(kThreads, 1) void int4_gemm_bf16_kernel(
     gemm_tile_bf16<MT, BIAS>(lds, a, codes, scales, zeros, out, m0, M, n0, K, N, bias);
 }
 
-// Ragged grouped form: blockIdx.x is the column tile, blockIdx.y the
-// position in the list of (expert, row block) pairs, walked from the
-// offsets; blocks past the list's end exit.  Expert e's rows are
-// [off[e], min(off[e+1], T)) (groupedtiled.go:87-91); a block takes up to
-// BM of them, with as many active m-tiles as it has rows.
+// Ragged grouped form: the work is the list of (expert, row block, column
+// tile) triples, row blocks of up to BM rows walked from the offsets: expert
+// e's rows are [off[e], min(off[e+1], T)) (groupedtiled.go:87-91), and a
+// block runs as many 32-row m-tiles as it has rows.  The launch is sized for
+// the most blocks the offsets can make; every workgroup counts the real
+// ones and deals the list to the XCDs in contiguous eighths (the dispatcher
+// deals workgroup b to XCD b % 8), so that the column tiles of one row
+// block -- which share its activation rows -- meet in one L2.  The
+// placement affects speed only.  Surplus workgroups exit.
 __global__ __launch_bounds__(kThreads, 1) void int4_grouped_bf16_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
     const uint32_t* __restrict__ off, uint16_t* __restrict__ out, int E, int T, int K,
     int N) {
     __shared__ GemmLds lds;
-    int idx = blockIdx.y;
+    const int tiles_n = N / BN;
+    auto rows_of = [&](int e, uint32_t& first, uint32_t& last) {
+        first = off[e];
+        last = off[e + 1];
+        if (last > (uint32_t)T) last = (uint32_t)T;
+        return last > first ? (int)(last - first) : 0;
+    };
+    int blocks_all = 0;
+    for (int e = 0; e < E; e++) {
+        uint32_t f, l;
+        blocks_all += (rows_of(e, f, l) + BM - 1) / BM;
+    }
+    const int work = blocks_all * tiles_n;
+    const int per_xcd = (work + 7) / 8;
+    const int slot = blockIdx.x >> 3;
+    if (slot >= per_xcd) return;
+    const int li = (blockIdx.x & 7) * per_xcd + slot;
+    if (li >= work) return;
+    int idx = li / tiles_n;
+    const int n0 = (li % tiles_n) * BN;
     int e = 0, m0 = 0, m_end = 0;
     bool found = false;
     for (; e < E; e++) {
-        const uint32_t first = off[e];
-        uint32_t last = off[e + 1];
-        if (last > (uint32_t)T) last = (uint32_t)T;
-        const int rows = last > first ? (int)(last - first) : 0;
-        const int blocks = (rows + BM - 1) / BM;
+        uint32_t first, last;
+        const int blocks = (rows_of(e, first, last) + BM - 1) / BM;
         if (idx < blocks) {
             m0 = (int)first + idx * BM;
             m_end = (int)last;
@@ -510,7 +565,6 @@ __global__ __launch_bounds__(kThreads, 1) void int4_grouped_bf16_kernel(
     const uint32_t* c = codes + e * (per_expert >> 3);
     const uint16_t* s = scales + e * (per_expert >> 7);
     const uint16_t* z = zeros + e * (per_expert >> 7);
-    const int n0 = blockIdx.x * BN;
     switch ((min(m_end - m0, BM) + 31) / 32) {
         case 1: gemm_tile_bf16<1, false>(lds, x, c, s, z, out, m0, m_end, n0, K, N, nullptr); break;
         case 2: gemm_tile_bf16<2, false>(lds, x, c, s, z, out, m0, m_end, n0, K, N, nullptr); break;
@@ -520,6 +574,379 @@ __global__ __launch_bounds__(kThreads, 1) void int4_grouped_bf16_kernel(
         case 6: gemm_tile_bf16<6, false>(lds, x, c, s, z, out, m0, m_end, n0, K, N, nullptr); break;
         case 7: gemm_tile_bf16<7, false>(lds, x, c, s, z, out, m0, m_end, n0, K, N, nullptr); break;
         default: gemm_tile_bf16<8, false>(lds, x, c, s, z, out, m0, m_end, n0, K, N, nullptr); break;
+    }
+}
+
+// ---- f32 activations on the matrix cores ---------------------------------
+//
+// The reference API's own dtype (f32 activations and result) to f32
+// accuracy.  Within a 128-column tile every row k has one scale s and zero
+// z, so with add = (s == 0 ? z : -z*s) and q the code,
+//     sum_k x[m,k] w[k,n] = sum_k (x[m,k] 512 s_k) (q[k,n] 2^-9) + sum_k x[m,k] add_k
+// (s_k taken as 0 where it is 0).  The first sum runs on the bf16 matrix
+// cores: B is the code itself, q 2^-9, exact in bf16, and A' = x 512 s is
+// split exactly into three bf16 terms hi + mid + lo (each the RNE rounding of
+// what the previous ones leave; the residue is below 2^-27 |A'|), three MFMAs
+// per tile step.  The second sum, one value per row, is accumulated in f32
+// while the A tile is staged and added to the row at the end.
+//
+// A workgroup of four waves computes 128 rows (four 32-row m-tiles) by 128
+// columns; wave w owns the column half w & 1 and the 16-k substeps of parity
+// w >> 1, as in the bf16 tiles.  Per 64-k stage the workgroup turns the f32
+// activations (staged through registers two stages ahead) into the three
+// bf16 terms in LDS, each lane eight consecutive k of one row per m-tile,
+// reading the (512 s, add) fold of the stage's rows from LDS (published a
+// stage earlier); codes go to LDS transposed as in the bf16 tiles.
+
+constexpr int XBM = 128;            // rows of an f32 tile: four m-tiles
+constexpr int kXTerms = 3;
+
+struct __attribute__((aligned(16))) XStage {
+    char a[kXTerms][XBM * kARowBytes];        // 3 x 16 KB: hi, mid, lo, swizzled rows
+    uint32_t b[(BK / 4) * kBQuadWords];       // 4 KB: [row quad][code byte]
+};
+struct __attribute__((aligned(16))) XLds {
+    union {
+        XStage st[2];
+        // accumulator hand-off of the k-parity wave pairs:
+        // [column half][m-tile][n-tile][register quad][lane]
+        f32x4 red[2][4][2][4][64];
+    };
+    f32x2 fold[2][BK];     // (512 s, add) of the stage rows, double-buffered
+    float corr[XBM];       // sum_k x add of each row, at the end
+};
+
+// Two values -> three bf16 pairs whose sum is (v0, v1) to 2^-27 relative:
+// each term is the RNE bf16 of what the previous ones leave, and the
+// remainder v - term is exact in f32, taken with one v_dot2 (-1 * term + v).
+// The pairs (-1, 0) and (0, -1) come in as SGPRs: the compiler would encode
+// the first as the inline constant -1.0, which the hardware does not expand
+// to bf16 -1 in the low half.
+__device__ __forceinline__ bf16x2 xbf16_pair(uint32_t bits) {
+    uint32_t r;
+    asm("s_mov_b32 %0, %1" : "=s"(r) : "i"(bits));
+    return __builtin_bit_cast(bf16x2, r);
+}
+__device__ __forceinline__ void xsplit3(float v0, float v1, uint32_t& hi, uint32_t& mid,
+                                        uint32_t& lo) {
+    const bf16x2 m10 = xbf16_pair(0x0000BF80u);   // (-1, 0)
+    const bf16x2 m01 = xbf16_pair(0xBF800000u);   // (0, -1)
+    const bf16x2 h = __builtin_convertvector((f32x2){v0, v1}, bf16x2);
+    const float r0 = __builtin_amdgcn_fdot2_f32_bf16(h, m10, v0, false);
+    const float r1 = __builtin_amdgcn_fdot2_f32_bf16(h, m01, v1, false);
+    const bf16x2 m = __builtin_convertvector((f32x2){r0, r1}, bf16x2);
+    const float s0 = __builtin_amdgcn_fdot2_f32_bf16(m, m10, r0, false);
+    const float s1 = __builtin_amdgcn_fdot2_f32_bf16(m, m01, r1, false);
+    const bf16x2 l = __builtin_convertvector((f32x2){s0, s1}, bf16x2);
+    hi = __builtin_bit_cast(uint32_t, h);
+    mid = __builtin_bit_cast(uint32_t, m);
+    lo = __builtin_bit_cast(uint32_t, l);
+}
+
+__global__ __launch_bounds__(kThreads, 1) void int4_gemm_f32x3_kernel(
+    const float* __restrict__ a, const uint32_t* __restrict__ codes,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
+    void* __restrict__ out, int M, int K, int N, Epilogue ep) {
+    __shared__ XLds lds;
+    const int tiles_n = N / BN;
+    const int grid = gridDim.x;
+    int bid = blockIdx.x;
+    if ((grid & 7) == 0) bid = (bid & 7) * (grid >> 3) + (bid >> 3);
+    const int m0 = (bid / tiles_n) * XBM;
+    const int n0 = (bid % tiles_n) * BN;
+    const int m_end = M;
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int ch = wave & 1;
+    const int kp = wave >> 1;
+    const int lane = tid & 63;
+    const int c32 = lane & 31;
+    const int kg = lane >> 5;
+    const size_t groups_per_row = (size_t)(N >> 7);
+    const size_t words_per_row = (size_t)(N >> 3);
+    const int ktiles = K / BK;
+
+    // Activation staging: m-tile i, row (tid >> 3) + 32 i, k 8 (tid & 7) ..
+    // + 7 of a stage: two 16-byte loads each.
+    const int x_row = tid >> 3;
+    const int x_c8 = tid & 7;
+    const float* x_src[4];
+    int x_dst[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int r = x_row + 32 * i;
+        x_src[i] = a + (size_t)min(m0 + r, m_end - 1) * K + 8 * x_c8;
+        x_dst[i] = a_off(r, x_c8);
+    }
+    // codes and fold staging as in the bf16 tiles
+    const int b_rq = tid >> 4;
+    const int b_cc = tid & 15;
+    const uint32_t* b_src = codes + (size_t)(4 * b_rq) * words_per_row + (n0 >> 3) + b_cc;
+    const int b_dst = b_off(b_rq, 4 * b_cc);
+    const int f_row = lane;
+    const size_t f_g = (size_t)(n0 >> 7);
+    const uint16_t* s_src = scales + (size_t)f_row * groups_per_row + f_g;
+    const uint16_t* z_src = zeros + (size_t)f_row * groups_per_row + f_g;
+    const int my_bc = 32 * ch + c32;
+
+    struct XRegs { f32x4 x[4][2]; };
+    struct CRegs2 { uint32_t b[4]; };
+    struct SZ { uint16_t s, z; };
+    auto load_x = [&](XRegs& g, int kt) {
+        const int k0 = min(kt, ktiles - 1) * BK;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            g.x[i][0] = *reinterpret_cast<const f32x4*>(x_src[i] + k0);
+            g.x[i][1] = *reinterpret_cast<const f32x4*>(x_src[i] + k0 + 4);
+        }
+    };
+    auto load_b = [&](CRegs2& g, int kt) {
+        const int k0 = min(kt, ktiles - 1) * BK;
+        const uint32_t* bp = b_src + (size_t)k0 * words_per_row;
+#pragma unroll
+        for (int i = 0; i < 4; i++) g.b[i] = bp[(size_t)i * words_per_row];
+    };
+    auto load_sz = [&](SZ& g, int kt) {
+        const int k0 = min(kt, ktiles - 1) * BK;
+        g.s = s_src[(size_t)k0 * groups_per_row];
+        g.z = z_src[(size_t)k0 * groups_per_row];
+    };
+    auto write_fold = [&](const SZ& g, int fb) {
+        const float sv = half_bits_to_float(g.s);
+        const float zv = half_bits_to_float(g.z);
+        f32x2 f;
+        f.x = sv * 512.0f;
+        f.y = (sv == 0.0f) ? zv : -(zv * sv);
+        lds.fold[fb][f_row] = f;
+    };
+    float corr[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    // The three terms of m-tile i's chunk, from its activations and the
+    // stage's fold (fv: the eight k of this lane), into LDS buffer `buf`;
+    // `real` is false for the stage past the last, staged (from clamped
+    // loads) but never read, whose rows must not reach the corrections.
+    auto stage_x = [&](const f32x4 (&xv)[2], const f32x2 (&fv)[8], int i, int buf, bool real) {
+        const float x8[8] = {xv[0].x, xv[0].y, xv[0].z, xv[0].w,
+                             xv[1].x, xv[1].y, xv[1].z, xv[1].w};
+        uint32_t h[4], md[4], lo[4];
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const float v0 = x8[2 * p] * fv[2 * p].x;
+            const float v1 = x8[2 * p + 1] * fv[2 * p + 1].x;
+            const float c0 = __builtin_fmaf(x8[2 * p], fv[2 * p].y, corr[i]);
+            corr[i] = real ? __builtin_fmaf(x8[2 * p + 1], fv[2 * p + 1].y, c0) : corr[i];
+            xsplit3(v0, v1, h[p], md[p], lo[p]);
+        }
+        XStage& S = lds.st[buf];
+        *reinterpret_cast<u32x4*>(S.a[0] + x_dst[i]) = (u32x4){h[0], h[1], h[2], h[3]};
+        *reinterpret_cast<u32x4*>(S.a[1] + x_dst[i]) = (u32x4){md[0], md[1], md[2], md[3]};
+        *reinterpret_cast<u32x4*>(S.a[2] + x_dst[i]) = (u32x4){lo[0], lo[1], lo[2], lo[3]};
+    };
+    auto read_fold = [&](f32x2 (&fv)[8], int fb) {
+        const f32x4* fp = reinterpret_cast<const f32x4*>(&lds.fold[fb][8 * x_c8]);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const f32x4 t = fp[j];
+            fv[2 * j] = (f32x2){t.x, t.y};
+            fv[2 * j + 1] = (f32x2){t.z, t.w};
+        }
+    };
+
+    // One substep's operands: the three terms' A fragments of the four
+    // m-tiles, one code byte of eight rows.
+    struct XSub {
+        bf16x8 af[kXTerms][4];
+        uint32_t tw[2];
+    };
+    auto read_sub = [&](XSub& r, int buf, int ks) {
+        const XStage& S = lds.st[buf];
+#pragma unroll
+        for (int h = 0; h < 2; h++) r.tw[h] = S.b[b_off(ks * 4 + 2 * kg + h, my_bc)];
+#pragma unroll
+        for (int tt = 0; tt < kXTerms; tt++)
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+                r.af[tt][t] = *reinterpret_cast<const bf16x8*>(
+                    S.a[tt] + a_off(t * 32 + c32, ks * 2 + kg));
+    };
+    // B of the two n-tiles: q 2^-9 as bf16, exact (byte 0000qqqq as e4m3).
+    auto codes_b = [&](const XSub& r, bf16x8 (&bfr)[2]) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const uint32_t t = r.tw[h];
+            const uint32_t lo = t & 0x0F0F0F0Fu;
+            const uint32_t hi = (t >> 4) & 0x0F0F0F0Fu;
+            const bf16x2 l01 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false);
+            const bf16x2 l23 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, true);
+            const bf16x2 h01 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, false);
+            const bf16x2 h23 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true);
+            bfr[0][4 * h + 0] = l01[0];
+            bfr[0][4 * h + 1] = l01[1];
+            bfr[0][4 * h + 2] = l23[0];
+            bfr[0][4 * h + 3] = l23[1];
+            bfr[1][4 * h + 0] = h01[0];
+            bfr[1][4 * h + 1] = h01[1];
+            bfr[1][4 * h + 2] = h23[0];
+            bfr[1][4 * h + 3] = h23[1];
+        }
+    };
+
+    f32x16 acc[4][2];
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[t][j][r] = 0.0f;
+
+    // Prologue: folds of stages 0 and 1 published; stage 0 staged into LDS
+    // buffer 0; activations of stage 1 in set 1 and stage 2 in flight into
+    // set 0; codes of stage 1 held, s/z of stages 2 and 3 in flight.
+    XRegs gx[2];
+    CRegs2 gb[2];
+    SZ gz[2];
+    {
+        SZ z0, z1;
+        load_sz(z0, 0);
+        load_sz(z1, 1);
+        load_x(gx[0], 0);
+        load_b(gb[0], 0);
+        load_x(gx[1], 1);
+        load_b(gb[1], 1);
+        load_sz(gz[0], 2);
+        load_sz(gz[1], 3);
+        write_fold(z0, 0);
+        write_fold(z1, 1);
+    }
+    __syncthreads();
+    {
+        f32x2 fv[8];
+        read_fold(fv, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) stage_x(gx[0].x[i], fv, i, 0, true);
+        *reinterpret_cast<u32x4*>(&lds.st[0].b[b_dst]) =
+            transpose4(gb[0].b[0], gb[0].b[1], gb[0].b[2], gb[0].b[3]);
+    }
+    load_x(gx[0], 2);
+    load_b(gb[0], 2);
+    __syncthreads();
+    XSub sub[2];
+    bf16x8 bq[2][2];
+    read_sub(sub[0], 0, kp);
+    codes_b(sub[0], bq[0]);
+
+    auto mfma_all = [&](const XSub& r, const bf16x8 (&bfr)[2]) {
+#pragma unroll
+        for (int tt = 0; tt < kXTerms; tt++)
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    acc[t][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(r.af[tt][t], bfr[j],
+                                                                       acc[t][j], 0, 0, 0);
+    };
+
+    // Stage kt: substep u = 0 publishes the fold of stage kt+2, stages the
+    // activations and codes of stage kt+1 (fold kt+1, published a stage
+    // ago), issues the loads of stage kt+3 (activations, codes) and kt+4
+    // (scale, zero), and reads its second substep's operands; substep u = 1
+    // waits at the stage's barrier and reads the first substep of stage kt+1.
+    auto stage = [&](int kt, auto SET) {
+        constexpr int set = decltype(SET)::value;   // gx/gb[set ^ 1]: stage kt+1
+        const int buf = kt & 1;
+        {
+            write_fold(gz[kt & 1], kt & 1);           // stage kt+2
+            f32x2 fv[8];
+            read_fold(fv, (kt + 1) & 1);
+            read_sub(sub[1], buf, 2 + kp);
+            mfma_all(sub[0], bq[0]);
+#pragma unroll
+            for (int i = 0; i < 4; i++) stage_x(gx[set ^ 1].x[i], fv, i, buf ^ 1, kt + 1 < ktiles);
+            *reinterpret_cast<u32x4*>(&lds.st[buf ^ 1].b[b_dst]) =
+                transpose4(gb[set ^ 1].b[0], gb[set ^ 1].b[1], gb[set ^ 1].b[2], gb[set ^ 1].b[3]);
+            load_x(gx[set ^ 1], kt + 3);
+            load_b(gb[set ^ 1], kt + 3);
+            load_sz(gz[kt & 1], kt + 4);
+            codes_b(sub[1], bq[1]);
+        }
+        {
+            __syncthreads();                          // stage kt+1 and fold kt+2 visible
+            read_sub(sub[0], buf ^ 1, kp);
+            mfma_all(sub[1], bq[1]);
+            codes_b(sub[0], bq[0]);
+        }
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    int kt = 0;
+    for (; kt + 2 <= ktiles; kt += 2) {
+        stage(kt, I0{});
+        stage(kt + 1, I1{});
+    }
+    if (kt < ktiles) stage(kt, I0{});
+
+    // Row corrections: the eight lanes of a row (x_c8) add theirs; LDS holds
+    // one value per tile row.
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        float c = corr[i];
+        c += __shfl_xor(c, 1, 64);
+        c += __shfl_xor(c, 2, 64);
+        c += __shfl_xor(c, 4, 64);
+        corr[i] = c;
+    }
+    __syncthreads();
+    if (x_c8 == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) lds.corr[x_row + 32 * i] = corr[i];
+    }
+    // The odd-parity waves hand their accumulators to the even ones.
+    if (kp == 1) {
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const f32x16& v = acc[t][j];
+                    lds.red[ch][t][j][q][lane] =
+                        (f32x4){v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+                }
+    }
+    __syncthreads();
+    if (kp == 1) return;
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const f32x4 v = lds.red[ch][t][j][q][lane];
+                f32x16& d = acc[t][j];
+                d[4 * q] += v.x;
+                d[4 * q + 1] += v.y;
+                d[4 * q + 2] += v.z;
+                d[4 * q + 3] += v.w;
+            }
+    const int col = n0 + 64 * ch + 2 * c32;
+    float bj[2] = {0.0f, 0.0f};
+    if (ep.bias) {
+        bj[0] = ep.bias[col];
+        bj[1] = ep.bias[col + 1];
+    }
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int rl = t * 32 + 8 * (r >> 2) + 4 * kg + (r & 3);
+            const int row = m0 + rl;
+            if (row < m_end) {
+                const float cr = lds.corr[rl];
+                const size_t o = (size_t)row * N + col;
+                store_value(out, o, acc[t][0][r] + cr + bj[0], ep.bf16);
+                store_value(out, o + 1, acc[t][1][r] + cr + bj[1], ep.bf16);
+            }
+        }
     }
 }
 
@@ -644,11 +1071,24 @@ hipError_t launch_int4_grouped_bf16(Device*, hipStream_t st, const uint16_t* x,
                                     int T, int K, int N, bool) {
     // Upper bound on (expert, row block) pairs: every expert can add one
     // partial block.
-    const int max_blocks = (T + BM - 1) / BM + E;
-    if (max_blocks > 65535) return hipErrorInvalidConfiguration;
-    dim3 grid(N / BN, max_blocks);
+    const long long max_blocks = (T + BM - 1) / BM + (long long)E;
+    const long long wgs = (max_blocks * (N / BN) + 7) / 8 * 8;
+    if (wgs > (1ll << 31) - 8) return hipErrorInvalidConfiguration;
+    dim3 grid((unsigned)wgs);
     hipLaunchKernelGGL(int4_grouped_bf16_kernel, grid, dim3(kThreads), 0, st, x, w.codes,
                        w.scales, w.zeros, off, out, E, T, K, N);
+    return hipGetLastError();
+}
+
+bool int4_gemm_f32x3_supported(int K, int N) {
+    return K >= BK && K % BK == 0 && N >= BN && N % BN == 0 && K < (1 << 30) && N < (1 << 30);
+}
+
+hipError_t launch_int4_gemm_f32x3(Device*, hipStream_t st, const float* a, Int4Planes w,
+                                  void* out, int M, int K, int N, Epilogue ep) {
+    const int tiles = (M + XBM - 1) / XBM * (N / BN);
+    hipLaunchKernelGGL(int4_gemm_f32x3_kernel, dim3(tiles), dim3(kThreads), 0, st, a, w.codes,
+                       w.scales, w.zeros, out, M, K, N, ep);
     return hipGetLastError();
 }
 

@@ -112,6 +112,10 @@ SHAPES_F32 = [
     (6, 32, 128), (10, 4096, 1024),
     # config 5 at batch 8: q/o [4096,4096] and down [14336,4096] at their own size
     (8, 4096, 4096), (8, 14336, 4096),
+    # M > 16 on the matrix cores (three-term split): one stage and three row
+    # bands, a full band, a ragged band and several column tiles; K % 64 != 0
+    # takes the fp32 VALU tiles
+    (257, 64, 128), (128, 1024, 512), (300, 2048, 1024), (40, 96, 256),
 ]
 
 
@@ -145,15 +149,20 @@ def test_config2_decode_m16_full_size(dev):
     assert rel_l2(got, want) <= F32_TOL
 
 
-def test_weights_far_from_zero_keep_f32_accuracy(dev):
+@pytest.mark.parametrize("M", [1, 64])
+def test_weights_far_from_zero_keep_f32_accuracy(dev, M):
     # groups clustered at 1000 +- 0.5: the zero point is large (quant/int4_test.go:93-101)
     K, N = 512, 256
     rng = np.random.default_rng(77)
     w = (1000 + rng.random((K, N))).astype(np.float32)
-    x = rng.standard_normal((1, K)).astype(np.float32)
+    x = rng.standard_normal((M, K)).astype(np.float32)
     p, s, z = oracle.int4_quantize(w)
-    got = run_matvec(dev, x[0], p, s, z, K, N)
-    want = oracle.quant_matvec_int4(x[0], p, s, z, K, N)
+    if M == 1:
+        got = run_matvec(dev, x[0], p, s, z, K, N)[None]
+        want = oracle.quant_matvec_int4(x[0], p, s, z, K, N)[None]
+    else:
+        got = run_matmul(dev, x, p, s, z, M, K, N)
+        want = oracle.quant_matmul_int4(x, p, s, z, M, K, N, threads=8)
     assert rel_l2(got, want) <= F32_TOL
 
 
@@ -191,6 +200,21 @@ def test_bf16_products_match_the_oracle(dev, M, K, N):
     got = run_matmul(dev, x, p, s, z, M, K, N, bf16=True)
     want = _bf16_oracle(x, p, s, z, M, K, N)
     assert rel_l2(got, want) <= BF16_TOL
+
+
+def test_config3_shape_in_f32_sampled_rows(dev):
+    # config 3's product in the reference API's dtype: f32 activations and
+    # result on the matrix cores, against the oracle on sampled rows and a
+    # column-sum checksum of every row in f64
+    L = workloads.linear(2048, 4096, 4096, seed=2)
+    got = run_matmul(dev, L.x, L.packed, L.scales, L.zeros, L.M, L.K, L.N)
+    rows = np.array([0, 1, 127, 128, 1000, 1023, 1024, 2047])
+    want = oracle.quant_matmul_int4(np.ascontiguousarray(L.x[rows]), L.packed, L.scales,
+                                    L.zeros, len(rows), L.K, L.N, threads=8)
+    assert rel_l2(got[rows], want) <= F32_TOL
+    wd = oracle.int4_dequantize(L.packed, L.scales, L.zeros, L.K * L.N).reshape(L.K, L.N)
+    col_sums = L.x.astype(np.float64).sum(axis=0) @ wd.astype(np.float64)
+    assert rel_l2(got.astype(np.float64).sum(axis=0), col_sums) <= F32_TOL
 
 
 def test_config3_prefill_full_size_sampled_rows(dev):
