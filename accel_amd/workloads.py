@@ -58,6 +58,8 @@ CONFIGS = {
     "gemv_m1": dict(M=1, K=4096, N=4096, seed=0, bf16=False),
     "decode_m16": dict(M=16, K=4096, N=14336, seed=1, bf16=False),
     "prefill_m2048": dict(M=2048, K=4096, N=4096, seed=2, bf16=True),
+    # config 3's shape in the reference API's own dtype (f32 activations)
+    "prefill_m2048_f32": dict(M=2048, K=4096, N=4096, seed=2, bf16=False),
 }
 
 

@@ -52,7 +52,8 @@ METRIC = ("int4 linear: HBM GB/s (% peak) at M=1; TFLOP/s (% MFMA peak) at M=204
 ROTATE_BYTES = 544 << 20       # weight copies in rotation, > 2x the Infinity Cache
 TRAFFIC_FILE = os.path.join(HERE, "profiles", "traffic.json")
 GEMV_KERNEL = "int4_decode_f32_kernel<1, 256, 32, false>"
-GEMM_KERNEL = "int4_gemm_bf16_kernel<false>"
+GEMM_KERNEL = "int4_gemm_bf16_kernel<8, false>"
+GEMM_F32_KERNEL = "int4_gemm_f32x3_kernel"
 DECODE_MFMA_KERNEL = "int4_decode_mfma_kernel<2, 8>"
 GROUPED_KERNEL = "int4_grouped_bf16_kernel"
 FLUSH_BYTES = 512 << 20        # device copy that evicts the Infinity Cache
@@ -919,6 +920,17 @@ def main():
             p, "Int4MatMul M=2048 K=4096 N=4096, bf16 x/out, fp32 accumulate (BASELINE "
                "config 3, the metric's M=2048 leg)", GEMM_KERNEL, "mfma",
             2 * 2048 * 4096 * 4096, p["bytes"])
+        progress("config 3 in f32: prefill M=2048 in the reference API's dtype")
+        pf = bench_gemm(dev, stream, "prefill_m2048_f32", steps=20, warmup=2)
+        lf = gemm_line(
+            pf, "Int4MatMul M=2048 K=4096 N=4096, f32 x/out: config 3's shape in the reference "
+                "API's own dtype (tensor/int4.go:176-179), on the bf16 matrix cores to f32 "
+                "accuracy (x*512s in three bf16 terms against the exact codes)",
+            GEMM_F32_KERNEL, "mfma", 2 * 2048 * 4096 * 4096, pf["bytes"])
+        lf["roofline"]["mfma_issued_flops_per_launch"] = 3 * 2 * 2048 * 4096 * 4096
+        lf["roofline"]["note"] = ("achieved counts the product's own flops; the three-term "
+                                  "split issues three times as many on the matrix cores")
+        extra["prefill_m2048_f32"] = lf
         progress("config 2: decode M=16 K=4096 N=14336")
         d = bench_gemm(dev, stream, "decode_m16", steps=200, warmup=10)
         extra["decode_m16_f32"] = gemm_line(
