@@ -1506,6 +1506,125 @@ hipError_t launch_int4_decode_f32(Device* d, hipStream_t st, const float* a, Int
     return launch_int4_decode_f32(d, st, a + (size_t)8 * K, w, rest, M - 8, K, N, status, ep);
 }
 
+namespace {
+
+// ---- ragged int4 GEMV: the decode form of the grouped product -------------
+//
+// The counterpart of GroupedMatVec / GroupedMatMul (internal/kernels/
+// grouped.go:47-97, groupedtiled.go:77-134) over per-expert int4 weights when
+// there are few routed rows (decode MoE): every row t is a one-row decode
+// product against its expert's matrix, e(t) = #{r : off[r+1] <= t}, with the
+// same workgroup tile, batches and split-K hand-off as Int4MatVec.  Rows past
+// every segment (t >= off[E]) are written 0 by the matvec form and left alone
+// by the matmul form.  Workgroups are ordered (K slice, column tile, row) with
+// the row fastest and dealt to the XCDs in contiguous runs, so the rows of one
+// expert -- adjacent, rows being sorted by expert -- read the same code lines
+// together through one L2.
+
+__device__ __forceinline__ int grouped_expert_of(const uint32_t* off, int E, uint32_t t) {
+    int e = 0;
+    for (int r = 0; r < E; r++) e += (off[r + 1] <= t) ? 1 : 0;
+    return e;
+}
+
+template <int TILE, int CPL, bool PIPE>
+__global__ __launch_bounds__(kDecThreads) void int4_grouped_decode_kernel(
+    const float* __restrict__ x, const uint32_t* __restrict__ codes,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
+    const uint32_t* __restrict__ off, float* __restrict__ out, float* partial,
+    uint32_t* tickets, int ticket_stride, int E, int T, int K, int N, int rows_per_slice,
+    int slices, bool write_padding) {
+    const int tiles = N / TILE;
+    const int grid = gridDim.x;
+    int b = blockIdx.x;
+    if ((grid & 7) == 0) b = (b & 7) * (grid >> 3) + (b >> 3);
+    const int t = b % T;
+    const int tile = (b / T) % tiles;
+    const int slice = b / (T * tiles);
+    const int e = grouped_expert_of(off, E, (uint32_t)t);
+    if (e >= E) {
+        // past every segment: the matvec form writes zeros, once per column tile
+        if (write_padding && slice == 0)
+            for (int c = threadIdx.x; c < TILE; c += kDecThreads)
+                out[(size_t)t * N + tile * TILE + c] = 0.0f;
+        return;
+    }
+    const size_t per = (size_t)K * N;
+    decode_tile<1, TILE, CPL, PIPE>(x + (size_t)t * K, codes + (size_t)e * (per >> 3),
+                                    scales + (size_t)e * (per >> 7),
+                                    zeros + (size_t)e * (per >> 7), out + (size_t)t * N,
+                                    partial ? partial + (size_t)t * slices * N : nullptr,
+                                    tickets + ((size_t)t * tiles + tile) * ticket_stride, K, N,
+                                    tile, slice, rows_per_slice, slices, Epilogue{});
+}
+
+template <int TILE>
+hipError_t launch_grouped_decode_tile(Device* d, hipStream_t st, const float* x, Int4Planes w,
+                                      const uint32_t* off, float* out, int E, int T, int K,
+                                      int N, bool write_padding, int* status) {
+    constexpr int CPL = 32;
+    constexpr int LPR = TILE / CPL;
+    constexpr int RP = kDecThreads / LPR;
+    constexpr int kRowsPerBatch = kBatch * RP;
+    const int tiles = N / TILE;
+    const int batches = (K + kRowsPerBatch - 1) / kRowsPerBatch;
+    // K slices: enough workgroups for two per CU across all rows, at most
+    // one batch each beyond that (the rows already fill the chip)
+    const long long pairs = (long long)T * tiles;
+    int want = (int)std::max(1LL, (2LL * d->cu_count + pairs - 1) / pairs);
+    want = std::min(want, std::min(batches, kMaxSlices));
+    const int per_slice = (batches + want - 1) / want;
+    const int rows = per_slice * kRowsPerBatch;
+    const int slices = (K + rows - 1) / rows;
+    if (pairs * slices > (1ll << 31) - 8) {
+        *status = fail(ACCEL_E_INVALID, "grouped decode product: %d rows x %d tiles is too large",
+                       T, tiles);
+        return hipSuccess;
+    }
+    const int stride = ticket_stride((int)pairs);
+    if (stride == 0) {
+        *status = fail(ACCEL_E_INVALID,
+                       "grouped decode product: %d rows x %d tiles need more tickets than the "
+                       "workspace holds",
+                       T, tiles);
+        return hipSuccess;
+    }
+    float* partial = nullptr;
+    void* ws = workspace(d, st, slices > 1 ? (size_t)T * slices * N * sizeof(float) : 0, status);
+    if (!ws) return hipSuccess;
+    uint32_t* tickets = static_cast<uint32_t*>(ws);
+    if (slices > 1)
+        partial = reinterpret_cast<float*>(static_cast<char*>(ws) + kWorkspaceCounterBytes);
+    const dim3 grid((unsigned)(pairs * slices));
+    if (per_slice > 1)
+        hipLaunchKernelGGL((int4_grouped_decode_kernel<TILE, CPL, true>), grid,
+                           dim3(kDecThreads), 0, st, x, w.codes, w.scales, w.zeros, off, out,
+                           partial, tickets, stride, E, T, K, N, rows, slices, write_padding);
+    else
+        hipLaunchKernelGGL((int4_grouped_decode_kernel<TILE, CPL, false>), grid,
+                           dim3(kDecThreads), 0, st, x, w.codes, w.scales, w.zeros, off, out,
+                           partial, tickets, stride, E, T, K, N, rows, slices, write_padding);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool int4_grouped_decode_supported(int T, int K, int N, const void* codes) {
+    return T >= 1 && T <= kGroupedDecodeRows && K >= 1 && N >= 128 && N % 128 == 0 &&
+           (reinterpret_cast<uintptr_t>(codes) & 15) == 0 && K < (1 << 30) && N < (1 << 30);
+}
+
+hipError_t launch_int4_grouped_decode(Device* d, hipStream_t st, const float* x, Int4Planes w,
+                                      const uint32_t* off, float* out, int E, int T, int K,
+                                      int N, bool write_padding, int* status) {
+    *status = ACCEL_OK;
+    if (N % 256 == 0)
+        return launch_grouped_decode_tile<256>(d, st, x, w, off, out, E, T, K, N, write_padding,
+                                               status);
+    return launch_grouped_decode_tile<128>(d, st, x, w, off, out, E, T, K, N, write_padding,
+                                           status);
+}
+
 // ---- the no-allocation Int4MatVec -----------------------------------------
 //
 // A caller that cannot allocate (code under graph capture, a serving loop

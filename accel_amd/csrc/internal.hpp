@@ -164,6 +164,14 @@ hipError_t launch_grouped_f32(hipStream_t st, const float* x, const float* w,
 hipError_t launch_int4_grouped_f32(hipStream_t st, const float* x, Int4Planes w,
                                    const uint32_t* off, float* out, int E, int T,
                                    int K, int N, bool write_padding);
+// Ragged int4 GEMV (decode MoE): f32 x [T, K], T <= kGroupedDecodeRows, each
+// row against its expert's [K, N] matrix with the decode kernel; the
+// matvec form (write_padding) writes 0 to rows past every segment.
+constexpr int kGroupedDecodeRows = 64;
+bool int4_grouped_decode_supported(int T, int K, int N, const void* codes);
+hipError_t launch_int4_grouped_decode(Device* d, hipStream_t st, const float* x, Int4Planes w,
+                                      const uint32_t* off, float* out, int E, int T, int K,
+                                      int N, bool write_padding, int* status);
 hipError_t launch_int4_grouped_bf16(Device* d, hipStream_t st, const uint16_t* x,
                                     Int4Planes w, const uint32_t* off, uint16_t* out,
                                     int E, int T, int K, int N, bool write_padding);

@@ -649,9 +649,17 @@ int run_grouped_int4(const char* op, int dev, void* stream, const accel_tensor_t
     const Int4Planes p = planes(w);
     hipError_t e;
     if (x->dtype == ACCEL_F32) {
-        e = launch_int4_grouped_f32(st, static_cast<const float*>(x->data), p, off,
-                                    static_cast<float*>(out->data), (int)experts, (int)T,
-                                    (int)K, (int)N, matvec);
+        if (int4_grouped_decode_supported((int)T, (int)K, (int)N, w->codes) &&
+            (uint64_t)experts * (uint64_t)K * (uint64_t)N < (1ull << 40)) {
+            e = launch_int4_grouped_decode(d, st, static_cast<const float*>(x->data), p, off,
+                                           static_cast<float*>(out->data), (int)experts,
+                                           (int)T, (int)K, (int)N, matvec, &status);
+            if (e == hipSuccess && status != ACCEL_OK) return status;
+        } else {
+            e = launch_int4_grouped_f32(st, static_cast<const float*>(x->data), p, off,
+                                        static_cast<float*>(out->data), (int)experts, (int)T,
+                                        (int)K, (int)N, matvec);
+        }
     } else {
         const bool mfma = int4_gemm_bf16_supported(1, (int)K, (int)N) &&
                           (reinterpret_cast<uintptr_t>(x->data) & 15) == 0;

@@ -56,6 +56,7 @@ GEMM_KERNEL = "int4_gemm_bf16_kernel<8, false>"
 GEMM_F32_KERNEL = "int4_gemm_f32x3_kernel"
 DECODE_MFMA_KERNEL = "int4_decode_mfma_kernel<2, 8>"
 GROUPED_KERNEL = "int4_grouped_bf16_kernel"
+GROUPED_DECODE_KERNEL = "int4_grouped_decode_kernel<256, 32, false>"
 FLUSH_BYTES = 512 << 20        # device copy that evicts the Infinity Cache
 PUBLISHED_US = 760.0           # Int4MatVec [2048] x [2048,2048] on an M2, one plan a step
 PUBLISHED_SRC = "specs/010-kernel-corpus.md:593-602 (tensor/decodebench_darwin_test.go:148-189)"
@@ -290,6 +291,48 @@ def bench_moe(dev, stream, steps=20):
                           "traffic": traffic_of(GROUPED_KERNEL), "kernel": GROUPED_KERNEL,
                           "flops_per_launch": int(flops), "bytes_per_launch": int(nbytes),
                           "hbm_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)})
+
+
+def bench_moe_decode(dev, stream, tokens=8, steps=40):
+    """Decode MoE: `tokens` tokens routed top-2 over config 4's eight experts
+    (K=4096, N=14336) as f32 rows, Int4GroupedMatVec -- one decode product
+    per routed row against its expert.  Three copies of the experts (750 MB)
+    rotate and the cache is flushed before the timed replay."""
+    from accel_amd import F32, U32, workloads
+    progress(f"decode MoE: {tokens} tokens, top-2 of 8 experts")
+    m = workloads.moe_fast(tokens=tokens)
+    R = int(m.counts.sum())
+    copies = 3
+    ws = [dev.upload_int4(m.packed, m.scales, m.zeros, m.E * m.K * m.N) for _ in range(copies)]
+    xb = dev.upload(m.x)
+    cb = dev.upload(m.counts, U32)
+    ob = dev.alloc((R, m.N), F32)
+    for w in ws:
+        dev.Int4GroupedMatVec(xb, w, m.E, cb, ob, stream=stream)
+    dev.sync(stream)
+    t = Timed(dev, stream,
+              lambda i: dev.Int4GroupedMatVec(xb, ws[i % copies], m.E, cb, ob, stream=stream),
+              steps)
+    ms = median_replay(t) / steps
+    t.close()
+    active = int((m.counts > 0).sum())
+    per_expert = (m.packed.nbytes + m.scales.nbytes + m.zeros.nbytes) // m.E
+    nbytes = active * per_expert + R * m.K * 4 + R * m.N * 4
+    for b in (xb, cb, ob):
+        b.free()
+    for w in ws:
+        w.free()
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return dict(workload=f"Int4GroupedMatVec, decode MoE: {tokens} tokens routed top-2 over 8 "
+                         f"experts ({R} f32 rows, seed 3's routing), K={m.K}, N={m.N}, f32 out; "
+                         f"the {active} active experts' weights read once; experts rotated over "
+                         f"{copies} copies",
+                us=round(ms * 1e3, 2), rows=R, active_experts=active,
+                counts=[int(c) for c in m.counts],
+                roofline={"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                          "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                          "traffic": traffic_of(GROUPED_DECODE_KERNEL),
+                          "kernel": GROUPED_DECODE_KERNEL, "bytes_per_launch": int(nbytes)})
 
 
 _LAYER_PLANES = {}
@@ -939,6 +982,7 @@ def main():
             2 * 16 * 4096 * 14336, d["bytes"])
         progress("config 4: MoE grouped product")
         extra["moe_grouped_bf16"] = bench_moe(dev, stream)
+        extra["moe_decode_f32"] = bench_moe_decode(dev, stream)
         for b in (1, 8):
             progress(f"config 5: layer chain at batch {b}")
             extra[f"layer_chain_b{b}"] = bench_layer_chain(dev, stream, b)
