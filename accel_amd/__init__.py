@@ -77,6 +77,13 @@ class Int4Desc(ctypes.Structure):
                 ("weights", ctypes.c_int64)]
 
 
+class Int4G32Desc(ctypes.Structure):
+    """accel_int4_g32_t: BASELINE config 1's literal format (32-row groups
+    along K, f32 scale, no zero)."""
+    _fields_ = [("codes", ctypes.c_void_p), ("scales", ctypes.c_void_p),
+                ("K", ctypes.c_int64), ("N", ctypes.c_int64)]
+
+
 QFMT_AWQ, QFMT_GPTQ, QFMT_GPTQ_V2 = 1, 2, 3
 
 
@@ -130,6 +137,8 @@ SIGNATURES = {
     "accel_int4_matvec": ([_i, _vp, _P(Tensor), _P(Int4Desc), _P(Tensor)], _i),
     "accel_int4_matmul": ([_i, _vp, _P(Tensor), _P(Int4Desc), _P(Tensor)], _i),
     "accel_int4_matvec_noalloc": ([_i, _vp, _P(Tensor), _P(Int4Desc), _P(Tensor)], _i),
+    "accel_int4_g32_quantize": ([_vp, ctypes.c_int64, ctypes.c_int64, _vp, _vp], _i),
+    "accel_int4_g32_matvec": ([_i, _vp, _P(Tensor), _P(Int4G32Desc), _P(Tensor)], _i),
     "accel_int4_linear": ([_i, _vp, _P(Tensor), _P(Int4Desc), _P(Tensor), _P(Tensor)], _i),
     "accel_int4_matvec_set": ([_i, _vp, _P(Tensor), _P(Int4Desc), _P(Tensor), _i], _i),
     "accel_int4_matmul_set": ([_i, _vp, _P(Tensor), _P(Int4Desc), _P(Tensor), _i], _i),
@@ -200,6 +209,17 @@ def int4_quantize(w: np.ndarray):
     if n:
         _check(_lib.accel_int4_quantize(_ptr(w), n, _ptr(packed), _ptr(scales), _ptr(zeros)))
     return packed, scales, zeros
+
+
+def int4_g32_quantize(w: np.ndarray):
+    """BASELINE config 1's literal format on host memory: w f32 [K, N] ->
+    (packed u32 [K*N/8], scales f32 [K/32, N])."""
+    w = np.ascontiguousarray(w, np.float32)
+    K, N = w.shape
+    packed = np.zeros(K * N // 8, np.uint32)
+    scales = np.zeros((K // 32, N), np.float32)
+    _check(_lib.accel_int4_g32_quantize(_ptr(w), K, N, _ptr(packed), _ptr(scales)))
+    return packed, scales
 
 
 def int8_quantize(w: np.ndarray):
@@ -495,6 +515,16 @@ class Device:
         ta, tw, to = a.tensor(), w.desc(), out.tensor()
         _check(_lib.accel_int4_matvec_noalloc(self.index, stream, ctypes.byref(ta),
                                               ctypes.byref(tw), ctypes.byref(to)))
+
+    def Int4G32MatVec(self, a: Buffer, codes: Buffer, scales: Buffer, K: int, N: int,
+                      out: Buffer, stream=None) -> None:
+        """BASELINE config 1's literal format: out[N] = a[K] @ ((q - 8) * s),
+        32-row groups along K with an f32 scale (no counterpart in the
+        reference)."""
+        ta, to = a.tensor(), out.tensor()
+        tw = Int4G32Desc(codes.ptr, scales.ptr, K, N)
+        _check(_lib.accel_int4_g32_matvec(self.index, stream, ctypes.byref(ta),
+                                          ctypes.byref(tw), ctypes.byref(to)))
 
     def Int4MatMul(self, a: Buffer, w: Int4Weights, out: Buffer, stream=None) -> None:
         ta, tw, to = a.tensor(), w.desc(), out.tensor()

@@ -1625,6 +1625,138 @@ hipError_t launch_int4_grouped_decode(Device* d, hipStream_t st, const float* x,
                                            status);
 }
 
+namespace {
+
+// ---- BASELINE config 1's literal format ----------------------------------
+//
+// int4 with 32-row groups along K, one f32 scale per (group, column) and no
+// zero point: w = (q - 8) s.  No counterpart in the reference (its groups run
+// along N with an f16 scale and zero); an additive variant, reported
+// separately.  A workgroup of eight waves owns 256 columns and a K slice;
+// wave w takes the slice's 32-row groups w, w + 8, ...: lane (row phase p,
+// column chunk c) decodes rows 4p .. 4p+3 of the group for columns 32c ..
+// 32c+31, the wave's eight row phases are summed across lanes, and each
+// lane scales its four reduced columns once per group:
+//     sum_k x w = s (512 sum_k x (q 2^-9) - 8 sum_k x)
+// (codes through the fp8 converter as in the other decode kernels).  Waves
+// meet in LDS; K slices through the split-K hand-off.
+constexpr int kG32Tile = 256;
+
+__global__ __launch_bounds__(kDecThreads) void int4_g32_matvec_kernel(
+    const float* __restrict__ a, const uint32_t* __restrict__ codes,
+    const float* __restrict__ scales, float* __restrict__ out, float* partial,
+    uint32_t* tickets, int ticket_stride, int K, int N, int rows_per_slice, int slices) {
+    constexpr int TILE = kG32Tile, CPL = 32, LPR = 8, NWAVE = kDecThreads / 64;
+    __shared__ __attribute__((aligned(16))) float red[NWAVE][TILE];
+    __shared__ int last_flag;
+    int tile, slice;
+    place(blockIdx.x, N / TILE, slices, tile, slice);
+    const int tid = threadIdx.x;
+    const int l64 = tid & 63;
+    const int wave = tid >> 6;
+    const int chunk = l64 % LPR;
+    const int phase = l64 / LPR;
+    const int col0 = tile * TILE + chunk * CPL;
+    const int cred = reduced_offset<CPL, 32, LPR>(l64);   // first of this lane's 4 reduced columns
+    const size_t words_per_row = (size_t)(N >> 3);
+    const int k_begin = slice * rows_per_slice;
+    const int k_end = min(K, k_begin + rows_per_slice);
+    const uint32_t* qcol = codes + (col0 >> 3);
+
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int g0 = k_begin + 32 * wave; g0 < k_end; g0 += 32 * NWAVE) {
+        const int r0 = g0 + 4 * phase;
+        uint32_t q[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) load_words<4>(qcol + (size_t)(r0 + i) * words_per_row, q[i]);
+        const f32x4 xv = *reinterpret_cast<const f32x4*>(a + r0);
+        const f32x4 sv =
+            *reinterpret_cast<const f32x4*>(scales + (size_t)(g0 >> 5) * N + col0 + cred);
+        const float xr[4] = {xv.x, xv.y, xv.z, xv.w};
+        float v[CPL];
+#pragma unroll
+        for (int j = 0; j < CPL; j++) v[j] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+#pragma unroll
+            for (int wi = 0; wi < 4; wi++) {
+                float f[8];
+                unpack8(q[i][wi], f);
+#pragma unroll
+                for (int j = 0; j < 8; j++) v[wi * 8 + j] = __builtin_fmaf(xr[i], f[j], v[wi * 8 + j]);
+            }
+        }
+        transpose_reduce<CPL, 32, LPR>(v, l64);
+        // the group's activation sum: the lane's four rows, then the eight
+        // row phases (lanes l ^ 8, ^ 16, ^ 32 hold the other phases)
+        float xs = (xr[0] + xr[1]) + (xr[2] + xr[3]);
+        xs += __shfl_xor(xs, 8, 64);
+        xs += __shfl_xor(xs, 16, 64);
+        xs += __shfl_xor(xs, 32, 64);
+        const float sc[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            acc[e] = __builtin_fmaf(sc[e], __builtin_fmaf(kNibbleScale, v[e], -8.0f * xs), acc[e]);
+    }
+    // after the reduction each lane holds four distinct columns of its wave's
+    // sums; the waves meet in LDS
+#pragma unroll
+    for (int e = 0; e < 4; e++) red[wave][chunk * CPL + cred + e] = acc[e];
+    __syncthreads();
+    const bool split = slices > 1;
+    for (int c = tid; c < TILE; c += kDecThreads) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NWAVE; w++) sum += red[w][c];
+        const int col = tile * TILE + c;
+        if (split)
+            store_device(&partial[(size_t)slice * N + col], sum);
+        else
+            out[col] = sum;
+    }
+    if (!split) return;
+    split_k_finish(partial, tickets + (size_t)tile * ticket_stride, out, tile * TILE, TILE, 1, N,
+                   slices, &last_flag, Epilogue{});
+}
+
+}  // namespace
+
+bool int4_g32_matvec_supported(int K, int N) {
+    return K >= 32 && K % 32 == 0 && N >= kG32Tile && N % kG32Tile == 0 && K < (1 << 30) &&
+           N < (1 << 30);
+}
+
+hipError_t launch_int4_g32_matvec(Device* d, hipStream_t st, const float* a,
+                                  const uint32_t* codes, const float* scales, float* out, int K,
+                                  int N, int* status) {
+    *status = ACCEL_OK;
+    const int tiles = N / kG32Tile;
+    constexpr int kRowsPerPass = 32 * (kDecThreads / 64);   // one group per wave
+    const int passes = (K + kRowsPerPass - 1) / kRowsPerPass;
+    // one pass a workgroup up to 64 slices, as the reference-format GEMV
+    const int per_slice = (passes + kMaxSlices - 1) / kMaxSlices;
+    const int rows = per_slice * kRowsPerPass;
+    const int slices = (K + rows - 1) / rows;
+    float* partial = nullptr;
+    uint32_t* tickets = nullptr;
+    int stride = 0;
+    if (slices > 1) {
+        stride = ticket_stride(tiles);
+        if (stride == 0) {
+            *status = fail(ACCEL_E_INVALID,
+                           "g32 matvec: N=%d needs more tickets than the workspace holds", N);
+            return hipSuccess;
+        }
+        void* ws = workspace(d, st, (size_t)slices * N * sizeof(float), status);
+        if (!ws) return hipSuccess;
+        tickets = static_cast<uint32_t*>(ws);
+        partial = reinterpret_cast<float*>(static_cast<char*>(ws) + kWorkspaceCounterBytes);
+    }
+    hipLaunchKernelGGL(int4_g32_matvec_kernel, dim3(tiles * slices), dim3(kDecThreads), 0, st, a,
+                       codes, scales, out, partial, tickets, stride, K, N, rows, slices);
+    return hipGetLastError();
+}
+
 // ---- the no-allocation Int4MatVec -----------------------------------------
 //
 // A caller that cannot allocate (code under graph capture, a serving loop

@@ -164,6 +164,12 @@ hipError_t launch_grouped_f32(hipStream_t st, const float* x, const float* w,
 hipError_t launch_int4_grouped_f32(hipStream_t st, const float* x, Int4Planes w,
                                    const uint32_t* off, float* out, int E, int T,
                                    int K, int N, bool write_padding);
+// BASELINE config 1's literal format (32-row groups along K, f32 scale, no
+// zero): f32 x [K] -> f32 out [N]; K % 32 == 0, N % 256 == 0.
+bool int4_g32_matvec_supported(int K, int N);
+hipError_t launch_int4_g32_matvec(Device* d, hipStream_t st, const float* a,
+                                  const uint32_t* codes, const float* scales, float* out, int K,
+                                  int N, int* status);
 // Ragged int4 GEMV (decode MoE): f32 x [T, K], T <= kGroupedDecodeRows, each
 // row against its expert's [K, N] matrix with the decode kernel; the
 // matvec form (write_padding) writes 0 to rows past every segment.

@@ -185,6 +185,47 @@ ACCEL_API int accel_int4_matvec(int dev, void* stream, const accel_tensor_t* a,
                             (int)k, (int)n);
 }
 
+// BASELINE config 1's literal format (32-row groups along K, f32 scale, no
+// zero): no counterpart in the reference; Int4MatVec's checks on a and out.
+ACCEL_API int accel_int4_g32_matvec(int dev, void* stream, const accel_tensor_t* a,
+                                    const accel_int4_g32_t* w, accel_tensor_t* out) {
+    clear_error();
+    const char* op = "Int4G32MatVec";
+    if (!w || !w->codes || !w->scales) return refuse(op, "the weight matrix is missing");
+    if (!valid_tensor(a) || !a->data) return refuse(op, "the activations are missing");
+    char buf[256];
+    if (a->dtype != ACCEL_F32 || a->rank != 1) {
+        snprintf(buf, sizeof buf, "activations are %s %s; this kernel reads an f32 vector",
+                 dtype_name(a->dtype), shape_str(a).c_str());
+        return refuse(op, buf);
+    }
+    const int64_t K = w->K, N = w->N;
+    if (a->shape[0] != K) {
+        snprintf(buf, sizeof buf, "activations are %lld long and the matrix is [%lld, %lld]",
+                 (long long)a->shape[0], (long long)K, (long long)N);
+        return refuse(op, buf);
+    }
+    if (K > INT32_MAX || N > INT32_MAX || !int4_g32_matvec_supported((int)K, (int)N)) {
+        snprintf(buf, sizeof buf,
+                 "[%lld, %lld]: this kernel takes K a multiple of 32 and N of 256",
+                 (long long)K, (long long)N);
+        return refuse(op, buf);
+    }
+    if (((reinterpret_cast<uintptr_t>(w->codes) | reinterpret_cast<uintptr_t>(w->scales) |
+          reinterpret_cast<uintptr_t>(a->data)) & 15) != 0)
+        return refuse(op, "codes, scales and activations must be 16-byte aligned");
+    int rc = check_out(op, out, ACCEL_F32, 1, N, true);
+    if (rc != ACCEL_OK) return rc;
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    int status = begin_submission(d);
+    if (status != ACCEL_OK) return status;
+    const hipError_t e = launch_int4_g32_matvec(
+        d, (hipStream_t)stream, static_cast<const float*>(a->data), w->codes, w->scales,
+        static_cast<float*>(out->data), (int)K, (int)N, &status);
+    return finish(d, e, status, "Int4G32MatVec launch");
+}
+
 // Int4MatVec without allocating: the same checks and kernels, with the
 // split-K buffers in the library's static scratch.
 ACCEL_API int accel_int4_matvec_noalloc(int dev, void* stream, const accel_tensor_t* a,

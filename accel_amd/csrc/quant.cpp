@@ -193,6 +193,42 @@ ACCEL_API int accel_int4_quantize(const float* w, int64_t n, uint32_t* packed,
     return ACCEL_OK;
 }
 
+// BASELINE config 1's literal format (no counterpart in the reference, whose
+// groups are 128 flat weights with an f16 scale and zero): groups of 32 rows
+// of one column, s = f32(amax / 7), q = clamp(rne(f32(w / s)), -8, 7) + 8,
+// packed as quant/int4 packs (element k*N + n, low nibble first); a group of
+// zeros has s = 0 and codes 8.  Finite weights.
+ACCEL_API int accel_int4_g32_quantize(const float* w, int64_t K, int64_t N, uint32_t* packed,
+                                      float* scales) {
+    accel::clear_error();
+    if (K < 0 || N < 0 || K % 32 != 0 || (K * N) % 8 != 0)
+        return accel::fail(ACCEL_E_INVALID,
+                           "accel_int4_g32_quantize: K=%lld, N=%lld (K must be a multiple of "
+                           "32 and K*N of 8)",
+                           (long long)K, (long long)N);
+    if (K == 0 || N == 0) return ACCEL_OK;
+    if (!w || !packed || !scales)
+        return accel::fail(ACCEL_E_INVALID, "accel_int4_g32_quantize: NULL pointer");
+    std::fill(packed, packed + K * N / 8, 0u);
+    for (int64_t g = 0; g < K / 32; g++) {
+        for (int64_t n = 0; n < N; n++) {
+            float amax = 0.0f;
+            for (int64_t r = 0; r < 32; r++) amax = std::fmax(amax, std::fabs(w[(g * 32 + r) * N + n]));
+            const float sc = amax / 7.0f;
+            scales[g * N + n] = sc;
+            for (int64_t r = 0; r < 32; r++) {
+                const int64_t i = (g * 32 + r) * N + n;
+                float rq = 0.0f;
+                if (sc != 0.0f) rq = std::nearbyint(w[i] / sc);
+                rq = std::fmin(std::fmax(rq, -8.0f), 7.0f);
+                const uint32_t q = (uint32_t)(int)(rq + 8.0f);
+                packed[i >> 3] |= q << (4 * (i & 7));
+            }
+        }
+    }
+    return ACCEL_OK;
+}
+
 ACCEL_API int accel_int4_dequantize(const uint32_t* packed, const uint16_t* scales,
                                     const uint16_t* zeros, int64_t n, float* out) {
     accel::clear_error();

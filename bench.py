@@ -56,6 +56,7 @@ GEMM_KERNEL = "int4_gemm_bf16_kernel<8, false>"
 GEMM_F32_KERNEL = "int4_gemm_f32x3_kernel"
 DECODE_MFMA_KERNEL = "int4_decode_mfma_kernel<2, 8>"
 GROUPED_KERNEL = "int4_grouped_bf16_kernel"
+G32_KERNEL = "int4_g32_matvec_kernel"
 GROUPED_DECODE_KERNEL = "int4_grouped_decode_kernel<256, 32, false>"
 FLUSH_BYTES = 512 << 20        # device copy that evicts the Infinity Cache
 PUBLISHED_US = 760.0           # Int4MatVec [2048] x [2048,2048] on an M2, one plan a step
@@ -236,6 +237,51 @@ def bench_gemv(dev, stream, steps, warmup):
     bytes_per = workloads.algorithmic_bytes(1, L.K, L.N)
     return dict(ms=ms, bytes=bytes_per, gbs=bytes_per / (ms * 1e-3) / 1e9, copies=copies,
                 L=L, out=got)
+
+
+def bench_gemv_g32(dev, stream, steps=640, warmup=64):
+    """Config 1 in BASELINE's literal format (32-row groups along K, f32 scale,
+    no zero: no counterpart in the reference), the additive variant reported
+    beside the reference-format headline.  Weights rotated over copies
+    totalling more than 512 MB; cache flushed before the timed replay."""
+    import accel_amd
+    from accel_amd import F32, U32
+    rng = np.random.Generator(np.random.PCG64(0))
+    x = rng.standard_normal((1, 4096)).astype(np.float32)
+    w = np.ascontiguousarray((rng.standard_normal((4096, 4096)) * 0.02).astype(np.float32).T)
+    p, sc = accel_amd.int4_g32_quantize(w)
+    K = N = 4096
+    per = p.nbytes + sc.nbytes
+    copies = max(1, -(-ROTATE_BYTES // per))
+    cs = [dev.upload(p, U32) for _ in range(copies)]
+    ss = [dev.upload(sc.reshape(-1), F32) for _ in range(copies)]
+    a = dev.upload(x[0])
+    out = dev.alloc((N,), F32)
+    for i in range(copies):
+        dev.Int4G32MatVec(a, cs[i], ss[i], K, N, out, stream)
+    dev.sync(stream)
+    if warmup:
+        wt = Timed(dev, stream, lambda i: dev.Int4G32MatVec(a, cs[i % copies], ss[i % copies],
+                                                             K, N, out, stream), warmup)
+        wt.run()
+        wt.close()
+    t = Timed(dev, stream, lambda i: dev.Int4G32MatVec(a, cs[i % copies], ss[i % copies], K, N,
+                                                        out, stream), steps)
+    ms = median_replay(t) / steps
+    t.close()
+    for b in cs + ss + [a, out]:
+        b.free()
+    nbytes = K * N // 2 + 4 * (K // 32) * N + 4 * K + 4 * N
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return dict(workload="config 1 in BASELINE's literal format -- int4, 32-row groups along K, "
+                         "f32 scale, no zero point (an additive variant: the reference format "
+                         "has 128-weight groups with f16 scale and zero); Int4G32MatVec M=1 "
+                         f"K=N=4096, f32 x/out, seed 0; weights rotated over {copies} copies",
+                us=round(ms * 1e3, 3),
+                roofline={"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                          "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                          "traffic": traffic_of(G32_KERNEL), "kernel": G32_KERNEL,
+                          "bytes_per_launch": int(nbytes)})
 
 
 def bench_gemm(dev, stream, name, steps=40, warmup=4):
@@ -957,6 +1003,8 @@ def main():
     }
     if not args.no_extra:
         extra = {}
+        progress("config 1 in BASELINE's literal format (G=32 along K, f32 scale)")
+        extra["gemv_m1_g32_literal"] = bench_gemv_g32(dev, stream)
         progress("config 3: prefill M=2048 bf16")
         p = bench_gemm(dev, stream, "prefill_m2048")
         extra["prefill_m2048_bf16"] = gemm_line(

@@ -291,6 +291,30 @@ int accel_int4_repack(int dev, void* stream, const accel_foreign_int4_t* src,
 int accel_int4_matvec(int dev, void* stream, const accel_tensor_t* a,
                       const accel_int4_t* w, accel_tensor_t* out);
 
+/* BASELINE config 1's literal weight format, an additive variant with no
+ * counterpart in the reference (whose groups are 128 flat weights with an f16
+ * scale and an f16 zero, quant/int4.go:29,71-138): groups of 32 rows of one
+ * column along K, one f32 scale per group, no zero point.  codes are packed
+ * as quant/int4 packs them (element k*N + n is nibble (k*N+n) % 8 of word
+ * (k*N+n) / 8, low nibble first, quant/int4.go:141-153); scales is [K/32, N];
+ * w = (q - 8) * s.  Reported separately from the reference format. */
+typedef struct accel_int4_g32 {
+    const uint32_t* codes;   /* K*N/8 words */
+    const float* scales;     /* K/32 * N */
+    int64_t K, N;
+} accel_int4_g32_t;
+
+/* Host packer of that format: s = f32(amax / 7) over the group (0 for a
+ * group of zeros), q = clamp(rne(f32(w / s)), -8, 7) + 8.  w is [K, N] f32,
+ * finite; K % 32 == 0, K*N % 8 == 0. */
+int accel_int4_g32_quantize(const float* w, int64_t K, int64_t N, uint32_t* packed,
+                            float* scales);
+
+/* out[N] = a[K] @ w for the format above, f32 activations and result
+ * (Int4MatVec's shape and checks on a and out); K % 32 == 0, N % 256 == 0. */
+int accel_int4_g32_matvec(int dev, void* stream, const accel_tensor_t* a,
+                          const accel_int4_g32_t* w, accel_tensor_t* out);
+
 /* Int4MatVec that allocates nothing: the same checks, kernels and results
  * (bit for bit) as accel_int4_matvec, with the K-split's tickets and partial
  * sums in a static device array of 4 MiB + 64 KiB that every GPU the library
