@@ -57,7 +57,7 @@ GEMM_F32_KERNEL = "int4_gemm_f32x3_kernel"
 DECODE_MFMA_KERNEL = "int4_decode_mfma_kernel<2, 8>"
 GROUPED_KERNEL = "int4_grouped_bf16_kernel"
 G32_KERNEL = "int4_g32_matvec_kernel"
-GROUPED_DECODE_KERNEL = "int4_grouped_decode_kernel<256, 32, false>"
+GROUPED_DECODE_KERNEL = "int4_grouped_decode_kernel<256, 32, true>"
 FLUSH_BYTES = 512 << 20        # device copy that evicts the Infinity Cache
 PUBLISHED_US = 760.0           # Int4MatVec [2048] x [2048,2048] on an M2, one plan a step
 PUBLISHED_SRC = "specs/010-kernel-corpus.md:593-602 (tensor/decodebench_darwin_test.go:148-189)"
