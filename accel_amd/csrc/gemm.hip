@@ -61,6 +61,7 @@ constexpr int BM = 256, BN = 128, BK = 64;
 constexpr int kThreads = 256;        // four waves, one per SIMD
 constexpr int kARowBytes = BK * 2;   // one LDS activation row: 64 bf16
 constexpr int kBQuadWords = BN / 2;  // u32 words per row quad: one per code byte
+constexpr int MAX_MT = BM / 32;      // 32-row m-tiles of a full tile
 
 // Byte offset of 16-byte chunk `c` of activation row `r` under the swizzle:
 // LDS has 64 banks (256 bytes), two rows wide; each row pair puts a chunk
@@ -95,14 +96,16 @@ __device__ __forceinline__ u32x4 transpose4(uint32_t r0, uint32_t r1, uint32_t r
 struct __attribute__((aligned(16))) GemmStage {
     char a[BM * kARowBytes];                  // 32 KB, swizzled rows
     uint32_t b[(BK / 4) * kBQuadWords];       // 4 KB: [row quad][code byte]
-    f32x2 fold[BK];                           // (512 s, add) per row of the stage
+    f32x2 fold[BK + 64];                      // (512 s, add) per row of the stage; 64 spare
 };
+// The stages, and after the last one the accumulator hand-off of the
+// k-parity wave pairs: [column half][m-tile][n-tile][register quad][lane],
+// 16 KB an m-tile.  MTR: the m-tiles a kernel may run.
+template <int MTR>
 struct __attribute__((aligned(16))) GemmLds {
     union {
         GemmStage st[2];
-        // Accumulator hand-off of the k-parity wave pairs, four m-tiles at a
-        // time: [column half][m-tile][n-tile][register quad][lane].
-        f32x4 red[2][4][2][4][64];
+        f32x4 red[2][MTR][2][4][64];
     };
 };
 
@@ -142,18 +145,19 @@ struct SubstepRegs {
 // kt+1 visible before that substep reads the next stage's operands.  A
 // wave pipelines its substeps: while the MFMAs of one run, it dequantises
 // the next one's codes, read from LDS at the start of the current one.
-template <int MT, bool BIAS>
-__device__ __forceinline__ void gemm_tile_bf16(GemmLds& lds, const uint16_t* __restrict__ a,
+template <int MT, bool BIAS, int MTR>
+__device__ __forceinline__ void gemm_tile_bf16(GemmLds<MTR>& lds, const uint16_t* __restrict__ a,
                                                const uint32_t* __restrict__ codes,
                                                const uint16_t* __restrict__ scales,
                                                const uint16_t* __restrict__ zeros,
                                                uint16_t* __restrict__ out, int m0, int m_end,
                                                int n0, int K, int N,
                                                const float* __restrict__ bias) {
+    static_assert(MT <= MTR, "hand-off slots");
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int ch = wave & 1;     // column half
-    const int kp = wave >> 1;    // substep parity
+    const int kp = __builtin_amdgcn_readfirstlane(wave >> 1);    // substep parity
     const int lane = tid & 63;
     const int c32 = lane & 31;   // MFMA row (A) / column (B, D) within a 32 x 32 tile
     const int kg = lane >> 5;    // MFMA k-group (8 consecutive k)
@@ -179,9 +183,13 @@ __device__ __forceinline__ void gemm_tile_bf16(GemmLds& lds, const uint16_t* __r
     const int b_cc = tid & 15;
     const uint32_t* b_src = codes + (size_t)(4 * b_rq) * words_per_row + (n0 >> 3) + b_cc;
     const int b_dst = b_off(b_rq, 4 * b_cc);
-    // Fold staging: one row per lane, every wave alike (the same value to the
-    // same place), so the stage code has no branch to cut the schedule.
-    const int f_row = lane;
+    // Fold staging: wave w folds the stage's rows 16w .. 16w + 15, four lanes
+    // a row.  A load whose lanes name many rows costs the address unit about
+    // a cycle a row, so the 64 rows are split over the waves rather than
+    // loaded by each; lanes 16 .. 63 write their duplicate to spare slots, so
+    // the stage code has no branch to cut the schedule.
+    const int f_row = 16 * wave + (lane & 15);
+    const int f_dst = lane < 16 ? f_row : BK + lane;
     const size_t f_g = (size_t)(n0 >> 7);
     const uint16_t* s_src = scales + (size_t)f_row * groups_per_row + f_g;
     const uint16_t* z_src = zeros + (size_t)f_row * groups_per_row + f_g;
@@ -211,7 +219,7 @@ __device__ __forceinline__ void gemm_tile_bf16(GemmLds& lds, const uint16_t* __r
         f32x2 f;
         f.x = s * 512.0f;
         f.y = (s == 0.0f) ? z : -(z * s);
-        S.fold[f_row] = f;
+        S.fold[f_dst] = f;
     };
     // This lane's code byte: 32*ch + c32 (columns 64ch + 2c32, + 1).
     const int my_bc = 32 * ch + c32;
@@ -365,7 +373,7 @@ __device__ __forceinline__ void gemm_tile_bf16(GemmLds& lds, const uint16_t* __r
                     f32x2 f;
                     f.x = sv * 512.0f;
                     f.y = (sv == 0.0f) ? zv : -(zv * sv);
-                    WS.fold[f_row] = f;
+                    WS.fold[f_dst] = f;
                     return;
                 }
                 if (it == 6) { cs.s = s_src[(size_t)k0c * groups_per_row]; return; }
@@ -426,72 +434,70 @@ __device__ __forceinline__ void gemm_tile_bf16(GemmLds& lds, const uint16_t* __r
     const int col = n0 + 64 * ch + 2 * c32;
     float bj[2] = {0.0f, 0.0f};
     if constexpr (BIAS) {
-        if (kp == 0) {
-            bj[0] = bias[col];
-            bj[1] = bias[col + 1];
-        }
+        bj[0] = bias[col];
+        bj[1] = bias[col + 1];
     }
 
-    // The odd-parity waves hand their accumulators to the even ones through
-    // LDS, four m-tiles at a time.
-    __syncthreads();
+    // The two parities of a column half split the m-tiles: parity 0 finishes
+    // [0, MT0), parity 1 [MT0, MT).  Each hands the other the partial sums
+    // of the m-tiles it does not finish through LDS (one round, every m-tile
+    // its own slot), then adds what it received: the sum of the two
+    // parities' f32 values, the same whichever wave adds them.
+    constexpr int MT0 = (MT + 1) / 2;
+    auto give = [&](auto KP) {
+        constexpr int p = decltype(KP)::value;
 #pragma unroll
-    for (int hp = 0; hp < (MT + 3) / 4; hp++) {
-        if (kp == 1) {
+        for (int t = p == 0 ? MT0 : 0; t < (p == 0 ? MT : MT0); t++) {
 #pragma unroll
-            for (int tt = 0; tt < 4; tt++) {
-                const int t = 4 * hp + tt;
-                if (t >= MT) break;
+            for (int j = 0; j < 2; j++)
 #pragma unroll
-                for (int j = 0; j < 2; j++)
-#pragma unroll
-                    for (int q = 0; q < 4; q++) {
-                        const f32x16& v = acc[t][j];
-                        lds.red[ch][tt][j][q][lane] =
-                            (f32x4){v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
-                    }
-            }
+                for (int q = 0; q < 4; q++) {
+                    const f32x16& v = acc[t][j];
+                    lds.red[ch][t][j][q][lane] =
+                        (f32x4){v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+                }
+            __builtin_amdgcn_sched_barrier(0);   // one m-tile at a time
         }
-        __syncthreads();
-        if (kp == 0) {
-#pragma unroll
-            for (int tt = 0; tt < 4; tt++) {
-                const int t = 4 * hp + tt;
-                if (t >= MT) break;
-#pragma unroll
-                for (int j = 0; j < 2; j++)
-#pragma unroll
-                    for (int q = 0; q < 4; q++) {
-                        const f32x4 v = lds.red[ch][tt][j][q][lane];
-                        f32x16& d = acc[t][j];
-                        d[4 * q] += v.x;
-                        d[4 * q + 1] += v.y;
-                        d[4 * q + 2] += v.z;
-                        d[4 * q + 3] += v.w;
-                    }
-            }
-        }
-        __syncthreads();
-    }
-    if (kp == 1) return;
-
+    };
     // D of a 32 x 32 tile: lane holds column lane % 32; register r is row
     // 8*(r/4) + 4*(lane/32) + r%4.  A lane's two n-tiles are two adjacent
     // columns; the fused bias is one f32 value per column, added before the
-    // one rounding.
+    // one rounding.  Row addresses are a uniform row base plus this lane's
+    // offset; a tile wholly inside [m0, m_end) stores without row checks.
+    const bool whole = m0 + 32 * MT <= m_end;
+    const uint32_t lane_off = (uint32_t)(4 * kg) * (uint32_t)N + (uint32_t)col;
+    auto take_store = [&](auto KP) {
+        constexpr int p = decltype(KP)::value;
 #pragma unroll
-    for (int t = 0; t < MT; t++) {
+        for (int t = p == 0 ? 0 : MT0; t < (p == 0 ? MT0 : MT); t++) {
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int row = m0 + t * 32 + 8 * (r >> 2) + 4 * kg + (r & 3);
-            if (row < m_end) {
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const f32x4 v = lds.red[ch][t][j][q][lane];
+                    f32x16& d = acc[t][j];
+                    d[4 * q] += v.x;
+                    d[4 * q + 1] += v.y;
+                    d[4 * q + 2] += v.z;
+                    d[4 * q + 3] += v.w;
+                }
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int dr = t * 32 + 8 * (r >> 2) + (r & 3);   // row - m0 - 4 kg
                 bf16x2 v;
                 v[0] = (__bf16)(BIAS ? acc[t][0][r] + bj[0] : acc[t][0][r]);
                 v[1] = (__bf16)(BIAS ? acc[t][1][r] + bj[1] : acc[t][1][r]);
-                *reinterpret_cast<bf16x2*>(out + (size_t)row * N + col) = v;
+                uint16_t* rowp = out + (size_t)(m0 + dr) * N;
+                if (whole || m0 + dr + 4 * kg < m_end)
+                    *reinterpret_cast<bf16x2*>(rowp + lane_off) = v;
             }
+            __builtin_amdgcn_sched_barrier(0);   // one m-tile at a time
         }
-    }
+    };
+    __syncthreads();   // every wave is past its last read of the stages
+    if (kp == 0) give(I0{}); else give(I1{});
+    __syncthreads();
+    if (kp == 0) take_store(I0{}); else take_store(I1{});
 }
 
 // Row bands of BM rows by column tiles of BN; MT = 8 for the full bands, the
@@ -502,7 +508,7 @@ __global__ __launch_bounds__(kThreads, 1) void int4_gemm_bf16_kernel(
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
     uint16_t* __restrict__ out, int m_first, int M, int K, int N,
     const float* __restrict__ bias) {
-    __shared__ GemmLds lds;
+    __shared__ GemmLds<MT> lds;
     const int tiles_n = N / BN;
     const int grid = gridDim.x;
     int b = blockIdx.x;
@@ -526,7 +532,7 @@ __global__ __launch_bounds__(kThreads, 1) void int4_grouped_bf16_kernel(
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
     const uint32_t* __restrict__ off, uint16_t* __restrict__ out, int E, int T, int K,
     int N) {
-    __shared__ GemmLds lds;
+    __shared__ GemmLds<MAX_MT> lds;
     const int tiles_n = N / BN;
     auto rows_of = [&](int e, uint32_t& first, uint32_t& last) {
         first = off[e];
@@ -612,7 +618,7 @@ struct __attribute__((aligned(16))) XLds {
         // [column half][m-tile][n-tile][register quad][lane]
         f32x4 red[2][4][2][4][64];
     };
-    f32x2 fold[2][BK];     // (512 s, add) of the stage rows, double-buffered
+    f32x2 fold[2][BK + 64];   // (512 s, add) of the stage rows, double-buffered; 64 spare
     float corr[XBM];       // sum_k x add of each row, at the end
 };
 
@@ -684,7 +690,8 @@ __global__ __launch_bounds__(kThreads, 1) void int4_gemm_f32x3_kernel(
     const int b_cc = tid & 15;
     const uint32_t* b_src = codes + (size_t)(4 * b_rq) * words_per_row + (n0 >> 3) + b_cc;
     const int b_dst = b_off(b_rq, 4 * b_cc);
-    const int f_row = lane;
+    const int f_row = 16 * wave + (lane & 15);
+    const int f_dst = lane < 16 ? f_row : BK + lane;
     const size_t f_g = (size_t)(n0 >> 7);
     const uint16_t* s_src = scales + (size_t)f_row * groups_per_row + f_g;
     const uint16_t* z_src = zeros + (size_t)f_row * groups_per_row + f_g;
@@ -718,7 +725,7 @@ __global__ __launch_bounds__(kThreads, 1) void int4_gemm_f32x3_kernel(
         f32x2 f;
         f.x = sv * 512.0f;
         f.y = (sv == 0.0f) ? zv : -(zv * sv);
-        lds.fold[fb][f_row] = f;
+        lds.fold[fb][f_dst] = f;
     };
     float corr[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     // The three terms of m-tile i's chunk, from its activations and the
