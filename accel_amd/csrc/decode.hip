@@ -1558,24 +1558,41 @@ __global__ __launch_bounds__(kDecThreads) void int4_grouped_decode_kernel(
                                     tile, slice, rows_per_slice, slices, Epilogue{});
 }
 
+// K slices of a grouped decode launch: enough workgroups for two per CU
+// across all rows, at most one batch each beyond that (the rows already fill
+// the chip).
+template <int TILE>
+struct GroupedDecodeShape {
+    static constexpr int CPL = 32;
+    static constexpr int LPR = TILE / CPL;
+    static constexpr int RP = kDecThreads / LPR;
+    static constexpr int kRowsPerBatch = kBatch * RP;
+    int tiles, per_slice, rows, slices;
+    long long pairs;
+    GroupedDecodeShape(const Device* d, int T, int K, int N) {
+        tiles = N / TILE;
+        const int batches = (K + kRowsPerBatch - 1) / kRowsPerBatch;
+        pairs = (long long)T * tiles;
+        int want = (int)std::max(1LL, (2LL * d->cu_count + pairs - 1) / pairs);
+        want = std::min(want, std::min(batches, kMaxSlices));
+        per_slice = (batches + want - 1) / want;
+        rows = per_slice * kRowsPerBatch;
+        slices = (K + rows - 1) / rows;
+    }
+    size_t area_bytes(int T, int N) const {
+        return slices > 1 ? (size_t)T * slices * N * sizeof(float) : 0;
+    }
+};
+
 template <int TILE>
 hipError_t launch_grouped_decode_tile(Device* d, hipStream_t st, const float* x, Int4Planes w,
                                       const uint32_t* off, float* out, int E, int T, int K,
-                                      int N, bool write_padding, int* status) {
-    constexpr int CPL = 32;
-    constexpr int LPR = TILE / CPL;
-    constexpr int RP = kDecThreads / LPR;
-    constexpr int kRowsPerBatch = kBatch * RP;
-    const int tiles = N / TILE;
-    const int batches = (K + kRowsPerBatch - 1) / kRowsPerBatch;
-    // K slices: enough workgroups for two per CU across all rows, at most
-    // one batch each beyond that (the rows already fill the chip)
-    const long long pairs = (long long)T * tiles;
-    int want = (int)std::max(1LL, (2LL * d->cu_count + pairs - 1) / pairs);
-    want = std::min(want, std::min(batches, kMaxSlices));
-    const int per_slice = (batches + want - 1) / want;
-    const int rows = per_slice * kRowsPerBatch;
-    const int slices = (K + rows - 1) / rows;
+                                      int N, bool write_padding, int* status,
+                                      uint32_t* tickets, float* area) {
+    constexpr int CPL = GroupedDecodeShape<TILE>::CPL;
+    const GroupedDecodeShape<TILE> sh(d, T, K, N);
+    const int tiles = sh.tiles, per_slice = sh.per_slice, rows = sh.rows, slices = sh.slices;
+    const long long pairs = sh.pairs;
     if (pairs * slices > (1ll << 31) - 8) {
         *status = fail(ACCEL_E_INVALID, "grouped decode product: %d rows x %d tiles is too large",
                        T, tiles);
@@ -1589,12 +1606,8 @@ hipError_t launch_grouped_decode_tile(Device* d, hipStream_t st, const float* x,
                        T, tiles);
         return hipSuccess;
     }
-    float* partial = nullptr;
-    void* ws = workspace(d, st, slices > 1 ? (size_t)T * slices * N * sizeof(float) : 0, status);
-    if (!ws) return hipSuccess;
-    uint32_t* tickets = static_cast<uint32_t*>(ws);
-    if (slices > 1)
-        partial = reinterpret_cast<float*>(static_cast<char*>(ws) + kWorkspaceCounterBytes);
+    // the split-K sums live in the caller's area, past the offsets
+    float* partial = slices > 1 ? area : nullptr;
     const dim3 grid((unsigned)(pairs * slices));
     if (per_slice > 1)
         hipLaunchKernelGGL((int4_grouped_decode_kernel<TILE, CPL, true>), grid,
@@ -1614,15 +1627,21 @@ bool int4_grouped_decode_supported(int T, int K, int N, const void* codes) {
            (reinterpret_cast<uintptr_t>(codes) & 15) == 0 && K < (1 << 30) && N < (1 << 30);
 }
 
+size_t int4_grouped_decode_area(const Device* d, int T, int K, int N) {
+    if (N % 256 == 0) return GroupedDecodeShape<256>(d, T, K, N).area_bytes(T, N);
+    return GroupedDecodeShape<128>(d, T, K, N).area_bytes(T, N);
+}
+
 hipError_t launch_int4_grouped_decode(Device* d, hipStream_t st, const float* x, Int4Planes w,
                                       const uint32_t* off, float* out, int E, int T, int K,
-                                      int N, bool write_padding, int* status) {
+                                      int N, bool write_padding, int* status,
+                                      uint32_t* tickets, float* area) {
     *status = ACCEL_OK;
     if (N % 256 == 0)
         return launch_grouped_decode_tile<256>(d, st, x, w, off, out, E, T, K, N, write_padding,
-                                               status);
+                                               status, tickets, area);
     return launch_grouped_decode_tile<128>(d, st, x, w, off, out, E, T, K, N, write_padding,
-                                           status);
+                                           status, tickets, area);
 }
 
 namespace {

@@ -174,10 +174,16 @@ hipError_t launch_int4_g32_matvec(Device* d, hipStream_t st, const float* a,
 // row against its expert's [K, N] matrix with the decode kernel; the
 // matvec form (write_padding) writes 0 to rows past every segment.
 constexpr int kGroupedDecodeRows = 64;
+// The grouped decode launch takes the workspace's counters (`tickets`) and an
+// area past the offsets for its split-K sums, of the size
+// int4_grouped_decode_area gives (the workspace is sized once, before the
+// offsets are computed, so it cannot grow and move them).
 bool int4_grouped_decode_supported(int T, int K, int N, const void* codes);
+size_t int4_grouped_decode_area(const Device* d, int T, int K, int N);
 hipError_t launch_int4_grouped_decode(Device* d, hipStream_t st, const float* x, Int4Planes w,
                                       const uint32_t* off, float* out, int E, int T, int K,
-                                      int N, bool write_padding, int* status);
+                                      int N, bool write_padding, int* status,
+                                      uint32_t* tickets, float* area);
 hipError_t launch_int4_grouped_bf16(Device* d, hipStream_t st, const uint16_t* x,
                                     Int4Planes w, const uint32_t* off, uint16_t* out,
                                     int E, int T, int K, int N, bool write_padding);

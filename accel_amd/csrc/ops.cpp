@@ -586,13 +586,20 @@ int check_grouped(const char* op, const accel_tensor_t* x, const accel_tensor_t*
 }
 
 // Offsets for `experts` counts into the workspace; returns the device
-// pointer or nullptr with status set.
+// pointer or nullptr with status set.  The workspace is laid out as its
+// counters, the offsets [experts + 1] (rounded up to 256 bytes), then
+// `area_bytes` for the product's own sums (*area, when asked for).  It is
+// sized for all of that here, once, before the offsets are written, so no
+// later request can grow it and move them.
 uint32_t* offsets_in_workspace(Device* d, hipStream_t st, const uint32_t* counts,
-                               int64_t experts, int* status) {
-    void* ws = workspace(d, st, (size_t)(experts + 1) * sizeof(uint32_t), status);
+                               int64_t experts, int* status, size_t area_bytes = 0,
+                               void** area = nullptr) {
+    const size_t off_bytes = ((size_t)(experts + 1) * sizeof(uint32_t) + 255) / 256 * 256;
+    void* ws = workspace(d, st, off_bytes + area_bytes, status);
     if (!ws) return nullptr;
-    uint32_t* off =
-        reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + kWorkspaceCounterBytes);
+    char* data = static_cast<char*>(ws) + kWorkspaceCounterBytes;
+    uint32_t* off = reinterpret_cast<uint32_t*>(data);
+    if (area) *area = area_bytes ? data + off_bytes : nullptr;
     hipError_t e = launch_segment_offsets(st, counts, off, (int)experts);
     if (e != hipSuccess) {
         *status = classify(d, e, "SegmentOffsets launch");
@@ -684,17 +691,28 @@ int run_grouped_int4(const char* op, int dev, void* stream, const accel_tensor_t
     int status = begin_submission(d);
     if (status != ACCEL_OK) return status;
     hipStream_t st = (hipStream_t)stream;
+    // the path, and the workspace it needs past the offsets
+    const bool f32 = x->dtype == ACCEL_F32;
+    const bool decode = f32 && int4_grouped_decode_supported((int)T, (int)K, (int)N, w->codes) &&
+                        (uint64_t)experts * (uint64_t)K * (uint64_t)N < (1ull << 40);
+    if (!f32 && !(int4_gemm_bf16_supported(1, (int)K, (int)N) &&
+                  (reinterpret_cast<uintptr_t>(x->data) & 15) == 0))
+        return refuse(op, "bf16 grouped products need K % 64 == 0 and N % 128 == 0");
+    const size_t area_bytes = decode ? int4_grouped_decode_area(d, (int)T, (int)K, (int)N) : 0;
+    void* area = nullptr;
     uint32_t* off = offsets_in_workspace(d, st, static_cast<const uint32_t*>(counts->data),
-                                         experts, &status);
+                                         experts, &status, area_bytes, &area);
     if (!off) return status;
+    uint32_t* tickets = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(off) -
+                                                    kWorkspaceCounterBytes);
     const Int4Planes p = planes(w);
     hipError_t e;
-    if (x->dtype == ACCEL_F32) {
-        if (int4_grouped_decode_supported((int)T, (int)K, (int)N, w->codes) &&
-            (uint64_t)experts * (uint64_t)K * (uint64_t)N < (1ull << 40)) {
+    if (f32) {
+        if (decode) {
             e = launch_int4_grouped_decode(d, st, static_cast<const float*>(x->data), p, off,
                                            static_cast<float*>(out->data), (int)experts,
-                                           (int)T, (int)K, (int)N, matvec, &status);
+                                           (int)T, (int)K, (int)N, matvec, &status, tickets,
+                                           static_cast<float*>(area));
             if (e == hipSuccess && status != ACCEL_OK) return status;
         } else {
             e = launch_int4_grouped_f32(st, static_cast<const float*>(x->data), p, off,
@@ -702,10 +720,6 @@ int run_grouped_int4(const char* op, int dev, void* stream, const accel_tensor_t
                                         (int)K, (int)N, matvec);
         }
     } else {
-        const bool mfma = int4_gemm_bf16_supported(1, (int)K, (int)N) &&
-                          (reinterpret_cast<uintptr_t>(x->data) & 15) == 0;
-        if (!mfma)
-            return refuse(op, "bf16 grouped products need K % 64 == 0 and N % 128 == 0");
         e = launch_int4_grouped_bf16(d, st, static_cast<const uint16_t*>(x->data), p, off,
                                      static_cast<uint16_t*>(out->data), (int)experts, (int)T,
                                      (int)K, (int)N, matvec);
