@@ -157,7 +157,7 @@ __device__ __forceinline__ void gemm_tile_bf16(GemmLds<MTR>& lds, const uint16_t
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int ch = wave & 1;     // column half
-    const int kp = __builtin_amdgcn_readfirstlane(wave >> 1);    // substep parity
+    const int kp = wave >> 1;    // substep parity
     const int lane = tid & 63;
     const int c32 = lane & 31;   // MFMA row (A) / column (B, D) within a 32 x 32 tile
     const int kg = lane >> 5;    // MFMA k-group (8 consecutive k)
