@@ -907,10 +907,20 @@ __global__ __launch_bounds__(kThreads, 1) void int4_gemm_f32x3_kernel(
 #pragma unroll
         for (int i = 0; i < 4; i++) lds.corr[x_row + 32 * i] = corr[i];
     }
-    // The odd-parity waves hand their accumulators to the even ones.
-    if (kp == 1) {
+    // The two parities of a column half split the four m-tiles: parity 0
+    // finishes m-tiles 0 and 1, parity 1 m-tiles 2 and 3, each handing the
+    // other its partial sums of the rest through LDS (the sum of the two
+    // parities' f32 values, the same whichever wave adds them).
+    const int col = n0 + 64 * ch + 2 * c32;
+    float bj[2] = {0.0f, 0.0f};
+    if (ep.bias) {
+        bj[0] = ep.bias[col];
+        bj[1] = ep.bias[col + 1];
+    }
+    auto give = [&](auto KP) {
+        constexpr int p = decltype(KP)::value;
 #pragma unroll
-        for (int t = 0; t < 4; t++)
+        for (int t = p == 0 ? 2 : 0; t < (p == 0 ? 4 : 2); t++)
 #pragma unroll
             for (int j = 0; j < 2; j++)
 #pragma unroll
@@ -919,42 +929,40 @@ __global__ __launch_bounds__(kThreads, 1) void int4_gemm_f32x3_kernel(
                     lds.red[ch][t][j][q][lane] =
                         (f32x4){v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
                 }
-    }
-    __syncthreads();
-    if (kp == 1) return;
+    };
+    auto take_store = [&](auto KP) {
+        constexpr int p = decltype(KP)::value;
 #pragma unroll
-    for (int t = 0; t < 4; t++)
+        for (int t = p == 0 ? 0 : 2; t < (p == 0 ? 2 : 4); t++) {
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+            for (int j = 0; j < 2; j++)
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const f32x4 v = lds.red[ch][t][j][q][lane];
-                f32x16& d = acc[t][j];
-                d[4 * q] += v.x;
-                d[4 * q + 1] += v.y;
-                d[4 * q + 2] += v.z;
-                d[4 * q + 3] += v.w;
-            }
-    const int col = n0 + 64 * ch + 2 * c32;
-    float bj[2] = {0.0f, 0.0f};
-    if (ep.bias) {
-        bj[0] = ep.bias[col];
-        bj[1] = ep.bias[col + 1];
-    }
+                for (int q = 0; q < 4; q++) {
+                    const f32x4 v = lds.red[ch][t][j][q][lane];
+                    f32x16& d = acc[t][j];
+                    d[4 * q] += v.x;
+                    d[4 * q + 1] += v.y;
+                    d[4 * q + 2] += v.z;
+                    d[4 * q + 3] += v.w;
+                }
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int rl = t * 32 + 8 * (r >> 2) + 4 * kg + (r & 3);
-            const int row = m0 + rl;
-            if (row < m_end) {
-                const float cr = lds.corr[rl];
-                const size_t o = (size_t)row * N + col;
-                store_value(out, o, acc[t][0][r] + cr + bj[0], ep.bf16);
-                store_value(out, o + 1, acc[t][1][r] + cr + bj[1], ep.bf16);
+            for (int r = 0; r < 16; r++) {
+                const int rl = t * 32 + 8 * (r >> 2) + 4 * kg + (r & 3);
+                const int row = m0 + rl;
+                if (row < m_end) {
+                    const float cr = lds.corr[rl];
+                    const size_t o = (size_t)row * N + col;
+                    store_value(out, o, acc[t][0][r] + cr + bj[0], ep.bf16);
+                    store_value(out, o + 1, acc[t][1][r] + cr + bj[1], ep.bf16);
+                }
             }
         }
-    }
+    };
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, 1>;
+    if (kp == 0) give(P0{}); else give(P1{});
+    __syncthreads();
+    if (kp == 0) take_store(P0{}); else take_store(P1{});
 }
 
 // ---- f32 activations, fp32 VALU tiles -------------------------------------
