@@ -1512,9 +1512,11 @@ namespace {
 //
 // The counterpart of GroupedMatVec / GroupedMatMul (internal/kernels/
 // grouped.go:47-97, groupedtiled.go:77-134) over per-expert int4 weights when
-// there are few routed rows (decode MoE): every row t is a one-row decode
-// product against its expert's matrix, e(t) = #{r : off[r+1] <= t}, with the
-// same workgroup tile, batches and split-K hand-off as Int4MatVec.  Rows past
+// there are few routed rows (decode MoE): the rows t of an expert,
+// e(t) = #{r : off[r+1] <= t}, are decode products against its matrix two at
+// a time (an odd one out alone), with the same batches and split-K hand-off
+// as Int4MatVec.  A pair runs 16 columns a lane, which keeps the kernel at
+// two workgroups a CU; a lone row runs the matvec's 32.  Rows past
 // every segment (t >= off[E]) are written 0 by the matvec form and left alone
 // by the matmul form.  Workgroups are ordered (K slice, column tile, row) with
 // the row fastest and dealt to the XCDs in contiguous runs, so the rows of one
@@ -1525,6 +1527,14 @@ __device__ __forceinline__ int grouped_expert_of(const uint32_t* off, int E, uin
     int e = 0;
     for (int r = 0; r < E; r++) e += (off[r + 1] <= t) ? 1 : 0;
     return e;
+}
+
+// Offsets that never decrease (every count sum short of the u32 wrap): then
+// the rows of expert e are exactly [off[e], min(off[e+1], T)).
+__device__ __forceinline__ bool grouped_offsets_sorted(const uint32_t* off, int E) {
+    bool ok = true;
+    for (int r = 0; r < E; r++) ok = ok && off[r] <= off[r + 1];
+    return ok;
 }
 
 template <int TILE, int CPL, bool PIPE>
@@ -1549,13 +1559,27 @@ __global__ __launch_bounds__(kDecThreads) void int4_grouped_decode_kernel(
                 out[(size_t)t * N + tile * TILE + c] = 0.0f;
         return;
     }
+    // An expert's rows go two at a time (its weights read once for both): the
+    // first row of a pair takes both, the second has nothing to do, and an
+    // odd one out goes alone.  A pair's split-K sums take the two rows' slots
+    // and the first row's ticket.  Offsets that wrapped (no longer sorted)
+    // leave every row alone.
+    const bool sorted = grouped_offsets_sorted(off, E);
+    if (sorted && (((uint32_t)t - off[e]) & 1u) != 0) return;
+    const bool pair = sorted && (uint32_t)t + 1 < min(off[e + 1], (uint32_t)T);
     const size_t per = (size_t)K * N;
-    decode_tile<1, TILE, CPL, PIPE>(x + (size_t)t * K, codes + (size_t)e * (per >> 3),
-                                    scales + (size_t)e * (per >> 7),
-                                    zeros + (size_t)e * (per >> 7), out + (size_t)t * N,
-                                    partial ? partial + (size_t)t * slices * N : nullptr,
-                                    tickets + ((size_t)t * tiles + tile) * ticket_stride, K, N,
-                                    tile, slice, rows_per_slice, slices, Epilogue{});
+    const uint32_t* c = codes + (size_t)e * (per >> 3);
+    const uint16_t* s = scales + (size_t)e * (per >> 7);
+    const uint16_t* z = zeros + (size_t)e * (per >> 7);
+    float* p = partial ? partial + (size_t)t * slices * N : nullptr;
+    uint32_t* tk = tickets + ((size_t)t * tiles + tile) * ticket_stride;
+    if (pair)
+        decode_tile<2, TILE, CPL / 2, PIPE>(x + (size_t)t * K, c, s, z, out + (size_t)t * N, p,
+                                            tk, K, N, tile, slice, rows_per_slice, slices,
+                                            Epilogue{});
+    else
+        decode_tile<1, TILE, CPL, PIPE>(x + (size_t)t * K, c, s, z, out + (size_t)t * N, p, tk,
+                                        K, N, tile, slice, rows_per_slice, slices, Epilogue{});
 }
 
 // K slices of a grouped decode launch: enough workgroups for two per CU

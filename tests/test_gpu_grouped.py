@@ -177,6 +177,25 @@ def test_int4_grouped_matches_the_oracle(dev, bf16, form, E, K, N, counts, pad):
         assert np.all(got[covered:] == 7.0)
 
 
+def test_int4_grouped_matvec_wrapped_offsets(dev):
+    """Counts whose running sum wraps u32 (segmentOffsets keeps the wrap,
+    tensor/segment.go:40-50): off = [0, 2^32 - 1, 2, 4] is not sorted, and the
+    row -> expert rule e(t) = #{r : off[r+1] <= t} (internal/kernels/
+    grouped.go:66-77) puts rows 0-1, 2-3 and 4-5 on experts 0, 1 and 2.  The
+    decode path pairs rows of one expert only under sorted offsets; here every
+    row has to be computed on its own."""
+    E, K, N, counts, pad = 3, 512, 256, [0xFFFFFFFF, 3, 2], 2
+    x, p, s, z, off, T = int4_case(E, K, N, counts, pad, seed=11, bf16=False)
+    assert T == 6 and list(off) == [0, 0xFFFFFFFF, 2, 4]
+    got = run_int4_grouped(dev, "Int4GroupedMatVec", x, p, s, z, counts, E, T, K, N, False)
+    want = oracle.int4_grouped_matvec(x, p, s, z, off, E, T, K, N, threads=8,
+                                      out=np.full(T * N, 7.0, np.float32))
+    assert np.all(np.abs(want).sum(axis=1) > 0)   # every row belongs to an expert
+    assert rel_l2(got, want) <= 1e-5
+    for t in range(T):
+        assert rel_l2(got[t], want[t]) <= 1e-5, t
+
+
 def test_config4_moe_full_size(dev):
     """Config 4 at full size (1024 routed rows, 8 experts of [4096, 14336]):
     every row through two per-expert f64 checksums of the output columns, the
