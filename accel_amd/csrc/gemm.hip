@@ -77,6 +77,15 @@ __device__ __forceinline__ int b_off(int rq, int bc) {
     return rq * kBQuadWords + (bc ^ (((rq >> 1) & 1) << 5));
 }
 
+// A buffer resource over `base` (raw, no stride): loads through it take a
+// workgroup-uniform base in scalar registers and a 32-bit per-lane byte
+// offset, so they cost no vector address arithmetic.  Offsets stay below
+// the 2^31 - 1 byte extent given here (the callers' shape limits ensure it).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff,
+                                             0x00020000);
+}
+
 // 4 x 4 byte transpose: out[b] = byte b of r0, r1, r2, r3 (low to high).
 __device__ __forceinline__ u32x4 transpose4(uint32_t r0, uint32_t r1, uint32_t r2,
                                             uint32_t r3) {
@@ -165,23 +174,30 @@ __device__ __forceinline__ void gemm_tile_bf16(GemmLds<MTR>& lds, const uint16_t
     const size_t words_per_row = (size_t)(N >> 3);
     const int ktiles = K / BK;
 
+    // Global loads are buffer loads: a per-stage resource over the tile's
+    // first row, column and stage, and a 32-bit per-lane byte offset fixed
+    // for the whole tile (below 2^31 for K < 2^22 and N < 2^26,
+    // int4_gemm_bf16_supported).
+    //
     // Activation staging: 32 rows (256 chunks of 16 bytes) per m-tile a
     // stage, one chunk per lane and m-tile.
-    const uint16_t* a_src[MT];
+    const char* a_tile = reinterpret_cast<const char*>(a + (size_t)m0 * K);
+    uint32_t a_src[MT];
     int a_dst[MT];
 #pragma unroll
     for (int i = 0; i < MT; i++) {
         const int q = tid + kThreads * i;
         const int r = q >> 3, c = q & 7;
         const int row = min(m0 + r, m_end - 1);
-        a_src[i] = a + (size_t)row * K + c * 8;
+        a_src[i] = (uint32_t)(((size_t)(row - m0) * K + c * 8) * 2);
         a_dst[i] = a_off(r, c);
     }
     // Code staging: row quad tid / 16 and 4-byte column chunk tid % 16 (eight
     // columns) of each of the quad's four rows.
     const int b_rq = tid >> 4;
     const int b_cc = tid & 15;
-    const uint32_t* b_src = codes + (size_t)(4 * b_rq) * words_per_row + (n0 >> 3) + b_cc;
+    const char* b_tile = reinterpret_cast<const char*>(codes + (n0 >> 3));
+    const uint32_t b_src = (uint32_t)(((size_t)(4 * b_rq) * words_per_row + b_cc) * 4);
     const int b_dst = b_off(b_rq, 4 * b_cc);
     // Fold staging: wave w folds the stage's rows 16w .. 16w + 15, four lanes
     // a row.  A load whose lanes name many rows costs the address unit about
@@ -191,23 +207,30 @@ __device__ __forceinline__ void gemm_tile_bf16(GemmLds<MTR>& lds, const uint16_t
     const int f_row = 16 * wave + (lane & 15);
     const int f_dst = lane < 16 ? f_row : BK + lane;
     const size_t f_g = (size_t)(n0 >> 7);
-    const uint16_t* s_src = scales + (size_t)f_row * groups_per_row + f_g;
-    const uint16_t* z_src = zeros + (size_t)f_row * groups_per_row + f_g;
+    const char* s_tile = reinterpret_cast<const char*>(scales + f_g);
+    const char* z_tile = reinterpret_cast<const char*>(zeros + f_g);
+    const uint32_t f_src = (uint32_t)((size_t)f_row * groups_per_row * 2);
 
     // Stage indices past the end are clamped to the last stage: the loads
     // repeat valid data and land in buffers no later stage reads.
+    const int row_bytes = (int)(words_per_row * 4);   // one row of codes
+    auto a_rsrc = [&](int k0) { return tile_rsrc(a_tile + (size_t)k0 * 2); };
+    auto b_rsrc = [&](int k0) { return tile_rsrc(b_tile + (size_t)k0 * row_bytes); };
+    auto s_rsrc = [&](int k0) { return tile_rsrc(s_tile + (size_t)k0 * groups_per_row * 2); };
+    auto z_rsrc = [&](int k0) { return tile_rsrc(z_tile + (size_t)k0 * groups_per_row * 2); };
     auto load_a = [&](ARegs<MT>& g, int kt) {
-        const int k0 = min(kt, ktiles - 1) * BK;
+        const auto r = a_rsrc(min(kt, ktiles - 1) * BK);
 #pragma unroll
-        for (int i = 0; i < MT; i++) g.a[i] = *reinterpret_cast<const u32x4*>(a_src[i] + k0);
+        for (int i = 0; i < MT; i++) g.a[i] = __builtin_amdgcn_raw_buffer_load_b128(r, a_src[i], 0, 0);
     };
     auto load_c = [&](CRegs& g, int kt) {
         const int k0 = min(kt, ktiles - 1) * BK;
-        const uint32_t* bp = b_src + (size_t)k0 * words_per_row;
+        const auto r = b_rsrc(k0);
 #pragma unroll
-        for (int i = 0; i < 4; i++) g.b[i] = bp[(size_t)i * words_per_row];
-        g.s = s_src[(size_t)k0 * groups_per_row];
-        g.z = z_src[(size_t)k0 * groups_per_row];
+        for (int i = 0; i < 4; i++)
+            g.b[i] = __builtin_amdgcn_raw_buffer_load_b32(r, b_src, i * row_bytes, 0);
+        g.s = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc(k0), f_src, 0, 0);
+        g.z = __builtin_amdgcn_raw_buffer_load_b16(z_rsrc(k0), f_src, 0, 0);
     };
     auto store_lds = [&](const ARegs<MT>& ga, const CRegs& g, int buf) {
         GemmStage& S = lds.st[buf];
@@ -354,7 +377,8 @@ __device__ __forceinline__ void gemm_tile_bf16(GemmLds<MTR>& lds, const uint16_t
                     if ((it & 1) == 0)
                         *reinterpret_cast<u32x4*>(WS.a + a_dst[p]) = gs.a[p];
                     else
-                        gs.a[p] = *reinterpret_cast<const u32x4*>(a_src[p] + k0n);
+                        gs.a[p] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc(k0n), a_src[p],
+                                                                        0, 0);
                     return;
                 }
                 it -= 2 * MT;
@@ -364,7 +388,8 @@ __device__ __forceinline__ void gemm_tile_bf16(GemmLds<MTR>& lds, const uint16_t
                     return;
                 }
                 if (it <= 4) {
-                    cs.b[it - 1] = b_src[(size_t)(k0c + it - 1) * words_per_row];
+                    cs.b[it - 1] = __builtin_amdgcn_raw_buffer_load_b32(
+                        b_rsrc(k0c), b_src, (it - 1) * row_bytes, 0);
                     return;
                 }
                 if (it == 5) {
@@ -376,8 +401,14 @@ __device__ __forceinline__ void gemm_tile_bf16(GemmLds<MTR>& lds, const uint16_t
                     WS.fold[f_dst] = f;
                     return;
                 }
-                if (it == 6) { cs.s = s_src[(size_t)k0c * groups_per_row]; return; }
-                if (it == 7) { cs.z = z_src[(size_t)k0c * groups_per_row]; return; }
+                if (it == 6) {
+                    cs.s = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc(k0c), f_src, 0, 0);
+                    return;
+                }
+                if (it == 7) {
+                    cs.z = __builtin_amdgcn_raw_buffer_load_b16(z_rsrc(k0c), f_src, 0, 0);
+                    return;
+                }
                 it -= 8;
             }
             const int q = tail_is_d(it);
@@ -1042,8 +1073,9 @@ __global__ __launch_bounds__(256) void int4_gemm_f32_kernel(
 }  // namespace
 
 bool int4_gemm_bf16_supported(int M, int K, int N) {
+    // per-lane load offsets within a tile stay below 2^31 (gemm_tile_bf16)
     return M >= 1 && K >= BK && K % BK == 0 && N >= BN && N % BN == 0 &&
-           K < (1 << 30) && N < (1 << 30);
+           K < (1 << 22) && N < (1 << 26);
 }
 
 template <int MT>

@@ -697,7 +697,8 @@ int run_grouped_int4(const char* op, int dev, void* stream, const accel_tensor_t
                         (uint64_t)experts * (uint64_t)K * (uint64_t)N < (1ull << 40);
     if (!f32 && !(int4_gemm_bf16_supported(1, (int)K, (int)N) &&
                   (reinterpret_cast<uintptr_t>(x->data) & 15) == 0))
-        return refuse(op, "bf16 grouped products need K % 64 == 0 and N % 128 == 0");
+        return refuse(op, "bf16 grouped products need K % 64 == 0, N % 128 == 0, K < 2^22 and "
+                          "N < 2^26");
     const size_t area_bytes = decode ? int4_grouped_decode_area(d, (int)T, (int)K, (int)N) : 0;
     void* area = nullptr;
     uint32_t* off = offsets_in_workspace(d, st, static_cast<const uint32_t*>(counts->data),
