@@ -359,11 +359,27 @@ hipError_t launch_decode(Device* d, hipStream_t st, const float* a, Int4Planes w
     return hipGetLastError();
 }
 
+// Column tile of a one-row product: 512 columns for wide matrices (a row's
+// scale and zero lines then serve 256 code bytes instead of 128; measured
+// 12.8 -> 12.1 us at K = 4096, N = 14336 and 20.9 -> 18.7 at N = 28672),
+// 256 where N allows (at N = 4096 the 512 tile's 32 slices make the hand-off
+// longer than the lines it saves: 6.64 against 6.26 us), else 128.  Every
+// one-row launch of a matrix -- alone, in a set or without allocation --
+// takes the same width, so their results agree bit for bit.
+int matvec_tile(int N) {
+    if (N >= 8192 && N % 512 == 0) return 512;
+    return N % 256 == 0 ? 256 : 128;
+}
+
 // Columns per lane by row count: the accumulators (M * CPL) stay near 64.
 template <int M>
 hipError_t launch_decode_m(Device* d, hipStream_t st, const float* a, Int4Planes w,
                            void* out, int K, int N, int* status, Epilogue ep) {
     constexpr int CPL = M <= 2 ? 32 : (M <= 4 ? 16 : 8);
+    if constexpr (M == 1) {
+        if (matvec_tile(N) == 512)
+            return launch_decode<M, 512, CPL>(d, st, a, w, out, K, N, status, ep);
+    }
     if (N % 256 == 0) return launch_decode<M, 256, CPL>(d, st, a, w, out, K, N, status, ep);
     return launch_decode<M, 128, CPL>(d, st, a, w, out, K, N, status, ep);
 }
@@ -1457,22 +1473,25 @@ hipError_t launch_int4_matvec_set(Device* d, hipStream_t st, const float* a, con
                                   float* const* out, const int* N, int count, int K,
                                   int* status) {
     *status = ACCEL_OK;
-    // Each matrix keeps the tile width its own launch would take (256 columns
-    // where N allows, else 128), so its sums are added in the same order and
-    // its result is its own Int4MatVec's: one launch per width present.
-    Int4Planes wg[2][kMaxSet];
-    float* og[2][kMaxSet];
-    int ng[2][kMaxSet], cnt[2] = {0, 0};
+    // Each matrix keeps the tile width its own launch would take
+    // (matvec_tile), so its sums are added in the same order and its result
+    // is its own Int4MatVec's: one launch per width present.
+    Int4Planes wg[3][kMaxSet];
+    float* og[3][kMaxSet];
+    int ng[3][kMaxSet], cnt[3] = {0, 0, 0};
     for (int i = 0; i < count; i++) {
-        const int g = N[i] % 256 == 0 ? 0 : 1;
+        const int tw = matvec_tile(N[i]);
+        const int g = tw == 512 ? 0 : (tw == 256 ? 1 : 2);
         wg[g][cnt[g]] = w[i];
         og[g][cnt[g]] = out[i];
         ng[g][cnt[g]++] = N[i];
     }
     hipError_t e = hipSuccess;
-    if (cnt[0]) e = launch_matvec_set<256>(d, st, a, wg[0], og[0], ng[0], cnt[0], K, status);
+    if (cnt[0]) e = launch_matvec_set<512>(d, st, a, wg[0], og[0], ng[0], cnt[0], K, status);
     if (e != hipSuccess || *status != ACCEL_OK) return e;
-    if (cnt[1]) e = launch_matvec_set<128>(d, st, a, wg[1], og[1], ng[1], cnt[1], K, status);
+    if (cnt[1]) e = launch_matvec_set<256>(d, st, a, wg[1], og[1], ng[1], cnt[1], K, status);
+    if (e != hipSuccess || *status != ACCEL_OK) return e;
+    if (cnt[2]) e = launch_matvec_set<128>(d, st, a, wg[2], og[2], ng[2], cnt[2], K, status);
     return e;
 }
 
@@ -1835,7 +1854,10 @@ hipError_t launch_int4_matvec_noalloc(Device* d, hipStream_t st, const float* a,
     }
     if (!int4_decode_f32_supported(1, K, N, w.codes))
         return launch_int4_generic_f32(st, a, w, out, 1, K, N, Epilogue{});   // no scratch
-    if (N % 256 == 0)
+    const int tw = matvec_tile(N);
+    if (tw == 512)
+        return launch_decode<1, 512, 32>(d, st, a, w, out, K, N, status, Epilogue{}, d->scratch);
+    if (tw == 256)
         return launch_decode<1, 256, 32>(d, st, a, w, out, K, N, status, Epilogue{}, d->scratch);
     return launch_decode<1, 128, 32>(d, st, a, w, out, K, N, status, Epilogue{}, d->scratch);
 }

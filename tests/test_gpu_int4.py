@@ -106,6 +106,9 @@ SHAPES_F32 = [
     # K long enough that a workgroup loops over several batches of rows (256-
     # and 128-column tiles), and the layer chain's down projection
     (1, 16640, 256), (2, 33000, 128), (1, 14336, 4096),
+    # 512-column tiles of wide one-row products: one batch a slice, and
+    # several (pipelined) with a short last slice
+    (1, 2048, 8192), (1, 9000, 8704),
     # the matrix-core decode kernel: one- and two-group tiles, one step, a few
     # steps, several slices, the layer chain's down projection
     (4, 4096, 4096), (9, 1024, 384), (11, 2048, 768), (15, 14336, 4096), (16, 96, 256),

@@ -25,6 +25,8 @@ def _weights(dev, K, N, rng):
     (20000, [256, 512]),              # more batches than slices: the pipelined kernel
     (300, [40, 256]),                 # 40 columns: one launch per matrix
     (512, [256]),
+    (2048, [8192, 4096, 384]),        # 512-, 256- and 128-column tiles in one set
+    (9000, [8704, 256]),              # the 512-column tile's pipelined kernel
 ])
 def test_set_equals_separate_matvecs(dev, K, Ns):
     rng = np.random.Generator(np.random.PCG64(K + sum(Ns)))
