@@ -1670,8 +1670,21 @@ bool int4_grouped_decode_supported(int T, int K, int N, const void* codes) {
            (reinterpret_cast<uintptr_t>(codes) & 15) == 0 && K < (1 << 30) && N < (1 << 30);
 }
 
+// Column tile of the ragged GEMV: 512 columns for wide matrices when the
+// rows are few (rows x tiles at most half the CUs, so the launch is mostly
+// K slices and the halved scale/zero lines pay), else the matvec's 256 or 128.
+// Measured at K = 4096, N = 14336 (decode MoE, top-2 of 8 experts): 1 token
+// 27.1 -> 24.1-24.8 us, 2 tokens 45.1 -> 43.4; at 4 tokens (8 rows) 512
+// columns lose, 78.6 -> 84.5, and at 8 tokens 120 -> 121-126.
+static int grouped_decode_tile(const Device* d, int T, int N) {
+    if (N >= 8192 && N % 512 == 0 && (long long)T * (N / 512) <= d->cu_count / 2) return 512;
+    return N % 256 == 0 ? 256 : 128;
+}
+
 size_t int4_grouped_decode_area(const Device* d, int T, int K, int N) {
-    if (N % 256 == 0) return GroupedDecodeShape<256>(d, T, K, N).area_bytes(T, N);
+    const int tw = grouped_decode_tile(d, T, N);
+    if (tw == 512) return GroupedDecodeShape<512>(d, T, K, N).area_bytes(T, N);
+    if (tw == 256) return GroupedDecodeShape<256>(d, T, K, N).area_bytes(T, N);
     return GroupedDecodeShape<128>(d, T, K, N).area_bytes(T, N);
 }
 
@@ -1680,7 +1693,11 @@ hipError_t launch_int4_grouped_decode(Device* d, hipStream_t st, const float* x,
                                       int N, bool write_padding, int* status,
                                       uint32_t* tickets, float* area) {
     *status = ACCEL_OK;
-    if (N % 256 == 0)
+    const int tw = grouped_decode_tile(d, T, N);
+    if (tw == 512)
+        return launch_grouped_decode_tile<512>(d, st, x, w, off, out, E, T, K, N, write_padding,
+                                               status, tickets, area);
+    if (tw == 256)
         return launch_grouped_decode_tile<256>(d, st, x, w, off, out, E, T, K, N, write_padding,
                                                status, tickets, area);
     return launch_grouped_decode_tile<128>(d, st, x, w, off, out, E, T, K, N, write_padding,

@@ -151,13 +151,18 @@ def run_int4_grouped(dev, form, x, p, s, z, counts, E, T, K, N, bf16):
 @pytest.mark.parametrize("E,K,N,counts,pad", [(3, 128, 128, [5, 0, 9], 2),
                                               (8, 256, 384, [1, 130, 0, 7, 64, 0, 3, 260], 3),
                                               (2, 64, 256, [0, 0], 4),
-                                              # decode MoE (f32: a decode product per row):
+                                              # decode MoE (f32: decode products, rows of
+                                              # an expert two at a time):
                                               # split-K over 4096 rows, 128-column tiles,
                                               # the 64-row limit, one row
                                               (8, 4096, 1024, [2, 0, 3, 1, 0, 4, 2, 4], 1),
                                               (4, 512, 640, [3, 1, 0, 2], 2),
                                               (4, 1024, 256, [20, 10, 30, 4], 0),
-                                              (5, 2048, 512, [0, 0, 1, 0, 0], 0)])
+                                              (5, 2048, 512, [0, 0, 1, 0, 0], 0),
+                                              # few rows of a wide matrix: 512-column
+                                              # tiles, a pair and single rows
+                                              (3, 512, 8192, [1, 0, 1], 1),
+                                              (2, 1024, 8192, [2, 1], 0)])
 def test_int4_grouped_matches_the_oracle(dev, bf16, form, E, K, N, counts, pad):
     x, p, s, z, off, T = int4_case(E, K, N, counts, pad, seed=E + K, bf16=bf16)
     got = run_int4_grouped(dev, form, x, p, s, z, counts, E, T, K, N, bf16)
