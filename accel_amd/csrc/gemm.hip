@@ -41,6 +41,7 @@
 // LDS-tiled fp32 VALU product, exact up to f32 rounding order.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <type_traits>
 
 #include "internal.hpp"
@@ -154,14 +155,19 @@ struct SubstepRegs {
 // kt+1 visible before that substep reads the next stage's operands.  A
 // wave pipelines its substeps: while the MFMAs of one run, it dequantises
 // the next one's codes, read from LDS at the start of the current one.
-template <int MT, bool BIAS, int MTR>
+//
+// A K slice (split K, for products with too few tiles to fill the chip)
+// runs stages [kt0, kt0 + ktiles) and, with PART, stores its f32 sums to
+// `part` ([M, N], row stride N) instead of the bf16 result.
+template <int MT, bool BIAS, int MTR, bool PART = false>
 __device__ __forceinline__ void gemm_tile_bf16(GemmLds<MTR>& lds, const uint16_t* __restrict__ a,
                                                const uint32_t* __restrict__ codes,
                                                const uint16_t* __restrict__ scales,
                                                const uint16_t* __restrict__ zeros,
                                                uint16_t* __restrict__ out, int m0, int m_end,
                                                int n0, int K, int N,
-                                               const float* __restrict__ bias) {
+                                               const float* __restrict__ bias, int kt0 = 0,
+                                               int kt_count = -1, float* part = nullptr) {
     static_assert(MT <= MTR, "hand-off slots");
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
@@ -172,7 +178,8 @@ __device__ __forceinline__ void gemm_tile_bf16(GemmLds<MTR>& lds, const uint16_t
     const int kg = lane >> 5;    // MFMA k-group (8 consecutive k)
     const size_t groups_per_row = (size_t)(N >> 7);
     const size_t words_per_row = (size_t)(N >> 3);
-    const int ktiles = K / BK;
+    const int ktiles = kt_count < 0 ? K / BK : kt_count;   // stages of this slice
+    auto kofs = [&](int kt) { return (kt0 + min(kt, ktiles - 1)) * BK; };
 
     // Global loads are buffer loads: a per-stage resource over the tile's
     // first row, column and stage, and a 32-bit per-lane byte offset fixed
@@ -219,12 +226,12 @@ __device__ __forceinline__ void gemm_tile_bf16(GemmLds<MTR>& lds, const uint16_t
     auto s_rsrc = [&](int k0) { return tile_rsrc(s_tile + (size_t)k0 * groups_per_row * 2); };
     auto z_rsrc = [&](int k0) { return tile_rsrc(z_tile + (size_t)k0 * groups_per_row * 2); };
     auto load_a = [&](ARegs<MT>& g, int kt) {
-        const auto r = a_rsrc(min(kt, ktiles - 1) * BK);
+        const auto r = a_rsrc(kofs(kt));
 #pragma unroll
         for (int i = 0; i < MT; i++) g.a[i] = __builtin_amdgcn_raw_buffer_load_b128(r, a_src[i], 0, 0);
     };
     auto load_c = [&](CRegs& g, int kt) {
-        const int k0 = min(kt, ktiles - 1) * BK;
+        const int k0 = kofs(kt);
         const auto r = b_rsrc(k0);
 #pragma unroll
         for (int i = 0; i < 4; i++)
@@ -345,8 +352,8 @@ __device__ __forceinline__ void gemm_tile_bf16(GemmLds<MTR>& lds, const uint16_t
         CRegs& cs = cg[cset];
         const GemmStage& RS = lds.st[rbuf];
         GemmStage& WS = lds.st[buf ^ 1];
-        const int k0n = min(kt + 3, ktiles - 1) * BK;        // activations loaded now
-        const int k0c = min(kt + 1 + PD, ktiles - 1) * BK;   // codes loaded now
+        const int k0n = kofs(kt + 3);        // activations loaded now
+        const int k0c = kofs(kt + 1 + PD);   // codes loaded now
         const f32x4* fp = reinterpret_cast<const f32x4*>(&RS.fold[rks * 16 + 8 * kg]);
 
         auto dq = [&](int q) {
@@ -515,12 +522,19 @@ __device__ __forceinline__ void gemm_tile_bf16(GemmLds<MTR>& lds, const uint16_t
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int dr = t * 32 + 8 * (r >> 2) + (r & 3);   // row - m0 - 4 kg
-                bf16x2 v;
-                v[0] = (__bf16)(BIAS ? acc[t][0][r] + bj[0] : acc[t][0][r]);
-                v[1] = (__bf16)(BIAS ? acc[t][1][r] + bj[1] : acc[t][1][r]);
-                uint16_t* rowp = out + (size_t)(m0 + dr) * N;
-                if (whole || m0 + dr + 4 * kg < m_end)
-                    *reinterpret_cast<bf16x2*>(rowp + lane_off) = v;
+                const bool keep = whole || m0 + dr + 4 * kg < m_end;
+                if constexpr (PART) {
+                    float* rowp = part + (size_t)(m0 + dr) * N;
+                    if (keep)
+                        *reinterpret_cast<f32x2*>(rowp + lane_off) =
+                            (f32x2){acc[t][0][r], acc[t][1][r]};
+                } else {
+                    bf16x2 v;
+                    v[0] = (__bf16)(BIAS ? acc[t][0][r] + bj[0] : acc[t][0][r]);
+                    v[1] = (__bf16)(BIAS ? acc[t][1][r] + bj[1] : acc[t][1][r]);
+                    uint16_t* rowp = out + (size_t)(m0 + dr) * N;
+                    if (keep) *reinterpret_cast<bf16x2*>(rowp + lane_off) = v;
+                }
             }
             __builtin_amdgcn_sched_barrier(0);   // one m-tile at a time
         }
@@ -547,6 +561,74 @@ __global__ __launch_bounds__(kThreads, 1) void int4_gemm_bf16_kernel(
     const int m0 = m_first + (b / tiles_n) * BM;
     const int n0 = (b % tiles_n) * BN;
     gemm_tile_bf16<MT, BIAS>(lds, a, codes, scales, zeros, out, m0, M, n0, K, N, bias);
+}
+
+// Split K: workgroup (band, column tile, slice) runs slice `slice` of the
+// stages, kt_per stages each (the last takes the rest), into the f32 sums
+// part[slice] ([M, N]); int4_gemm_reduce_kernel adds the slices in slice
+// order and rounds once to bf16.
+template <int MT>
+__global__ __launch_bounds__(kThreads, 1) void int4_gemm_bf16_splitk_kernel(
+    const uint16_t* __restrict__ a, const uint32_t* __restrict__ codes,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
+    float* __restrict__ part, int m_first, int M, int K, int N, int slices, int kt_per) {
+    __shared__ GemmLds<MT> lds;
+    const int tiles_n = N / BN;
+    const int grid = gridDim.x;
+    int b = blockIdx.x;
+    if ((grid & 7) == 0) b = (b & 7) * (grid >> 3) + (b >> 3);
+    // slices of one tile are consecutive: they share its codes' lines
+    const int slice = b % slices;
+    const int tile = b / slices;
+    const int m0 = m_first + (tile / tiles_n) * BM;
+    const int n0 = (tile % tiles_n) * BN;
+    const int kt0 = slice * kt_per;
+    const int count = slice == slices - 1 ? K / BK - kt0 : kt_per;
+    gemm_tile_bf16<MT, false, MT, true>(lds, a, codes, scales, zeros, nullptr, m0, M, n0, K, N,
+                                        nullptr, kt0, count,
+                                        part + (size_t)slice * M * N);
+}
+
+// out[m, n] = sum over s in order of part[s][m, n] (+ bias[n]), rounded once
+// to bf16 or stored as f32; four columns a lane.
+__global__ __launch_bounds__(256) void int4_gemm_reduce_kernel(const float* __restrict__ part,
+                                                               void* __restrict__ out,
+                                                               long long quads, int N, int slices,
+                                                               long long stride,
+                                                               const float* __restrict__ bias,
+                                                               bool bf16) {
+    const long long q = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (q >= quads) return;
+    const size_t i = (size_t)q * 4;
+    // eight slices' loads in flight at a time, added in slice order
+    f32x4 sum = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < slices; s0 += 8) {
+        f32x4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            v[u] = s0 + u < slices
+                       ? __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(
+                             part + (size_t)(s0 + u) * stride + i))
+                       : (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (s0 + u < slices) sum = s0 + u == 0 ? v[u] : sum + v[u];
+    }
+    if (bias) {
+        const int c = (int)(i % (size_t)N);
+        sum += (f32x4){bias[c], bias[c + 1], bias[c + 2], bias[c + 3]};
+    }
+    if (!bf16) {
+        *reinterpret_cast<f32x4*>(static_cast<float*>(out) + i) = sum;
+        return;
+    }
+    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+    bf16x4 v;
+    v[0] = (__bf16)sum.x;
+    v[1] = (__bf16)sum.y;
+    v[2] = (__bf16)sum.z;
+    v[3] = (__bf16)sum.w;
+    *reinterpret_cast<bf16x4*>(static_cast<uint16_t*>(out) + i) = v;
 }
 
 // Ragged grouped form: the work is the list of (expert, row block, column
@@ -680,18 +762,27 @@ __device__ __forceinline__ void xsplit3(float v0, float v1, uint32_t& hi, uint32
     lo = __builtin_bit_cast(uint32_t, l);
 }
 
+// With `part`, split K: workgroup (tile, slice) runs slice `slice` of the
+// stages (kt_per each, the last the rest) and stores its f32 sums, row
+// corrections included, to part[slice] ([M, N]); int4_gemm_reduce_kernel
+// adds the slices in order and applies the epilogue.
 __global__ __launch_bounds__(kThreads, 1) void int4_gemm_f32x3_kernel(
     const float* __restrict__ a, const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
-    void* __restrict__ out, int M, int K, int N, Epilogue ep) {
+    void* __restrict__ out, int M, int K, int N, Epilogue ep, float* part, int slices,
+    int kt_per) {
     __shared__ XLds lds;
     const int tiles_n = N / BN;
     const int grid = gridDim.x;
     int bid = blockIdx.x;
     if ((grid & 7) == 0) bid = (bid & 7) * (grid >> 3) + (bid >> 3);
+    const int slice = part ? bid % slices : 0;
+    if (part) bid /= slices;
     const int m0 = (bid / tiles_n) * XBM;
     const int n0 = (bid % tiles_n) * BN;
     const int m_end = M;
+    const int kt0 = slice * kt_per;
+    float* my_part = part ? part + (size_t)slice * M * N : nullptr;
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
@@ -702,7 +793,7 @@ __global__ __launch_bounds__(kThreads, 1) void int4_gemm_f32x3_kernel(
     const int kg = lane >> 5;
     const size_t groups_per_row = (size_t)(N >> 7);
     const size_t words_per_row = (size_t)(N >> 3);
-    const int ktiles = K / BK;
+    const int ktiles = !part ? K / BK : (slice == slices - 1 ? K / BK - kt0 : kt_per);
 
     // Activation staging: m-tile i, row (tid >> 3) + 32 i, k 8 (tid & 7) ..
     // + 7 of a stage: two 16-byte loads each.
@@ -732,7 +823,7 @@ __global__ __launch_bounds__(kThreads, 1) void int4_gemm_f32x3_kernel(
     struct CRegs2 { uint32_t b[4]; };
     struct SZ { uint16_t s, z; };
     auto load_x = [&](XRegs& g, int kt) {
-        const int k0 = min(kt, ktiles - 1) * BK;
+        const int k0 = (kt0 + min(kt, ktiles - 1)) * BK;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             g.x[i][0] = *reinterpret_cast<const f32x4*>(x_src[i] + k0);
@@ -740,13 +831,13 @@ __global__ __launch_bounds__(kThreads, 1) void int4_gemm_f32x3_kernel(
         }
     };
     auto load_b = [&](CRegs2& g, int kt) {
-        const int k0 = min(kt, ktiles - 1) * BK;
+        const int k0 = (kt0 + min(kt, ktiles - 1)) * BK;
         const uint32_t* bp = b_src + (size_t)k0 * words_per_row;
 #pragma unroll
         for (int i = 0; i < 4; i++) g.b[i] = bp[(size_t)i * words_per_row];
     };
     auto load_sz = [&](SZ& g, int kt) {
-        const int k0 = min(kt, ktiles - 1) * BK;
+        const int k0 = (kt0 + min(kt, ktiles - 1)) * BK;
         g.s = s_src[(size_t)k0 * groups_per_row];
         g.z = z_src[(size_t)k0 * groups_per_row];
     };
@@ -983,8 +1074,13 @@ __global__ __launch_bounds__(kThreads, 1) void int4_gemm_f32x3_kernel(
                 if (row < m_end) {
                     const float cr = lds.corr[rl];
                     const size_t o = (size_t)row * N + col;
-                    store_value(out, o, acc[t][0][r] + cr + bj[0], ep.bf16);
-                    store_value(out, o + 1, acc[t][1][r] + cr + bj[1], ep.bf16);
+                    if (my_part) {
+                        *reinterpret_cast<f32x2*>(my_part + o) =
+                            (f32x2){acc[t][0][r] + cr, acc[t][1][r] + cr};
+                    } else {
+                        store_value(out, o, acc[t][0][r] + cr + bj[0], ep.bf16);
+                        store_value(out, o + 1, acc[t][1][r] + cr + bj[1], ep.bf16);
+                    }
                 }
             }
         }
@@ -1090,8 +1186,58 @@ void launch_band(hipStream_t st, const uint16_t* a, Int4Planes w, uint16_t* out,
                            w.codes, w.scales, w.zeros, out, m_first, M, K, N, bias);
 }
 
-hipError_t launch_int4_gemm_bf16(Device*, hipStream_t st, const uint16_t* a, Int4Planes w,
-                                 uint16_t* out, int M, int K, int N, const float* bias) {
+template <int MT>
+void launch_band_splitk(hipStream_t st, const uint16_t* a, Int4Planes w, float* part,
+                        int m_first, int bands, int M, int K, int N, int slices, int kt_per) {
+    const dim3 grid(bands * (N / BN) * slices);
+    hipLaunchKernelGGL((int4_gemm_bf16_splitk_kernel<MT>), grid, dim3(kThreads), 0, st, a,
+                       w.codes, w.scales, w.zeros, part, m_first, M, K, N, slices, kt_per);
+}
+
+// K slices for a product whose tiles leave CUs idle: as many as fill the
+// chip once, each of at least four stages.
+static int gemm_slices(const Device* d, int M, int K, int N) {
+    const int tiles = (M + BM - 1) / BM * (N / BN);
+    const int ktiles = K / BK;
+    if (tiles * 2 > d->cu_count) return 1;
+    return std::max(1, std::min(d->cu_count / tiles, ktiles / 4));
+}
+
+hipError_t launch_int4_gemm_bf16(Device* d, hipStream_t st, const uint16_t* a, Int4Planes w,
+                                 uint16_t* out, int M, int K, int N, const float* bias,
+                                 int* status) {
+    *status = ACCEL_OK;
+    const int slices = gemm_slices(d, M, K, N);
+    if (slices > 1) {
+        // Split K: each slice's f32 sums to the workspace, then one pass adds
+        // them in slice order and rounds.
+        const size_t stride = (size_t)M * N;
+        void* ws = workspace(d, st, (size_t)slices * stride * sizeof(float), status);
+        if (!ws) return hipSuccess;
+        float* part = reinterpret_cast<float*>(static_cast<char*>(ws) + kWorkspaceCounterBytes);
+        const int kt_per = (K / BK) / slices;
+        const int full = M / BM;
+        if (full > 0) launch_band_splitk<8>(st, a, w, part, 0, full, M, K, N, slices, kt_per);
+        const int rest = M - full * BM;
+        if (rest > 0) {
+            const int mf = full * BM;
+            switch ((rest + 31) / 32) {
+                case 1: launch_band_splitk<1>(st, a, w, part, mf, 1, M, K, N, slices, kt_per); break;
+                case 2: launch_band_splitk<2>(st, a, w, part, mf, 1, M, K, N, slices, kt_per); break;
+                case 3: launch_band_splitk<3>(st, a, w, part, mf, 1, M, K, N, slices, kt_per); break;
+                case 4: launch_band_splitk<4>(st, a, w, part, mf, 1, M, K, N, slices, kt_per); break;
+                case 5: launch_band_splitk<5>(st, a, w, part, mf, 1, M, K, N, slices, kt_per); break;
+                case 6: launch_band_splitk<6>(st, a, w, part, mf, 1, M, K, N, slices, kt_per); break;
+                case 7: launch_band_splitk<7>(st, a, w, part, mf, 1, M, K, N, slices, kt_per); break;
+                default: launch_band_splitk<8>(st, a, w, part, mf, 1, M, K, N, slices, kt_per); break;
+            }
+        }
+        const long long quads = (long long)stride / 4;
+        hipLaunchKernelGGL(int4_gemm_reduce_kernel, dim3((unsigned)((quads + 255) / 256)),
+                           dim3(256), 0, st, part, (void*)out, quads, N, slices,
+                           (long long)stride, bias, true);
+        return hipGetLastError();
+    }
     // full 256-row bands in one launch, a partial last band in another with
     // only its own m-tiles
     const int full = M / BM;
@@ -1131,11 +1277,29 @@ bool int4_gemm_f32x3_supported(int K, int N) {
     return K >= BK && K % BK == 0 && N >= BN && N % BN == 0 && K < (1 << 30) && N < (1 << 30);
 }
 
-hipError_t launch_int4_gemm_f32x3(Device*, hipStream_t st, const float* a, Int4Planes w,
-                                  void* out, int M, int K, int N, Epilogue ep) {
+hipError_t launch_int4_gemm_f32x3(Device* d, hipStream_t st, const float* a, Int4Planes w,
+                                  void* out, int M, int K, int N, Epilogue ep, int* status) {
+    *status = ACCEL_OK;
     const int tiles = (M + XBM - 1) / XBM * (N / BN);
-    hipLaunchKernelGGL(int4_gemm_f32x3_kernel, dim3(tiles), dim3(kThreads), 0, st, a, w.codes,
-                       w.scales, w.zeros, out, M, K, N, ep);
+    const int ktiles = K / BK;
+    // K slices when the tiles leave CUs idle, as for the bf16 tiles
+    const int slices =
+        tiles * 2 > d->cu_count ? 1 : std::max(1, std::min(d->cu_count / tiles, ktiles / 4));
+    if (slices == 1) {
+        hipLaunchKernelGGL(int4_gemm_f32x3_kernel, dim3(tiles), dim3(kThreads), 0, st, a,
+                           w.codes, w.scales, w.zeros, out, M, K, N, ep, (float*)nullptr, 1, 0);
+        return hipGetLastError();
+    }
+    const size_t stride = (size_t)M * N;
+    void* ws = workspace(d, st, (size_t)slices * stride * sizeof(float), status);
+    if (!ws) return hipSuccess;
+    float* part = reinterpret_cast<float*>(static_cast<char*>(ws) + kWorkspaceCounterBytes);
+    hipLaunchKernelGGL(int4_gemm_f32x3_kernel, dim3(tiles * slices), dim3(kThreads), 0, st, a,
+                       w.codes, w.scales, w.zeros, out, M, K, N, ep, part, slices,
+                       ktiles / slices);
+    const long long quads = (long long)stride / 4;
+    hipLaunchKernelGGL(int4_gemm_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256),
+                       0, st, part, out, quads, N, slices, (long long)stride, ep.bias, ep.bf16);
     return hipGetLastError();
 }
 

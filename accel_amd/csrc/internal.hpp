@@ -124,17 +124,20 @@ hipError_t launch_int4_generic_f32(hipStream_t st, const float* a, Int4Planes w,
 hipError_t launch_int4_generic_bf16(hipStream_t st, const uint16_t* a, Int4Planes w,
                                     uint16_t* out, int M, int K, int N,
                                     const float* bias = nullptr);
-// Prefill product on MFMA: bf16 activations [M,K] -> bf16 out [M,N].
+// Prefill product on MFMA: bf16 activations [M,K] -> bf16 out [M,N].  Products
+// with too few tiles to fill the chip split K (f32 sums in the workspace,
+// then one reduction pass); *status reports a workspace that cannot grow.
 hipError_t launch_int4_gemm_bf16(Device* d, hipStream_t st, const uint16_t* a,
                                  Int4Planes w, uint16_t* out, int M, int K, int N,
-                                 const float* bias = nullptr);
+                                 const float* bias, int* status);
 bool int4_gemm_bf16_supported(int M, int K, int N);
 // f32 activations with M > 16 on the bf16 matrix cores to f32 accuracy
 // (three-term split of x * 512 s against the exact codes); K % 64 == 0,
 // N % 128 == 0 and 16-byte aligned activations.
+// Too few tiles to fill the chip split K as the bf16 tiles do.
 hipError_t launch_int4_gemm_f32x3(Device* d, hipStream_t st, const float* a,
                                   Int4Planes w, void* out, int M, int K, int N,
-                                  Epilogue ep = Epilogue{});
+                                  Epilogue ep, int* status);
 bool int4_gemm_f32x3_supported(int K, int N);
 // f32 activations with M > 16, fp32 arithmetic: the other shapes.
 hipError_t launch_int4_gemm_f32(Device* d, hipStream_t st, const float* a,

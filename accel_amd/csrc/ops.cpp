@@ -151,7 +151,7 @@ int run_int4_product(Device* d, hipStream_t st, const void* a, int32_t dtype,
             e = launch_int4_decode_f32(d, st, af, p, out, M, K, N, &status, ep);
         else if (M > 16 && int4_gemm_f32x3_supported(K, N) &&
                  (reinterpret_cast<uintptr_t>(a) & 15) == 0)
-            e = launch_int4_gemm_f32x3(d, st, af, p, out, M, K, N, ep);
+            e = launch_int4_gemm_f32x3(d, st, af, p, out, M, K, N, ep, &status);
         else if (M > 16 && aligned128)
             e = launch_int4_gemm_f32(d, st, af, p, out, M, K, N, ep);
         else
@@ -160,7 +160,7 @@ int run_int4_product(Device* d, hipStream_t st, const void* a, int32_t dtype,
         const uint16_t* ab = static_cast<const uint16_t*>(a);
         uint16_t* ob = static_cast<uint16_t*>(out);
         if (int4_gemm_bf16_supported(M, K, N) && (reinterpret_cast<uintptr_t>(a) & 15) == 0)
-            e = launch_int4_gemm_bf16(d, st, ab, p, ob, M, K, N, ep.bias);
+            e = launch_int4_gemm_bf16(d, st, ab, p, ob, M, K, N, ep.bias, &status);
         else
             e = launch_int4_generic_bf16(st, ab, p, ob, M, K, N, ep.bias);
     }

@@ -119,6 +119,9 @@ SHAPES_F32 = [
     # bands, a full band, a ragged band and several column tiles; K % 64 != 0
     # takes the fp32 VALU tiles
     (257, 64, 128), (128, 1024, 512), (300, 2048, 1024), (40, 96, 256),
+    # split K on the matrix cores (too few tiles to fill the chip): eight
+    # slices at M = 64, a last slice longer than the others (17 stages over 4)
+    (64, 4096, 4096), (33, 1088, 256),
 ]
 
 
@@ -184,7 +187,11 @@ SHAPES_BF16 = [(1, 64, 128), (64, 256, 256), (100, 512, 384), (128, 128, 128),
                # ragged last row band
                (300, 64, 128), (256, 192, 384), (511, 320, 256),
                # last bands of 2, 4, 7 and 8 active 32-row m-tiles
-               (832, 128, 256), (97, 64, 256), (200, 256, 128), (480, 128, 128)]
+               (832, 128, 256), (97, 64, 256), (200, 256, 128), (480, 128, 128),
+               # split K (too few tiles to fill the chip): eight slices of a
+               # prefill at M = 64, a ragged one-m-tile band, a last slice
+               # longer than the others (17 stages over 4)
+               (64, 4096, 4096), (17, 4096, 1024), (96, 1088, 256)]
 
 
 def _bf16_oracle(x, p, s, z, M, K, N, rows=None):
