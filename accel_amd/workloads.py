@@ -60,6 +60,10 @@ CONFIGS = {
     "prefill_m2048": dict(M=2048, K=4096, N=4096, seed=2, bf16=True),
     # config 3's shape in the reference API's own dtype (f32 activations)
     "prefill_m2048_f32": dict(M=2048, K=4096, N=4096, seed=2, bf16=False),
+    # a short prefill (M >= 64 is the batched-GEMM range): too few tiles to
+    # fill the chip, so the products split K
+    "prefill_m64": dict(M=64, K=4096, N=4096, seed=2, bf16=True),
+    "prefill_m64_f32": dict(M=64, K=4096, N=4096, seed=2, bf16=False),
 }
 
 

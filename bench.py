@@ -55,6 +55,8 @@ GEMV_KERNEL = "int4_decode_f32_kernel<1, 256, 32, false>"
 GEMM_KERNEL = "int4_gemm_bf16_kernel<8, false>"
 GEMM_F32_KERNEL = "int4_gemm_f32x3_kernel"
 DECODE_MFMA_KERNEL = "int4_decode_mfma_kernel<2, 8>"
+SPLITK_BF16_KERNEL = "int4_gemm_bf16_splitk_kernel<2>"
+SPLITK_F32_KERNEL = "int4_gemm_f32x3_kernel (split K, M=64)"
 GROUPED_KERNEL = "int4_grouped_bf16_kernel"
 G32_KERNEL = "int4_g32_matvec_kernel"
 GROUPED_DECODE_KERNEL = "int4_grouped_decode_kernel<256, 32, true>"
@@ -1022,6 +1024,16 @@ def main():
         lf["roofline"]["note"] = ("achieved counts the product's own flops; the three-term "
                                   "split issues three times as many on the matrix cores")
         extra["prefill_m2048_f32"] = lf
+        progress("short prefill: M=64 bf16 and f32 (split K)")
+        for key, name, kern in (("prefill_m64_bf16", "prefill_m64", SPLITK_BF16_KERNEL),
+                                ("prefill_m64_f32", "prefill_m64_f32", SPLITK_F32_KERNEL)):
+            q = bench_gemm(dev, stream, name, steps=100, warmup=10)
+            dt = "bf16" if name == "prefill_m64" else "f32"
+            extra[key] = gemm_line(
+                q, f"Int4MatMul M=64 K=4096 N=4096, {dt} x/out: a short prefill, whose 32 "
+                   "tiles split K across the CUs (f32 sums per slice, one reduction pass)",
+                kern, "hbm", 2 * 64 * 4096 * 4096, q["bytes"])
+            extra[key]["tflops"] = round(q["tflops"], 1)
         progress("config 2: decode M=16 K=4096 N=14336")
         d = bench_gemm(dev, stream, "decode_m16", steps=200, warmup=10)
         extra["decode_m16_f32"] = gemm_line(
