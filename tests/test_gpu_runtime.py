@@ -8,6 +8,8 @@
   device's fault word at the next wait (forced from the host with a zero wait
   limit, so every kernel still exits normally), and products are correct
   again afterwards.
+* A split-K prefill (slices, then a reduction pass) replays from a graph
+  bit for bit like the eager call.
 """
 import numpy as np
 import pytest
@@ -145,3 +147,44 @@ def test_bounded_wait_that_gives_up_is_reported(dev):
     for b in (a, out):
         b.free()
     w.free()
+
+
+@pytest.mark.parametrize("bf16", [True, False])
+def test_split_k_prefill_replays_like_eager(dev, bf16):
+    """A short prefill (M = 64: its 32 tiles split K, then a reduction pass)
+    captured in a graph replays bit for bit like the eager call, three times
+    with eager work between the replays."""
+    M, K, N = 64, 2048, 1024
+    rng = np.random.Generator(np.random.PCG64(77 + bf16))
+    p, s, z = workloads.fast_int4(K, N, rng)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = dev.upload_int4(p, s, z, K * N)
+    if bf16:
+        a = dev.upload(workloads.bf16_bits(x), accel_amd.BF16)
+        eager, replayed = dev.alloc((M, N), accel_amd.BF16), dev.alloc((M, N), accel_amd.BF16)
+    else:
+        a = dev.upload(x)
+        eager, replayed = dev.alloc((M, N), F32), dev.alloc((M, N), F32)
+    stream = dev.stream()
+    dev.Int4MatMul(a, w, eager, stream)        # sizes the workspace outside the capture
+    dev.sync(stream)
+    dev.capture_begin(stream)
+    dev.Int4MatMul(a, w, replayed, stream)
+    ex = dev.capture_end(stream)
+    want = eager.numpy().copy()
+    for _ in range(3):
+        dev.Int4MatMul(a, w, eager, stream)    # eager work between the replays
+        dev.sync(stream)
+        dev.launch(ex, stream)
+        dev.sync(stream)
+        assert np.array_equal(replayed.numpy().view(np.uint16 if bf16 else np.uint32),
+                              want.view(np.uint16 if bf16 else np.uint32))
+    xf = workloads.bf16_to_f32(workloads.bf16_bits(x)) if bf16 else x
+    ref = oracle.quant_matmul_int4(xf, p, s, z, M, K, N, threads=8)
+    got = workloads.bf16_to_f32(want) if bf16 else want
+    assert rel_l2(got, ref) <= (2e-2 if bf16 else 1e-5)
+    dev.destroy_exec(ex)
+    for b in (a, eager, replayed):
+        b.free()
+    w.free()
+    dev.destroy_stream(stream)
