@@ -577,7 +577,8 @@ __global__ __launch_bounds__(kThreads, 1) void int4_gemm_bf16_splitk_kernel(
     const int grid = gridDim.x;
     int b = blockIdx.x;
     if ((grid & 7) == 0) b = (b & 7) * (grid >> 3) + (b >> 3);
-    // slices of one tile are consecutive: they share its codes' lines
+    // the slices of one tile are consecutive (one XCD); measured faster than
+    // the column tiles of a slice consecutive (M = 64: 14.9 against 16.5 us)
     const int slice = b % slices;
     const int tile = b / slices;
     const int m0 = m_first + (tile / tiles_n) * BM;
@@ -776,6 +777,8 @@ __global__ __launch_bounds__(kThreads, 1) void int4_gemm_f32x3_kernel(
     const int grid = gridDim.x;
     int bid = blockIdx.x;
     if ((grid & 7) == 0) bid = (bid & 7) * (grid >> 3) + (bid >> 3);
+    // split K: the slices of one tile are consecutive (one XCD), as in the
+    // bf16 split kernel
     const int slice = part ? bid % slices : 0;
     if (part) bid /= slices;
     const int m0 = (bid / tiles_n) * XBM;
