@@ -1541,6 +1541,19 @@ namespace {
 // the row fastest and dealt to the XCDs in contiguous runs, so the rows of one
 // expert -- adjacent, rows being sorted by expert -- read the same code lines
 // together through one L2.
+//
+// With sorted offsets and enough rows, an expert's rows are cut into blocks
+// of 16 from its first row; a block of at least 3 rows goes to the
+// matrix-core decode kernel (one read of the expert's weights for up to 16
+// rows, int4_grouped_decode_mfma_kernel, a second launch) and the VALU kernel
+// skips its rows; blocks of 1 or 2 rows (an expert's remainder) stay here.
+constexpr int kMfBlockRows = 16;   // rows of a matrix-core block, at most
+constexpr int kMfBlockMin = 3;     // and at least
+
+// Matrix-core blocks of an expert with c rows.
+__device__ __forceinline__ uint32_t grouped_mfma_blocks(uint32_t c) {
+    return c / kMfBlockRows + (c % kMfBlockRows >= (uint32_t)kMfBlockMin ? 1u : 0u);
+}
 
 __device__ __forceinline__ int grouped_expert_of(const uint32_t* off, int E, uint32_t t) {
     int e = 0;
@@ -1562,7 +1575,7 @@ __global__ __launch_bounds__(kDecThreads) void int4_grouped_decode_kernel(
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
     const uint32_t* __restrict__ off, float* __restrict__ out, float* partial,
     uint32_t* tickets, int ticket_stride, int E, int T, int K, int N, int rows_per_slice,
-    int slices, bool write_padding) {
+    int slices, bool write_padding, bool mfma_blocks) {
     const int tiles = N / TILE;
     const int grid = gridDim.x;
     int b = blockIdx.x;
@@ -1584,6 +1597,13 @@ __global__ __launch_bounds__(kDecThreads) void int4_grouped_decode_kernel(
     // and the first row's ticket.  Offsets that wrapped (no longer sorted)
     // leave every row alone.
     const bool sorted = grouped_offsets_sorted(off, E);
+    if (sorted && mfma_blocks) {
+        // rows of a block of 3 or more are the matrix-core launch's
+        const uint32_t i = (uint32_t)t - off[e];
+        const uint32_t c = min(off[e + 1], (uint32_t)T) - off[e];
+        const uint32_t j = i / kMfBlockRows;
+        if (min((uint32_t)kMfBlockRows, c - j * kMfBlockRows) >= (uint32_t)kMfBlockMin) return;
+    }
     if (sorted && (((uint32_t)t - off[e]) & 1u) != 0) return;
     const bool pair = sorted && (uint32_t)t + 1 < min(off[e + 1], (uint32_t)T);
     const size_t per = (size_t)K * N;
@@ -1601,6 +1621,90 @@ __global__ __launch_bounds__(kDecThreads) void int4_grouped_decode_kernel(
                                         K, N, tile, slice, rows_per_slice, slices, Epilogue{});
 }
 
+// The matrix-core blocks of a grouped decode product: workgroup b takes
+// block u -- the u-th block of 3..16 rows in (expert, first row) order, found
+// from the offsets by one wave's prefix sum over the experts' block counts --
+// and within it a K slice and column tile, as a lone 16-row matrix-core
+// decode launch would.  The grid is sized for the most blocks the rows can
+// make; workgroups past the real blocks return at once, as do all when the
+// offsets are not sorted (the VALU launch then takes every row).  A block's
+// split-K sums sit at slices x (its first row) x N floats into `partial`, so
+// blocks never share them; block u's tickets are the tile pairs past the
+// earlier blocks'.  (A persistent form, each workgroup looping over the
+// blocks, spilled registers and ran 3% slower.)
+template <int G, int NW>
+__global__ __launch_bounds__(64 * NW) void int4_grouped_decode_mfma_kernel(
+    const float* __restrict__ x, const uint32_t* __restrict__ codes,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
+    const uint32_t* __restrict__ off, float* __restrict__ out, float* partial,
+    uint32_t* tickets, int ticket_stride, int E, int T, int K, int N, int rows_per_slice,
+    int slices, uint32_t* fault, int wait_limit) {
+    using Tl = MfTile<G, NW>;
+    __shared__ int blk_e, blk_row0, blk_rows;
+    const int tiles = N / Tl::kCols;
+    const int per_block = tiles * slices;
+    // Blocks in dispatch order, each dealt to the eight XCDs (workgroups go
+    // to them round robin) in contiguous eighths of its (slice, tile) list,
+    // as a lone launch places them: the real blocks, which come first, keep
+    // every XCD busy, and the grid's surplus workgroups come last.
+    const int b = blockIdx.x;
+    uint32_t u;
+    int r;
+    if ((per_block & 7) == 0) {
+        const int q = per_block >> 3;
+        u = (uint32_t)((b >> 3) / q);
+        r = (b & 7) * q + (b >> 3) % q;
+    } else {
+        u = (uint32_t)(b / per_block);
+        r = b % per_block;
+    }
+    const int tile = r % tiles;
+    const int slice = r / tiles;
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        if (lane == 0) blk_e = -1;
+        if (grouped_offsets_sorted(off, E)) {
+            uint32_t base = 0;   // blocks of the experts before this run of 64
+            for (int e0 = 0; e0 < E && base <= u; e0 += 64) {
+                const int e = e0 + lane;
+                uint32_t start = 0, c = 0;
+                if (e < E) {
+                    start = min(off[e], (uint32_t)T);
+                    c = min(off[e + 1], (uint32_t)T) - start;
+                }
+                const uint32_t n = grouped_mfma_blocks(c);
+                uint32_t incl = n;   // inclusive prefix sum over the wave
+#pragma unroll
+                for (int dd = 1; dd < 64; dd <<= 1) {
+                    const uint32_t v = __shfl_up(incl, dd, 64);
+                    if (lane >= dd) incl += v;
+                }
+                const uint32_t first = base + incl - n;
+                if (u >= first && u < base + incl) {
+                    const uint32_t j = u - first;
+                    blk_e = e;
+                    blk_row0 = (int)(start + j * kMfBlockRows);
+                    blk_rows = (int)min((uint32_t)kMfBlockRows, c - j * kMfBlockRows);
+                }
+                base += __shfl(incl, 63, 64);
+            }
+        }
+    }
+    __syncthreads();
+    const int e = blk_e;
+    if (e < 0) return;
+    const int row0 = blk_row0;
+    const size_t per = (size_t)K * N;
+    decode_mfma_tile<G, NW>(x + (size_t)row0 * K, codes + (size_t)e * (per >> 3),
+                            scales + (size_t)e * (per >> 7), zeros + (size_t)e * (per >> 7),
+                            out + (size_t)row0 * N,
+                            partial ? partial + (size_t)slices * row0 * N : nullptr,
+                            tickets ? tickets + ((size_t)u * tiles + tile) * ticket_stride
+                                    : nullptr,
+                            blk_rows, K, N, tile, slice, rows_per_slice, slices, Epilogue{},
+                            fault, wait_limit);
+}
+
 // K slices of a grouped decode launch: enough workgroups for two per CU
 // across all rows, at most one batch each beyond that (the rows already fill
 // the chip).
@@ -1612,11 +1716,14 @@ struct GroupedDecodeShape {
     static constexpr int kRowsPerBatch = kBatch * RP;
     int tiles, per_slice, rows, slices;
     long long pairs;
-    GroupedDecodeShape(const Device* d, int T, int K, int N) {
+    // busy: the rows expected to have work (T, or one per expert when the
+    // matrix-core launch takes every block of 3 or more rows)
+    GroupedDecodeShape(const Device* d, int T, int K, int N, int busy) {
         tiles = N / TILE;
         const int batches = (K + kRowsPerBatch - 1) / kRowsPerBatch;
         pairs = (long long)T * tiles;
-        int want = (int)std::max(1LL, (2LL * d->cu_count + pairs - 1) / pairs);
+        const long long busy_wgs = (long long)std::max(1, std::min(busy, T)) * tiles;
+        int want = (int)std::max(1LL, (2LL * d->cu_count + busy_wgs - 1) / busy_wgs);
         want = std::min(want, std::min(batches, kMaxSlices));
         per_slice = (batches + want - 1) / want;
         rows = per_slice * kRowsPerBatch;
@@ -1627,13 +1734,49 @@ struct GroupedDecodeShape {
     }
 };
 
+// Whether a grouped decode product runs its blocks of 3..16 rows on the
+// matrix cores (a second launch), and that launch's plan: a lone 16-row
+// product's tile width and K slices, and the most blocks T rows over E
+// experts can make (each has 3 rows at least; an expert's blocks past its
+// first are full).  The launch is made only when the rows average two or
+// more an expert: with fewer, blocks of three rows are rare, and a launch
+// that finds none costs a round of workgroups (measured at 4 tokens routed
+// top-2 over 8 experts: 78 -> 82.7 us).
+struct GroupedMfma {
+    bool on = false;
+    MfPlan plan{1, 1, 0};
+    int blocks = 0;    // blocks the grid and the tickets are sized for
+    int stride = 0;    // ticket spacing (two counters a tile)
+};
+GroupedMfma grouped_mfma(const Device* d, const float* x, Int4Planes w, int E, int T, int K,
+                         int N) {
+    GroupedMfma g;
+    g.blocks = std::min(T / kMfBlockMin, T / kMfBlockRows + E);
+    if (g.blocks == 0 || (long long)T < 2LL * E || K % 32 != 0 || N >= (1 << 27) ||
+        (reinterpret_cast<uintptr_t>(x) & 15) != 0)
+        return g;
+    // an expert's scale and zero planes start 4-byte aligned when the base does
+    // and K * N / 128 is even
+    const size_t per = (size_t)K * N;
+    const bool planes_4b = ((reinterpret_cast<uintptr_t>(w.scales) |
+                             reinterpret_cast<uintptr_t>(w.zeros)) & 3) == 0 &&
+                           ((per >> 7) & 1) == 0;
+    g.plan = plan_decode_mfma(d, kMfBlockRows, K, N, planes_4b);
+    if (g.plan.slices > 1) {
+        g.stride = ticket_stride(g.blocks * (N / (128 * g.plan.groups)));
+        if (g.stride < 2) return g;
+    }
+    g.on = true;
+    return g;
+}
+
 template <int TILE>
 hipError_t launch_grouped_decode_tile(Device* d, hipStream_t st, const float* x, Int4Planes w,
                                       const uint32_t* off, float* out, int E, int T, int K,
                                       int N, bool write_padding, int* status,
-                                      uint32_t* tickets, float* area) {
+                                      uint32_t* tickets, float* area, bool mfma_blocks) {
     constexpr int CPL = GroupedDecodeShape<TILE>::CPL;
-    const GroupedDecodeShape<TILE> sh(d, T, K, N);
+    const GroupedDecodeShape<TILE> sh(d, T, K, N, mfma_blocks ? E : T);
     const int tiles = sh.tiles, per_slice = sh.per_slice, rows = sh.rows, slices = sh.slices;
     const long long pairs = sh.pairs;
     if (pairs * slices > (1ll << 31) - 8) {
@@ -1655,11 +1798,27 @@ hipError_t launch_grouped_decode_tile(Device* d, hipStream_t st, const float* x,
     if (per_slice > 1)
         hipLaunchKernelGGL((int4_grouped_decode_kernel<TILE, CPL, true>), grid,
                            dim3(kDecThreads), 0, st, x, w.codes, w.scales, w.zeros, off, out,
-                           partial, tickets, stride, E, T, K, N, rows, slices, write_padding);
+                           partial, tickets, stride, E, T, K, N, rows, slices, write_padding,
+                           mfma_blocks);
     else
         hipLaunchKernelGGL((int4_grouped_decode_kernel<TILE, CPL, false>), grid,
                            dim3(kDecThreads), 0, st, x, w.codes, w.scales, w.zeros, off, out,
-                           partial, tickets, stride, E, T, K, N, rows, slices, write_padding);
+                           partial, tickets, stride, E, T, K, N, rows, slices, write_padding,
+                           mfma_blocks);
+    return hipGetLastError();
+}
+
+template <int G>
+hipError_t launch_grouped_mfma(Device* d, hipStream_t st, const float* x, Int4Planes w,
+                               const uint32_t* off, float* out, int E, int T, int K, int N,
+                               const GroupedMfma& g, uint32_t* tickets, float* area) {
+    const int tiles = N / (128 * G);
+    const bool split = g.plan.slices > 1;
+    const dim3 grid((unsigned)(g.blocks * tiles * g.plan.slices));
+    hipLaunchKernelGGL((int4_grouped_decode_mfma_kernel<G, 8>), grid, dim3(64 * 8), 0, st, x,
+                       w.codes, w.scales, w.zeros, off, out, split ? area : nullptr,
+                       split ? tickets : nullptr, g.stride, E, T, K, N, g.plan.rows,
+                       g.plan.slices, d->fault_dev, d->wait_limit);
     return hipGetLastError();
 }
 
@@ -1681,11 +1840,22 @@ static int grouped_decode_tile(const Device* d, int T, int N) {
     return N % 256 == 0 ? 256 : 128;
 }
 
-size_t int4_grouped_decode_area(const Device* d, int T, int K, int N) {
+size_t int4_grouped_decode_area(const Device* d, const float* x, Int4Planes w, int E, int T,
+                                int K, int N) {
+    const GroupedMfma g = grouped_mfma(d, x, w, E, T, K, N);
+    const int busy = g.on ? E : T;
     const int tw = grouped_decode_tile(d, T, N);
-    if (tw == 512) return GroupedDecodeShape<512>(d, T, K, N).area_bytes(T, N);
-    if (tw == 256) return GroupedDecodeShape<256>(d, T, K, N).area_bytes(T, N);
-    return GroupedDecodeShape<128>(d, T, K, N).area_bytes(T, N);
+    size_t bytes;
+    if (tw == 512)
+        bytes = GroupedDecodeShape<512>(d, T, K, N, busy).area_bytes(T, N);
+    else if (tw == 256)
+        bytes = GroupedDecodeShape<256>(d, T, K, N, busy).area_bytes(T, N);
+    else
+        bytes = GroupedDecodeShape<128>(d, T, K, N, busy).area_bytes(T, N);
+    // the two launches run in turn on one stream, so their sums share the area
+    if (g.on && g.plan.slices > 1)
+        bytes = std::max(bytes, (size_t)g.plan.slices * T * N * sizeof(float));
+    return bytes;
 }
 
 hipError_t launch_int4_grouped_decode(Device* d, hipStream_t st, const float* x, Int4Planes w,
@@ -1693,15 +1863,22 @@ hipError_t launch_int4_grouped_decode(Device* d, hipStream_t st, const float* x,
                                       int N, bool write_padding, int* status,
                                       uint32_t* tickets, float* area) {
     *status = ACCEL_OK;
+    const GroupedMfma g = grouped_mfma(d, x, w, E, T, K, N);
     const int tw = grouped_decode_tile(d, T, N);
+    hipError_t e;
     if (tw == 512)
-        return launch_grouped_decode_tile<512>(d, st, x, w, off, out, E, T, K, N, write_padding,
-                                               status, tickets, area);
-    if (tw == 256)
-        return launch_grouped_decode_tile<256>(d, st, x, w, off, out, E, T, K, N, write_padding,
-                                               status, tickets, area);
-    return launch_grouped_decode_tile<128>(d, st, x, w, off, out, E, T, K, N, write_padding,
-                                           status, tickets, area);
+        e = launch_grouped_decode_tile<512>(d, st, x, w, off, out, E, T, K, N, write_padding,
+                                            status, tickets, area, g.on);
+    else if (tw == 256)
+        e = launch_grouped_decode_tile<256>(d, st, x, w, off, out, E, T, K, N, write_padding,
+                                            status, tickets, area, g.on);
+    else
+        e = launch_grouped_decode_tile<128>(d, st, x, w, off, out, E, T, K, N, write_padding,
+                                            status, tickets, area, g.on);
+    if (e != hipSuccess || *status != ACCEL_OK || !g.on) return e;
+    if (g.plan.groups == 2)
+        return launch_grouped_mfma<2>(d, st, x, w, off, out, E, T, K, N, g, tickets, area);
+    return launch_grouped_mfma<1>(d, st, x, w, off, out, E, T, K, N, g, tickets, area);
 }
 
 namespace {

@@ -174,15 +174,17 @@ hipError_t launch_int4_g32_matvec(Device* d, hipStream_t st, const float* a,
                                   const uint32_t* codes, const float* scales, float* out, int K,
                                   int N, int* status);
 // Ragged int4 GEMV (decode MoE): f32 x [T, K], T <= kGroupedDecodeRows, each
-// row against its expert's [K, N] matrix with the decode kernel; the
+// row against its expert's [K, N] matrix with the decode kernels (an
+// expert's blocks of 3..16 rows on the matrix cores, in a second launch); the
 // matvec form (write_padding) writes 0 to rows past every segment.
 constexpr int kGroupedDecodeRows = 64;
-// The grouped decode launch takes the workspace's counters (`tickets`) and an
-// area past the offsets for its split-K sums, of the size
-// int4_grouped_decode_area gives (the workspace is sized once, before the
-// offsets are computed, so it cannot grow and move them).
+// The grouped decode launches take the workspace's counters (`tickets`) and an
+// area past the offsets for their split-K sums, of the size
+// int4_grouped_decode_area gives for the same x, w and shape (the workspace is
+// sized once, before the offsets are computed, so it cannot grow and move them).
 bool int4_grouped_decode_supported(int T, int K, int N, const void* codes);
-size_t int4_grouped_decode_area(const Device* d, int T, int K, int N);
+size_t int4_grouped_decode_area(const Device* d, const float* x, Int4Planes w, int E, int T,
+                                int K, int N);
 hipError_t launch_int4_grouped_decode(Device* d, hipStream_t st, const float* x, Int4Planes w,
                                       const uint32_t* off, float* out, int E, int T, int K,
                                       int N, bool write_padding, int* status,

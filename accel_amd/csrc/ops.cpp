@@ -699,7 +699,10 @@ int run_grouped_int4(const char* op, int dev, void* stream, const accel_tensor_t
                   (reinterpret_cast<uintptr_t>(x->data) & 15) == 0))
         return refuse(op, "bf16 grouped products need K % 64 == 0, N % 128 == 0, K < 2^22 and "
                           "N < 2^26");
-    const size_t area_bytes = decode ? int4_grouped_decode_area(d, (int)T, (int)K, (int)N) : 0;
+    const size_t area_bytes =
+        decode ? int4_grouped_decode_area(d, static_cast<const float*>(x->data), planes(w),
+                                          (int)experts, (int)T, (int)K, (int)N)
+               : 0;
     void* area = nullptr;
     uint32_t* off = offsets_in_workspace(d, st, static_cast<const uint32_t*>(counts->data),
                                          experts, &status, area_bytes, &area);

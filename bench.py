@@ -59,7 +59,10 @@ SPLITK_BF16_KERNEL = "int4_gemm_bf16_splitk_kernel<2>"
 SPLITK_F32_KERNEL = "int4_gemm_f32x3_kernel (split K, M=64)"
 GROUPED_KERNEL = "int4_grouped_bf16_kernel"
 G32_KERNEL = "int4_g32_matvec_kernel"
-GROUPED_DECODE_KERNEL = "int4_grouped_decode_kernel<256, 32, true>"
+# the decode MoE is two launches: rows alone or in pairs, then blocks of 3..16
+# rows of one expert on the matrix cores
+GROUPED_DECODE_KERNELS = ("int4_grouped_decode_kernel<256, 32, true>",
+                          "int4_grouped_decode_mfma_kernel<2, 8>")
 FLUSH_BYTES = 512 << 20        # device copy that evicts the Infinity Cache
 PUBLISHED_US = 760.0           # Int4MatVec [2048] x [2048,2048] on an M2, one plan a step
 PUBLISHED_SRC = "specs/010-kernel-corpus.md:593-602 (tensor/decodebench_darwin_test.go:148-189)"
@@ -98,6 +101,13 @@ def traffic_of(kernel: str):
         return int(t["hbm_bytes_per_launch"])
     except (OSError, KeyError, ValueError):
         return None
+
+
+def traffic_sum(kernels):
+    """HBM bytes of a call made of one launch of each of `kernels`, or None
+    when the summary lacks any of them."""
+    parts = [traffic_of(k) for k in kernels]
+    return None if any(p is None for p in parts) else sum(parts)
 
 
 class Flusher:
@@ -343,9 +353,10 @@ def bench_moe(dev, stream, steps=20):
 
 def bench_moe_decode(dev, stream, tokens=8, steps=40):
     """Decode MoE: `tokens` tokens routed top-2 over config 4's eight experts
-    (K=4096, N=14336) as f32 rows, Int4GroupedMatVec -- one decode product
-    per routed row against its expert.  Three copies of the experts (750 MB)
-    rotate and the cache is flushed before the timed replay."""
+    (K=4096, N=14336) as f32 rows, Int4GroupedMatVec -- decode products of
+    each expert's routed rows against its matrix (blocks of 3..16 rows on the
+    matrix cores, the rest alone or in pairs).  Three copies of the experts
+    (750 MB) rotate and the cache is flushed before the timed replay."""
     from accel_amd import F32, U32, workloads
     progress(f"decode MoE: {tokens} tokens, top-2 of 8 experts")
     m = workloads.moe_fast(tokens=tokens)
@@ -379,8 +390,9 @@ def bench_moe_decode(dev, stream, tokens=8, steps=40):
                 counts=[int(c) for c in m.counts],
                 roofline={"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                           "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                          "traffic": traffic_of(GROUPED_DECODE_KERNEL),
-                          "kernel": GROUPED_DECODE_KERNEL, "bytes_per_launch": int(nbytes)})
+                          "traffic": traffic_sum(GROUPED_DECODE_KERNELS),
+                          "kernel": " + ".join(GROUPED_DECODE_KERNELS),
+                          "bytes_per_launch": int(nbytes)})
 
 
 _LAYER_PLANES = {}

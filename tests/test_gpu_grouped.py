@@ -162,7 +162,18 @@ def run_int4_grouped(dev, form, x, p, s, z, counts, E, T, K, N, bf16):
                                               # few rows of a wide matrix: 512-column
                                               # tiles, a pair and single rows
                                               (3, 512, 8192, [1, 0, 1], 1),
-                                              (2, 1024, 8192, [2, 1], 0)])
+                                              (2, 1024, 8192, [2, 1], 0),
+                                              # blocks of 3..16 rows on the matrix
+                                              # cores (T >= 2E), the remainder of
+                                              # 1 or 2 rows on the VALU kernel:
+                                              # 16 + 1, 16 + 2, 16 + 3 rows; 16 and
+                                              # 16 + 16 + 3 with one-group tiles;
+                                              # 5 and 3 rows over split K
+                                              (3, 256, 512, [17, 18, 19], 1),
+                                              (2, 2048, 384, [16, 35], 2),
+                                              (2, 4096, 2048, [5, 3], 0),
+                                              # T < 2E: every row on the VALU kernel
+                                              (8, 256, 256, [3, 0, 0, 0, 0, 0, 0, 1], 1)])
 def test_int4_grouped_matches_the_oracle(dev, bf16, form, E, K, N, counts, pad):
     x, p, s, z, off, T = int4_case(E, K, N, counts, pad, seed=E + K, bf16=bf16)
     got = run_int4_grouped(dev, form, x, p, s, z, counts, E, T, K, N, bf16)
