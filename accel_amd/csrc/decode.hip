@@ -1543,12 +1543,14 @@ namespace {
 // together through one L2.
 //
 // With sorted offsets and enough rows, an expert's rows are cut into blocks
-// of 16 from its first row; a block of at least 3 rows goes to the
+// of 16 from its first row; a block of at least 2 rows goes to the
 // matrix-core decode kernel (one read of the expert's weights for up to 16
 // rows, int4_grouped_decode_mfma_kernel, a second launch) and the VALU kernel
-// skips its rows; blocks of 1 or 2 rows (an expert's remainder) stay here.
+// skips its rows; a block of one row (an expert's remainder) stays here.
+// Measured at 8 tokens routed top-2 over config 4's experts: pairs on the
+// VALU kernel 102.5 us, on the matrix cores 98-99 us.
 constexpr int kMfBlockRows = 16;   // rows of a matrix-core block, at most
-constexpr int kMfBlockMin = 3;     // and at least
+constexpr int kMfBlockMin = 2;     // and at least
 
 // Matrix-core blocks of an expert with c rows.
 __device__ __forceinline__ uint32_t grouped_mfma_blocks(uint32_t c) {
@@ -1598,7 +1600,7 @@ __global__ __launch_bounds__(kDecThreads) void int4_grouped_decode_kernel(
     // leave every row alone.
     const bool sorted = grouped_offsets_sorted(off, E);
     if (sorted && mfma_blocks) {
-        // rows of a block of 3 or more are the matrix-core launch's
+        // rows of a block of kMfBlockMin or more are the matrix-core launch's
         const uint32_t i = (uint32_t)t - off[e];
         const uint32_t c = min(off[e + 1], (uint32_t)T) - off[e];
         const uint32_t j = i / kMfBlockRows;
@@ -1622,7 +1624,7 @@ __global__ __launch_bounds__(kDecThreads) void int4_grouped_decode_kernel(
 }
 
 // The matrix-core blocks of a grouped decode product: workgroup b takes
-// block u -- the u-th block of 3..16 rows in (expert, first row) order, found
+// block u -- the u-th block of 2..16 rows in (expert, first row) order, found
 // from the offsets by one wave's prefix sum over the experts' block counts --
 // and within it a K slice and column tile, as a lone 16-row matrix-core
 // decode launch would.  The grid is sized for the most blocks the rows can
@@ -1717,7 +1719,7 @@ struct GroupedDecodeShape {
     int tiles, per_slice, rows, slices;
     long long pairs;
     // busy: the rows expected to have work (T, or one per expert when the
-    // matrix-core launch takes every block of 3 or more rows)
+    // matrix-core launch takes every block of two or more rows)
     GroupedDecodeShape(const Device* d, int T, int K, int N, int busy) {
         tiles = N / TILE;
         const int batches = (K + kRowsPerBatch - 1) / kRowsPerBatch;
@@ -1734,12 +1736,12 @@ struct GroupedDecodeShape {
     }
 };
 
-// Whether a grouped decode product runs its blocks of 3..16 rows on the
+// Whether a grouped decode product runs its blocks of 2..16 rows on the
 // matrix cores (a second launch), and that launch's plan: a lone 16-row
 // product's tile width and K slices, and the most blocks T rows over E
-// experts can make (each has 3 rows at least; an expert's blocks past its
+// experts can make (each has 2 rows at least; an expert's blocks past its
 // first are full).  The launch is made only when the rows average two or
-// more an expert: with fewer, blocks of three rows are rare, and a launch
+// more an expert: with fewer, blocks of several rows are rare, and a launch
 // that finds none costs a round of workgroups (measured at 4 tokens routed
 // top-2 over 8 experts: 78 -> 82.7 us).
 struct GroupedMfma {
