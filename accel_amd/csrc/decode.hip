@@ -1543,16 +1543,20 @@ namespace {
 // together through one L2.
 //
 // With sorted offsets and enough rows, an expert's rows are cut into blocks
-// of 16 from its first row; a block of at least 2 rows goes to the
-// matrix-core decode kernel (one read of the expert's weights for up to 16
-// rows, int4_grouped_decode_mfma_kernel, a second launch) and the VALU kernel
-// skips its rows; a block of one row (an expert's remainder) stays here.
-// Measured at 8 tokens routed top-2 over config 4's experts: pairs on the
-// VALU kernel 102.5 us, on the matrix cores 98-99 us.
+// of 16 from its first row and every block goes to the matrix-core decode
+// kernel (one read of the expert's weights for up to 16 rows,
+// int4_grouped_decode_mfma_kernel, a second launch); this kernel then only
+// writes the padding rows, or takes every row when the offsets wrapped.
+// Measured at 4, 8, 16 and 32 tokens routed top-2 over config 4's experts
+// (us): rows alone or in pairs here 78.8, 119.4, 208.3, 372; blocks of 3..16
+// rows on the matrix cores 78.7, 102.1, 154.1, 140.8; of 2..16 78.6, 98.6,
+// 154.5, 140.7; of 1..16, with this launch at one K slice and 512-column
+// tiles, 79.1, 93.9, 116.1, 123.8.
 constexpr int kMfBlockRows = 16;   // rows of a matrix-core block, at most
-constexpr int kMfBlockMin = 2;     // and at least
+constexpr int kMfBlockMin = 1;     // and at least
 
-// Matrix-core blocks of an expert with c rows.
+// Matrix-core blocks of an expert with c rows (a block of kMfBlockMin rows
+// or more past the full ones).
 __device__ __forceinline__ uint32_t grouped_mfma_blocks(uint32_t c) {
     return c / kMfBlockRows + (c % kMfBlockRows >= (uint32_t)kMfBlockMin ? 1u : 0u);
 }
@@ -1624,7 +1628,7 @@ __global__ __launch_bounds__(kDecThreads) void int4_grouped_decode_kernel(
 }
 
 // The matrix-core blocks of a grouped decode product: workgroup b takes
-// block u -- the u-th block of 2..16 rows in (expert, first row) order, found
+// block u -- the u-th block of 1..16 rows in (expert, first row) order, found
 // from the offsets by one wave's prefix sum over the experts' block counts --
 // and within it a K slice and column tile, as a lone 16-row matrix-core
 // decode launch would.  The grid is sized for the most blocks the rows can
@@ -1718,14 +1722,16 @@ struct GroupedDecodeShape {
     static constexpr int kRowsPerBatch = kBatch * RP;
     int tiles, per_slice, rows, slices;
     long long pairs;
-    // busy: the rows expected to have work (T, or one per expert when the
-    // matrix-core launch takes every block of two or more rows)
-    GroupedDecodeShape(const Device* d, int T, int K, int N, int busy) {
+    // singles: the matrix-core launch takes the rows, which leaves this launch
+    // the padding rows (or every row, should the offsets have wrapped): one K
+    // slice, so that the grid its workgroups without rows return from stays
+    // small (8 tokens routed top-2 over config 4's experts: 8.0 us with two
+    // slices)
+    GroupedDecodeShape(const Device* d, int T, int K, int N, bool singles) {
         tiles = N / TILE;
         const int batches = (K + kRowsPerBatch - 1) / kRowsPerBatch;
         pairs = (long long)T * tiles;
-        const long long busy_wgs = (long long)std::max(1, std::min(busy, T)) * tiles;
-        int want = (int)std::max(1LL, (2LL * d->cu_count + busy_wgs - 1) / busy_wgs);
+        int want = singles ? 1 : (int)std::max(1LL, (2LL * d->cu_count + pairs - 1) / pairs);
         want = std::min(want, std::min(batches, kMaxSlices));
         per_slice = (batches + want - 1) / want;
         rows = per_slice * kRowsPerBatch;
@@ -1736,10 +1742,10 @@ struct GroupedDecodeShape {
     }
 };
 
-// Whether a grouped decode product runs its blocks of 2..16 rows on the
+// Whether a grouped decode product runs its blocks of up to 16 rows on the
 // matrix cores (a second launch), and that launch's plan: a lone 16-row
 // product's tile width and K slices, and the most blocks T rows over E
-// experts can make (each has 2 rows at least; an expert's blocks past its
+// experts can make (each has a row at least; an expert's blocks past its
 // first are full).  The launch is made only when the rows average two or
 // more an expert: with fewer, blocks of several rows are rare, and a launch
 // that finds none costs a round of workgroups (measured at 4 tokens routed
@@ -1778,7 +1784,7 @@ hipError_t launch_grouped_decode_tile(Device* d, hipStream_t st, const float* x,
                                       int N, bool write_padding, int* status,
                                       uint32_t* tickets, float* area, bool mfma_blocks) {
     constexpr int CPL = GroupedDecodeShape<TILE>::CPL;
-    const GroupedDecodeShape<TILE> sh(d, T, K, N, mfma_blocks ? E : T);
+    const GroupedDecodeShape<TILE> sh(d, T, K, N, mfma_blocks);
     const int tiles = sh.tiles, per_slice = sh.per_slice, rows = sh.rows, slices = sh.slices;
     const long long pairs = sh.pairs;
     if (pairs * slices > (1ll << 31) - 8) {
@@ -1845,15 +1851,14 @@ static int grouped_decode_tile(const Device* d, int T, int N) {
 size_t int4_grouped_decode_area(const Device* d, const float* x, Int4Planes w, int E, int T,
                                 int K, int N) {
     const GroupedMfma g = grouped_mfma(d, x, w, E, T, K, N);
-    const int busy = g.on ? E : T;
-    const int tw = grouped_decode_tile(d, T, N);
+    const int tw = g.on && N % 512 == 0 ? 512 : grouped_decode_tile(d, T, N);
     size_t bytes;
     if (tw == 512)
-        bytes = GroupedDecodeShape<512>(d, T, K, N, busy).area_bytes(T, N);
+        bytes = GroupedDecodeShape<512>(d, T, K, N, g.on).area_bytes(T, N);
     else if (tw == 256)
-        bytes = GroupedDecodeShape<256>(d, T, K, N, busy).area_bytes(T, N);
+        bytes = GroupedDecodeShape<256>(d, T, K, N, g.on).area_bytes(T, N);
     else
-        bytes = GroupedDecodeShape<128>(d, T, K, N, busy).area_bytes(T, N);
+        bytes = GroupedDecodeShape<128>(d, T, K, N, g.on).area_bytes(T, N);
     // the two launches run in turn on one stream, so their sums share the area
     if (g.on && g.plan.slices > 1)
         bytes = std::max(bytes, (size_t)g.plan.slices * T * N * sizeof(float));
@@ -1866,7 +1871,8 @@ hipError_t launch_int4_grouped_decode(Device* d, hipStream_t st, const float* x,
                                       uint32_t* tickets, float* area) {
     *status = ACCEL_OK;
     const GroupedMfma g = grouped_mfma(d, x, w, E, T, K, N);
-    const int tw = grouped_decode_tile(d, T, N);
+    // with the rows on the matrix cores, the widest tile (fewest workgroups)
+    const int tw = g.on && N % 512 == 0 ? 512 : grouped_decode_tile(d, T, N);
     hipError_t e;
     if (tw == 512)
         e = launch_grouped_decode_tile<512>(d, st, x, w, off, out, E, T, K, N, write_padding,

@@ -175,7 +175,7 @@ hipError_t launch_int4_g32_matvec(Device* d, hipStream_t st, const float* a,
                                   int N, int* status);
 // Ragged int4 GEMV (decode MoE): f32 x [T, K], T <= kGroupedDecodeRows, each
 // row against its expert's [K, N] matrix with the decode kernels (an
-// expert's blocks of 2..16 rows on the matrix cores, in a second launch); the
+// expert's rows in blocks of up to 16 on the matrix cores, in a second launch); the
 // matvec form (write_padding) writes 0 to rows past every segment.
 constexpr int kGroupedDecodeRows = 64;
 // The grouped decode launches take the workspace's counters (`tickets`) and an

@@ -59,9 +59,9 @@ SPLITK_BF16_KERNEL = "int4_gemm_bf16_splitk_kernel<2>"
 SPLITK_F32_KERNEL = "int4_gemm_f32x3_kernel (split K, M=64)"
 GROUPED_KERNEL = "int4_grouped_bf16_kernel"
 G32_KERNEL = "int4_g32_matvec_kernel"
-# the decode MoE is two launches: single rows, then blocks of 2..16
-# rows of one expert on the matrix cores
-GROUPED_DECODE_KERNELS = ("int4_grouped_decode_kernel<256, 32, true>",
+# the decode MoE is two launches: the padding rows, then each expert's rows in
+# blocks of up to 16 on the matrix cores
+GROUPED_DECODE_KERNELS = ("int4_grouped_decode_kernel<512, 32, true>",
                           "int4_grouped_decode_mfma_kernel<2, 8>")
 FLUSH_BYTES = 512 << 20        # device copy that evicts the Infinity Cache
 PUBLISHED_US = 760.0           # Int4MatVec [2048] x [2048,2048] on an M2, one plan a step
@@ -354,8 +354,8 @@ def bench_moe(dev, stream, steps=20):
 def bench_moe_decode(dev, stream, tokens=8, steps=40):
     """Decode MoE: `tokens` tokens routed top-2 over config 4's eight experts
     (K=4096, N=14336) as f32 rows, Int4GroupedMatVec -- decode products of
-    each expert's routed rows against its matrix (blocks of 2..16 rows on the
-    matrix cores, single rows on the VALU kernel).  Three copies of the experts
+    each expert's routed rows against its matrix (blocks of up to 16 rows on
+    the matrix cores).  Three copies of the experts
     (750 MB) rotate and the cache is flushed before the timed replay."""
     from accel_amd import F32, U32, workloads
     progress(f"decode MoE: {tokens} tokens, top-2 of 8 experts")

@@ -163,9 +163,8 @@ def run_int4_grouped(dev, form, x, p, s, z, counts, E, T, K, N, bf16):
                                               # tiles, a pair and single rows
                                               (3, 512, 8192, [1, 0, 1], 1),
                                               (2, 1024, 8192, [2, 1], 0),
-                                              # blocks of 2..16 rows on the matrix
-                                              # cores (T >= 2E), a remainder of one
-                                              # row on the VALU kernel:
+                                              # blocks of up to 16 rows on the
+                                              # matrix cores (T >= 2E):
                                               # 16 + 1, 16 + 2, 16 + 3 rows; 16 and
                                               # 16 + 16 + 3 with one-group tiles;
                                               # 5 and 3 rows over split K
