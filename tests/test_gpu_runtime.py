@@ -188,3 +188,44 @@ def test_split_k_prefill_replays_like_eager(dev, bf16):
         b.free()
     w.free()
     dev.destroy_stream(stream)
+
+
+def test_decode_moe_replays_like_eager(dev):
+    """The decode MoE (f32 rows, two rows or more an expert: the padding-row
+    launch, then each expert's rows as matrix-core blocks with split K)
+    captured in a graph replays bit for bit like the eager call, three times
+    with eager work between the replays; the matvec form's padding rows stay
+    zero."""
+    E, K, N, counts, pad = 4, 1024, 1024, [5, 0, 19, 3], 2
+    rng = np.random.Generator(np.random.PCG64(78))
+    off = oracle.segment_offsets(np.array(counts, np.uint32))
+    T = int(off[E]) + pad
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    w32 = (rng.standard_normal(E * K * N) * 0.02).astype(np.float32)
+    p, s, z = oracle.int4_quantize(w32)
+    w = dev.upload_int4(p, s, z, E * K * N)
+    a = dev.upload(x)
+    cb = dev.upload(np.array(counts, np.uint32), accel_amd.U32)
+    eager, replayed = dev.alloc((T, N), F32), dev.alloc((T, N), F32)
+    replayed.write(np.full((T, N), 7.0, np.float32))
+    stream = dev.stream()
+    dev.Int4GroupedMatVec(a, w, E, cb, eager, stream)   # sizes the workspace outside the capture
+    dev.sync(stream)
+    dev.capture_begin(stream)
+    dev.Int4GroupedMatVec(a, w, E, cb, replayed, stream)
+    ex = dev.capture_end(stream)
+    want = eager.numpy().copy()
+    for _ in range(3):
+        dev.Int4GroupedMatVec(a, w, E, cb, eager, stream)   # eager work between the replays
+        dev.sync(stream)
+        dev.launch(ex, stream)
+        dev.sync(stream)
+        assert np.array_equal(replayed.numpy().view(np.uint32), want.view(np.uint32))
+    ref = oracle.int4_grouped_matvec(x, p, s, z, off, E, T, K, N, threads=8,
+                                     out=np.full(T * N, 7.0, np.float32))
+    assert rel_l2(want.ravel(), np.asarray(ref).ravel()) <= 1e-5
+    assert np.all(want[int(off[E]):] == 0)
+    dev.destroy_exec(ex)
+    for b in (a, cb, eager, replayed, w):
+        b.free()
+    dev.destroy_stream(stream)
