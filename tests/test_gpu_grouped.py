@@ -253,3 +253,24 @@ def test_config4_moe_full_size(dev):
     for b in (xb, cb, ob):
         b.free()
     w.free()
+
+
+@pytest.mark.parametrize("form", ["Int4GroupedMatVec", "Int4GroupedMatMul"])
+def test_int4_grouped_decode_clamps_counts_past_the_rows(dev, form):
+    """Counts that run past the T rows (`groupedtiled.go:87-91`: expert e's
+    rows are [off[e], min(off[e+1], T))): with 10 + 30 routed rows over 24,
+    expert 1 keeps 14, one matrix-core block; a third expert starting past T
+    has none."""
+    E, K, N, counts, T = 3, 1024, 512, [10, 30, 5], 24
+    rng = np.random.Generator(np.random.PCG64(90))
+    off = oracle.segment_offsets(np.array(counts, np.uint32))
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    w = (rng.standard_normal(E * K * N) * 0.02).astype(np.float32)
+    p, s, z = oracle.int4_quantize(w)
+    got = run_int4_grouped(dev, form, x, p, s, z, counts, E, T, K, N, False)
+    ref = oracle.int4_grouped_matvec if form == "Int4GroupedMatVec" else \
+        oracle.int4_grouped_matmul
+    want = ref(x, p, s, z, off, E, T, K, N, threads=8, out=np.full(T * N, 7.0, np.float32))
+    assert rel_l2(got, want) <= 1e-5
+    for t in (0, 9, 10, 23):
+        assert rel_l2(got[t], want[t]) <= 1e-5, t
