@@ -569,9 +569,9 @@ __global__ void int4_generic_bf16_kernel(const uint16_t* __restrict__ a,
     out[i] = float_to_bf16_bits(acc);
 }
 
-// ---- 3..16 rows: the matrix cores ------------------------------------------
+// ---- 2..16 rows: the matrix cores ------------------------------------------
 //
-// With M rows of activations every weight feeds M FMAs, and past two rows the
+// With M rows of activations every weight feeds M FMAs, and from two rows the
 // VALU (not HBM) bounds a VALU product.  This kernel moves the arithmetic
 // onto v_mfma_f32_16x16x32_bf16 and keeps f32 accuracy:
 //   * the activation rows are the MFMA's A side (16 rows; rows >= M are
@@ -1427,7 +1427,7 @@ hipError_t launch_matvec_f32_f16(Device* d, hipStream_t st, const float* a, cons
 
 bool int4_matmul_set_supported(const float* a, const Int4Planes* w, const int* N, int count,
                                int M, int K) {
-    if (count < 1 || count > kMaxSet || M < 3 || M > 16 || K % 32 != 0 ||
+    if (count < 1 || count > kMaxSet || M < 2 || M > 16 || K % 32 != 0 ||
         (reinterpret_cast<uintptr_t>(a) & 15) != 0)
         return false;
     for (int i = 0; i < count; i++)
@@ -1503,9 +1503,12 @@ bool int4_decode_f32_supported(int M, int K, int N, const void* codes) {
 hipError_t launch_int4_decode_f32(Device* d, hipStream_t st, const float* a, Int4Planes w,
                                   void* out, int M, int K, int N, int* status, Epilogue ep) {
     *status = ACCEL_OK;
-    // Three or more rows: the matrix-core kernel, where its shape holds (its
-    // per-lane code offsets within a 32-row step are 32-bit).
-    if (M >= 3 && K % 32 == 0 && N < (1 << 27) && (reinterpret_cast<uintptr_t>(a) & 15) == 0)
+    // Two or more rows: the matrix-core kernel, where its shape holds (its
+    // per-lane code offsets within a 32-row step are 32-bit).  Two rows
+    // measured against the VALU kernel (us): K x N = 4096 x 1024 7.9 / 9.8,
+    // 1024 x 4096 7.2 / 9.7, 2048 x 2048 7.4 / 9.8, 4096 x 14336 16.6 / 20.9,
+    // 14336 x 4096 16.1 / 19.0, 4096 x 28672 25.2 / 34.8; 4096 x 4096 10.4 / 10.0.
+    if (M >= 2 && K % 32 == 0 && N < (1 << 27) && (reinterpret_cast<uintptr_t>(a) & 15) == 0)
         return launch_decode_mfma(d, st, a, w, out, M, K, N, status, ep);
     switch (M) {
         case 1: return launch_decode_m<1>(d, st, a, w, out, K, N, status, ep);

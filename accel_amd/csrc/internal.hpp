@@ -150,7 +150,7 @@ bool int4_matvec_set_supported(const Int4Planes* w, const int* N, int count, int
 hipError_t launch_int4_matvec_set(Device* d, hipStream_t st, const float* a, const Int4Planes* w,
                                   float* const* out, const int* N, int count, int K,
                                   int* status);
-// The same for M = 3..16 rows of f32 activations on the matrix-core decode
+// The same for M = 2..16 rows of f32 activations on the matrix-core decode
 // kernel, each matrix with its own launch's plan.
 bool int4_matmul_set_supported(const float* a, const Int4Planes* w, const int* N, int count,
                                int M, int K);

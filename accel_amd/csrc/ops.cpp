@@ -290,7 +290,7 @@ ACCEL_API int accel_int4_matvec_set(int dev, void* stream, const accel_tensor_t*
 
 // Int4MatMul over several matrices that share one f32 activation block
 // [M, K]: one launch per tile width where they all take the matrix-core
-// decode kernel (3 <= M <= 16), each with its own launch's plan, so each
+// decode kernel (2 <= M <= 16), each with its own launch's plan, so each
 // result is its own Int4MatMul's; else one Int4MatMul each.
 ACCEL_API int accel_int4_matmul_set(int dev, void* stream, const accel_tensor_t* a,
                                     const accel_int4_t* w, accel_tensor_t* out, int count) {

@@ -339,7 +339,7 @@ int accel_int4_matvec_set(int dev, void* stream, const accel_tensor_t* a,
                           const accel_int4_t* w, accel_tensor_t* out, int count);
 
 /* The same for f32 rows a [M,K] and out[i] f32 [M,N_i] (Int4MatMul's checks
- * per matrix): M = 1 as above; 3 <= M <= 16 with K % 32 == 0 and 16-byte
+ * per matrix): M = 1 as above; 2 <= M <= 16 with K % 32 == 0 and 16-byte
  * aligned a on the matrix-core decode kernel, one launch per tile width, each
  * matrix with the plan its own launch takes, so out[i] is exactly
  * Int4MatMul(a, w[i]); other shapes one Int4MatMul each. */

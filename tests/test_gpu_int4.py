@@ -100,9 +100,11 @@ SHAPES_F32 = [
     (1, 1000, 384), (2, 512, 1024), (3, 256, 640), (5, 200, 20), (7, 384, 256),
     (8, 4096, 1024), (13, 200, 20), (16, 4096, 14336), (17, 256, 512),
     (64, 512, 256), (65, 320, 384),
-    # the VALU decode kernel at its other widths: K % 32 != 0 keeps M >= 3 off
+    # the VALU decode kernel at its other widths: K % 32 != 0 keeps M >= 2 off
     # the matrix cores; 128-column tiles; two passes of eight rows
-    (3, 200, 640), (6, 100, 1024), (12, 72, 512), (2, 4096, 14336), (1, 4096, 640),
+    (3, 200, 640), (6, 100, 1024), (12, 72, 512), (2, 4100, 1024), (1, 4096, 640),
+    # two rows on the matrix-core decode kernel: one- and two-group tiles
+    (2, 4096, 14336), (2, 1024, 640),
     # K long enough that a workgroup loops over several batches of rows (256-
     # and 128-column tiles), and the layer chain's down projection
     (1, 16640, 256), (2, 33000, 128), (1, 14336, 4096),

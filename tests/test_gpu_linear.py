@@ -46,7 +46,8 @@ def _free(*bufs):
 @pytest.mark.parametrize("M,K,N,vector", [
     (1, 4096, 4096, True),     # VALU decode, one row, split K
     (1, 300, 256, False),
-    (2, 1024, 384, False),     # VALU decode, 128-column tiles
+    (2, 1024, 384, False),     # matrix-core decode, two rows, one-group tiles
+    (2, 1000, 384, False),     # K % 32 != 0: VALU decode, 128-column tiles
     (5, 4096, 4096, False),    # matrix-core decode
     (16, 1024, 768, False),
     (12, 200, 256, False),     # K % 32 != 0: VALU decode, eight rows then four

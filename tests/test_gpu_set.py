@@ -58,7 +58,8 @@ def test_set_equals_separate_matvecs(dev, K, Ns):
     (5, 1024, [384, 256, 512]),       # one- and two-group tiles: two launches
     (16, 2048, [1024, 2048]),
     (3, 512, [128]),
-    (2, 1024, [256, 512]),            # two rows: one Int4MatMul each
+    (2, 1024, [256, 512]),            # two rows: matrix-core decode too
+    (2, 100, [256, 128]),             # two rows, K % 32 != 0: one Int4MatMul each
     (1, 4096, [4096, 1024]),          # one row: the vector set
     (4, 100, [256, 128]),             # K % 32 != 0: one Int4MatMul each
 ])
