@@ -116,6 +116,13 @@ hipError_t launch_int4_matvec_noalloc(Device* d, hipStream_t st, const float* a,
 hipError_t launch_int4_decode_f32(Device* d, hipStream_t st, const float* a,
                                   Int4Planes w, void* out, int M, int K, int N,
                                   int* status, Epilogue ep = Epilogue{});
+// 17..48 rows of f32 activations as consecutive 16-row decode products,
+// where that beats the f32 matrix-core tiles (int4_decode_rows_pay); the same
+// shape limits as launch_int4_decode_f32 at 16 rows.
+bool int4_decode_rows_pay(int M, int K, int N);
+hipError_t launch_int4_decode_f32_rows(Device* d, hipStream_t st, const float* a,
+                                       Int4Planes w, void* out, int M, int K, int N,
+                                       int* status, Epilogue ep = Epilogue{});
 // Any shape, f32 activations: one thread per output element (small or ragged
 // shapes).
 hipError_t launch_int4_generic_f32(hipStream_t st, const float* a, Int4Planes w,

@@ -149,6 +149,10 @@ int run_int4_product(Device* d, hipStream_t st, const void* a, int32_t dtype,
         const float* af = static_cast<const float*>(a);
         if (int4_decode_f32_supported(M, K, N, w->codes))
             e = launch_int4_decode_f32(d, st, af, p, out, M, K, N, &status, ep);
+        else if (int4_decode_rows_pay(M, K, N) && K % 32 == 0 &&
+                 int4_decode_f32_supported(16, K, N, w->codes) &&
+                 (reinterpret_cast<uintptr_t>(a) & 15) == 0)
+            e = launch_int4_decode_f32_rows(d, st, af, p, out, M, K, N, &status, ep);
         else if (M > 16 && int4_gemm_f32x3_supported(K, N) &&
                  (reinterpret_cast<uintptr_t>(a) & 15) == 0)
             e = launch_int4_gemm_f32x3(d, st, af, p, out, M, K, N, ep, &status);
