@@ -97,9 +97,13 @@ __device__ __forceinline__ void load_words(const uint32_t* p, uint32_t* w) {
 // batches.
 // One workgroup's share: column tile `tile` of the matrix, K slice `slice`;
 // `ticket` is this tile's split-K ticket.
-template <int M, int TILE, int CPL, bool PIPE>
+// An activation as f32: f32 as is, bf16 bits widened exactly.
+__device__ __forceinline__ float x_value(float v) { return v; }
+__device__ __forceinline__ float x_value(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+template <int M, int TILE, int CPL, bool PIPE, typename XT = float>
 __device__ __forceinline__ void decode_tile(
-    const float* __restrict__ a, const uint32_t* __restrict__ codes,
+    const XT* __restrict__ a, const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
     void* __restrict__ out, float* partial, uint32_t* ticket, int K, int N, int tile, int slice,
     int rows_per_slice, int slices, const Epilogue& ep) {
@@ -135,9 +139,9 @@ __device__ __forceinline__ void decode_tile(
 
     uint32_t q[kBatch][WPL];
     uint16_t sb[kBatch], zb[kBatch];
-    float xv[kBatch][M];
+    XT xv[kBatch][M];   // raw: widened where used, so no load waits early
     auto fetch = [&](int kb, uint32_t (&qq)[kBatch][WPL], uint16_t (&ss)[kBatch],
-                     uint16_t (&zz)[kBatch], float (&xx)[kBatch][M]) {
+                     uint16_t (&zz)[kBatch], XT (&xx)[kBatch][M]) {
 #pragma unroll
         for (int i = 0; i < kBatch; i++) {
             const int row = min(kb + rp + i * RP, k_end - 1);
@@ -161,8 +165,9 @@ __device__ __forceinline__ void decode_tile(
             float c[M];
 #pragma unroll
             for (int m = 0; m < M; m++) {
-                const float xs = xv[i][m] * s;
-                const float bterm = (s == 0.0f) ? xv[i][m] * z : -(xs * z);
+                const float x = x_value(xv[i][m]);
+                const float xs = x * s;
+                const float bterm = (s == 0.0f) ? x * z : -(xs * z);
                 c[m] = valid ? xs * kNibbleScale : 0.0f;
                 bsum[m] += valid ? bterm : 0.0f;
             }
@@ -185,7 +190,7 @@ __device__ __forceinline__ void decode_tile(
         for (int kb = k_begin; kb < k_end; kb += kBatch * RP) {
             uint32_t qn[kBatch][WPL];
             uint16_t sn[kBatch], zn[kBatch];
-            float xn[kBatch][M];
+            XT xn[kBatch][M];
             const bool more = kb + kBatch * RP < k_end;
             if (more) fetch(kb + kBatch * RP, qn, sn, zn, xn);
             compute(kb);
@@ -251,15 +256,16 @@ __device__ __forceinline__ void place(int b, int tiles, int slices, int& tile, i
     slice = b / tiles;
 }
 
-template <int M, int TILE, int CPL, bool PIPE>
+// XT: the activations' type, f32 or bf16 bits (one-row bf16 products).
+template <int M, int TILE, int CPL, bool PIPE, typename XT = float>
 __global__ __launch_bounds__(kDecThreads) void int4_decode_f32_kernel(
-    const float* __restrict__ a, const uint32_t* __restrict__ codes,
+    const XT* __restrict__ a, const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
     void* __restrict__ out, float* partial, uint32_t* tickets, int ticket_stride, int K, int N,
     int rows_per_slice, int slices, Epilogue ep) {
     int tile, slice;
     place(blockIdx.x, N / TILE, slices, tile, slice);
-    decode_tile<M, TILE, CPL, PIPE>(a, codes, scales, zeros, out, partial,
+    decode_tile<M, TILE, CPL, PIPE, XT>(a, codes, scales, zeros, out, partial,
                                     tickets + (size_t)tile * ticket_stride, K, N, tile, slice,
                                     rows_per_slice, slices, ep);
 }
@@ -300,8 +306,8 @@ __global__ __launch_bounds__(kDecThreads) void int4_decode_set_kernel(
 // waits for one memory latency; past the slice cap a workgroup loops over
 // several batches instead (pipelined), which bounds the partial sums and the
 // hand-off's reads.
-template <int M, int TILE, int CPL>
-hipError_t launch_decode(Device* d, hipStream_t st, const float* a, Int4Planes w,
+template <int M, int TILE, int CPL, typename XT = float>
+hipError_t launch_decode(Device* d, hipStream_t st, const XT* a, Int4Planes w,
                          void* out, int K, int N, int* status, Epilogue ep,
                          void* fixed_scratch = nullptr) {
     constexpr int LPR = TILE / CPL;
@@ -349,13 +355,13 @@ hipError_t launch_decode(Device* d, hipStream_t st, const float* a, Int4Planes w
         partial = reinterpret_cast<float*>(static_cast<char*>(ws) + kWorkspaceCounterBytes);
     }
     if (per_slice > 1)
-        hipLaunchKernelGGL((int4_decode_f32_kernel<M, TILE, CPL, true>), dim3(tiles * slices),
-                           dim3(kDecThreads), 0, st, a, w.codes, w.scales, w.zeros, out, partial,
-                           tickets, stride, K, N, rows, slices, ep);
+        hipLaunchKernelGGL((int4_decode_f32_kernel<M, TILE, CPL, true, XT>),
+                           dim3(tiles * slices), dim3(kDecThreads), 0, st, a, w.codes, w.scales,
+                           w.zeros, out, partial, tickets, stride, K, N, rows, slices, ep);
     else
-        hipLaunchKernelGGL((int4_decode_f32_kernel<M, TILE, CPL, false>), dim3(tiles * slices),
-                           dim3(kDecThreads), 0, st, a, w.codes, w.scales, w.zeros, out, partial,
-                           tickets, stride, K, N, rows, slices, ep);
+        hipLaunchKernelGGL((int4_decode_f32_kernel<M, TILE, CPL, false, XT>),
+                           dim3(tiles * slices), dim3(kDecThreads), 0, st, a, w.codes, w.scales,
+                           w.zeros, out, partial, tickets, stride, K, N, rows, slices, ep);
     return hipGetLastError();
 }
 
@@ -372,16 +378,17 @@ int matvec_tile(int N) {
 }
 
 // Columns per lane by row count: the accumulators (M * CPL) stay near 64.
-template <int M>
-hipError_t launch_decode_m(Device* d, hipStream_t st, const float* a, Int4Planes w,
+template <int M, typename XT = float>
+hipError_t launch_decode_m(Device* d, hipStream_t st, const XT* a, Int4Planes w,
                            void* out, int K, int N, int* status, Epilogue ep) {
     constexpr int CPL = M <= 2 ? 32 : (M <= 4 ? 16 : 8);
     if constexpr (M == 1) {
         if (matvec_tile(N) == 512)
-            return launch_decode<M, 512, CPL>(d, st, a, w, out, K, N, status, ep);
+            return launch_decode<M, 512, CPL, XT>(d, st, a, w, out, K, N, status, ep);
     }
-    if (N % 256 == 0) return launch_decode<M, 256, CPL>(d, st, a, w, out, K, N, status, ep);
-    return launch_decode<M, 128, CPL>(d, st, a, w, out, K, N, status, ep);
+    if (N % 256 == 0)
+        return launch_decode<M, 256, CPL, XT>(d, st, a, w, out, K, N, status, ep);
+    return launch_decode<M, 128, CPL, XT>(d, st, a, w, out, K, N, status, ep);
 }
 
 // ---- MatVecF32F16: f32 activations against f16 weights --------------------
@@ -1526,6 +1533,24 @@ hipError_t launch_int4_decode_f32(Device* d, hipStream_t st, const float* a, Int
     if (e != hipSuccess || *status != ACCEL_OK) return e;
     char* rest = static_cast<char*>(out) + (size_t)8 * N * (ep.bf16 ? 2 : 4);
     return launch_int4_decode_f32(d, st, a + (size_t)8 * K, w, rest, M - 8, K, N, status, ep);
+}
+
+// One row of bf16 activations: the VALU decode kernel reading bf16 (widened
+// exactly to f32), the f32 arithmetic of a one-row f32 product, and one
+// rounding of each sum (plus bias) to bf16.  The bf16 tiles take a 32-row
+// band for it; measured (us, this / the tiles / a one-row f32 product):
+// K x N = 4096 x 4096 6.24 / 10.6 / 6.11, 4096 x 14336 13.5 / 23.1 / 12.0,
+// 14336 x 4096 14.0 / 19.8 / 12.8.  The activations stay raw bf16 in
+// registers until they are used: widened as they were loaded, they made the
+// compiler wait for each load before issuing the next (7.0, 14.6, 14.8 us).
+hipError_t launch_int4_decode_bf16_row(Device* d, hipStream_t st, const uint16_t* a,
+                                       Int4Planes w, uint16_t* out, int K, int N, int* status,
+                                       const float* bias) {
+    *status = ACCEL_OK;
+    Epilogue ep;
+    ep.bias = bias;
+    ep.bf16 = true;
+    return launch_decode_m<1, uint16_t>(d, st, a, w, out, K, N, status, ep);
 }
 
 // 17..48 f32 rows as 16-row decode launches (the last with the rest): each

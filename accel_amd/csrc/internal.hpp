@@ -116,6 +116,12 @@ hipError_t launch_int4_matvec_noalloc(Device* d, hipStream_t st, const float* a,
 hipError_t launch_int4_decode_f32(Device* d, hipStream_t st, const float* a,
                                   Int4Planes w, void* out, int M, int K, int N,
                                   int* status, Epilogue ep = Epilogue{});
+// One row of bf16 activations (a [1, K] or [K]) -> bf16 out [N] on the VALU
+// decode kernel (f32 arithmetic, one rounding); int4_decode_f32_supported(1,
+// K, N, codes) limits.
+hipError_t launch_int4_decode_bf16_row(Device* d, hipStream_t st, const uint16_t* a,
+                                       Int4Planes w, uint16_t* out, int K, int N, int* status,
+                                       const float* bias);
 // 17..48 rows of f32 activations as consecutive 16-row decode products,
 // where that beats the f32 matrix-core tiles (int4_decode_rows_pay); the same
 // shape limits as launch_int4_decode_f32 at 16 rows.
