@@ -756,16 +756,20 @@ __device__ __forceinline__ void codes_to_b(const uint32_t (&w)[8], bf16x8 (&b)[8
 
 // One workgroup's share: column tile `tile`, K slice `slice`; `ticket` is
 // the tile's pair of hand-off counters.
-template <int G, int NW>
+// XT: the activations' type, f32 or bf16 bits (a bf16 step is one 16-byte
+// chunk a lane, eight values, widened in registers).
+template <int G, int NW, typename XT = float>
 __device__ __forceinline__ void decode_mfma_tile(
-    const float* __restrict__ a, const uint32_t* __restrict__ codes,
+    const XT* __restrict__ a, const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
     void* __restrict__ out, float* partial, uint32_t* ticket, int M, int K, int N, int tile,
     int slice, int rows_per_slice, int slices, const Epilogue& ep, uint32_t* fault,
     int wait_limit) {
     using T = MfTile<G, NW>;
+    constexpr bool kBf16X = sizeof(XT) == 2;
+    constexpr int kXDma = kBf16X ? 1 : 2;                 // activation loads a step
     constexpr int D = T::kDepth;
-    constexpr int V = T::kVmemPerStep;
+    constexpr int V = T::kVmemPerStep - 2 + kXDma;
     __shared__ __attribute__((aligned(16))) uint8_t lds[kMfLdsBytes];
     __shared__ int last_flag;
     __shared__ int waited;
@@ -797,13 +801,18 @@ __device__ __forceinline__ void decode_mfma_tile(
         code_off[i] = (uint32_t)r * (uint32_t)row_bytes + 16u * (uint32_t)ch;
     }
     // activations: instruction j, lane l fills position (64 j + l) % 8 of row
-    // (64 j + l) / 8 of the step's 16 x 32 block (rows >= M repeat row M - 1)
-    const float* x_src[2];
+    // (64 j + l) / 8 of the step's 16 x 32 block (rows >= M repeat row M - 1);
+    // bf16: one instruction, lane l fills chunk l % 4 (eight values) of row l / 4
+    const XT* x_src[2];
+    if constexpr (kBf16X) {
+        x_src[0] = x_src[1] = a + (size_t)min(lane >> 2, M - 1) * K + 8 * (lane & 3);
+    } else {
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-        const int s = 64 * j + lane;
-        const int m = s >> 3;
-        x_src[j] = a + (size_t)min(m, M - 1) * K + 4 * mf_x_pos(m, s & 7);
+        for (int j = 0; j < 2; j++) {
+            const int s = 64 * j + lane;
+            const int m = s >> 3;
+            x_src[j] = a + (size_t)min(m, M - 1) * K + 4 * mf_x_pos(m, s & 7);
+        }
     }
     // scales (lanes 0..31) or zeros (32..63) of row lane % 32: G f16 values,
     // landing in dword `lane` of the step's raw block
@@ -816,7 +825,7 @@ __device__ __forceinline__ void decode_mfma_tile(
 #pragma unroll
         for (int c = 0; c < T::kCodeDma; c++) lds_load16(src + code_off[c], buf + 1024 * c);
 #pragma unroll
-        for (int j = 0; j < 2; j++) lds_load16(x_src[j] + row0, buf + T::kXOff + 1024 * j);
+        for (int j = 0; j < kXDma; j++) lds_load16(x_src[j] + row0, buf + T::kXOff + 1024 * j);
         if constexpr (G == 1)
             lds_load2(raw_src + (size_t)row0 * gpr, buf + T::kRawOff);
         else
@@ -843,9 +852,12 @@ __device__ __forceinline__ void decode_mfma_tile(
             cbase[2 * g + 1] = goff + 128 * (1 - bb);
         }
     }
-    // activations: row c16, columns 8 kg .. 8 kg + 7
-    const uint32_t xoff0 = T::kXOff + 128 * c16 + 16 * mf_x_pos(c16, 2 * kg);
-    const uint32_t xoff1 = T::kXOff + 128 * c16 + 16 * mf_x_pos(c16, 2 * kg + 1);
+    // activations: row c16, columns 8 kg .. 8 kg + 7 (bf16: one chunk, read
+    // twice so that the read sequence stays that of f32)
+    const uint32_t xoff0 = kBf16X ? T::kXOff + 64 * c16 + 16 * kg
+                                  : T::kXOff + 128 * c16 + 16 * mf_x_pos(c16, 2 * kg);
+    const uint32_t xoff1 = kBf16X ? xoff0
+                                  : T::kXOff + 128 * c16 + 16 * mf_x_pos(c16, 2 * kg + 1);
     // fold: rows 8 kg .. 8 kg + 7, all groups; the lane folding (row, group)
     // pair `fold_p` (G == 1: lanes 16 r + e, e < 8, fold row 8 r + e)
     const uint32_t foff = T::kFoldOff + 64 * G * kg;
@@ -938,7 +950,18 @@ __device__ __forceinline__ void decode_mfma_tile(
                   "v"(sb + cbase[1]), "v"(sb + cbase[2]), "v"(sb + cbase[3])
                 : "memory");
         }
-        const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        float xv[8];
+        if constexpr (kBf16X) {
+            const u32x4 r = __builtin_bit_cast(u32x4, x0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                xv[2 * i] = __uint_as_float(r[i] << 16);
+                xv[2 * i + 1] = __uint_as_float(r[i] & 0xffff0000u);
+            }
+        } else {
+            xv[0] = x0.x; xv[1] = x0.y; xv[2] = x0.z; xv[3] = x0.w;
+            xv[4] = x1.x; xv[5] = x1.y; xv[6] = x1.z; xv[7] = x1.w;
+        }
         f32x2 fe[G][8];
 #pragma unroll
         for (int q = 0; q < 4 * G; q++) {
@@ -1185,9 +1208,9 @@ __device__ __forceinline__ void decode_mfma_tile(
     }
 }
 
-template <int G, int NW>
+template <int G, int NW, typename XT = float>
 __global__ __launch_bounds__(64 * NW) void int4_decode_mfma_kernel(
-    const float* __restrict__ a, const uint32_t* __restrict__ codes,
+    const XT* __restrict__ a, const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
     void* __restrict__ out, float* partial, uint32_t* tickets, int ticket_stride, int M, int K,
     int N, int rows_per_slice, int slices, Epilogue ep, uint32_t* fault, int wait_limit) {
@@ -1198,9 +1221,9 @@ __global__ __launch_bounds__(64 * NW) void int4_decode_mfma_kernel(
     if ((grid & 7) == 0) b = (b & 7) * (grid >> 3) + (b >> 3);
     const int tile = b % tiles;
     const int slice = b / tiles;
-    decode_mfma_tile<G, NW>(a, codes, scales, zeros, out, partial,
-                            tickets + (size_t)tile * ticket_stride, M, K, N, tile, slice,
-                            rows_per_slice, slices, ep, fault, wait_limit);
+    decode_mfma_tile<G, NW, XT>(a, codes, scales, zeros, out, partial,
+                                tickets + (size_t)tile * ticket_stride, M, K, N, tile, slice,
+                                rows_per_slice, slices, ep, fault, wait_limit);
 }
 
 // Several matrices against one activation block in one launch, each with the
@@ -1277,8 +1300,8 @@ MfPlan plan_decode_mfma(const Device* d, int M, int K, int N, bool planes_4b) {
     return best;
 }
 
-template <int G, int NW>
-hipError_t launch_mfma(Device* d, hipStream_t st, const float* a, Int4Planes w, void* out,
+template <int G, int NW, typename XT = float>
+hipError_t launch_mfma(Device* d, hipStream_t st, const XT* a, Int4Planes w, void* out,
                        int M, int K, int N, const MfPlan& p, int* status, Epilogue ep) {
     const int tiles = N / (128 * G);
     float* partial = nullptr;
@@ -1296,9 +1319,10 @@ hipError_t launch_mfma(Device* d, hipStream_t st, const float* a, Int4Planes w, 
         tickets = static_cast<uint32_t*>(ws);
         partial = reinterpret_cast<float*>(static_cast<char*>(ws) + kWorkspaceCounterBytes);
     }
-    hipLaunchKernelGGL((int4_decode_mfma_kernel<G, NW>), dim3(tiles * p.slices), dim3(64 * NW),
-                       0, st, a, w.codes, w.scales, w.zeros, out, partial, tickets, stride, M, K,
-                       N, p.rows, p.slices, ep, d->fault_dev, d->wait_limit);
+    hipLaunchKernelGGL((int4_decode_mfma_kernel<G, NW, XT>), dim3(tiles * p.slices),
+                       dim3(64 * NW), 0, st, a, w.codes, w.scales, w.zeros, out, partial,
+                       tickets, stride, M, K, N, p.rows, p.slices, ep, d->fault_dev,
+                       d->wait_limit);
     return hipGetLastError();
 }
 
@@ -1353,13 +1377,14 @@ hipError_t launch_mfma_set(Device* d, hipStream_t st, const float* a, const Int4
     return hipGetLastError();
 }
 
-hipError_t launch_decode_mfma(Device* d, hipStream_t st, const float* a, Int4Planes w,
+template <typename XT = float>
+hipError_t launch_decode_mfma(Device* d, hipStream_t st, const XT* a, Int4Planes w,
                               void* out, int M, int K, int N, int* status, Epilogue ep) {
     const bool planes_4b = ((reinterpret_cast<uintptr_t>(w.scales) |
                              reinterpret_cast<uintptr_t>(w.zeros)) & 3) == 0;
     const MfPlan p = plan_decode_mfma(d, M, K, N, planes_4b);
-    if (p.groups == 2) return launch_mfma<2, 8>(d, st, a, w, out, M, K, N, p, status, ep);
-    return launch_mfma<1, 8>(d, st, a, w, out, M, K, N, p, status, ep);
+    if (p.groups == 2) return launch_mfma<2, 8, XT>(d, st, a, w, out, M, K, N, p, status, ep);
+    return launch_mfma<1, 8, XT>(d, st, a, w, out, M, K, N, p, status, ep);
 }
 
 template <int TILE>
@@ -1551,6 +1576,24 @@ hipError_t launch_int4_decode_bf16_row(Device* d, hipStream_t st, const uint16_t
     ep.bias = bias;
     ep.bf16 = true;
     return launch_decode_m<1, uint16_t>(d, st, a, w, out, K, N, status, ep);
+}
+
+// 2..16 rows of bf16 activations on the matrix-core decode kernel (bf16
+// staged, widened in registers, the f32 product's arithmetic), one rounding
+// to bf16: where the bf16 tiles would run a mostly empty 32-row band.
+bool int4_decode_bf16_rows_supported(int M, int K, int N, const void* a, const void* codes) {
+    return M >= 2 && M <= 16 && K % 32 == 0 && int4_decode_f32_supported(M, K, N, codes) &&
+           N < (1 << 27) && (reinterpret_cast<uintptr_t>(a) & 15) == 0;
+}
+
+hipError_t launch_int4_decode_bf16_rows(Device* d, hipStream_t st, const uint16_t* a,
+                                        Int4Planes w, uint16_t* out, int M, int K, int N,
+                                        int* status, const float* bias) {
+    *status = ACCEL_OK;
+    Epilogue ep;
+    ep.bias = bias;
+    ep.bf16 = true;
+    return launch_decode_mfma<uint16_t>(d, st, a, w, out, M, K, N, status, ep);
 }
 
 // 17..48 f32 rows as 16-row decode launches (the last with the rest): each

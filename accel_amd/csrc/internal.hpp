@@ -122,6 +122,12 @@ hipError_t launch_int4_decode_f32(Device* d, hipStream_t st, const float* a,
 hipError_t launch_int4_decode_bf16_row(Device* d, hipStream_t st, const uint16_t* a,
                                        Int4Planes w, uint16_t* out, int K, int N, int* status,
                                        const float* bias);
+// 2..16 rows of bf16 activations (16-byte aligned, K % 32 == 0) -> bf16 out
+// [M, N] on the matrix-core decode kernel (f32 arithmetic, one rounding).
+bool int4_decode_bf16_rows_supported(int M, int K, int N, const void* a, const void* codes);
+hipError_t launch_int4_decode_bf16_rows(Device* d, hipStream_t st, const uint16_t* a,
+                                        Int4Planes w, uint16_t* out, int M, int K, int N,
+                                        int* status, const float* bias);
 // 17..48 rows of f32 activations as consecutive 16-row decode products,
 // where that beats the f32 matrix-core tiles (int4_decode_rows_pay); the same
 // shape limits as launch_int4_decode_f32 at 16 rows.

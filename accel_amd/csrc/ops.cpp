@@ -165,6 +165,8 @@ int run_int4_product(Device* d, hipStream_t st, const void* a, int32_t dtype,
         uint16_t* ob = static_cast<uint16_t*>(out);
         if (M == 1 && int4_decode_f32_supported(1, K, N, w->codes))
             e = launch_int4_decode_bf16_row(d, st, ab, p, ob, K, N, &status, ep.bias);
+        else if (int4_decode_bf16_rows_supported(M, K, N, a, w->codes))
+            e = launch_int4_decode_bf16_rows(d, st, ab, p, ob, M, K, N, &status, ep.bias);
         else if (int4_gemm_bf16_supported(M, K, N) && (reinterpret_cast<uintptr_t>(a) & 15) == 0)
             e = launch_int4_gemm_bf16(d, st, ab, p, ob, M, K, N, ep.bias, &status);
         else

@@ -187,6 +187,11 @@ def test_decode_is_deterministic(dev):
 # ---- bf16 prefill -------------------------------------------------------------
 
 SHAPES_BF16 = [(1, 64, 128), (64, 256, 256), (100, 512, 384), (128, 128, 128),
+               # decode sizes: one row on the VALU decode kernel, 2..16 rows on
+               # the matrix-core decode kernel (bf16 staged), one- and two-group
+               # tiles, and K % 32 != 0 (the tiles)
+               (1, 4096, 14336), (2, 4096, 14336), (8, 1024, 640), (16, 2048, 4096),
+               (5, 96, 256),
                (257, 1024, 640), (512, 2048, 1024),
                # the 256-row tiles with one stage, an odd stage count and a
                # ragged last row band
