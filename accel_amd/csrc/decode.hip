@@ -1674,11 +1674,12 @@ __device__ __forceinline__ bool grouped_offsets_sorted(const uint32_t* off, int 
     return ok;
 }
 
-template <int TILE, int CPL, bool PIPE>
+// XT: f32 or bf16 bits; the result is written in the same type.
+template <int TILE, int CPL, bool PIPE, typename XT = float>
 __global__ __launch_bounds__(kDecThreads) void int4_grouped_decode_kernel(
-    const float* __restrict__ x, const uint32_t* __restrict__ codes,
+    const XT* __restrict__ x, const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
-    const uint32_t* __restrict__ off, float* __restrict__ out, float* partial,
+    const uint32_t* __restrict__ off, void* __restrict__ out, float* partial,
     uint32_t* tickets, int ticket_stride, int E, int T, int K, int N, int rows_per_slice,
     int slices, bool write_padding, bool mfma_blocks) {
     const int tiles = N / TILE;
@@ -1692,8 +1693,13 @@ __global__ __launch_bounds__(kDecThreads) void int4_grouped_decode_kernel(
     if (e >= E) {
         // past every segment: the matvec form writes zeros, once per column tile
         if (write_padding && slice == 0)
-            for (int c = threadIdx.x; c < TILE; c += kDecThreads)
-                out[(size_t)t * N + tile * TILE + c] = 0.0f;
+            for (int c = threadIdx.x; c < TILE; c += kDecThreads) {
+                const size_t o = (size_t)t * N + tile * TILE + c;
+                if constexpr (sizeof(XT) == 2)
+                    static_cast<uint16_t*>(out)[o] = 0;
+                else
+                    static_cast<float*>(out)[o] = 0.0f;
+            }
         return;
     }
     // An expert's rows go two at a time (its weights read once for both): the
@@ -1716,14 +1722,16 @@ __global__ __launch_bounds__(kDecThreads) void int4_grouped_decode_kernel(
     const uint16_t* s = scales + (size_t)e * (per >> 7);
     const uint16_t* z = zeros + (size_t)e * (per >> 7);
     float* p = partial ? partial + (size_t)t * slices * N : nullptr;
+    void* o = static_cast<char*>(out) + (size_t)t * N * sizeof(XT);
+    Epilogue ep;
+    ep.bf16 = sizeof(XT) == 2;
     uint32_t* tk = tickets + ((size_t)t * tiles + tile) * ticket_stride;
     if (pair)
-        decode_tile<2, TILE, CPL / 2, PIPE>(x + (size_t)t * K, c, s, z, out + (size_t)t * N, p,
-                                            tk, K, N, tile, slice, rows_per_slice, slices,
-                                            Epilogue{});
+        decode_tile<2, TILE, CPL / 2, PIPE, XT>(x + (size_t)t * K, c, s, z, o, p, tk, K, N, tile,
+                                                slice, rows_per_slice, slices, ep);
     else
-        decode_tile<1, TILE, CPL, PIPE>(x + (size_t)t * K, c, s, z, out + (size_t)t * N, p, tk,
-                                        K, N, tile, slice, rows_per_slice, slices, Epilogue{});
+        decode_tile<1, TILE, CPL, PIPE, XT>(x + (size_t)t * K, c, s, z, o, p, tk, K, N, tile,
+                                            slice, rows_per_slice, slices, ep);
 }
 
 // The matrix-core blocks of a grouped decode product: workgroup b takes
@@ -1737,11 +1745,11 @@ __global__ __launch_bounds__(kDecThreads) void int4_grouped_decode_kernel(
 // blocks never share them; block u's tickets are the tile pairs past the
 // earlier blocks'.  (A persistent form, each workgroup looping over the
 // blocks, spilled registers and ran 3% slower.)
-template <int G, int NW>
+template <int G, int NW, typename XT = float>
 __global__ __launch_bounds__(64 * NW) void int4_grouped_decode_mfma_kernel(
-    const float* __restrict__ x, const uint32_t* __restrict__ codes,
+    const XT* __restrict__ x, const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
-    const uint32_t* __restrict__ off, float* __restrict__ out, float* partial,
+    const uint32_t* __restrict__ off, void* __restrict__ out, float* partial,
     uint32_t* tickets, int ticket_stride, int E, int T, int K, int N, int rows_per_slice,
     int slices, uint32_t* fault, int wait_limit) {
     using Tl = MfTile<G, NW>;
@@ -1800,13 +1808,15 @@ __global__ __launch_bounds__(64 * NW) void int4_grouped_decode_mfma_kernel(
     if (e < 0) return;
     const int row0 = blk_row0;
     const size_t per = (size_t)K * N;
-    decode_mfma_tile<G, NW>(x + (size_t)row0 * K, codes + (size_t)e * (per >> 3),
+    Epilogue ep;
+    ep.bf16 = sizeof(XT) == 2;
+    decode_mfma_tile<G, NW, XT>(x + (size_t)row0 * K, codes + (size_t)e * (per >> 3),
                             scales + (size_t)e * (per >> 7), zeros + (size_t)e * (per >> 7),
-                            out + (size_t)row0 * N,
+                            static_cast<char*>(out) + (size_t)row0 * N * sizeof(XT),
                             partial ? partial + (size_t)slices * row0 * N : nullptr,
                             tickets ? tickets + ((size_t)u * tiles + tile) * ticket_stride
                                     : nullptr,
-                            blk_rows, K, N, tile, slice, rows_per_slice, slices, Epilogue{},
+                            blk_rows, K, N, tile, slice, rows_per_slice, slices, ep,
                             fault, wait_limit);
 }
 
@@ -1855,7 +1865,7 @@ struct GroupedMfma {
     int blocks = 0;    // blocks the grid and the tickets are sized for
     int stride = 0;    // ticket spacing (two counters a tile)
 };
-GroupedMfma grouped_mfma(const Device* d, const float* x, Int4Planes w, int E, int T, int K,
+GroupedMfma grouped_mfma(const Device* d, const void* x, Int4Planes w, int E, int T, int K,
                          int N) {
     GroupedMfma g;
     g.blocks = std::min(T / kMfBlockMin, T / kMfBlockRows + E);
@@ -1877,9 +1887,9 @@ GroupedMfma grouped_mfma(const Device* d, const float* x, Int4Planes w, int E, i
     return g;
 }
 
-template <int TILE>
-hipError_t launch_grouped_decode_tile(Device* d, hipStream_t st, const float* x, Int4Planes w,
-                                      const uint32_t* off, float* out, int E, int T, int K,
+template <int TILE, typename XT>
+hipError_t launch_grouped_decode_tile(Device* d, hipStream_t st, const XT* x, Int4Planes w,
+                                      const uint32_t* off, void* out, int E, int T, int K,
                                       int N, bool write_padding, int* status,
                                       uint32_t* tickets, float* area, bool mfma_blocks) {
     constexpr int CPL = GroupedDecodeShape<TILE>::CPL;
@@ -1903,26 +1913,26 @@ hipError_t launch_grouped_decode_tile(Device* d, hipStream_t st, const float* x,
     float* partial = slices > 1 ? area : nullptr;
     const dim3 grid((unsigned)(pairs * slices));
     if (per_slice > 1)
-        hipLaunchKernelGGL((int4_grouped_decode_kernel<TILE, CPL, true>), grid,
+        hipLaunchKernelGGL((int4_grouped_decode_kernel<TILE, CPL, true, XT>), grid,
                            dim3(kDecThreads), 0, st, x, w.codes, w.scales, w.zeros, off, out,
                            partial, tickets, stride, E, T, K, N, rows, slices, write_padding,
                            mfma_blocks);
     else
-        hipLaunchKernelGGL((int4_grouped_decode_kernel<TILE, CPL, false>), grid,
+        hipLaunchKernelGGL((int4_grouped_decode_kernel<TILE, CPL, false, XT>), grid,
                            dim3(kDecThreads), 0, st, x, w.codes, w.scales, w.zeros, off, out,
                            partial, tickets, stride, E, T, K, N, rows, slices, write_padding,
                            mfma_blocks);
     return hipGetLastError();
 }
 
-template <int G>
-hipError_t launch_grouped_mfma(Device* d, hipStream_t st, const float* x, Int4Planes w,
-                               const uint32_t* off, float* out, int E, int T, int K, int N,
+template <int G, typename XT>
+hipError_t launch_grouped_mfma(Device* d, hipStream_t st, const XT* x, Int4Planes w,
+                               const uint32_t* off, void* out, int E, int T, int K, int N,
                                const GroupedMfma& g, uint32_t* tickets, float* area) {
     const int tiles = N / (128 * G);
     const bool split = g.plan.slices > 1;
     const dim3 grid((unsigned)(g.blocks * tiles * g.plan.slices));
-    hipLaunchKernelGGL((int4_grouped_decode_mfma_kernel<G, 8>), grid, dim3(64 * 8), 0, st, x,
+    hipLaunchKernelGGL((int4_grouped_decode_mfma_kernel<G, 8, XT>), grid, dim3(64 * 8), 0, st, x,
                        w.codes, w.scales, w.zeros, off, out, split ? area : nullptr,
                        split ? tickets : nullptr, g.stride, E, T, K, N, g.plan.rows,
                        g.plan.slices, d->fault_dev, d->wait_limit);
@@ -1947,7 +1957,7 @@ static int grouped_decode_tile(const Device* d, int T, int N) {
     return N % 256 == 0 ? 256 : 128;
 }
 
-size_t int4_grouped_decode_area(const Device* d, const float* x, Int4Planes w, int E, int T,
+size_t int4_grouped_decode_area(const Device* d, const void* x, Int4Planes w, int E, int T,
                                 int K, int N) {
     const GroupedMfma g = grouped_mfma(d, x, w, E, T, K, N);
     const int tw = g.on && N % 512 == 0 ? 512 : grouped_decode_tile(d, T, N);
@@ -1964,8 +1974,9 @@ size_t int4_grouped_decode_area(const Device* d, const float* x, Int4Planes w, i
     return bytes;
 }
 
-hipError_t launch_int4_grouped_decode(Device* d, hipStream_t st, const float* x, Int4Planes w,
-                                      const uint32_t* off, float* out, int E, int T, int K,
+template <typename XT>
+hipError_t launch_grouped_decode_t(Device* d, hipStream_t st, const XT* x, Int4Planes w,
+                                  const uint32_t* off, void* out, int E, int T, int K,
                                       int N, bool write_padding, int* status,
                                       uint32_t* tickets, float* area) {
     *status = ACCEL_OK;
@@ -1974,18 +1985,29 @@ hipError_t launch_int4_grouped_decode(Device* d, hipStream_t st, const float* x,
     const int tw = g.on && N % 512 == 0 ? 512 : grouped_decode_tile(d, T, N);
     hipError_t e;
     if (tw == 512)
-        e = launch_grouped_decode_tile<512>(d, st, x, w, off, out, E, T, K, N, write_padding,
+        e = launch_grouped_decode_tile<512, XT>(d, st, x, w, off, out, E, T, K, N, write_padding,
                                             status, tickets, area, g.on);
     else if (tw == 256)
-        e = launch_grouped_decode_tile<256>(d, st, x, w, off, out, E, T, K, N, write_padding,
+        e = launch_grouped_decode_tile<256, XT>(d, st, x, w, off, out, E, T, K, N, write_padding,
                                             status, tickets, area, g.on);
     else
-        e = launch_grouped_decode_tile<128>(d, st, x, w, off, out, E, T, K, N, write_padding,
+        e = launch_grouped_decode_tile<128, XT>(d, st, x, w, off, out, E, T, K, N, write_padding,
                                             status, tickets, area, g.on);
     if (e != hipSuccess || *status != ACCEL_OK || !g.on) return e;
     if (g.plan.groups == 2)
-        return launch_grouped_mfma<2>(d, st, x, w, off, out, E, T, K, N, g, tickets, area);
-    return launch_grouped_mfma<1>(d, st, x, w, off, out, E, T, K, N, g, tickets, area);
+        return launch_grouped_mfma<2, XT>(d, st, x, w, off, out, E, T, K, N, g, tickets, area);
+    return launch_grouped_mfma<1, XT>(d, st, x, w, off, out, E, T, K, N, g, tickets, area);
+}
+
+hipError_t launch_int4_grouped_decode(Device* d, hipStream_t st, const void* x, bool bf16,
+                                      Int4Planes w, const uint32_t* off, void* out, int E, int T,
+                                      int K, int N, bool write_padding, int* status,
+                                      uint32_t* tickets, float* area) {
+    if (bf16)
+        return launch_grouped_decode_t(d, st, static_cast<const uint16_t*>(x), w, off, out, E, T,
+                                       K, N, write_padding, status, tickets, area);
+    return launch_grouped_decode_t(d, st, static_cast<const float*>(x), w, off, out, E, T, K, N,
+                                   write_padding, status, tickets, area);
 }
 
 namespace {

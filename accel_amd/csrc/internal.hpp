@@ -192,7 +192,8 @@ bool int4_g32_matvec_supported(int K, int N);
 hipError_t launch_int4_g32_matvec(Device* d, hipStream_t st, const float* a,
                                   const uint32_t* codes, const float* scales, float* out, int K,
                                   int N, int* status);
-// Ragged int4 GEMV (decode MoE): f32 x [T, K], T <= kGroupedDecodeRows, each
+// Ragged int4 GEMV (decode MoE): f32 or bf16 x [T, K] (out in the same type),
+// T <= kGroupedDecodeRows, each
 // row against its expert's [K, N] matrix with the decode kernels (an
 // expert's rows in blocks of up to 16 on the matrix cores, in a second launch); the
 // matvec form (write_padding) writes 0 to rows past every segment.
@@ -202,11 +203,11 @@ constexpr int kGroupedDecodeRows = 64;
 // int4_grouped_decode_area gives for the same x, w and shape (the workspace is
 // sized once, before the offsets are computed, so it cannot grow and move them).
 bool int4_grouped_decode_supported(int T, int K, int N, const void* codes);
-size_t int4_grouped_decode_area(const Device* d, const float* x, Int4Planes w, int E, int T,
+size_t int4_grouped_decode_area(const Device* d, const void* x, Int4Planes w, int E, int T,
                                 int K, int N);
-hipError_t launch_int4_grouped_decode(Device* d, hipStream_t st, const float* x, Int4Planes w,
-                                      const uint32_t* off, float* out, int E, int T, int K,
-                                      int N, bool write_padding, int* status,
+hipError_t launch_int4_grouped_decode(Device* d, hipStream_t st, const void* x, bool bf16,
+                                      Int4Planes w, const uint32_t* off, void* out, int E, int T,
+                                      int K, int N, bool write_padding, int* status,
                                       uint32_t* tickets, float* area);
 hipError_t launch_int4_grouped_bf16(Device* d, hipStream_t st, const uint16_t* x,
                                     Int4Planes w, const uint32_t* off, uint16_t* out,

@@ -701,15 +701,16 @@ int run_grouped_int4(const char* op, int dev, void* stream, const accel_tensor_t
     hipStream_t st = (hipStream_t)stream;
     // the path, and the workspace it needs past the offsets
     const bool f32 = x->dtype == ACCEL_F32;
-    const bool decode = f32 && int4_grouped_decode_supported((int)T, (int)K, (int)N, w->codes) &&
-                        (uint64_t)experts * (uint64_t)K * (uint64_t)N < (1ull << 40);
     if (!f32 && !(int4_gemm_bf16_supported(1, (int)K, (int)N) &&
                   (reinterpret_cast<uintptr_t>(x->data) & 15) == 0))
         return refuse(op, "bf16 grouped products need K % 64 == 0, N % 128 == 0, K < 2^22 and "
                           "N < 2^26");
+    // few routed rows (f32 or bf16): the decode kernels
+    const bool decode = int4_grouped_decode_supported((int)T, (int)K, (int)N, w->codes) &&
+                        (uint64_t)experts * (uint64_t)K * (uint64_t)N < (1ull << 40);
     const size_t area_bytes =
-        decode ? int4_grouped_decode_area(d, static_cast<const float*>(x->data), planes(w),
-                                          (int)experts, (int)T, (int)K, (int)N)
+        decode ? int4_grouped_decode_area(d, x->data, planes(w), (int)experts, (int)T, (int)K,
+                                          (int)N)
                : 0;
     void* area = nullptr;
     uint32_t* off = offsets_in_workspace(d, st, static_cast<const uint32_t*>(counts->data),
@@ -719,18 +720,15 @@ int run_grouped_int4(const char* op, int dev, void* stream, const accel_tensor_t
                                                     kWorkspaceCounterBytes);
     const Int4Planes p = planes(w);
     hipError_t e;
-    if (f32) {
-        if (decode) {
-            e = launch_int4_grouped_decode(d, st, static_cast<const float*>(x->data), p, off,
-                                           static_cast<float*>(out->data), (int)experts,
-                                           (int)T, (int)K, (int)N, matvec, &status, tickets,
-                                           static_cast<float*>(area));
-            if (e == hipSuccess && status != ACCEL_OK) return status;
-        } else {
-            e = launch_int4_grouped_f32(st, static_cast<const float*>(x->data), p, off,
-                                        static_cast<float*>(out->data), (int)experts, (int)T,
-                                        (int)K, (int)N, matvec);
-        }
+    if (decode) {
+        e = launch_int4_grouped_decode(d, st, x->data, !f32, p, off, out->data, (int)experts,
+                                       (int)T, (int)K, (int)N, matvec, &status, tickets,
+                                       static_cast<float*>(area));
+        if (e == hipSuccess && status != ACCEL_OK) return status;
+    } else if (f32) {
+        e = launch_int4_grouped_f32(st, static_cast<const float*>(x->data), p, off,
+                                    static_cast<float*>(out->data), (int)experts, (int)T,
+                                    (int)K, (int)N, matvec);
     } else {
         e = launch_int4_grouped_bf16(d, st, static_cast<const uint16_t*>(x->data), p, off,
                                      static_cast<uint16_t*>(out->data), (int)experts, (int)T,
