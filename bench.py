@@ -51,18 +51,18 @@ BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, vendor figure
 METRIC = ("int4 linear: HBM GB/s (% peak) at M=1; TFLOP/s (% MFMA peak) at M=2048")
 ROTATE_BYTES = 544 << 20       # weight copies in rotation, > 2x the Infinity Cache
 TRAFFIC_FILE = os.path.join(HERE, "profiles", "traffic.json")
-GEMV_KERNEL = "int4_decode_f32_kernel<1, 256, 32, false>"
+GEMV_KERNEL = "int4_decode_f32_kernel<1, 256, 32, false, float>"
 GEMM_KERNEL = "int4_gemm_bf16_kernel<8, false>"
 GEMM_F32_KERNEL = "int4_gemm_f32x3_kernel"
-DECODE_MFMA_KERNEL = "int4_decode_mfma_kernel<2, 8>"
+DECODE_MFMA_KERNEL = "int4_decode_mfma_kernel<2, 8, float>"
 SPLITK_BF16_KERNEL = "int4_gemm_bf16_splitk_kernel<2>"
 SPLITK_F32_KERNEL = "int4_gemm_f32x3_kernel (split K, M=64)"
 GROUPED_KERNEL = "int4_grouped_bf16_kernel"
 G32_KERNEL = "int4_g32_matvec_kernel"
 # the decode MoE is two launches: the padding rows, then each expert's rows in
 # blocks of up to 16 on the matrix cores
-GROUPED_DECODE_KERNELS = ("int4_grouped_decode_kernel<512, 32, true>",
-                          "int4_grouped_decode_mfma_kernel<2, 8>")
+GROUPED_DECODE_KERNELS = ("int4_grouped_decode_kernel<512, 32, true, float>",
+                          "int4_grouped_decode_mfma_kernel<2, 8, float>")
 FLUSH_BYTES = 512 << 20        # device copy that evicts the Infinity Cache
 PUBLISHED_US = 760.0           # Int4MatVec [2048] x [2048,2048] on an M2, one plan a step
 PUBLISHED_SRC = "specs/010-kernel-corpus.md:593-602 (tensor/decodebench_darwin_test.go:148-189)"
