@@ -1901,8 +1901,9 @@ hipError_t launch_grouped_decode_tile(Device* d, hipStream_t st, const XT* x, In
                        T, tiles);
         return hipSuccess;
     }
-    const int stride = ticket_stride((int)pairs);
-    if (stride == 0) {
+    // tickets only where K is split (rows x tiles then under twice the CUs)
+    const int stride = slices > 1 ? ticket_stride((int)pairs) : 0;
+    if (slices > 1 && stride == 0) {
         *status = fail(ACCEL_E_INVALID,
                        "grouped decode product: %d rows x %d tiles need more tickets than the "
                        "workspace holds",
@@ -1941,8 +1942,9 @@ hipError_t launch_grouped_mfma(Device* d, hipStream_t st, const XT* x, Int4Plane
 
 }  // namespace
 
-bool int4_grouped_decode_supported(int T, int K, int N, const void* codes) {
-    return T >= 1 && T <= kGroupedDecodeRows && K >= 1 && N >= 128 && N % 128 == 0 &&
+bool int4_grouped_decode_supported(int T, int K, int N, const void* codes, bool bf16) {
+    return T >= 1 && T <= (bf16 ? kGroupedDecodeRows : kGroupedDecodeRowsF32) && K >= 1 &&
+           N >= 128 && N % 128 == 0 &&
            (reinterpret_cast<uintptr_t>(codes) & 15) == 0 && K < (1 << 30) && N < (1 << 30);
 }
 

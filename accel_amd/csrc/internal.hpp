@@ -198,11 +198,17 @@ hipError_t launch_int4_g32_matvec(Device* d, hipStream_t st, const float* a,
 // expert's rows in blocks of up to 16 on the matrix cores, in a second launch); the
 // matvec form (write_padding) writes 0 to rows past every segment.
 constexpr int kGroupedDecodeRows = 64;
+// f32 rows take the decode kernels up to this many: past it (and past 64 bf16
+// rows, which have the grouped tiles) they run one lane per element.  Measured
+// (us, decode kernels / one lane per element), 8 experts of 4096 x 14336, top-2
+// routing: 128 rows 173 / 6543, 256 rows 288 / 11139, 512 rows 484 / 20581.
+// The split-K sums of 1024 rows at N = 14336 take 235 MB of workspace.
+constexpr int kGroupedDecodeRowsF32 = 1024;
 // The grouped decode launches take the workspace's counters (`tickets`) and an
 // area past the offsets for their split-K sums, of the size
 // int4_grouped_decode_area gives for the same x, w and shape (the workspace is
 // sized once, before the offsets are computed, so it cannot grow and move them).
-bool int4_grouped_decode_supported(int T, int K, int N, const void* codes);
+bool int4_grouped_decode_supported(int T, int K, int N, const void* codes, bool bf16);
 size_t int4_grouped_decode_area(const Device* d, const void* x, Int4Planes w, int E, int T,
                                 int K, int N);
 hipError_t launch_int4_grouped_decode(Device* d, hipStream_t st, const void* x, bool bf16,

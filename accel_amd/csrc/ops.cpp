@@ -706,7 +706,7 @@ int run_grouped_int4(const char* op, int dev, void* stream, const accel_tensor_t
         return refuse(op, "bf16 grouped products need K % 64 == 0, N % 128 == 0, K < 2^22 and "
                           "N < 2^26");
     // few routed rows (f32 or bf16): the decode kernels
-    const bool decode = int4_grouped_decode_supported((int)T, (int)K, (int)N, w->codes) &&
+    const bool decode = int4_grouped_decode_supported((int)T, (int)K, (int)N, w->codes, !f32) &&
                         (uint64_t)experts * (uint64_t)K * (uint64_t)N < (1ull << 40);
     const size_t area_bytes =
         decode ? int4_grouped_decode_area(d, x->data, planes(w), (int)experts, (int)T, (int)K,

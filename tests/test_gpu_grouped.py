@@ -172,7 +172,11 @@ def run_int4_grouped(dev, form, x, p, s, z, counts, E, T, K, N, bf16):
                                               (2, 2048, 384, [16, 35], 2),
                                               (2, 4096, 2048, [5, 3], 0),
                                               # T < 2E: every row on the VALU kernel
-                                              (8, 256, 256, [3, 0, 0, 0, 0, 0, 0, 1], 1)])
+                                              (8, 256, 256, [3, 0, 0, 0, 0, 0, 0, 1], 1),
+                                              # f32 past 64 rows: the decode kernels up
+                                              # to 1024 rows, one lane per element past
+                                              (4, 512, 1024, [300, 0, 41, 260], 2),
+                                              (2, 64, 128, [600, 500], 0)])
 def test_int4_grouped_matches_the_oracle(dev, bf16, form, E, K, N, counts, pad):
     x, p, s, z, off, T = int4_case(E, K, N, counts, pad, seed=E + K, bf16=bf16)
     got = run_int4_grouped(dev, form, x, p, s, z, counts, E, T, K, N, bf16)
