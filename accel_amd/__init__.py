@@ -84,6 +84,31 @@ class Int4G32Desc(ctypes.Structure):
                 ("K", ctypes.c_int64), ("N", ctypes.c_int64)]
 
 
+class SelectionDesc(ctypes.Structure):
+    """accel_selection_t: KernelSelection{Op, Kernel, Reason, Rejected}."""
+    _fields_ = [("op", ctypes.c_char * 32), ("kernel", ctypes.c_char * 320),
+                ("reason", ctypes.c_char * 320), ("rejected", ctypes.c_char * 1024)]
+
+
+class Selection:
+    """Which kernels an int4 product became, and why (tensor/compile.go:36-42):
+    ``kernel`` is the launches in order, ``rejected`` the routes turned down,
+    each with its reason."""
+
+    def __init__(self, d: SelectionDesc):
+        self.op = d.op.decode()
+        self.launches = [k for k in d.kernel.decode().split(" + ") if k]
+        self.kernel = d.kernel.decode()
+        self.reason = d.reason.decode()
+        self.rejected = [r for r in d.rejected.decode().split("; ") if r]
+
+    def __repr__(self) -> str:
+        return (f"Selection(op={self.op!r}, kernel={self.kernel!r}, reason={self.reason!r}, "
+                f"rejected={self.rejected!r})")
+
+
+SELECT_BIAS, SELECT_BF16_OUT = 1, 2
+
 QFMT_AWQ, QFMT_GPTQ, QFMT_GPTQ_V2 = 1, 2, 3
 
 
@@ -140,6 +165,10 @@ SIGNATURES = {
     "accel_int4_g32_quantize": ([_vp, ctypes.c_int64, ctypes.c_int64, _vp, _vp], _i),
     "accel_int4_g32_matvec": ([_i, _vp, _P(Tensor), _P(Int4G32Desc), _P(Tensor)], _i),
     "accel_int4_linear": ([_i, _vp, _P(Tensor), _P(Int4Desc), _P(Tensor), _P(Tensor)], _i),
+    "accel_int4_select": ([_i, ctypes.c_char_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_int64,
+                           ctypes.c_int64, _vp, _P(Int4Desc), ctypes.c_int32,
+                           _P(SelectionDesc)], _i),
+    "accel_hip_last_selection": ([_i, _P(SelectionDesc)], _i),
     "accel_int4_matvec_set": ([_i, _vp, _P(Tensor), _P(Int4Desc), _P(Tensor), _i], _i),
     "accel_int4_matmul_set": ([_i, _vp, _P(Tensor), _P(Int4Desc), _P(Tensor), _i], _i),
     "accel_segment_offsets": ([_i, _vp, _P(Tensor), _P(Tensor)], _i),
@@ -185,6 +214,20 @@ def _check(rc: int) -> int:
     if rc == E_INVALID:
         raise Refused(rc, msg)
     raise AccelError(rc, msg)
+
+
+def select(M: int, K: int, N: int, dtype: int = None, a: int = None, codes: int = None,
+           op: str = None, flags: int = 0, dev: int = -1) -> Selection:
+    """The kernels an int4 product would become (accel_int4_select), planned
+    without running: dev < 0 plans for the modelled MI355X (no GPU needed).
+    ``a`` and ``codes`` are addresses whose alignment matters (None: aligned)."""
+    dtype = F32 if dtype is None else dtype
+    desc = SelectionDesc()
+    w = Int4Desc(codes or 0, 0, 0, 0, 0, 0, int(K) * int(N))
+    _check(_lib.accel_int4_select(int(dev), op.encode() if op else None, int(dtype), int(M),
+                                  int(K), int(N), a, ctypes.byref(w), int(flags),
+                                  ctypes.byref(desc)))
+    return Selection(desc)
 
 
 def device_count() -> int:
@@ -424,6 +467,13 @@ class Device:
         _check(_lib.accel_hip_floor(self.index, stream, kind, src.ptr if src else None, nbytes,
                                     sink.ptr))
 
+    def last_selection(self) -> Selection:
+        """What the last int4 product on this device became
+        (accel_hip_last_selection)."""
+        desc = SelectionDesc()
+        _check(_lib.accel_hip_last_selection(self.index, ctypes.byref(desc)))
+        return Selection(desc)
+
     def workspace_generation(self):
         """(allocations of the workspace so far, replaced workspaces still held
         by live executables)."""
@@ -520,7 +570,23 @@ class Device:
                       out: Buffer, stream=None) -> None:
         """BASELINE config 1's literal format: out[N] = a[K] @ ((q - 8) * s),
         32-row groups along K with an f32 scale (no counterpart in the
-        reference)."""
+        reference).  The C struct carries no plane lengths, so the buffers
+        are checked against K and N here: undersized planes would be read
+        past their end on the device."""
+        K, N = int(K), int(N)
+        if K <= 0 or N <= 0:
+            raise ValueError(f"Int4G32MatVec: K={K} and N={N} must be positive")
+        need = {"codes": (codes, K * N // 2), "scales": (scales, (K // 32) * N * 4)}
+        for name, (buf, nbytes) in need.items():
+            if buf.nbytes < nbytes:
+                raise ValueError(f"Int4G32MatVec: the {name} buffer holds {buf.nbytes} bytes "
+                                 f"and [{K}, {N}] needs {nbytes}")
+        if a.nbytes < K * 4:
+            raise ValueError(f"Int4G32MatVec: the activations hold {a.nbytes} bytes and "
+                             f"K={K} needs {K * 4}")
+        if out.nbytes < N * 4:
+            raise ValueError(f"Int4G32MatVec: the output holds {out.nbytes} bytes and "
+                             f"N={N} needs {N * 4}")
         ta, to = a.tensor(), out.tensor()
         tw = Int4G32Desc(codes.ptr, scales.ptr, K, N)
         _check(_lib.accel_int4_g32_matvec(self.index, stream, ctypes.byref(ta),

@@ -355,14 +355,18 @@ hipError_t launch_decode(Device* d, hipStream_t st, const XT* a, Int4Planes w,
         partial = reinterpret_cast<float*>(static_cast<char*>(ws) + kWorkspaceCounterBytes);
     }
     if (per_slice > 1)
-        hipLaunchKernelGGL((int4_decode_f32_kernel<M, TILE, CPL, true, XT>),
+        ACCEL_LAUNCH(tname("int4_decode_f32_kernel", M, TILE, CPL, true, type_name<XT>()) +
+                         grid_note(tiles, slices),
+                     (int4_decode_f32_kernel<M, TILE, CPL, true, XT>),
                            dim3(tiles * slices), dim3(kDecThreads), 0, st, a, w.codes, w.scales,
                            w.zeros, out, partial, tickets, stride, K, N, rows, slices, ep);
     else
-        hipLaunchKernelGGL((int4_decode_f32_kernel<M, TILE, CPL, false, XT>),
+        ACCEL_LAUNCH(tname("int4_decode_f32_kernel", M, TILE, CPL, false, type_name<XT>()) +
+                         grid_note(tiles, slices),
+                     (int4_decode_f32_kernel<M, TILE, CPL, false, XT>),
                            dim3(tiles * slices), dim3(kDecThreads), 0, st, a, w.codes, w.scales,
                            w.zeros, out, partial, tickets, stride, K, N, rows, slices, ep);
-    return hipGetLastError();
+    return launch_status();
 }
 
 // Column tile of a one-row product: 512 columns for wide matrices (a row's
@@ -523,9 +527,9 @@ hipError_t launch_matvec_f16_tiled(Device* d, hipStream_t st, const float* a, co
         tickets = static_cast<uint32_t*>(ws);
         partial = reinterpret_cast<float*>(static_cast<char*>(ws) + kWorkspaceCounterBytes);
     }
-    hipLaunchKernelGGL((matvec_f16_kernel<TILE>), dim3(tiles * slices), dim3(kDecThreads), 0, st,
+    ACCEL_LAUNCH(tname("matvec_f16_kernel", TILE) + grid_note(tiles, slices), (matvec_f16_kernel<TILE>), dim3(tiles * slices), dim3(kDecThreads), 0, st,
                        a, w, out, partial, tickets, stride, K, N, rows, slices);
-    return hipGetLastError();
+    return launch_status();
 }
 
 // Any shape: one lane per output element, decoding with the flat index.
@@ -1319,11 +1323,13 @@ hipError_t launch_mfma(Device* d, hipStream_t st, const XT* a, Int4Planes w, voi
         tickets = static_cast<uint32_t*>(ws);
         partial = reinterpret_cast<float*>(static_cast<char*>(ws) + kWorkspaceCounterBytes);
     }
-    hipLaunchKernelGGL((int4_decode_mfma_kernel<G, NW, XT>), dim3(tiles * p.slices),
+    ACCEL_LAUNCH(tname("int4_decode_mfma_kernel", G, NW, type_name<XT>()) +
+                     grid_note(tiles, p.slices),
+                 (int4_decode_mfma_kernel<G, NW, XT>), dim3(tiles * p.slices),
                        dim3(64 * NW), 0, st, a, w.codes, w.scales, w.zeros, out, partial,
                        tickets, stride, M, K, N, p.rows, p.slices, ep, d->fault_dev,
                        d->wait_limit);
-    return hipGetLastError();
+    return launch_status();
 }
 
 // Matrices of one tile width G in one launch, each with its own plan.
@@ -1372,9 +1378,10 @@ hipError_t launch_mfma_set(Device* d, hipStream_t st, const float* a, const Int4
             p += (size_t)plan[i].slices * M * N[i];
         }
     }
-    hipLaunchKernelGGL((int4_decode_mfma_set_kernel<G, 8>), dim3(wgs), dim3(64 * 8), 0, st, a,
+    ACCEL_LAUNCH(tname("int4_decode_mfma_set_kernel", G, 8) + grid_note(wgs, 0),
+                 (int4_decode_mfma_set_kernel<G, 8>), dim3(wgs), dim3(64 * 8), 0, st, a,
                        set, tickets, stride, M, K, d->fault_dev, d->wait_limit);
-    return hipGetLastError();
+    return launch_status();
 }
 
 template <typename XT = float>
@@ -1433,12 +1440,14 @@ hipError_t launch_matvec_set(Device* d, hipStream_t st, const float* a, const In
         }
     }
     if (per_slice > 1)
-        hipLaunchKernelGGL((int4_decode_set_kernel<1, TILE, CPL, true>), dim3(tiles * slices),
+        ACCEL_LAUNCH(tname("int4_decode_set_kernel", 1, TILE, CPL, true) + grid_note(tiles, slices),
+                     (int4_decode_set_kernel<1, TILE, CPL, true>), dim3(tiles * slices),
                            dim3(kDecThreads), 0, st, a, set, tickets, stride, K, rows, slices);
     else
-        hipLaunchKernelGGL((int4_decode_set_kernel<1, TILE, CPL, false>), dim3(tiles * slices),
+        ACCEL_LAUNCH(tname("int4_decode_set_kernel", 1, TILE, CPL, false) + grid_note(tiles, slices),
+                     (int4_decode_set_kernel<1, TILE, CPL, false>), dim3(tiles * slices),
                            dim3(kDecThreads), 0, st, a, set, tickets, stride, K, rows, slices);
-    return hipGetLastError();
+    return launch_status();
 }
 
 }  // namespace
@@ -1452,9 +1461,9 @@ hipError_t launch_matvec_f32_f16(Device* d, hipStream_t st, const float* a, cons
         return launch_matvec_f16_tiled<256>(d, st, a, w, out, K, N, status);
     if (aligned && N % 128 == 0 && N < (1 << 30))
         return launch_matvec_f16_tiled<128>(d, st, a, w, out, K, N, status);
-    hipLaunchKernelGGL(matvec_f16_generic_kernel, dim3((N + 255) / 256), dim3(256), 0, st, a, w,
+    ACCEL_LAUNCH(std::string("matvec_f16_generic_kernel"), matvec_f16_generic_kernel, dim3((N + 255) / 256), dim3(256), 0, st, a, w,
                        out, K, N);
-    return hipGetLastError();
+    return launch_status();
 }
 
 bool int4_matmul_set_supported(const float* a, const Int4Planes* w, const int* N, int count,
@@ -1879,6 +1888,14 @@ GroupedMfma grouped_mfma(const Device* d, const void* x, Int4Planes w, int E, in
                              reinterpret_cast<uintptr_t>(w.zeros)) & 3) == 0 &&
                            ((per >> 7) & 1) == 0;
     g.plan = plan_decode_mfma(d, kMfBlockRows, K, N, planes_4b);
+    // The plan above fills the CUs from one block.  The rows make at least
+    // ceil(T / 16) blocks; once those blocks' column tiles alone fill the
+    // CUs, K is not split: no tickets, no sums area, no hand-off.
+    const long long min_blocks = (T + kMfBlockRows - 1) / kMfBlockRows;
+    if (min_blocks * (N / (128 * g.plan.groups)) >= d->cu_count) {
+        g.plan.slices = 1;
+        g.plan.rows = K;
+    }
     if (g.plan.slices > 1) {
         g.stride = ticket_stride(g.blocks * (N / (128 * g.plan.groups)));
         if (g.stride < 2) return g;
@@ -1914,16 +1931,20 @@ hipError_t launch_grouped_decode_tile(Device* d, hipStream_t st, const XT* x, In
     float* partial = slices > 1 ? area : nullptr;
     const dim3 grid((unsigned)(pairs * slices));
     if (per_slice > 1)
-        hipLaunchKernelGGL((int4_grouped_decode_kernel<TILE, CPL, true, XT>), grid,
+        ACCEL_LAUNCH(tname("int4_grouped_decode_kernel", TILE, CPL, true, type_name<XT>()) +
+                         grid_note(tiles, slices),
+                     (int4_grouped_decode_kernel<TILE, CPL, true, XT>), grid,
                            dim3(kDecThreads), 0, st, x, w.codes, w.scales, w.zeros, off, out,
                            partial, tickets, stride, E, T, K, N, rows, slices, write_padding,
                            mfma_blocks);
     else
-        hipLaunchKernelGGL((int4_grouped_decode_kernel<TILE, CPL, false, XT>), grid,
+        ACCEL_LAUNCH(tname("int4_grouped_decode_kernel", TILE, CPL, false, type_name<XT>()) +
+                         grid_note(tiles, slices),
+                     (int4_grouped_decode_kernel<TILE, CPL, false, XT>), grid,
                            dim3(kDecThreads), 0, st, x, w.codes, w.scales, w.zeros, off, out,
                            partial, tickets, stride, E, T, K, N, rows, slices, write_padding,
                            mfma_blocks);
-    return hipGetLastError();
+    return launch_status();
 }
 
 template <int G, typename XT>
@@ -1933,11 +1954,13 @@ hipError_t launch_grouped_mfma(Device* d, hipStream_t st, const XT* x, Int4Plane
     const int tiles = N / (128 * G);
     const bool split = g.plan.slices > 1;
     const dim3 grid((unsigned)(g.blocks * tiles * g.plan.slices));
-    hipLaunchKernelGGL((int4_grouped_decode_mfma_kernel<G, 8, XT>), grid, dim3(64 * 8), 0, st, x,
+    ACCEL_LAUNCH(tname("int4_grouped_decode_mfma_kernel", G, 8, type_name<XT>()) +
+                     grid_note(tiles, g.plan.slices),
+                 (int4_grouped_decode_mfma_kernel<G, 8, XT>), grid, dim3(64 * 8), 0, st, x,
                        w.codes, w.scales, w.zeros, off, out, split ? area : nullptr,
                        split ? tickets : nullptr, g.stride, E, T, K, N, g.plan.rows,
                        g.plan.slices, d->fault_dev, d->wait_limit);
-    return hipGetLastError();
+    return launch_status();
 }
 
 }  // namespace
@@ -2139,9 +2162,9 @@ hipError_t launch_int4_g32_matvec(Device* d, hipStream_t st, const float* a,
         tickets = static_cast<uint32_t*>(ws);
         partial = reinterpret_cast<float*>(static_cast<char*>(ws) + kWorkspaceCounterBytes);
     }
-    hipLaunchKernelGGL(int4_g32_matvec_kernel, dim3(tiles * slices), dim3(kDecThreads), 0, st, a,
+    ACCEL_LAUNCH(std::string("int4_g32_matvec_kernel") + grid_note(tiles, slices), int4_g32_matvec_kernel, dim3(tiles * slices), dim3(kDecThreads), 0, st, a,
                        codes, scales, out, partial, tickets, stride, K, N, rows, slices);
-    return hipGetLastError();
+    return launch_status();
 }
 
 // ---- the no-allocation Int4MatVec -----------------------------------------
@@ -2193,9 +2216,9 @@ hipError_t launch_int4_generic_f32(hipStream_t st, const float* a, Int4Planes w,
     if (total == 0) return hipSuccess;
     const int threads = 256;
     const int64_t blocks = (total + threads - 1) / threads;
-    hipLaunchKernelGGL(int4_generic_f32_kernel, dim3((unsigned)blocks), dim3(threads), 0, st,
+    ACCEL_LAUNCH(std::string("int4_generic_f32_kernel"), int4_generic_f32_kernel, dim3((unsigned)blocks), dim3(threads), 0, st,
                        a, w.codes, w.scales, w.zeros, out, M, K, N, ep);
-    return hipGetLastError();
+    return launch_status();
 }
 
 hipError_t launch_int4_generic_bf16(hipStream_t st, const uint16_t* a, Int4Planes w,
@@ -2204,9 +2227,9 @@ hipError_t launch_int4_generic_bf16(hipStream_t st, const uint16_t* a, Int4Plane
     if (total == 0) return hipSuccess;
     const int threads = 256;
     const int64_t blocks = (total + threads - 1) / threads;
-    hipLaunchKernelGGL(int4_generic_bf16_kernel, dim3((unsigned)blocks), dim3(threads), 0,
+    ACCEL_LAUNCH(std::string("int4_generic_bf16_kernel"), int4_generic_bf16_kernel, dim3((unsigned)blocks), dim3(threads), 0,
                        st, a, w.codes, w.scales, w.zeros, out, M, K, N, bias);
-    return hipGetLastError();
+    return launch_status();
 }
 
 }  // namespace accel

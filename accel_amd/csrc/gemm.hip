@@ -1182,10 +1182,12 @@ void launch_band(hipStream_t st, const uint16_t* a, Int4Planes w, uint16_t* out,
                  int bands, int M, int K, int N, const float* bias) {
     const dim3 grid(bands * (N / BN));
     if (bias)
-        hipLaunchKernelGGL((int4_gemm_bf16_kernel<MT, true>), grid, dim3(kThreads), 0, st, a,
+        ACCEL_LAUNCH(tname("int4_gemm_bf16_kernel", MT, true) + grid_note(bands * (N / BN), 1),
+                     (int4_gemm_bf16_kernel<MT, true>), grid, dim3(kThreads), 0, st, a,
                            w.codes, w.scales, w.zeros, out, m_first, M, K, N, bias);
     else
-        hipLaunchKernelGGL((int4_gemm_bf16_kernel<MT, false>), grid, dim3(kThreads), 0, st, a,
+        ACCEL_LAUNCH(tname("int4_gemm_bf16_kernel", MT, false) + grid_note(bands * (N / BN), 1),
+                     (int4_gemm_bf16_kernel<MT, false>), grid, dim3(kThreads), 0, st, a,
                            w.codes, w.scales, w.zeros, out, m_first, M, K, N, bias);
 }
 
@@ -1193,7 +1195,8 @@ template <int MT>
 void launch_band_splitk(hipStream_t st, const uint16_t* a, Int4Planes w, float* part,
                         int m_first, int bands, int M, int K, int N, int slices, int kt_per) {
     const dim3 grid(bands * (N / BN) * slices);
-    hipLaunchKernelGGL((int4_gemm_bf16_splitk_kernel<MT>), grid, dim3(kThreads), 0, st, a,
+    ACCEL_LAUNCH(tname("int4_gemm_bf16_splitk_kernel", MT) + grid_note(bands * (N / BN), slices),
+                 (int4_gemm_bf16_splitk_kernel<MT>), grid, dim3(kThreads), 0, st, a,
                        w.codes, w.scales, w.zeros, part, m_first, M, K, N, slices, kt_per);
 }
 
@@ -1236,10 +1239,11 @@ hipError_t launch_int4_gemm_bf16(Device* d, hipStream_t st, const uint16_t* a, I
             }
         }
         const long long quads = (long long)stride / 4;
-        hipLaunchKernelGGL(int4_gemm_reduce_kernel, dim3((unsigned)((quads + 255) / 256)),
+        ACCEL_LAUNCH(std::string("int4_gemm_reduce_kernel"), int4_gemm_reduce_kernel,
+                     dim3((unsigned)((quads + 255) / 256)),
                            dim3(256), 0, st, part, (void*)out, quads, N, slices,
                            (long long)stride, bias, true);
-        return hipGetLastError();
+        return launch_status();
     }
     // full 256-row bands in one launch, a partial last band in another with
     // only its own m-tiles
@@ -1259,7 +1263,7 @@ hipError_t launch_int4_gemm_bf16(Device* d, hipStream_t st, const uint16_t* a, I
             default: launch_band<8>(st, a, w, out, m_first, 1, M, K, N, bias); break;
         }
     }
-    return hipGetLastError();
+    return launch_status();
 }
 
 hipError_t launch_int4_grouped_bf16(Device*, hipStream_t st, const uint16_t* x,
@@ -1271,9 +1275,9 @@ hipError_t launch_int4_grouped_bf16(Device*, hipStream_t st, const uint16_t* x,
     const long long wgs = (max_blocks * (N / BN) + 7) / 8 * 8;
     if (wgs > (1ll << 31) - 8) return hipErrorInvalidConfiguration;
     dim3 grid((unsigned)wgs);
-    hipLaunchKernelGGL(int4_grouped_bf16_kernel, grid, dim3(kThreads), 0, st, x, w.codes,
+    ACCEL_LAUNCH(std::string("int4_grouped_bf16_kernel"), int4_grouped_bf16_kernel, grid, dim3(kThreads), 0, st, x, w.codes,
                        w.scales, w.zeros, off, out, E, T, K, N);
-    return hipGetLastError();
+    return launch_status();
 }
 
 bool int4_gemm_f32x3_supported(int K, int N) {
@@ -1289,29 +1293,32 @@ hipError_t launch_int4_gemm_f32x3(Device* d, hipStream_t st, const float* a, Int
     const int slices =
         tiles * 2 > d->cu_count ? 1 : std::max(1, std::min(d->cu_count / tiles, ktiles / 4));
     if (slices == 1) {
-        hipLaunchKernelGGL(int4_gemm_f32x3_kernel, dim3(tiles), dim3(kThreads), 0, st, a,
+        ACCEL_LAUNCH(std::string("int4_gemm_f32x3_kernel") + grid_note(tiles, 1),
+                     int4_gemm_f32x3_kernel, dim3(tiles), dim3(kThreads), 0, st, a,
                            w.codes, w.scales, w.zeros, out, M, K, N, ep, (float*)nullptr, 1, 0);
-        return hipGetLastError();
+        return launch_status();
     }
     const size_t stride = (size_t)M * N;
     void* ws = workspace(d, st, (size_t)slices * stride * sizeof(float), status);
     if (!ws) return hipSuccess;
     float* part = reinterpret_cast<float*>(static_cast<char*>(ws) + kWorkspaceCounterBytes);
-    hipLaunchKernelGGL(int4_gemm_f32x3_kernel, dim3(tiles * slices), dim3(kThreads), 0, st, a,
+    ACCEL_LAUNCH(std::string("int4_gemm_f32x3_kernel") + grid_note(tiles, slices),
+                 int4_gemm_f32x3_kernel, dim3(tiles * slices), dim3(kThreads), 0, st, a,
                        w.codes, w.scales, w.zeros, out, M, K, N, ep, part, slices,
                        ktiles / slices);
     const long long quads = (long long)stride / 4;
-    hipLaunchKernelGGL(int4_gemm_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256),
+    ACCEL_LAUNCH(std::string("int4_gemm_reduce_kernel"), int4_gemm_reduce_kernel,
+                 dim3((unsigned)((quads + 255) / 256)), dim3(256),
                        0, st, part, out, quads, N, slices, (long long)stride, ep.bias, ep.bf16);
-    return hipGetLastError();
+    return launch_status();
 }
 
 hipError_t launch_int4_gemm_f32(Device*, hipStream_t st, const float* a, Int4Planes w,
                                 void* out, int M, int K, int N, Epilogue ep) {
     dim3 grid((N + FN - 1) / FN, (M + FM - 1) / FM);
-    hipLaunchKernelGGL(int4_gemm_f32_kernel, grid, dim3(256), 0, st, a, w.codes, w.scales,
+    ACCEL_LAUNCH(std::string("int4_gemm_f32_kernel"), int4_gemm_f32_kernel, grid, dim3(256), 0, st, a, w.codes, w.scales,
                        w.zeros, out, M, K, N, ep);
-    return hipGetLastError();
+    return launch_status();
 }
 
 }  // namespace accel

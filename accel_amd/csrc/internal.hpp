@@ -8,6 +8,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <mutex>
+#include <string>
 #include <unordered_map>
 #include <vector>
 
@@ -54,6 +55,9 @@ struct Device {
     void* scratch = nullptr;
     int cu_count = 256;
     size_t lds_per_block = 65536;
+    // The last int4 product's selection (accel_hip_last_selection), under mu.
+    bool sel_valid = false;
+    std::string sel_op, sel_kernel, sel_reason, sel_rejected;
 };
 
 // The open device `dev`, made current on this thread, or nullptr with the
@@ -82,6 +86,70 @@ void* workspace(Device* d, hipStream_t st, size_t bytes, int* status);
 // naming what a kernel reported in the fault word (which is then cleared,
 // together with the workspaces' counters, so later calls start clean).
 int take_fault(Device* d);
+
+// ---- the selection report: which kernels a product became -----------------
+//
+// Every launch site of the int4 products names its kernel, template
+// arguments included, the way a profiler's kernel trace shows it.  While the
+// calling thread records (LaunchRecord), the names collect in order; while it
+// plans without running (dry), nothing is launched and workspace() hands out
+// a placeholder address without allocating, so a selection can be asked for
+// on a host with no GPU.
+struct LaunchRecord {
+    explicit LaunchRecord(bool dry);
+    ~LaunchRecord();
+    std::vector<std::string> names;
+    std::string joined() const;   // the launches in order, " + " between them
+    LaunchRecord* outer;
+    bool dry;
+};
+// The calling thread's innermost record, or nullptr.
+LaunchRecord* launch_record();
+inline bool dry_run() {
+    const LaunchRecord* r = launch_record();
+    return r && r->dry;
+}
+
+inline void targ(std::string& s, int v) { s += std::to_string(v); }
+inline void targ(std::string& s, bool v) { s += v ? "true" : "false"; }
+inline void targ(std::string& s, const char* v) { s += v; }
+// "base<a, b, ...>" as a profiler names a template kernel.
+template <typename... A>
+std::string tname(const char* base, A... args) {
+    std::string s = base;
+    if constexpr (sizeof...(A) > 0) {
+        s += '<';
+        bool first = true;
+        ((s += first ? "" : ", ", first = false, targ(s, args)), ...);
+        s += '>';
+    }
+    return s;
+}
+// The grid beside a kernel's name: " [T tiles x S K slices]", " [T tiles]"
+// with one slice, " [W workgroups]" with slices 0.
+inline std::string grid_note(long long tiles, int slices) {
+    if (slices == 0) return " [" + std::to_string(tiles) + " workgroups]";
+    std::string s = " [" + std::to_string(tiles) + (tiles == 1 ? " tile" : " tiles");
+    if (slices > 1) s += " x " + std::to_string(slices) + " K slices";
+    return s + "]";
+}
+// A template type argument's name as the profiler prints it.
+template <typename T> constexpr const char* type_name();
+template <> constexpr const char* type_name<float>() { return "float"; }
+template <> constexpr const char* type_name<uint16_t>() { return "unsigned short"; }
+
+// A launcher's result: the launch error, or success while planning dry.
+inline hipError_t launch_status() { return dry_run() ? hipSuccess : hipGetLastError(); }
+
+// Launch `...` (hipLaunchKernelGGL's arguments) and note NAME in the
+// thread's record; under a dry record only the name is noted.  NAME is
+// evaluated only while recording.
+#define ACCEL_LAUNCH(NAME, ...)                                              \
+    do {                                                                     \
+        if (::accel::LaunchRecord* rec_ = ::accel::launch_record())          \
+            rec_->names.push_back(NAME);                                     \
+        if (!::accel::dry_run()) hipLaunchKernelGGL(__VA_ARGS__);            \
+    } while (0)
 
 // ---- kernel launchers (defined in the .hip files) ------------------------
 
@@ -202,7 +270,9 @@ constexpr int kGroupedDecodeRows = 64;
 // rows, which have the grouped tiles) they run one lane per element.  Measured
 // (us, decode kernels / one lane per element), 8 experts of 4096 x 14336, top-2
 // routing: 128 rows 173 / 6543, 256 rows 288 / 11139, 512 rows 484 / 20581.
-// The split-K sums of 1024 rows at N = 14336 take 235 MB of workspace.
+// K is split only while the rows' fewest blocks (ceil(T / 16)) times the
+// column tiles leave CUs idle, so the split-K sums stay small: at N = 14336
+// (56 tiles of 256 columns) rows past 64 run one slice and take none.
 constexpr int kGroupedDecodeRowsF32 = 1024;
 // The grouped decode launches take the workspace's counters (`tickets`) and an
 // area past the offsets for their split-K sums, of the size

@@ -4,11 +4,10 @@
 // and kernel-record dispatch for the backend seam.
 //
 // Kernel selection (the analogue of a plan's selection report,
-// tensor/compile.go:36-42):
-//   f32 activations, M <= 16, N % 128 == 0   -> the decode kernels (K split)
-//   f32 activations, M > 16,  N % 128 == 0   -> the fp32 tiled kernel
-//   bf16 activations, K % 64 == 0, N % 128 == 0 -> the MFMA tiles
-//   any other shape                          -> the per-element kernel
+// tensor/compile.go:36-42, tensor/plan.go:36-41): choose_int4 below picks a
+// product's route and says why, and names every route it turned down; the
+// launches it becomes are recorded as they are made (accel_hip_last_selection)
+// or planned without running (accel_int4_select).
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -133,45 +132,206 @@ int check_out(const char* op, const accel_tensor_t* out, int32_t dtype, int64_t 
     return ACCEL_OK;
 }
 
+// The routes of an int4 product, in the order they are tried.
+enum class Int4Route {
+    kNone,          // an empty product: nothing to launch
+    kDecodeF32,     // M <= 16 f32 rows: the decode kernels
+    kDecodeF32Rows, // 17..48 f32 rows as 16-row decode products
+    kGemmF32x3,     // M > 16 f32 rows on the matrix cores, three-term split
+    kGemmF32,       // M > 16 f32 rows, fp32 VALU tiles
+    kGenericF32,    // one lane per output element
+    kDecodeBf16Row, // one bf16 row: the VALU decode kernel
+    kDecodeBf16Rows,// 2..16 bf16 rows: the matrix-core decode kernel
+    kGemmBf16,      // bf16 rows on the matrix-core tiles
+    kGenericBf16,   // one lane per output element
+};
+
+struct Int4Choice {
+    Int4Route route = Int4Route::kNone;
+    std::string reason;
+    std::vector<std::string> rejected;
+};
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Which route an int4 product of M x K x N takes, why, and what it turned
+// down (KernelSelection's Reason and Rejected).  The shape limits are the
+// launchers' own predicates, so the answer is the route run_int4_product
+// takes.
+Int4Choice choose_int4(int32_t dtype, const void* a, const void* codes, int M, int K, int N) {
+    Int4Choice c;
+    char buf[320];
+    if (M == 0 || N == 0) {
+        c.reason = "an empty product: there is nothing to launch";
+        return c;
+    }
+    const bool aligned128 = N % 128 == 0 && (uint64_t)K * (uint64_t)N < (1ull << 32);
+    auto reject = [&](const char* route, const char* why) {
+        snprintf(buf, sizeof buf, "%s: %s", route, why);
+        c.rejected.push_back(buf);
+    };
+    if (dtype == ACCEL_F32) {
+        const bool decode = int4_decode_f32_supported(M, K, N, codes);
+        if (decode) {
+            c.route = Int4Route::kDecodeF32;
+            if (M == 1)
+                c.reason = "one f32 row: the VALU decode kernel streams the weights once, K "
+                           "split across workgroups so every CU reads";
+            else if (K % 32 == 0 && N < (1 << 27) && aligned16(a))
+                c.reason = "2..16 f32 rows: the matrix-core decode kernel (x*512s in three bf16 "
+                           "terms against the exact codes) reads the weights once for all rows";
+            else
+                c.reason = "2..16 f32 rows whose K is not a multiple of 32 or whose rows are "
+                           "not 16-byte aligned: the VALU decode kernel, rows in passes of up "
+                           "to eight";
+            if (M > 1) reject("the matrix-core tiles", "a 32-row band would be mostly empty");
+            return c;
+        }
+        if (M <= 16)
+            reject("the decode kernels",
+                   "they take N a multiple of 128 and 16-byte aligned codes");
+        else
+            reject("the decode kernels", "they take at most 16 rows a launch");
+        if (int4_decode_rows_pay(M, K, N) && K % 32 == 0 &&
+            int4_decode_f32_supported(16, K, N, codes) && aligned16(a)) {
+            c.route = Int4Route::kDecodeF32Rows;
+            c.reason = "17..48 f32 rows of a large matrix: consecutive 16-row matrix-core "
+                       "decode products beat a band of the f32 matrix-core tiles here";
+            return c;
+        }
+        if (M <= 48 && M > 16)
+            reject("16-row decode products",
+                   "they pay only for 17..32 rows with K*N >= 2^23 or 33..48 with K*N >= "
+                   "2^25, K % 32 == 0 and 16-byte aligned rows");
+        if (M > 16 && int4_gemm_f32x3_supported(K, N) && aligned16(a)) {
+            c.route = Int4Route::kGemmF32x3;
+            c.reason = "more than 16 f32 rows: the bf16 matrix-core tiles to f32 accuracy "
+                       "(x*512s in three bf16 terms against the exact codes); K split when "
+                       "the tiles leave CUs idle";
+            return c;
+        }
+        if (M > 16)
+            reject("the f32 matrix-core tiles",
+                   "they take K % 64 == 0, N % 128 == 0 and 16-byte aligned rows");
+        if (M > 16 && aligned128) {
+            c.route = Int4Route::kGemmF32;
+            c.reason = "more than 16 f32 rows that the matrix-core tiles cannot take: fp32 "
+                       "VALU tiles";
+            return c;
+        }
+        if (M > 16) reject("the fp32 VALU tiles", "they take N % 128 == 0 and K*N < 2^32");
+        c.route = Int4Route::kGenericF32;
+        c.reason = "no tiled kernel takes this shape: one lane per output element, decoding "
+                   "with the flat index (correct everywhere, not a speed path)";
+        return c;
+    }
+    if (M == 1 && int4_decode_f32_supported(1, K, N, codes)) {
+        c.route = Int4Route::kDecodeBf16Row;
+        c.reason = "one bf16 row: the VALU decode kernel reading bf16, f32 arithmetic, one "
+                   "rounding of each sum to bf16";
+        reject("the matrix-core tiles", "a 32-row band for one row would be mostly empty");
+        return c;
+    }
+    if (M == 1)
+        reject("the VALU decode kernel", "it takes N a multiple of 128 and 16-byte aligned codes");
+    if (int4_decode_bf16_rows_supported(M, K, N, a, codes)) {
+        c.route = Int4Route::kDecodeBf16Rows;
+        c.reason = "2..16 bf16 rows: the matrix-core decode kernel (bf16 staged, f32 "
+                   "arithmetic, one rounding to bf16) reads the weights once for all rows";
+        reject("the matrix-core tiles", "a 32-row band would be mostly empty");
+        return c;
+    }
+    if (M >= 2 && M <= 16)
+        reject("the matrix-core decode kernel",
+               "it takes K % 32 == 0, N a multiple of 128, 16-byte aligned rows and codes");
+    if (int4_gemm_bf16_supported(M, K, N) && aligned16(a)) {
+        c.route = Int4Route::kGemmBf16;
+        c.reason = "bf16 rows: the matrix-core tiles (codes dequantised to bf16 in registers, "
+                   "f32 accumulation); K split when the tiles leave CUs idle";
+        return c;
+    }
+    reject("the matrix-core tiles",
+           aligned16(a) ? "they take K % 64 == 0, N % 128 == 0, K < 2^22 and N < 2^26"
+                        : "the activations are not 16-byte aligned, and the tiles load them "
+                          "16 bytes at a time");
+    c.route = Int4Route::kGenericBf16;
+    c.reason = "no tiled kernel takes this shape or alignment: one lane per output element, "
+               "decoding with the flat index (correct everywhere, not a speed path)";
+    return c;
+}
+
+// Runs the launches of a chosen route.
+hipError_t launch_int4_route(Device* d, hipStream_t st, Int4Route r, const void* a,
+                             const Int4Planes& p, void* out, int M, int K, int N, Epilogue ep,
+                             int* status) {
+    const float* af = static_cast<const float*>(a);
+    const uint16_t* ab = static_cast<const uint16_t*>(a);
+    uint16_t* ob = static_cast<uint16_t*>(out);
+    switch (r) {
+        case Int4Route::kNone: return hipSuccess;
+        case Int4Route::kDecodeF32:
+            return launch_int4_decode_f32(d, st, af, p, out, M, K, N, status, ep);
+        case Int4Route::kDecodeF32Rows:
+            return launch_int4_decode_f32_rows(d, st, af, p, out, M, K, N, status, ep);
+        case Int4Route::kGemmF32x3:
+            return launch_int4_gemm_f32x3(d, st, af, p, out, M, K, N, ep, status);
+        case Int4Route::kGemmF32: return launch_int4_gemm_f32(d, st, af, p, out, M, K, N, ep);
+        case Int4Route::kGenericF32: return launch_int4_generic_f32(st, af, p, out, M, K, N, ep);
+        case Int4Route::kDecodeBf16Row:
+            return launch_int4_decode_bf16_row(d, st, ab, p, ob, K, N, status, ep.bias);
+        case Int4Route::kDecodeBf16Rows:
+            return launch_int4_decode_bf16_rows(d, st, ab, p, ob, M, K, N, status, ep.bias);
+        case Int4Route::kGemmBf16:
+            return launch_int4_gemm_bf16(d, st, ab, p, ob, M, K, N, ep.bias, status);
+        case Int4Route::kGenericBf16:
+            return launch_int4_generic_bf16(st, ab, p, ob, M, K, N, ep.bias);
+    }
+    return hipSuccess;
+}
+
+std::string join(const std::vector<std::string>& v, const char* sep) {
+    std::string s;
+    for (size_t i = 0; i < v.size(); i++) {
+        if (i) s += sep;
+        s += v[i];
+    }
+    return s;
+}
+
+void fill_selection(accel_selection_t* out, const std::string& op, const std::string& kernel,
+                    const std::string& reason, const std::string& rejected) {
+    memset(out, 0, sizeof *out);
+    snprintf(out->op, sizeof out->op, "%s", op.c_str());
+    snprintf(out->kernel, sizeof out->kernel, "%s", kernel.c_str());
+    snprintf(out->reason, sizeof out->reason, "%s", reason.c_str());
+    snprintf(out->rejected, sizeof out->rejected, "%s", rejected.c_str());
+}
+
+// Keeps what a call launched as the device's last selection.
+void keep_selection(Device* d, const char* op, const LaunchRecord& rec, const std::string& reason,
+                    const std::string& rejected) {
+    std::lock_guard<std::mutex> lk(d->mu);
+    d->sel_valid = true;
+    d->sel_op = op;
+    d->sel_kernel = rec.joined();
+    d->sel_reason = reason;
+    d->sel_rejected = rejected;
+}
+
 // The shared core of Int4MatVec, Int4MatMul and Int4Linear once validated.
 // `ep` is the fused epilogue (bias, bf16 result); bf16 activations always
-// give a bf16 result.
-int run_int4_product(Device* d, hipStream_t st, const void* a, int32_t dtype,
+// give a bf16 result.  The launches made are kept as the device's last
+// selection.
+int run_int4_product(Device* d, hipStream_t st, const char* op, const void* a, int32_t dtype,
                      const accel_int4_t* w, void* out, int M, int K, int N,
                      Epilogue ep = Epilogue{}) {
     int status = begin_submission(d);
     if (status != ACCEL_OK) return status;
-    if (M == 0 || N == 0) return ACCEL_OK;
-    const Int4Planes p = planes(w);
-    const bool aligned128 = N % 128 == 0 && (uint64_t)K * (uint64_t)N < (1ull << 32);
-    hipError_t e = hipSuccess;
-    if (dtype == ACCEL_F32) {
-        const float* af = static_cast<const float*>(a);
-        if (int4_decode_f32_supported(M, K, N, w->codes))
-            e = launch_int4_decode_f32(d, st, af, p, out, M, K, N, &status, ep);
-        else if (int4_decode_rows_pay(M, K, N) && K % 32 == 0 &&
-                 int4_decode_f32_supported(16, K, N, w->codes) &&
-                 (reinterpret_cast<uintptr_t>(a) & 15) == 0)
-            e = launch_int4_decode_f32_rows(d, st, af, p, out, M, K, N, &status, ep);
-        else if (M > 16 && int4_gemm_f32x3_supported(K, N) &&
-                 (reinterpret_cast<uintptr_t>(a) & 15) == 0)
-            e = launch_int4_gemm_f32x3(d, st, af, p, out, M, K, N, ep, &status);
-        else if (M > 16 && aligned128)
-            e = launch_int4_gemm_f32(d, st, af, p, out, M, K, N, ep);
-        else
-            e = launch_int4_generic_f32(st, af, p, out, M, K, N, ep);
-    } else {
-        const uint16_t* ab = static_cast<const uint16_t*>(a);
-        uint16_t* ob = static_cast<uint16_t*>(out);
-        if (M == 1 && int4_decode_f32_supported(1, K, N, w->codes))
-            e = launch_int4_decode_bf16_row(d, st, ab, p, ob, K, N, &status, ep.bias);
-        else if (int4_decode_bf16_rows_supported(M, K, N, a, w->codes))
-            e = launch_int4_decode_bf16_rows(d, st, ab, p, ob, M, K, N, &status, ep.bias);
-        else if (int4_gemm_bf16_supported(M, K, N) && (reinterpret_cast<uintptr_t>(a) & 15) == 0)
-            e = launch_int4_gemm_bf16(d, st, ab, p, ob, M, K, N, ep.bias, &status);
-        else
-            e = launch_int4_generic_bf16(st, ab, p, ob, M, K, N, ep.bias);
-    }
+    const Int4Choice c = choose_int4(dtype, a, w->codes, M, K, N);
+    LaunchRecord rec(false);
+    const hipError_t e = launch_int4_route(d, st, c.route, a, planes(w), out, M, K, N, ep,
+                                           &status);
+    keep_selection(d, op, rec, c.reason, join(c.rejected, "; "));
     return finish(d, e, status, "int4 product launch");
 }
 
@@ -189,8 +349,8 @@ ACCEL_API int accel_int4_matvec(int dev, void* stream, const accel_tensor_t* a,
     if (rc != ACCEL_OK) return rc;
     Device* d = device(dev);
     if (!d) return ACCEL_E_NO_DEVICE;
-    return run_int4_product(d, (hipStream_t)stream, a->data, ACCEL_F32, w, out->data, 1,
-                            (int)k, (int)n);
+    return run_int4_product(d, (hipStream_t)stream, "Int4MatVec", a->data, ACCEL_F32, w,
+                            out->data, 1, (int)k, (int)n);
 }
 
 // BASELINE config 1's literal format (32-row groups along K, f32 scale, no
@@ -247,11 +407,19 @@ ACCEL_API int accel_int4_matvec_noalloc(int dev, void* stream, const accel_tenso
     int status = begin_submission(d);
     if (status != ACCEL_OK) return status;
     if (n == 0) return ACCEL_OK;
+    LaunchRecord rec(false);
     const hipError_t e = launch_int4_matvec_noalloc(
         d, (hipStream_t)stream, static_cast<const float*>(a->data), planes(w),
         static_cast<float*>(out->data), (int)k, (int)n, &status);
+    keep_selection(d, "Int4MatVecNoAlloc", rec,
+                   "Int4MatVec's kernels and plan, the split-K sums in the static scratch",
+                   "the workspace: it may call hipMalloc to grow");
     return finish(d, e, status, "Int4MatVecNoAlloc launch");
 }
+
+const char* const kSetReason =
+    "matrices that share their input and all take the decode kernels: one launch per tile "
+    "width, each matrix with its own launch's plan, so each result is its own product's";
 
 // Int4MatVec over several matrices that share one input vector, in one
 // launch where they all take the decode kernel (the q, k, v or gate, up
@@ -283,7 +451,8 @@ ACCEL_API int accel_int4_matvec_set(int dev, void* stream, const accel_tensor_t*
     hipStream_t st = (hipStream_t)stream;
     if (!int4_matvec_set_supported(p, N, count, (int)K)) {
         for (int i = 0; i < count; i++) {
-            const int rc = run_int4_product(d, st, a->data, ACCEL_F32, &w[i], out[i].data, 1,
+            const int rc = run_int4_product(d, st, "Int4MatVec", a->data, ACCEL_F32, &w[i],
+                                            out[i].data, 1,
                                             (int)K, N[i]);
             if (rc != ACCEL_OK) return rc;
         }
@@ -291,8 +460,11 @@ ACCEL_API int accel_int4_matvec_set(int dev, void* stream, const accel_tensor_t*
     }
     int status = begin_submission(d);
     if (status != ACCEL_OK) return status;
+    LaunchRecord rec(false);
     hipError_t e = launch_int4_matvec_set(d, st, static_cast<const float*>(a->data), p, o, N,
                                           count, (int)K, &status);
+    keep_selection(d, op, rec, kSetReason, "one Int4MatVec launch per matrix: each would read "
+                   "the shared vector and pay its own launch");
     return finish(d, e, status, "Int4MatVecSet launch");
 }
 
@@ -346,17 +518,24 @@ ACCEL_API int accel_int4_matmul_set(int dev, void* stream, const accel_tensor_t*
     if (m == 1 && int4_matvec_set_supported(p, N, count, (int)k)) {
         int status = begin_submission(d);
         if (status != ACCEL_OK) return status;
+        LaunchRecord rec(false);
         hipError_t e = launch_int4_matvec_set(d, st, af, p, o, N, count, (int)k, &status);
+        keep_selection(d, op, rec, kSetReason, "one Int4MatMul launch per matrix: each would "
+                       "read the shared rows and pay its own launch");
         return finish(d, e, status, "Int4MatMulSet launch");
     }
     if (int4_matmul_set_supported(af, p, N, count, (int)m, (int)k)) {
         int status = begin_submission(d);
         if (status != ACCEL_OK) return status;
+        LaunchRecord rec(false);
         hipError_t e = launch_int4_matmul_set(d, st, af, p, o, N, count, (int)m, (int)k, &status);
+        keep_selection(d, op, rec, kSetReason, "one Int4MatMul launch per matrix: each would "
+                       "read the shared rows and pay its own launch");
         return finish(d, e, status, "Int4MatMulSet launch");
     }
     for (int i = 0; i < count; i++) {
-        const int rc = run_int4_product(d, st, a->data, ACCEL_F32, &w[i], out[i].data, (int)m,
+        const int rc = run_int4_product(d, st, "Int4MatMul", a->data, ACCEL_F32, &w[i],
+                                        out[i].data, (int)m,
                                         (int)k, N[i]);
         if (rc != ACCEL_OK) return rc;
     }
@@ -436,8 +615,8 @@ ACCEL_API int accel_int4_matmul(int dev, void* stream, const accel_tensor_t* a,
     if (rc != ACCEL_OK) return rc;
     Device* d = device(dev);
     if (!d) return ACCEL_E_NO_DEVICE;
-    return run_int4_product(d, (hipStream_t)stream, a->data, a->dtype, w, out->data, (int)m,
-                            (int)k, (int)n);
+    return run_int4_product(d, (hipStream_t)stream, "Int4MatMul", a->data, a->dtype, w,
+                            out->data, (int)m, (int)k, (int)n);
 }
 
 // The int4 analogue of tensor.Linear (tensor/matmul.go:184-225): the
@@ -512,8 +691,8 @@ ACCEL_API int accel_int4_linear(int dev, void* stream, const accel_tensor_t* x,
     Epilogue ep;
     ep.bias = bias ? static_cast<const float*>(bias->data) : nullptr;
     ep.bf16 = out->dtype == ACCEL_BF16;
-    return run_int4_product(d, (hipStream_t)stream, x->data, x->dtype, w, out->data, (int)m,
-                            (int)k, (int)n, ep);
+    return run_int4_product(d, (hipStream_t)stream, "Int4Linear", x->data, x->dtype, w,
+                            out->data, (int)m, (int)k, (int)n, ep);
 }
 
 ACCEL_API int accel_segment_offsets(int dev, void* stream, const accel_tensor_t* counts,
@@ -1011,6 +1190,91 @@ uint32_t u32_at(const void* p, size_t off) {
 }
 
 }  // namespace
+
+// ---- the selection report ------------------------------------------------
+
+namespace {
+
+// The device a selection is planned for: an open device, or (dev < 0) an
+// MI355X as this library models it, so the question can be asked on a host
+// without a GPU.
+Device* selection_device(int dev) {
+    if (dev >= 0) return device(dev);
+    static Device model;
+    model.cu_count = 256;
+    // a placeholder for the static scratch's address: a dry plan computes
+    // offsets from it and launches nothing
+    model.scratch = reinterpret_cast<void*>(uintptr_t(1) << 41);
+    return &model;
+}
+
+}  // namespace
+
+// Which kernels an int4 product would become on device dev (dev < 0: the
+// modelled MI355X), and why, without launching or allocating anything.
+// op names the entry point: "Int4MatVec", "Int4MatMul", "Int4Linear" or
+// "Int4MatVecNoAlloc" (NULL: Int4MatVec for M = 1, else Int4MatMul).
+ACCEL_API int accel_int4_select(int dev, const char* op, int32_t dtype, int64_t M, int64_t K,
+                                int64_t N, const void* a, const accel_int4_t* w, int32_t flags,
+                                accel_selection_t* sel) {
+    clear_error();
+    if (!sel) return fail(ACCEL_E_INVALID, "accel_int4_select: no selection to fill");
+    if (dtype != ACCEL_F32 && dtype != ACCEL_BF16)
+        return fail(ACCEL_E_INVALID, "accel_int4_select: activations are %s; int4 products "
+                                     "read f32 or bf16", dtype_name(dtype));
+    if (M < 0 || K < 1 || N < 0 || M > INT32_MAX || K > INT32_MAX || N > INT32_MAX)
+        return fail(ACCEL_E_INVALID, "accel_int4_select: [%lld, %lld] x [%lld, %lld] is not a "
+                    "product this backend takes", (long long)M, (long long)K, (long long)K,
+                    (long long)N);
+    std::string name = op ? op : (M == 1 ? "Int4MatVec" : "Int4MatMul");
+    Device* d = selection_device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    // plane addresses matter only for their alignment
+    const void* fake = reinterpret_cast<const void*>(uintptr_t(1) << 20);
+    Int4Planes p{static_cast<const uint32_t*>(w && w->codes ? w->codes : fake),
+                 static_cast<const uint16_t*>(w && w->scales ? w->scales : fake),
+                 static_cast<const uint16_t*>(w && w->zeros ? w->zeros : fake)};
+    if (!a) a = fake;
+    Epilogue ep;
+    ep.bias = (flags & ACCEL_SELECT_BIAS) ? static_cast<const float*>(fake) : nullptr;
+    ep.bf16 = dtype == ACCEL_BF16 || (flags & ACCEL_SELECT_BF16_OUT) != 0;
+    void* out = const_cast<void*>(fake);
+    int status = ACCEL_OK;
+    LaunchRecord rec(true);
+    if (name == "Int4MatVecNoAlloc") {
+        if (dtype != ACCEL_F32 || M != 1)
+            return fail(ACCEL_E_INVALID, "accel_int4_select: Int4MatVecNoAlloc takes one f32 "
+                                         "row");
+        (void)launch_int4_matvec_noalloc(d, nullptr, static_cast<const float*>(a), p,
+                                         static_cast<float*>(out), (int)K, (int)N, &status);
+        if (status != ACCEL_OK) return status;
+        fill_selection(sel, name, rec.joined(),
+                       "Int4MatVec's kernels and plan, the split-K sums in the static scratch",
+                       "the workspace: it may call hipMalloc to grow");
+        return ACCEL_OK;
+    }
+    const Int4Choice c = choose_int4(dtype, a, p.codes, (int)M, (int)K, (int)N);
+    (void)launch_int4_route(d, nullptr, c.route, a, p, out, (int)M, (int)K, (int)N, ep,
+                            &status);
+    if (status != ACCEL_OK) return status;
+    fill_selection(sel, name, rec.joined(), c.reason, join(c.rejected, "; "));
+    return ACCEL_OK;
+}
+
+// What the last int4 product on device dev became (any int4 product entry
+// point; the set entry points and Int4MatVecNoAlloc included).
+ACCEL_API int accel_hip_last_selection(int dev, accel_selection_t* sel) {
+    clear_error();
+    if (!sel) return fail(ACCEL_E_INVALID, "accel_hip_last_selection: no selection to fill");
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    std::lock_guard<std::mutex> lk(d->mu);
+    if (!d->sel_valid)
+        return fail(ACCEL_E_INVALID, "accel_hip_last_selection: device %d has run no int4 "
+                                     "product since it was opened", dev);
+    fill_selection(sel, d->sel_op, d->sel_kernel, d->sel_reason, d->sel_rejected);
+    return ACCEL_OK;
+}
 
 ACCEL_API int accel_hip_supports_kernel(const char* kernel) {
     if (!kernel) return 0;

@@ -31,6 +31,24 @@ int fail(int code, const char* fmt, ...) {
 
 void clear_error() { g_last_error[0] = '\0'; }
 
+namespace {
+thread_local LaunchRecord* g_record = nullptr;
+}  // namespace
+
+LaunchRecord::LaunchRecord(bool dry_) : outer(g_record), dry(dry_ || (g_record && g_record->dry)) {
+    g_record = this;
+}
+LaunchRecord::~LaunchRecord() { g_record = outer; }
+LaunchRecord* launch_record() { return g_record; }
+std::string LaunchRecord::joined() const {
+    std::string s;
+    for (size_t i = 0; i < names.size(); i++) {
+        if (i) s += " + ";
+        s += names[i];
+    }
+    return s;
+}
+
 Device* device(int dev) {
     if (dev < 0 || dev >= kMaxDevices) {
         fail(ACCEL_E_NO_DEVICE, "accel_hip: device %d does not exist", dev);
@@ -111,6 +129,8 @@ bool capturing(hipStream_t st) {
 void* workspace(Device* d, hipStream_t st, size_t bytes, int* status) {
     *status = ACCEL_OK;
     const size_t need = kWorkspaceCounterBytes + bytes;
+    // planning a selection: an address to compute offsets from, never used
+    if (dry_run()) return reinterpret_cast<void*>(uintptr_t(1) << 40);
     std::lock_guard<std::mutex> lk(d->mu);
     if (d->ws && d->ws_bytes >= need) return d->ws;
     if (capturing(st)) {
@@ -246,7 +266,9 @@ ACCEL_API int accel_hip_open(int dev) {
                     dev, p.gcnArchName);
     if (!d->fault_host) {
         void* h = nullptr;
-        e = hipHostMalloc(&h, 64, hipHostMallocDefault);
+        // mapped and coherent (fine-grained): the kernels' system-scope
+        // atomics must reach the host whatever HIP_HOST_COHERENT says
+        e = hipHostMalloc(&h, 64, hipHostMallocMapped | hipHostMallocCoherent);
         if (e != hipSuccess) return classify(nullptr, e, "fault word allocation");
         void* dp = nullptr;
         e = hipHostGetDevicePointer(&dp, h, 0);
@@ -269,6 +291,7 @@ ACCEL_API int accel_hip_open(int dev) {
     d->lost.store(0);
     d->submissions = 0;
     d->lose_at = 0;
+    d->sel_valid = false;
     d->open = true;
     return ACCEL_OK;
 }

@@ -322,8 +322,14 @@ int accel_int4_g32_matvec(int dev, void* stream, const accel_tensor_t* a,
  * call hipMalloc to grow).  No counterpart in the reference: it is for
  * callers that cannot allocate (code under graph capture, serving loops,
  * harnesses that forbid hipMalloc).  Refused (ACCEL_E_INVALID) when the
- * shape's split-K sums exceed 4 MiB (e.g. N > 16384 at K >= 16384).  Calls
- * that overlap on one GPU share the array and race; serialize them. */
+ * shape's split-K sums exceed 4 MiB: slices * N * 4 > 4 MiB, where the
+ * column tile is 512 for N >= 8192 with N % 512 == 0 (slices =
+ * min(64, ceil(K / 128))), else 256 for N % 256 == 0 (slices =
+ * min(64, ceil(K / 256))), else 128 (slices = min(64, ceil(K / 512))).
+ * So N <= 16384 passes at any K, and a 4096 x 128256 LM head (256-
+ * column tiles, 16 slices, 8.2 MB of sums) is refused; accel_int4_select
+ * answers the same question without running anything.  Calls that overlap
+ * on one GPU share the array and race; serialize them. */
 int accel_int4_matvec_noalloc(int dev, void* stream, const accel_tensor_t* a,
                               const accel_int4_t* w, accel_tensor_t* out);
 
@@ -365,6 +371,44 @@ int accel_int4_matmul(int dev, void* stream, const accel_tensor_t* a,
 int accel_int4_linear(int dev, void* stream, const accel_tensor_t* x,
                       const accel_int4_t* w, const accel_tensor_t* bias,
                       accel_tensor_t* out);
+
+/* Which kernel an operator became, and why: KernelSelection{Op, Kernel,
+ * Reason, Rejected} (tensor/compile.go:36-42), as Plan.Selections reports it
+ * (tensor/plan.go:36-41), for the int4 products.  kernel lists the launches
+ * in order, " + " between them, each named as a profiler's kernel trace
+ * names it (template arguments included) with its grid in brackets;
+ * rejected lists the routes turned down, each with its reason, "; " between
+ * them.  Strings are NUL-terminated and cut to fit. */
+typedef struct accel_selection {
+    char op[32];
+    char kernel[320];
+    char reason[320];
+    char rejected[1024];
+} accel_selection_t;
+
+#define ACCEL_SELECT_BIAS 1       /* the product adds a bias (Int4Linear) */
+#define ACCEL_SELECT_BF16_OUT 2   /* f32 rows with a bf16 result (Int4Linear) */
+
+/* The selection an int4 product of [M, K] x [K, N] with activations of
+ * `dtype` (ACCEL_F32 or ACCEL_BF16) at `a` over the planes of `w` would
+ * make on device dev, planned without launching or allocating anything (the
+ * addresses matter only for their alignment; NULL a or w: 256-byte aligned).
+ * dev < 0 plans for an MI355X as this library models it (256 CUs), so the
+ * question can be asked on a host without a GPU.  op is "Int4MatVec",
+ * "Int4MatMul", "Int4Linear" or "Int4MatVecNoAlloc" (NULL: Int4MatVec for
+ * M = 1, else Int4MatMul); flags are ACCEL_SELECT_*.  For Int4MatVecNoAlloc
+ * it returns that entry point's refusal (ACCEL_E_INVALID) for a shape whose
+ * split-K sums exceed its static scratch, so a caller can ask before it
+ * captures.  No reference counterpart as one call: the reference reports a
+ * selection only from a compiled plan. */
+int accel_int4_select(int dev, const char* op, int32_t dtype, int64_t M, int64_t K, int64_t N,
+                      const void* a, const accel_int4_t* w, int32_t flags,
+                      accel_selection_t* sel);
+
+/* The selection the last int4 product on device dev made (Int4MatVec,
+ * Int4MatMul, Int4Linear, the sets and Int4MatVecNoAlloc), as launched;
+ * ACCEL_E_INVALID before the first. */
+int accel_hip_last_selection(int dev, accel_selection_t* sel);
 
 /* The SegmentOffsets node (tensor/segment.go:31-50;
  * internal/kernels/segment.go:40-50): offsets[r] = sum of counts[<r],

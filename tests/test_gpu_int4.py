@@ -222,31 +222,60 @@ def test_bf16_products_match_the_oracle(dev, M, K, N):
     assert rel_l2(got, want) <= BF16_TOL
 
 
-def test_config3_shape_in_f32_sampled_rows(dev):
+# Config 3's full-size checks (both dtypes): 64 seeded rows and the first and
+# last row of every 256-row band against the oracle row for row, and every
+# row through f64 checksums per band of the output columns: the plain column
+# sum, one weighted by the row's position in its band (which a row moved far
+# or a wrong band changes) and two with seeded Gaussian weights per row
+# (which a dropped, duplicated or swapped row changes, neighbours included).
+# A checksum's tolerance: bf16 rounding of the outputs is ~0.11% rms per
+# element and, the outputs having random signs, about as much relative to a
+# band's sum, so 5e-3 holds it with room while one wrong row of a 256-row band
+# moves the sum by ~1/16; f32 sums keep the f32 tolerance.
+SUM_TOL_BF16 = 5e-3
+
+
+def _full_size_rows(got, L, row_tol, sum_tol, bf16):
+    M = L.M
+    rng = np.random.Generator(np.random.PCG64(2048))
+    rows = set(rng.choice(M, 64, replace=False).tolist())
+    for b0 in range(0, M, 256):
+        rows |= {b0, min(M, b0 + 256) - 1}
+    rows = np.array(sorted(rows))
+    if bf16:
+        want = _bf16_oracle(L.x, L.packed, L.scales, L.zeros, M, L.K, L.N, rows=rows)
+    else:
+        want = oracle.quant_matmul_int4(np.ascontiguousarray(L.x[rows]), L.packed, L.scales,
+                                        L.zeros, len(rows), L.K, L.N, threads=8)
+    assert rel_l2(got[rows], want) <= row_tol, rel_l2(got[rows], want)
+    for r in rows:   # row for row, so one wrong row is seen on its own
+        assert rel_l2(got[r], want[list(rows).index(r)]) <= row_tol, r
+    wd = oracle.int4_dequantize(L.packed, L.scales, L.zeros, L.K * L.N).reshape(L.K, L.N)
+    wd = wd.astype(np.float64)
+    g = got.astype(np.float64)
+    for b0 in range(0, M, 256):
+        b1 = min(M, b0 + 256)
+        xs = L.x[b0:b1].astype(np.float64)
+        pos = np.arange(1, b1 - b0 + 1, dtype=np.float64)[:, None]
+        gauss = np.random.Generator(np.random.PCG64(b0)).standard_normal((2, b1 - b0, 1))
+        for weights in (np.ones_like(pos), pos, gauss[0], gauss[1]):
+            have = (weights * g[b0:b1]).sum(axis=0)
+            expect = (weights * xs).sum(axis=0) @ wd
+            assert rel_l2(have, expect) <= sum_tol, (b0, rel_l2(have, expect))
+
+
+def test_config3_shape_in_f32_full_size(dev):
     # config 3's product in the reference API's dtype: f32 activations and
-    # result on the matrix cores, against the oracle on sampled rows and a
-    # column-sum checksum of every row in f64
+    # result on the matrix cores
     L = workloads.linear(2048, 4096, 4096, seed=2)
     got = run_matmul(dev, L.x, L.packed, L.scales, L.zeros, L.M, L.K, L.N)
-    rows = np.array([0, 1, 127, 128, 1000, 1023, 1024, 2047])
-    want = oracle.quant_matmul_int4(np.ascontiguousarray(L.x[rows]), L.packed, L.scales,
-                                    L.zeros, len(rows), L.K, L.N, threads=8)
-    assert rel_l2(got[rows], want) <= F32_TOL
-    wd = oracle.int4_dequantize(L.packed, L.scales, L.zeros, L.K * L.N).reshape(L.K, L.N)
-    col_sums = L.x.astype(np.float64).sum(axis=0) @ wd.astype(np.float64)
-    assert rel_l2(got.astype(np.float64).sum(axis=0), col_sums) <= F32_TOL
+    _full_size_rows(got, L, F32_TOL, F32_TOL, bf16=False)
 
 
-def test_config3_prefill_full_size_sampled_rows(dev):
+def test_config3_prefill_full_size(dev):
     L = workloads.linear(**workloads.CONFIGS["prefill_m2048"])
     got = run_matmul(dev, L.x, L.packed, L.scales, L.zeros, L.M, L.K, L.N, bf16=True)
-    rows = np.array([0, 1, 127, 128, 1000, 1023, 1024, 2047])
-    want = _bf16_oracle(L.x, L.packed, L.scales, L.zeros, L.M, L.K, L.N, rows=rows)
-    assert rel_l2(got[rows], want) <= BF16_TOL
-    # every row: a checksum of the product (ones @ out == (ones @ x) @ W) in f64
-    wd = oracle.int4_dequantize(L.packed, L.scales, L.zeros, L.K * L.N).reshape(L.K, L.N)
-    col_sums = (L.x.astype(np.float64).sum(axis=0) @ wd.astype(np.float64))
-    assert rel_l2(got.astype(np.float64).sum(axis=0), col_sums) <= BF16_TOL
+    _full_size_rows(got, L, BF16_TOL, SUM_TOL_BF16, bf16=True)
 
 
 # ---- the backend seam -----------------------------------------------------------

@@ -93,3 +93,37 @@ def test_noalloc_under_graph_capture(dev):
     for b in (a, eager, replayed):
         b.free()
     w.free()
+
+
+def test_noalloc_never_asks_for_the_workspace(dev):
+    """After a reopen the device has no workspace, and any call that asked
+    for one would allocate it and bump the generation: the no-allocation
+    entry point, eager and under capture, leaves the generation where it
+    was."""
+    dev.close()
+    accel_amd.Device(dev.index)
+    gen0, _ = dev.workspace_generation()
+    rng = np.random.Generator(np.random.PCG64(43))
+    K, N = 4096, 4096
+    p, s, z = workloads.fast_int4(K, N, rng)
+    x = rng.standard_normal(K).astype(np.float32)
+    w = dev.upload_int4(p, s, z, K * N)
+    a = dev.upload(x)
+    eager, replayed = dev.alloc((N,), F32), dev.alloc((N,), F32)
+    dev.Int4MatVecNoAlloc(a, w, eager)
+    dev.sync()
+    assert dev.workspace_generation()[0] == gen0
+    stream = dev.stream()
+    dev.capture_begin(stream)
+    dev.Int4MatVecNoAlloc(a, w, replayed, stream)
+    ex = dev.capture_end(stream)
+    dev.launch(ex, stream)
+    dev.sync(stream)
+    assert dev.workspace_generation()[0] == gen0
+    assert np.array_equal(replayed.numpy().view(np.uint32), eager.numpy().view(np.uint32))
+    assert rel_l2(eager.numpy(), oracle.quant_matvec_int4(x, p, s, z, K, N)) <= 1e-5
+    dev.destroy_exec(ex)
+    dev.destroy_stream(stream)
+    for b in (a, eager, replayed):
+        b.free()
+    w.free()
