@@ -169,6 +169,11 @@ SIGNATURES = {
                            ctypes.c_int64, _vp, _P(Int4Desc), ctypes.c_int32,
                            _P(SelectionDesc)], _i),
     "accel_hip_last_selection": ([_i, _P(SelectionDesc)], _i),
+    "accel_int4_prepare": ([_i, _vp, _P(Int4Desc), ctypes.c_int64, ctypes.c_int64, _P(_vp)], _i),
+    "accel_int4_prepared_free": ([_i, _vp], _i),
+    "accel_int4_prepared_bytes": ([_vp, _P(ctypes.c_uint64)], _i),
+    "accel_int4_matvec_prepared": ([_i, _vp, _P(Tensor), _vp, _P(Tensor)], _i),
+    "accel_int4_matvec_prepared_set": ([_i, _vp, _P(Tensor), _P(_vp), _P(Tensor), _i], _i),
     "accel_int4_matvec_set": ([_i, _vp, _P(Tensor), _P(Int4Desc), _P(Tensor), _i], _i),
     "accel_int4_matmul_set": ([_i, _vp, _P(Tensor), _P(Int4Desc), _P(Tensor), _i], _i),
     "accel_segment_offsets": ([_i, _vp, _P(Tensor), _P(Tensor)], _i),
@@ -409,6 +414,25 @@ class Buffer:
             self.ptr = 0
 
 
+class PreparedInt4:
+    """An Int4 weight bound for one-row products (accel_int4_prepare): the
+    library's K-major panel copy of its planes, K x N."""
+
+    def __init__(self, device: "Device", handle: int, K: int, N: int):
+        self.device, self.handle, self.K, self.N = device, handle, K, N
+
+    @property
+    def nbytes(self) -> int:
+        n = ctypes.c_uint64()
+        _check(_lib.accel_int4_prepared_bytes(self.handle, ctypes.byref(n)))
+        return n.value
+
+    def free(self) -> None:
+        if self.handle:
+            _check(_lib.accel_int4_prepared_free(self.device.index, self.handle))
+            self.handle = None
+
+
 @dataclass
 class Int4Weights:
     """tensor.Int4 on the device: codes, scales, zeros and the weight count."""
@@ -558,6 +582,30 @@ class Device:
         ta, tw, to = a.tensor(), w.desc(), out.tensor()
         _check(_lib.accel_int4_matvec(self.index, stream, ctypes.byref(ta), ctypes.byref(tw),
                                       ctypes.byref(to)))
+
+    def prepare_int4(self, w: "Int4Weights", K: int, N: int, stream=None) -> PreparedInt4:
+        """Binds w for one-row products (accel_int4_prepare): a panel copy of
+        its planes, made on the device and waited for."""
+        h = ctypes.c_void_p()
+        tw = w.desc()
+        _check(_lib.accel_int4_prepare(self.index, stream, ctypes.byref(tw), int(K), int(N),
+                                       ctypes.byref(h)))
+        return PreparedInt4(self, h.value, int(K), int(N))
+
+    def Int4MatVecPrepared(self, a: Buffer, w: PreparedInt4, out: Buffer, stream=None) -> None:
+        ta, to = a.tensor(), out.tensor()
+        _check(_lib.accel_int4_matvec_prepared(self.index, stream, ctypes.byref(ta), w.handle,
+                                               ctypes.byref(to)))
+
+    def Int4MatVecPreparedSet(self, a: Buffer, ws, outs, stream=None) -> None:
+        """Int4MatVecPrepared of each of ws (1..4 prepared weights sharing the
+        input vector a) into outs, in one launch."""
+        n = len(ws)
+        hs = (ctypes.c_void_p * max(n, 1))(*[w.handle for w in ws])
+        outt = (Tensor * max(n, 1))(*[o.tensor() for o in outs])
+        ta = a.tensor()
+        _check(_lib.accel_int4_matvec_prepared_set(self.index, stream, ctypes.byref(ta), hs,
+                                                   outt, n))
 
     def Int4MatVecNoAlloc(self, a: Buffer, w: Int4Weights, out: Buffer, stream=None) -> None:
         """Int4MatVec with its split-K buffers in the library's static scratch

@@ -21,7 +21,7 @@ LIB = os.path.join(HERE, "libaccel_hip.so")
 ARCH = "gfx950"
 
 SOURCES = ["runtime.cpp", "quant.cpp", "ops.cpp", "decode.hip", "gemm.hip",
-           "grouped.hip", "quantize.hip", "step.hip", "int8.hip", "repack.cpp"]
+           "grouped.hip", "quantize.hip", "step.hip", "int8.hip", "repack.cpp", "panel.hip"]
 
 COMMON = [
     f"--offload-arch={ARCH}",

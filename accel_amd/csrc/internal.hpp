@@ -289,6 +289,18 @@ hipError_t launch_int4_grouped_bf16(Device* d, hipStream_t st, const uint16_t* x
                                     Int4Planes w, const uint32_t* off, uint16_t* out,
                                     int E, int T, int K, int N, bool write_padding);
 
+// Prepared (bind-time) weights for one-row products: the planes copied into
+// 16-column K-major panels and per-group scale/zero rows (panel.hip).
+bool int4_panel_supported(int64_t K, int64_t N);
+size_t int4_panel_bytes(int K, int N, size_t* sz_offset);
+hipError_t launch_int4_panel_prepare(hipStream_t st, Int4Planes w, void* dst, int K, int N);
+// a f32 [K] -> out[i] [N[i]] (f32, or bf16 with ep.bf16) over `count` (1..4)
+// prepared matrices of K rows, in one launch.
+constexpr int kMaxPreparedSet = 4;
+hipError_t launch_int4_panel_matvec(hipStream_t st, const float* a, const void* const* prepared,
+                                    void* const* out, const int* N, int count, int K,
+                                    Epilogue ep);
+
 // Decode-step neighbours: MatVecF32F16 (f32 a [K], f16 w [K,N] -> f32 [N]),
 // SwiGLU over n elements, RMSNorm over `rows` rows of `width`.
 hipError_t launch_matvec_f32_f16(Device* d, hipStream_t st, const float* a, const uint16_t* w,

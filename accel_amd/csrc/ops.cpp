@@ -1191,6 +1191,191 @@ uint32_t u32_at(const void* p, size_t off) {
 
 }  // namespace
 
+// ---- prepared (bind-time) weights ----------------------------------------
+
+// An Int4 weight bound once for one-row products: its planes copied into the
+// K-major panel layout (panel.hip).  Owned by the caller; freed with
+// accel_int4_prepared_free.
+struct accel_int4_prepared {
+    uint32_t magic;
+    int dev;
+    int64_t K, N;
+    void* data;
+    size_t bytes;
+};
+static constexpr uint32_t kPreparedMagic = 0x34544e49u;   // "INT4"
+
+ACCEL_API int accel_int4_prepare(int dev, void* stream, const accel_int4_t* w, int64_t K,
+                                 int64_t N, accel_int4_prepared_t** out) {
+    clear_error();
+    const char* op = "Int4Prepare";
+    if (!out) return refuse(op, "no handle to return the prepared weight in");
+    *out = nullptr;
+    std::string why = check_int4(w, "the weight matrix");
+    if (!why.empty()) return refuse(op, why);
+    char buf[320];
+    if (K < 1 || N < 1 || w->weights != K * N) {
+        snprintf(buf, sizeof buf, "[%lld, %lld] is %lld weights and the matrix holds %lld",
+                 (long long)K, (long long)N, (long long)(K * N), (long long)w->weights);
+        return refuse(op, buf);
+    }
+    if (!int4_panel_supported(K, N)) {
+        snprintf(buf, sizeof buf,
+                 "[%lld, %lld]: the panel layout takes N a multiple of 128 (whole groups in "
+                 "a row) and K, N below 2^30",
+                 (long long)K, (long long)N);
+        return refuse(op, buf);
+    }
+    if ((reinterpret_cast<uintptr_t>(w->codes) & 7) != 0)
+        return refuse(op, "the code plane must be 8-byte aligned");
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    int status = begin_submission(d);
+    if (status != ACCEL_OK) return status;
+    const size_t bytes = int4_panel_bytes((int)K, (int)N, nullptr);
+    void* data = nullptr;
+    hipError_t e = hipMalloc(&data, bytes);
+    if (e != hipSuccess) return classify(d, e, "prepared weight allocation");
+    hipStream_t st = (hipStream_t)stream;
+    e = launch_int4_panel_prepare(st, planes(w), data, (int)K, (int)N);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess) {
+        (void)hipFree(data);
+        return classify(d, e, "prepared weight copy");
+    }
+    auto* p = new accel_int4_prepared{kPreparedMagic, dev, K, N, data, bytes};
+    *out = p;
+    return ACCEL_OK;
+}
+
+ACCEL_API int accel_int4_prepared_free(int dev, accel_int4_prepared_t* p) {
+    clear_error();
+    if (!p) return ACCEL_OK;
+    if (p->magic != kPreparedMagic || p->dev != dev)
+        return fail(ACCEL_E_INVALID, "accel_int4_prepared_free: not a prepared weight of "
+                                     "device %d", dev);
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    const hipError_t e = hipFree(p->data);
+    p->magic = 0;
+    delete p;
+    return classify(d, e, "prepared weight free");
+}
+
+ACCEL_API int accel_int4_prepared_bytes(const accel_int4_prepared_t* p, uint64_t* bytes) {
+    clear_error();
+    if (!p || p->magic != kPreparedMagic || !bytes)
+        return fail(ACCEL_E_INVALID, "accel_int4_prepared_bytes: not a prepared weight");
+    *bytes = p->bytes;
+    return ACCEL_OK;
+}
+
+// Int4MatVec over a prepared weight: Int4MatVec's checks on a and out, the
+// product from the panel layout (one launch, no workspace).
+ACCEL_API int accel_int4_matvec_prepared(int dev, void* stream, const accel_tensor_t* a,
+                                         const accel_int4_prepared_t* w, accel_tensor_t* out) {
+    clear_error();
+    const char* op = "Int4MatVecPrepared";
+    if (!w || w->magic != kPreparedMagic) return refuse(op, "the prepared weight is missing");
+    if (w->dev != dev) {
+        char b[128];
+        snprintf(b, sizeof b, "the weight was prepared on device %d", w->dev);
+        return refuse(op, b);
+    }
+    if (!valid_tensor(a) || !a->data) return refuse(op, "the activations are missing");
+    char buf[320];
+    if (a->dtype != ACCEL_F32 || a->rank != 1) {
+        snprintf(buf, sizeof buf,
+                 "activations are %s %s; a matvec takes an f32 vector, and a batch of them is "
+                 "the tiled form, Int4MatMul",
+                 dtype_name(a->dtype), shape_str(a).c_str());
+        return refuse(op, buf);
+    }
+    if (a->shape[0] != w->K) {
+        snprintf(buf, sizeof buf, "activations are %lld long and the matrix is [%lld, %lld]",
+                 (long long)a->shape[0], (long long)w->K, (long long)w->N);
+        return refuse(op, buf);
+    }
+    int rc = check_out(op, out, ACCEL_F32, 1, w->N, true);
+    if (rc != ACCEL_OK) return rc;
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    int status = begin_submission(d);
+    if (status != ACCEL_OK) return status;
+    LaunchRecord rec(false);
+    const void* data = w->data;
+    void* o = out->data;
+    const int n = (int)w->N;
+    const hipError_t e = launch_int4_panel_matvec((hipStream_t)stream,
+                                                  static_cast<const float*>(a->data), &data, &o,
+                                                  &n, 1, (int)w->K, Epilogue{});
+    keep_selection(d, op, rec,
+                   "a prepared weight: one workgroup a 16-column K-major panel over all of K, "
+                   "no K split and no hand-off",
+                   "the reference-format decode kernel: a column tile of those planes reads a "
+                   "narrow strip of every row, so K is split across workgroups and the slices "
+                   "meet in a hand-off");
+    return finish(d, e, status, "Int4MatVecPrepared launch");
+}
+
+// Int4MatVec over up to four prepared weights that share one input vector,
+// in one launch (a decode step's q, k, v or gate, up); each out[i] is exactly
+// accel_int4_matvec_prepared(a, w[i]).
+ACCEL_API int accel_int4_matvec_prepared_set(int dev, void* stream, const accel_tensor_t* a,
+                                             const accel_int4_prepared_t* const* w,
+                                             accel_tensor_t* out, int count) {
+    clear_error();
+    const char* op = "Int4MatVecPreparedSet";
+    char buf[320];
+    if (count < 1 || count > kMaxPreparedSet || !w || !out) {
+        snprintf(buf, sizeof buf, "%d matrices; a set holds one to %d", count, kMaxPreparedSet);
+        return refuse(op, buf);
+    }
+    if (!valid_tensor(a) || !a->data) return refuse(op, "the activations are missing");
+    if (a->dtype != ACCEL_F32 || a->rank != 1) {
+        snprintf(buf, sizeof buf, "activations are %s %s; a matvec takes an f32 vector",
+                 dtype_name(a->dtype), shape_str(a).c_str());
+        return refuse(op, buf);
+    }
+    const void* data[kMaxPreparedSet];
+    void* o[kMaxPreparedSet];
+    int N[kMaxPreparedSet];
+    for (int i = 0; i < count; i++) {
+        if (!w[i] || w[i]->magic != kPreparedMagic) {
+            snprintf(buf, sizeof buf, "prepared weight %d is missing", i);
+            return refuse(op, buf);
+        }
+        if (w[i]->dev != dev) {
+            snprintf(buf, sizeof buf, "weight %d was prepared on device %d", i, w[i]->dev);
+            return refuse(op, buf);
+        }
+        if (a->shape[0] != w[i]->K) {
+            snprintf(buf, sizeof buf, "activations are %lld long and matrix %d is [%lld, %lld]",
+                     (long long)a->shape[0], i, (long long)w[i]->K, (long long)w[i]->N);
+            return refuse(op, buf);
+        }
+        const int rc = check_out(op, &out[i], ACCEL_F32, 1, w[i]->N, true);
+        if (rc != ACCEL_OK) return rc;
+        data[i] = w[i]->data;
+        o[i] = out[i].data;
+        N[i] = (int)w[i]->N;
+    }
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    int status = begin_submission(d);
+    if (status != ACCEL_OK) return status;
+    LaunchRecord rec(false);
+    const hipError_t e = launch_int4_panel_matvec((hipStream_t)stream,
+                                                  static_cast<const float*>(a->data), data, o, N,
+                                                  count, (int)a->shape[0], Epilogue{});
+    keep_selection(d, op, rec,
+                   "prepared weights that share their input: their panels side by side in one "
+                   "launch, each matrix's results those of its own launch",
+                   "one launch per matrix: each would read the shared vector and pay its own "
+                   "launch");
+    return finish(d, e, status, "Int4MatVecPreparedSet launch");
+}
+
 // ---- the selection report ------------------------------------------------
 
 namespace {
@@ -1241,6 +1426,26 @@ ACCEL_API int accel_int4_select(int dev, const char* op, int32_t dtype, int64_t 
     void* out = const_cast<void*>(fake);
     int status = ACCEL_OK;
     LaunchRecord rec(true);
+    if (name == "Int4MatVecPrepared") {
+        if (dtype != ACCEL_F32 || M != 1)
+            return fail(ACCEL_E_INVALID, "accel_int4_select: Int4MatVecPrepared takes one f32 "
+                                         "row");
+        if (!int4_panel_supported(K, N))
+            return fail(ACCEL_E_INVALID, "accel_int4_select: [%lld, %lld] cannot be prepared "
+                        "(N a multiple of 128)", (long long)K, (long long)N);
+        const int n = (int)N;
+        const void* data = fake;
+        void* o = out;
+        (void)launch_int4_panel_matvec(nullptr, static_cast<const float*>(a), &data, &o, &n, 1,
+                                       (int)K, Epilogue{});
+        fill_selection(sel, name, rec.joined(),
+                       "a prepared weight: one workgroup a 16-column K-major panel over all of "
+                       "K, no K split and no hand-off",
+                       "the reference-format decode kernel: a column tile of those planes reads "
+                       "a narrow strip of every row, so K is split across workgroups and the "
+                       "slices meet in a hand-off");
+        return ACCEL_OK;
+    }
     if (name == "Int4MatVecNoAlloc") {
         if (dtype != ACCEL_F32 || M != 1)
             return fail(ACCEL_E_INVALID, "accel_int4_select: Int4MatVecNoAlloc takes one f32 "

@@ -580,6 +580,21 @@ __global__ __launch_bounds__(kFloorThreads) void floor_read_kernel(const floor_u
     if (x == 0x9e3779b9u) sink[blockIdx.x] = x;   // keeps the loads; almost never stores
 }
 
+// Reads `chunks` 16-byte chunks with a grid-stride loop and writes (almost)
+// nothing: evicts the device's caches with clean lines, so no writeback of
+// the eviction lands in the work timed after it (a copy would leave up to the
+// Infinity Cache's size of dirty lines behind).
+__global__ __launch_bounds__(256) void floor_evict_kernel(const floor_u32x4* src, size_t chunks,
+                                                          uint32_t* sink) {
+    uint32_t x = 0;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < chunks;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const floor_u32x4 v = __builtin_nontemporal_load(src + i);
+        x ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    if (x == 0x9e3779b9u) sink[blockIdx.x & 255] = x;
+}
+
 template <int L>
 void launch_floor_read(hipStream_t st, const void* src, size_t chunks, void* sink) {
     hipLaunchKernelGGL(floor_read_kernel<L>, dim3(kFloorBlocks), dim3(kFloorThreads), 0, st,
@@ -617,9 +632,18 @@ ACCEL_API int accel_hip_floor(int dev, void* stream, int kind, const void* src, 
             case 7: launch_floor_read<7>(st, src, chunks, sink); break;
             default: launch_floor_read<8>(st, src, chunks, sink); break;
         }
+    } else if (kind == 2) {
+        if (!src || bytes % 16 || reinterpret_cast<uintptr_t>(src) % 16 || bytes == 0)
+            return fail(ACCEL_E_INVALID,
+                        "accel_hip_floor: an eviction of %zu bytes needs a 16-byte aligned "
+                        "source and a multiple of 16 bytes",
+                        bytes);
+        hipLaunchKernelGGL(floor_evict_kernel, dim3(4096), dim3(256), 0, st,
+                           static_cast<const floor_u32x4*>(src), bytes / 16,
+                           static_cast<uint32_t*>(sink));
     } else {
-        return fail(ACCEL_E_INVALID, "accel_hip_floor: kind %d is neither 0 (empty) nor 1 (read)",
-                    kind);
+        return fail(ACCEL_E_INVALID,
+                    "accel_hip_floor: kind %d is not 0 (empty), 1 (read) or 2 (evict)", kind);
     }
     return classify(d, hipGetLastError(), "accel_hip_floor launch");
 }

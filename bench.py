@@ -51,7 +51,8 @@ BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, vendor figure
 METRIC = ("int4 linear: HBM GB/s (% peak) at M=1; TFLOP/s (% MFMA peak) at M=2048")
 ROTATE_BYTES = 544 << 20       # weight copies in rotation, > 2x the Infinity Cache
 TRAFFIC_FILE = os.path.join(HERE, "profiles", "traffic.json")
-GEMV_KERNEL = "int4_decode_f32_kernel<1, 256, 32, false, float>"
+GEMV_KERNEL = "int4_panel_matvec_kernel<4, false, true, true, false>"
+GEMV_REF_KERNEL = "int4_decode_f32_kernel<1, 256, 32, false, float>"
 GEMM_KERNEL = "int4_gemm_bf16_kernel<8, false>"
 GEMM_F32_KERNEL = "int4_gemm_f32x3_kernel"
 DECODE_MFMA_KERNEL = "int4_decode_mfma_kernel<2, 8, float>"
@@ -63,7 +64,8 @@ G32_KERNEL = "int4_g32_matvec_kernel"
 # blocks of up to 16 on the matrix cores
 GROUPED_DECODE_KERNELS = ("int4_grouped_decode_kernel<512, 32, true, float>",
                           "int4_grouped_decode_mfma_kernel<2, 8, float>")
-FLUSH_BYTES = 512 << 20        # device copy that evicts the Infinity Cache
+FLUSH_BYTES = 1 << 30          # device read that evicts the Infinity Cache
+EAGER_MAX = 64                 # timed regions of at most this many calls run as plain launches
 PUBLISHED_US = 760.0           # Int4MatVec [2048] x [2048,2048] on an M2, one plan a step
 PUBLISHED_SRC = "specs/010-kernel-corpus.md:593-602 (tensor/decodebench_darwin_test.go:148-189)"
 
@@ -111,23 +113,26 @@ def traffic_sum(kernels):
 
 
 class Flusher:
-    """Evicts the Infinity Cache with an untimed 512 MiB device-to-device copy,
-    so that the replay timed after it reads its weights from HBM."""
+    """Evicts the Infinity Cache with an untimed read of 1 GiB of device memory
+    (accel_hip_floor kind 2), so that the calls timed after it read their
+    weights from HBM.  A read, not a copy: a copy leaves up to the cache's
+    256 MB of dirty lines whose writeback would land in the timed region."""
 
     def __init__(self, dev):
         import accel_amd
         self.dev = dev
         self.src = dev.alloc((FLUSH_BYTES // 4,), accel_amd.U32)
-        self.dst = dev.alloc((FLUSH_BYTES // 4,), accel_amd.U32)
+        self.sink = dev.alloc((1024,), accel_amd.U32)
 
     def __call__(self, stream):
         import accel_amd
-        accel_amd._check(accel_amd.lib().accel_hip_copy(self.dev.index, stream, self.dst.ptr,
-                                                        self.src.ptr, FLUSH_BYTES))
+        accel_amd._check(accel_amd.lib().accel_hip_floor(self.dev.index, stream, 2,
+                                                         self.src.ptr, FLUSH_BYTES,
+                                                         self.sink.ptr))
 
     def free(self):
         self.src.free()
-        self.dst.free()
+        self.sink.free()
 
 
 _FLUSH = None
@@ -143,19 +148,24 @@ def flush(dev, stream):
 
 class Timed:
     """Captures `count` calls of `issue(i)` into a graph and times replays
-    with HIP events on the stream the graph runs on (or, with EAGER, issues
-    the calls as plain launches between the events).  The Infinity Cache is
-    flushed before every timed run."""
+    with HIP events on the stream the graph runs on (or, with EAGER or a
+    region of at most EAGER_MAX calls, issues the calls as plain launches
+    between the events).  The Infinity Cache is evicted before every timed
+    run, by a read that the calls and the events are queued behind, so the
+    host has queued the whole region before the device reaches it.  A short
+    region is timed as plain launches because a graph launch carries a fixed
+    start-up on the device (measured at config 1: 4.69 us a call at 20 steps
+    in a graph, 4.46 as plain launches, 4.35 either way at 640)."""
 
     def __init__(self, dev, stream, issue, count):
         self.dev, self.stream, self.issue, self.count = dev, stream, issue, count
         self.exec = None
-        if not EAGER:
+        self.e0, self.e1 = dev.event(), dev.event()
+        if not (EAGER or count <= EAGER_MAX):
             dev.capture_begin(stream)
             for i in range(count):
                 issue(i)
             self.exec = dev.capture_end(stream)
-        self.e0, self.e1 = dev.event(), dev.event()
         self.warm = False
 
     def _once(self):
@@ -165,20 +175,18 @@ class Timed:
             for i in range(self.count):
                 self.issue(i)
 
-    def run(self, replays: int = 1) -> float:
-        """Milliseconds for `replays` runs of the K calls, timed after one
-        untimed run (the first launch of a graph also uploads it)."""
+    def run(self) -> float:
+        """Milliseconds for the K calls, timed after one untimed run (the
+        first launch of a graph also uploads it)."""
         d = self.dev
         if not self.warm:
             self._once()
+            d.sync(self.stream)
             self.warm = True
         flush(d, self.stream)
-        d.sync(self.stream)
         d.record(self.e0, self.stream)
-        for _ in range(replays):
-            self._once()
+        self._once()
         d.record(self.e1, self.stream)
-        d.wait(self.e1)
         d.sync(self.stream)
         return d.elapsed_ms(self.e0, self.e1)
 
@@ -213,10 +221,23 @@ def rotated_weights(dev, stream, L, total_bytes=ROTATE_BYTES):
     return ws
 
 
-def time_product(dev, stream, L, call, steps, warmup, bf16=False):
-    """Per-call time of `call(a, w, out)` over rotated weights, in ms."""
+def time_product(dev, stream, L, call, steps, warmup, bf16=False, prepare=None):
+    """Per-call time of `call(a, w, out)` over rotated weights, in ms.  With
+    `prepare`, every copy is bound first (prepare(w), outside the timed
+    region, its reference planes then freed) and `call` takes the bound
+    weight."""
     from accel_amd import BF16, F32, workloads
     ws = rotated_weights(dev, stream, L)
+    bind_ms = None
+    if prepare is not None:
+        bound = []
+        for i, w in enumerate(ws):
+            t0 = time.perf_counter()
+            bound.append(prepare(w))
+            if i == 0:
+                bind_ms = (time.perf_counter() - t0) * 1e3
+            w.free()
+        ws = bound
     if bf16:
         a = dev.upload(workloads.bf16_bits(L.x), BF16)
         out = dev.alloc((L.M, L.N), BF16)
@@ -238,17 +259,27 @@ def time_product(dev, stream, L, call, steps, warmup, bf16=False):
         w.free()
     a.free()
     out.free()
+    if prepare is not None:
+        return ms, got, len(ws), bind_ms
     return ms, got, len(ws)
 
 
 def bench_gemv(dev, stream, steps, warmup):
+    """Config 1 on a bound weight: each rotated copy is prepared once
+    (accel_int4_prepare, outside the timed region, as a backend does when it
+    compiles a plan) and the step is Int4MatVecPrepared.  The same product on
+    the reference planes (accel_int4_matvec) is timed beside it."""
     from accel_amd import workloads
     L = workloads.linear(**workloads.CONFIGS["gemv_m1"])
-    ms, got, copies = time_product(dev, stream, L, lambda a, w, o, s: dev.Int4MatVec(a, w, o, s),
-                                   steps, warmup)
+    ms, got, copies, bind_ms = time_product(
+        dev, stream, L, lambda a, w, o, s: dev.Int4MatVecPrepared(a, w, o, s), steps, warmup,
+        prepare=lambda w: dev.prepare_int4(w, L.K, L.N, stream))
+    ms_ref, got_ref, _ = time_product(
+        dev, stream, L, lambda a, w, o, s: dev.Int4MatVec(a, w, o, s), steps, warmup)
     bytes_per = workloads.algorithmic_bytes(1, L.K, L.N)
     return dict(ms=ms, bytes=bytes_per, gbs=bytes_per / (ms * 1e-3) / 1e9, copies=copies,
-                L=L, out=got)
+                L=L, out=got, bind_ms=bind_ms, ms_ref=ms_ref,
+                gbs_ref=bytes_per / (ms_ref * 1e-3) / 1e9)
 
 
 def bench_gemv_g32(dev, stream, steps=640, warmup=64):
@@ -407,15 +438,20 @@ def layer_planes(rng):
     return _LAYER_PLANES
 
 
-def bench_layer_chain(dev, stream, batch, steps=100, merged=True, sets=5):
+def bench_layer_chain(dev, stream, batch, steps=100, merged=True, sets=5, prepared=None):
     """Config 5: one Llama-3-8B-shaped decoder layer's seven int4 products
-    as a decode step: q,k,v <- x; o <- q; gate,up <- o; down <- gate*up
-    (the gate*up product is the caller's; the step times the seven
-    products, chained on one stream).  merged: q, k, v and gate, up each as
-    one set (four launches, the same results bit for bit).  The layer's
-    115.9 MB of weights rotate over `sets` copies (580 MB), so with the cache
-    flushed before the timed replay each step reads its weights from HBM."""
+    as a decode step: q,k,v <- x; o <- q; gate,up <- o; down <- SwiGLU(gate,
+    up), the gate/up pair through tensor.SwiGLU (silu(gate) * up) on the
+    device, so the step is seven products and the one elementwise operation
+    that joins them.  merged: q, k, v and gate, up each as one set (the same
+    results bit for bit).  prepared (default: at batch 1): every matrix bound
+    once into the panel layout (outside the timed region) and the products
+    run as Int4MatVecPrepared[Set].  The layer's 115.9 MB of weights rotate
+    over `sets` copies (580 MB), so with the cache flushed before the timed
+    replay each step reads its weights from HBM."""
     from accel_amd import F32, workloads
+    if prepared is None:
+        prepared = batch == 1
     shapes = workloads.LAYER_SHAPES  # name -> (K, N)
     rng = np.random.Generator(np.random.PCG64(4))
     x = rng.standard_normal((batch, 4096)).astype(np.float32)
@@ -428,23 +464,33 @@ def bench_layer_chain(dev, stream, batch, steps=100, merged=True, sets=5):
         packed, scales, zeros = planes[name]
         total_bytes += packed.nbytes + scales.nbytes + zeros.nbytes
         bufs[name] = dev.alloc((batch, N) if batch > 1 else (N,), F32)
+    bind_ms = None
     for _ in range(sets):
-        wsets.append({name: dev.upload_int4(*planes[name], K * N)
-                      for name, (K, N) in shapes.items()})
+        ws = {name: dev.upload_int4(*planes[name], K * N) for name, (K, N) in shapes.items()}
+        if prepared:
+            t0 = time.perf_counter()
+            pws = {name: dev.prepare_int4(ws[name], K, N, stream)
+                   for name, (K, N) in shapes.items()}
+            bind_ms = bind_ms or (time.perf_counter() - t0) * 1e3
+            for w in ws.values():
+                w.free()
+            ws = pws
+        wsets.append(ws)
     xin = dev.upload(x if batch > 1 else x[0])
-    # the down projection's input (the caller's gate*up), as activations
-    hmid = rng.standard_normal((batch, 14336)).astype(np.float32)
-    inter = dev.upload(hmid if batch > 1 else hmid[0])
+    act = dev.alloc((batch, 14336) if batch > 1 else (14336,), F32)   # SwiGLU(gate, up)
 
     def op(a, w, o):
-        if batch > 1:
+        if prepared:
+            dev.Int4MatVecPrepared(a, w, o, stream)
+        elif batch > 1:
             dev.Int4MatMul(a, w, o, stream)
         else:
             dev.Int4MatVec(a, w, o, stream)
 
     def ops(a, ws, names):
         if merged:
-            fn = dev.Int4MatVecSet if batch == 1 else dev.Int4MatMulSet
+            fn = (dev.Int4MatVecPreparedSet if prepared else
+                  dev.Int4MatVecSet if batch == 1 else dev.Int4MatMulSet)
             fn(a, [ws[n] for n in names], [bufs[n] for n in names], stream)
         else:
             for n in names:
@@ -455,7 +501,8 @@ def bench_layer_chain(dev, stream, batch, steps=100, merged=True, sets=5):
         ops(xin, ws, ("q", "k", "v"))
         op(bufs["q"], ws["o"], bufs["o"])
         ops(bufs["o"], ws, ("gate", "up"))
-        op(inter, ws["down"], bufs["down"])
+        dev.SwiGLU(bufs["gate"], bufs["up"], act, stream)
+        op(act, ws["down"], bufs["down"])
 
     for i in range(sets):
         step(i)
@@ -466,22 +513,36 @@ def bench_layer_chain(dev, stream, batch, steps=100, merged=True, sets=5):
     for ws in wsets:
         for w in ws.values():
             w.free()
-    for b in list(bufs.values()) + [xin, inter]:
+    for b in list(bufs.values()) + [xin, act]:
         b.free()
-    act = 4 * batch * (4096 + 4096 + 4096 + 14336) + 4 * batch * (4096 + 1024 + 1024 + 4096
-                                                                   + 14336 + 14336 + 4096)
-    gbs = (total_bytes + act) / (ms * 1e-3) / 1e9
-    kernels = ("int4_decode_set_kernel + int4_decode_f32_kernel (VALU decode)" if batch == 1
-               else "int4_decode_mfma_set_kernel + int4_decode_mfma_kernel (matrix-core decode)")
-    return dict(workload=f"config 5: seven Llama-3-8B layer products as one decode step at "
-                         f"batch {batch} (q/k/v and gate/up as sets, {4 if merged else 7} "
-                         f"launches), f32 x, weights rotated over {sets} sets",
-                us_per_step=round(ms * 1e3, 2), batch=batch, launches=4 if merged else 7,
-                weight_bytes=total_bytes,
-                roofline={"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
-                          "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                          "traffic": None, "kernel": kernels,
-                          "bytes_per_step": int(total_bytes + act)})
+    # activations read and results written by the products, and SwiGLU's
+    # two reads and one write of the 14336-wide rows
+    act_bytes = 4 * batch * (4096 + 4096 + 4096 + 14336) + 4 * batch * (
+        4096 + 1024 + 1024 + 4096 + 14336 + 14336 + 4096) + 12 * batch * 14336
+    gbs = (total_bytes + act_bytes) / (ms * 1e-3) / 1e9
+    if prepared:
+        kernels = "int4_panel_matvec_kernel (prepared weights) + swiglu_kernel"
+    elif batch == 1:
+        kernels = "int4_decode_set_kernel + int4_decode_f32_kernel (VALU decode) + swiglu_kernel"
+    else:
+        kernels = ("int4_decode_mfma_set_kernel + int4_decode_mfma_kernel (matrix-core decode) "
+                   "+ swiglu_kernel")
+    launches = (4 if merged else 7) + 1
+    res = dict(workload=f"config 5: seven Llama-3-8B layer products as one decode step at "
+                        f"batch {batch}, down fed SwiGLU(gate, up) computed on the device "
+                        f"(q/k/v and gate/up as sets: {launches} launches), f32 x, "
+                        + ("weights bound once into the panel layout, " if prepared else
+                           "reference planes, ")
+                        + f"rotated over {sets} sets",
+               us_per_step=round(ms * 1e3, 2), batch=batch, launches=launches,
+               weight_bytes=total_bytes,
+               roofline={"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "traffic": None, "kernel": kernels,
+                         "bytes_per_step": int(total_bytes + act_bytes)})
+    if bind_ms is not None:
+        res["bind_ms_per_layer"] = round(bind_ms, 3)
+    return res
 
 
 def bench_published(dev, stream, steps=200):
@@ -997,8 +1058,11 @@ def main():
         "data": "synthetic",
         "config": {
             "workload": "Int4MatVec M=1 K=4096 N=4096 (BASELINE config 1's shape and the "
-                        "metric's M=1 leg) in the reference int4 format: 128-weight groups, "
-                        "f16 scale+zero; f32 activations and output; weights rotated over "
+                        "metric's M=1 leg) in the reference int4 format (128-weight groups, "
+                        "f16 scale+zero), the weight bound once into the backend's K-major "
+                        "panel layout (accel_int4_prepare, outside the timed region; "
+                        f"{r['bind_ms']:.2f} ms a matrix), then Int4MatVecPrepared; f32 "
+                        "activations and output; weights rotated over "
                         f"{r['copies']} device copies and the Infinity Cache flushed before "
                         "the timed replay, so every step reads HBM",
             "seed": 0,
@@ -1017,6 +1081,17 @@ def main():
     }
     if not args.no_extra:
         extra = {}
+        gref = r["gbs_ref"]
+        extra["gemv_m1_reference_planes"] = {
+            "workload": "config 1 on the reference planes as given (accel_int4_matvec: the "
+                        "decode kernel, K split across workgroups and a split-K hand-off), "
+                        "the same inputs, rotation and protocol as the headline",
+            "us": round(r["ms_ref"] * 1e3, 3),
+            "roofline": {"bound": "hbm", "achieved": round(gref, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(gref / HBM_PEAK_GBS, 4),
+                         "traffic": traffic_of(GEMV_REF_KERNEL), "kernel": GEMV_REF_KERNEL,
+                         "bytes_per_launch": r["bytes"]}}
+        extra["gemv_m1_bind_ms"] = round(r["bind_ms"], 3)
         progress("config 1 in BASELINE's literal format (G=32 along K, f32 scale)")
         extra["gemv_m1_g32_literal"] = bench_gemv_g32(dev, stream)
         progress("config 3: prefill M=2048 bf16")
@@ -1058,6 +1133,9 @@ def main():
         for b in (1, 8):
             progress(f"config 5: layer chain at batch {b}")
             extra[f"layer_chain_b{b}"] = bench_layer_chain(dev, stream, b)
+        progress("config 5 at batch 1 on the reference planes")
+        extra["layer_chain_b1_reference_planes"] = bench_layer_chain(dev, stream, 1,
+                                                                     prepared=False)
         progress("launch floors of the decode shape")
         extra["floors"] = bench_floors(dev, stream)
         progress("the reference's published workload (2048 x 2048, one wait a step)")

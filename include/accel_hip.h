@@ -169,8 +169,11 @@ int accel_hip_set_wait_limit(int dev, int32_t spins);
  * kernel's launch shape (256 workgroups of 512 lanes): kind 0 launches an
  * empty kernel; kind 1 reads `bytes` (a multiple of 16, at most 16 MiB) from
  * the 16-byte aligned device pointer `src` with 16-byte loads, all of a
- * lane's issued before any is used.  `sink` is a device buffer of at least
- * 1 KiB the read kernel may write.  Diagnostics for the benchmark. */
+ * lane's issued before any is used; kind 2 reads `bytes` (a multiple of 16,
+ * any size) from `src` with a grid-stride loop, which evicts the device's
+ * caches with clean lines (a copy would leave dirty lines whose writeback
+ * lands in the work after it).  `sink` is a device buffer of at least 1 KiB
+ * the read kernels may write.  Diagnostics for the benchmark. */
 int accel_hip_floor(int dev, void* stream, int kind, const void* src, size_t bytes, void* sink);
 int accel_hip_workspace_generation(int dev, uint64_t* gen, int32_t* retired);
 
@@ -372,6 +375,45 @@ int accel_int4_linear(int dev, void* stream, const accel_tensor_t* x,
                       const accel_int4_t* w, const accel_tensor_t* bias,
                       accel_tensor_t* out);
 
+/* A weight bound for one-row products (opaque; owned by the caller).  The
+ * reference binds a tensor.Int4's planes to a plan once
+ * (tensor/int4.go:82-127: Int4 is a Weight of the graph) and runs them many
+ * times; a backend may keep its own copy of a bound weight in the layout its
+ * kernels read best.  This one is K-major panels of 16 columns (each row's
+ * 8 code bytes, rows in pairs) with each group's f16 scale and zero side by
+ * side per row: one workgroup then owns a column strip over all of K, and
+ * the decode kernel's K split and its hand-off are gone.  The reference
+ * planes are not changed and stay the format everything else reads. */
+typedef struct accel_int4_prepared accel_int4_prepared_t;
+
+/* Copies w ([K, N] in the reference format: N % 128 == 0, 8-byte aligned
+ * codes) into a new device allocation in the panel layout, on `stream`, and
+ * waits for the copy.  The same bytes as the planes (plus one padding row
+ * for odd K).  No reference counterpart as one call: it is what a backend's
+ * GraphCompiler.Compile (internal/driver/plan.go:398-400) would do for an
+ * Int4 weight operand of a QuantMatVecInt4 node. */
+int accel_int4_prepare(int dev, void* stream, const accel_int4_t* w, int64_t K, int64_t N,
+                       accel_int4_prepared_t** out);
+int accel_int4_prepared_free(int dev, accel_int4_prepared_t* w);
+/* Device bytes the prepared copy holds. */
+int accel_int4_prepared_bytes(const accel_int4_prepared_t* w, uint64_t* bytes);
+
+/* tensor.Int4MatVec (tensor/int4.go:99-147) over a prepared weight: a f32
+ * [K] -> out f32 [N], the same arithmetic per weight as accel_int4_matvec
+ * (within f32 rounding of it: the sums are added in another order).  One
+ * launch; allocates nothing. */
+int accel_int4_matvec_prepared(int dev, void* stream, const accel_tensor_t* a,
+                               const accel_int4_prepared_t* w, accel_tensor_t* out);
+
+/* The same over `count` (1..4) prepared weights of K rows that share one f32
+ * vector a [K], out[i] f32 [N_i], in one launch; each out[i] is exactly
+ * accel_int4_matvec_prepared(a, w[i]).  No reference counterpart as one
+ * call: the plan-level merge of Int4MatVec dispatches that read the same
+ * activations (a decode step's q, k, v and gate, up). */
+int accel_int4_matvec_prepared_set(int dev, void* stream, const accel_tensor_t* a,
+                                   const accel_int4_prepared_t* const* w, accel_tensor_t* out,
+                                   int count);
+
 /* Which kernel an operator became, and why: KernelSelection{Op, Kernel,
  * Reason, Rejected} (tensor/compile.go:36-42), as Plan.Selections reports it
  * (tensor/plan.go:36-41), for the int4 products.  kernel lists the launches
@@ -395,7 +437,8 @@ typedef struct accel_selection {
  * addresses matter only for their alignment; NULL a or w: 256-byte aligned).
  * dev < 0 plans for an MI355X as this library models it (256 CUs), so the
  * question can be asked on a host without a GPU.  op is "Int4MatVec",
- * "Int4MatMul", "Int4Linear" or "Int4MatVecNoAlloc" (NULL: Int4MatVec for
+ * "Int4MatMul", "Int4Linear", "Int4MatVecPrepared" or "Int4MatVecNoAlloc"
+ * (NULL: Int4MatVec for
  * M = 1, else Int4MatMul); flags are ACCEL_SELECT_*.  For Int4MatVecNoAlloc
  * it returns that entry point's refusal (ACCEL_E_INVALID) for a shape whose
  * split-K sums exceed its static scratch, so a caller can ask before it

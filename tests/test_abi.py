@@ -401,3 +401,40 @@ def test_a_closed_device_is_refused():
     p = ctypes.c_void_p()
     assert lib.accel_hip_alloc(63, 16, ctypes.byref(p)) == accel_amd.E_NO_DEVICE
     assert lib.accel_hip_lost(63) == 0
+
+
+# ---- prepared weights: refusals made before any device is touched ----------
+
+def _fake_int4(K, N):
+    n = K * N
+    return accel_amd.Int4Desc(1 << 20, (n + 7) // 8, 1 << 21, (n + 127) // 128, 1 << 22,
+                              (n + 127) // 128, n)
+
+
+@pytest.mark.parametrize("K,N,why", [
+    (256, 100, "N a multiple of 128"),
+    (256, 200, "N a multiple of 128"),
+])
+def test_prepare_refuses_shapes_the_panels_cannot_hold(K, N, why):
+    h = ctypes.c_void_p()
+    d = _fake_int4(K, N)
+    rc = accel_amd.lib().accel_int4_prepare(0, None, ctypes.byref(d), K, N, ctypes.byref(h))
+    assert rc == accel_amd.E_INVALID
+    assert why in accel_amd.last_error()
+    assert h.value is None
+
+
+def test_prepare_refuses_a_count_that_is_not_k_times_n():
+    h = ctypes.c_void_p()
+    d = _fake_int4(256, 128)
+    rc = accel_amd.lib().accel_int4_prepare(0, None, ctypes.byref(d), 256, 256, ctypes.byref(h))
+    assert rc == accel_amd.E_INVALID
+    assert "is 65536 weights and the matrix holds 32768" in accel_amd.last_error()
+
+
+def test_prepared_matvec_refuses_a_missing_weight():
+    t = accel_amd.Tensor()
+    rc = accel_amd.lib().accel_int4_matvec_prepared(0, None, ctypes.byref(t), None,
+                                                   ctypes.byref(t))
+    assert rc == accel_amd.E_INVALID
+    assert "prepared weight is missing" in accel_amd.last_error()
