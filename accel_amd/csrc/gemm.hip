@@ -763,30 +763,18 @@ __device__ __forceinline__ void xsplit3(float v0, float v1, uint32_t& hi, uint32
     lo = __builtin_bit_cast(uint32_t, l);
 }
 
-// With `part`, split K: workgroup (tile, slice) runs slice `slice` of the
-// stages (kt_per each, the last the rest) and stores its f32 sums, row
-// corrections included, to part[slice] ([M, N]); int4_gemm_reduce_kernel
-// adds the slices in order and applies the epilogue.
-__global__ __launch_bounds__(kThreads, 1) void int4_gemm_f32x3_kernel(
-    const float* __restrict__ a, const uint32_t* __restrict__ codes,
-    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
-    void* __restrict__ out, int M, int K, int N, Epilogue ep, float* part, int slices,
-    int kt_per) {
-    __shared__ XLds lds;
-    const int tiles_n = N / BN;
-    const int grid = gridDim.x;
-    int bid = blockIdx.x;
-    if ((grid & 7) == 0) bid = (bid & 7) * (grid >> 3) + (bid >> 3);
-    // split K: the slices of one tile are consecutive (one XCD), as in the
-    // bf16 split kernel
-    const int slice = part ? bid % slices : 0;
-    if (part) bid /= slices;
-    const int m0 = (bid / tiles_n) * XBM;
-    const int n0 = (bid % tiles_n) * BN;
-    const int m_end = M;
-    const int kt0 = slice * kt_per;
-    float* my_part = part ? part + (size_t)slice * M * N : nullptr;
-
+// One 128-row x 128-column tile: rows [m0, min(m0 + 128, m_end)) of a (rows
+// past m_end are clamped copies, never stored), columns [n0, n0 + 128), the
+// stages [kt0, kt0 + ktiles) of K.  With `my_part` the f32 sums, row
+// corrections included, go to my_part ([M, N] of the slice) and the caller's
+// reduction applies the epilogue; else they go to `out` through `ep`.
+__device__ __forceinline__ void gemm_tile_f32x3(XLds& lds, const float* __restrict__ a,
+                                                const uint32_t* __restrict__ codes,
+                                                const uint16_t* __restrict__ scales,
+                                                const uint16_t* __restrict__ zeros,
+                                                void* __restrict__ out, int m0, int m_end,
+                                                int n0, int K, int N, const Epilogue& ep,
+                                                float* my_part, int kt0, int ktiles) {
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int ch = wave & 1;
@@ -796,7 +784,6 @@ __global__ __launch_bounds__(kThreads, 1) void int4_gemm_f32x3_kernel(
     const int kg = lane >> 5;
     const size_t groups_per_row = (size_t)(N >> 7);
     const size_t words_per_row = (size_t)(N >> 3);
-    const int ktiles = !part ? K / BK : (slice == slices - 1 ? K / BK - kt0 : kt_per);
 
     // Activation staging: m-tile i, row (tid >> 3) + 32 i, k 8 (tid & 7) ..
     // + 7 of a stage: two 16-byte loads each.
@@ -1095,6 +1082,84 @@ __global__ __launch_bounds__(kThreads, 1) void int4_gemm_f32x3_kernel(
     if (kp == 0) take_store(P0{}); else take_store(P1{});
 }
 
+// With `part`, split K: workgroup (tile, slice) runs slice `slice` of the
+// stages (kt_per each, the last the rest) and stores its f32 sums, row
+// corrections included, to part[slice] ([M, N]); int4_gemm_reduce_kernel
+// adds the slices in order and applies the epilogue.
+__global__ __launch_bounds__(kThreads, 1) void int4_gemm_f32x3_kernel(
+    const float* __restrict__ a, const uint32_t* __restrict__ codes,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
+    void* __restrict__ out, int M, int K, int N, Epilogue ep, float* part, int slices,
+    int kt_per) {
+    __shared__ XLds lds;
+    const int tiles_n = N / BN;
+    const int grid = gridDim.x;
+    int bid = blockIdx.x;
+    if ((grid & 7) == 0) bid = (bid & 7) * (grid >> 3) + (bid >> 3);
+    // split K: the slices of one tile are consecutive (one XCD), as in the
+    // bf16 split kernel
+    const int slice = part ? bid % slices : 0;
+    if (part) bid /= slices;
+    const int kt0 = slice * kt_per;
+    const int ktiles = !part ? K / BK : (slice == slices - 1 ? K / BK - kt0 : kt_per);
+    gemm_tile_f32x3(lds, a, codes, scales, zeros, out, (bid / tiles_n) * XBM, M,
+                    (bid % tiles_n) * BN, K, N, ep, part ? part + (size_t)slice * M * N : nullptr,
+                    kt0, ktiles);
+}
+
+// The grouped product of f32 rows (the reference API's grouped dtype,
+// tensor/grouped.go:138-212) on the matrix cores: the f32 tiles above walking
+// the (expert, 128-row block, column tile) list of the segments given by
+// `seg` ([E+1]: expert e's rows are [seg[e], min(seg[e+1], T))), each block
+// against its expert's planes, as int4_grouped_bf16_kernel does for bf16
+// rows.  The list is dealt to the XCDs in contiguous eighths so a block's
+// column tiles share its rows in one L2.  Rows past every segment are not
+// written here.
+__global__ __launch_bounds__(kThreads, 1) void int4_grouped_f32x3_kernel(
+    const float* __restrict__ x, const uint32_t* __restrict__ codes,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
+    const uint32_t* __restrict__ seg, float* __restrict__ out, int E, int T, int K, int N) {
+    __shared__ XLds lds;
+    const int tiles_n = N / BN;
+    auto rows_of = [&](int e, uint32_t& first, uint32_t& last) {
+        first = seg[e];
+        last = seg[e + 1];
+        if (last > (uint32_t)T) last = (uint32_t)T;
+        return last > first ? (int)(last - first) : 0;
+    };
+    int blocks_all = 0;
+    for (int e = 0; e < E; e++) {
+        uint32_t f, l;
+        blocks_all += (rows_of(e, f, l) + XBM - 1) / XBM;
+    }
+    const int work = blocks_all * tiles_n;
+    const int per_xcd = (work + 7) / 8;
+    const int slot = blockIdx.x >> 3;
+    if (slot >= per_xcd) return;
+    const int li = (blockIdx.x & 7) * per_xcd + slot;
+    if (li >= work) return;
+    int idx = li / tiles_n;
+    const int n0 = (li % tiles_n) * BN;
+    int e = 0, m0 = 0, m_end = 0;
+    bool found = false;
+    for (; e < E; e++) {
+        uint32_t first, last;
+        const int blocks = (rows_of(e, first, last) + XBM - 1) / XBM;
+        if (idx < blocks) {
+            m0 = (int)first + idx * XBM;
+            m_end = (int)last;
+            found = true;
+            break;
+        }
+        idx -= blocks;
+    }
+    if (!found) return;
+    const size_t per_expert = (size_t)K * N;
+    gemm_tile_f32x3(lds, x, codes + e * (per_expert >> 3), scales + e * (per_expert >> 7),
+                    zeros + e * (per_expert >> 7), out, m0, m_end, n0, K, N, Epilogue{},
+                    nullptr, 0, K / BK);
+}
+
 // ---- f32 activations, fp32 VALU tiles -------------------------------------
 
 constexpr int FM = 64, FN = 64, FK = 32;
@@ -1277,6 +1342,20 @@ hipError_t launch_int4_grouped_bf16(Device*, hipStream_t st, const uint16_t* x,
     dim3 grid((unsigned)wgs);
     ACCEL_LAUNCH(std::string("int4_grouped_bf16_kernel"), int4_grouped_bf16_kernel, grid, dim3(kThreads), 0, st, x, w.codes,
                        w.scales, w.zeros, off, out, E, T, K, N);
+    return launch_status();
+}
+
+hipError_t launch_int4_grouped_f32x3(hipStream_t st, const float* x, Int4Planes w,
+                                     const uint32_t* seg, float* out, int E, int T, int K,
+                                     int N) {
+    // upper bound on (expert, row block) pairs: every expert can add one
+    // partial block
+    const long long max_blocks = (T + XBM - 1) / XBM + (long long)E;
+    const long long wgs = (max_blocks * (N / BN) + 7) / 8 * 8;
+    if (wgs > (1ll << 31) - 8) return hipErrorInvalidConfiguration;
+    ACCEL_LAUNCH(std::string("int4_grouped_f32x3_kernel") + grid_note(wgs, 0),
+                 int4_grouped_f32x3_kernel, dim3((unsigned)wgs), dim3(kThreads), 0, st, x,
+                 w.codes, w.scales, w.zeros, seg, out, E, T, K, N);
     return launch_status();
 }
 

@@ -95,10 +95,11 @@ __global__ __launch_bounds__(256) void grouped_f32_kernel(
     }
 }
 
-// Zero rows [start, T) of a bf16 [T, N] output, start = min(off[E], T): the
-// matvec form's padding rows.
-__global__ void zero_tail_bf16_kernel(const uint32_t* __restrict__ off, uint16_t* out, int E,
-                                      int T, int N) {
+// Zero rows [start, T) of a [T, N] output, start = min(off[E], T): the
+// matvec form's padding rows (off: the segment bounds below).
+template <typename OT>
+__global__ void zero_tail_kernel(const uint32_t* __restrict__ off, OT* out, int E, int T,
+                                 int N) {
     uint32_t start = off[E];
     if (start > (uint32_t)T) start = (uint32_t)T;
     const size_t begin = (size_t)start * N, end = (size_t)T * N;
@@ -107,13 +108,36 @@ __global__ void zero_tail_bf16_kernel(const uint32_t* __restrict__ off, uint16_t
         out[i] = 0;
 }
 
+// The matvec form's segment bounds: token t belongs to expert
+// e(t) = #{r : off[r+1] <= t}, which never decreases as t grows, so expert
+// e's tokens are [S(e-1), S(e)) for S the offsets off[1..E] in increasing
+// order (S(-1) = 0), and the tokens from S(E-1) on are padding.  bounds[0] =
+// 0 and bounds[1 + rank of off[j+1]] = off[j+1], ties in index order.  For
+// offsets that do not wrap (sorted) the bounds are the offsets themselves;
+// counts whose sum wraps u32 leave them unsorted, and the tiled products
+// then walk the bounds rather than the offsets.
+__global__ __launch_bounds__(256) void segment_bounds_kernel(const uint32_t* __restrict__ off,
+                                                             uint32_t* __restrict__ bounds,
+                                                             int E) {
+    for (int j = blockIdx.x * blockDim.x + threadIdx.x; j < E; j += gridDim.x * blockDim.x) {
+        const uint32_t v = off[j + 1];
+        int rank = 0;
+        for (int i = 0; i < E; i++) {
+            const uint32_t u = off[i + 1];
+            rank += (u < v || (u == v && i < j)) ? 1 : 0;
+        }
+        bounds[rank + 1] = v;
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) bounds[0] = 0;
+}
+
 }  // namespace
 
 hipError_t launch_segment_offsets(hipStream_t st, const uint32_t* counts, uint32_t* offsets,
                                   int rows) {
-    hipLaunchKernelGGL(segment_offsets_kernel, dim3(1), dim3(64), 0, st, counts, offsets,
-                       rows);
-    return hipGetLastError();
+    ACCEL_LAUNCH(std::string("segment_offsets_kernel"), segment_offsets_kernel, dim3(1),
+                 dim3(64), 0, st, counts, offsets, rows);
+    return launch_status();
 }
 
 hipError_t launch_grouped_f32(hipStream_t st, const float* x, const float* w,
@@ -121,9 +145,10 @@ hipError_t launch_grouped_f32(hipStream_t st, const float* x, const float* w,
                               bool write_padding) {
     if (T == 0 || N == 0) return hipSuccess;
     dim3 grid((N + 255) / 256, T < 65535 ? T : 65535);
-    hipLaunchKernelGGL((grouped_f32_kernel<false>), grid, dim3(256), 0, st, x, w, nullptr,
-                       nullptr, nullptr, off, out, E, T, K, N, write_padding);
-    return hipGetLastError();
+    ACCEL_LAUNCH(tname("grouped_f32_kernel", false), (grouped_f32_kernel<false>), grid,
+                 dim3(256), 0, st, x, w, nullptr, nullptr, nullptr, off, out, E, T, K, N,
+                 write_padding);
+    return launch_status();
 }
 
 hipError_t launch_int4_grouped_f32(hipStream_t st, const float* x, Int4Planes w,
@@ -131,16 +156,32 @@ hipError_t launch_int4_grouped_f32(hipStream_t st, const float* x, Int4Planes w,
                                    int N, bool write_padding) {
     if (T == 0 || N == 0) return hipSuccess;
     dim3 grid((N + 255) / 256, T < 65535 ? T : 65535);
-    hipLaunchKernelGGL((grouped_f32_kernel<true>), grid, dim3(256), 0, st, x, nullptr,
-                       w.codes, w.scales, w.zeros, off, out, E, T, K, N, write_padding);
-    return hipGetLastError();
+    ACCEL_LAUNCH(tname("grouped_f32_kernel", true), (grouped_f32_kernel<true>), grid,
+                 dim3(256), 0, st, x, nullptr, w.codes, w.scales, w.zeros, off, out, E, T, K,
+                 N, write_padding);
+    return launch_status();
 }
 
 hipError_t launch_zero_tail_bf16(hipStream_t st, const uint32_t* off, uint16_t* out, int E,
                                  int T, int N) {
     if (T == 0 || N == 0) return hipSuccess;
-    hipLaunchKernelGGL(zero_tail_bf16_kernel, dim3(256), dim3(256), 0, st, off, out, E, T, N);
-    return hipGetLastError();
+    ACCEL_LAUNCH(tname("zero_tail_kernel", "unsigned short"), zero_tail_kernel<uint16_t>,
+                 dim3(256), dim3(256), 0, st, off, out, E, T, N);
+    return launch_status();
+}
+
+hipError_t launch_zero_tail_f32(hipStream_t st, const uint32_t* off, float* out, int E, int T,
+                                int N) {
+    if (T == 0 || N == 0) return hipSuccess;
+    ACCEL_LAUNCH(tname("zero_tail_kernel", "float"), zero_tail_kernel<float>, dim3(256),
+                 dim3(256), 0, st, off, out, E, T, N);
+    return launch_status();
+}
+
+hipError_t launch_segment_bounds(hipStream_t st, const uint32_t* off, uint32_t* bounds, int E) {
+    ACCEL_LAUNCH(std::string("segment_bounds_kernel"), segment_bounds_kernel,
+                 dim3((E + 255) / 256), dim3(256), 0, st, off, bounds, E);
+    return launch_status();
 }
 
 }  // namespace accel

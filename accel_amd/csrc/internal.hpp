@@ -285,6 +285,23 @@ hipError_t launch_int4_grouped_decode(Device* d, hipStream_t st, const void* x, 
                                       Int4Planes w, const uint32_t* off, void* out, int E, int T,
                                       int K, int N, bool write_padding, int* status,
                                       uint32_t* tickets, float* area);
+// f32 rows of a grouped int4 product on the matrix cores (the f32 tiles, to
+// f32 accuracy) over segment bounds `seg` [E+1] on the device: expert e's
+// rows are [seg[e], min(seg[e+1], T)); other rows are not written.  Shape
+// limits: int4_gemm_f32x3_supported(K, N) and 16-byte aligned x.  Used past
+// the decode kernels' kGroupedDecodeRowsF32 rows: measured at config 4's
+// experts (8 x [4096, 14336], top-2), tiles / decode kernels: 256 rows 462 /
+// 216 us, 512 rows 471 / 343, 1024 rows 637 / 636 -- a tile's 64 stages cost
+// the same for 30 rows as for 128, and an expert of 129..256 rows takes two.
+hipError_t launch_int4_grouped_f32x3(hipStream_t st, const float* x, Int4Planes w,
+                                     const uint32_t* seg, float* out, int E, int T, int K,
+                                     int N);
+// The matvec form's segment bounds from the offsets (grouped.hip): bounds[e]
+// .. bounds[e+1] are expert e's rows under e(t) = #{r : off[r+1] <= t}; the
+// offsets themselves when their sum did not wrap.
+hipError_t launch_segment_bounds(hipStream_t st, const uint32_t* off, uint32_t* bounds, int E);
+hipError_t launch_zero_tail_f32(hipStream_t st, const uint32_t* off, float* out, int E, int T,
+                                int N);
 hipError_t launch_int4_grouped_bf16(Device* d, hipStream_t st, const uint16_t* x,
                                     Int4Planes w, const uint32_t* off, uint16_t* out,
                                     int E, int T, int K, int N, bool write_padding);

@@ -884,13 +884,23 @@ int run_grouped_int4(const char* op, int dev, void* stream, const accel_tensor_t
                   (reinterpret_cast<uintptr_t>(x->data) & 15) == 0))
         return refuse(op, "bf16 grouped products need K % 64 == 0, N % 128 == 0, K < 2^22 and "
                           "N < 2^26");
-    // few routed rows (f32 or bf16): the decode kernels
-    const bool decode = int4_grouped_decode_supported((int)T, (int)K, (int)N, w->codes, !f32) &&
+    // many f32 rows: the f32 matrix-core tiles; few routed rows (f32 or
+    // bf16): the decode kernels; the rest of bf16: the bf16 tiles
+    const bool tiles_f32 = f32 && T > kGroupedDecodeRowsF32 &&
+                           int4_gemm_f32x3_supported((int)K, (int)N) &&
+                           (reinterpret_cast<uintptr_t>(x->data) & 15) == 0 &&
+                           (uint64_t)experts * (uint64_t)K * (uint64_t)N < (1ull << 40);
+    const bool decode = !tiles_f32 &&
+                        int4_grouped_decode_supported((int)T, (int)K, (int)N, w->codes, !f32) &&
                         (uint64_t)experts * (uint64_t)K * (uint64_t)N < (1ull << 40);
+    const bool tiles = tiles_f32 || (!decode && !f32);
+    // the tiles walk segments: the matvec form's rows follow e(t), whose
+    // bounds are the offsets sorted (segment_bounds), in the area
+    const size_t bounds_bytes = ((size_t)(experts + 1) * sizeof(uint32_t) + 255) / 256 * 256;
     const size_t area_bytes =
         decode ? int4_grouped_decode_area(d, x->data, planes(w), (int)experts, (int)T, (int)K,
                                           (int)N)
-               : 0;
+               : (tiles && matvec ? bounds_bytes : 0);
     void* area = nullptr;
     uint32_t* off = offsets_in_workspace(d, st, static_cast<const uint32_t*>(counts->data),
                                          experts, &status, area_bytes, &area);
@@ -898,24 +908,60 @@ int run_grouped_int4(const char* op, int dev, void* stream, const accel_tensor_t
     uint32_t* tickets = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(off) -
                                                     kWorkspaceCounterBytes);
     const Int4Planes p = planes(w);
-    hipError_t e;
+    hipError_t e = hipSuccess;
+    const uint32_t* seg = off;
+    LaunchRecord rec(false);
+    std::string reason, rejected;
     if (decode) {
+        reason = "few routed rows: each expert's rows in blocks of up to 16 on the "
+                 "matrix-core decode kernel (and the VALU decode kernel for the rest), the "
+                 "weights read once a block";
+        rejected = "the grouped tiles: a 128- or 256-row block for a few rows would be "
+                   "mostly empty";
+    } else if (tiles_f32) {
+        reason = "f32 rows: the f32 matrix-core tiles (x*512s in three bf16 terms) walking "
+                 "each expert's 128-row blocks";
+        rejected = "the decode kernels: they take at most 1024 f32 rows";
+    } else if (f32) {
+        reason = "no tiled kernel takes this shape or alignment: one lane per (row, column)";
+        rejected = "the f32 matrix-core tiles: they take K % 64 == 0, N % 128 == 0 and "
+                   "16-byte aligned rows; the decode kernels: at most 1024 rows";
+    } else {
+        reason = "bf16 rows: the matrix-core tiles walking each expert's blocks of up to 256 "
+                 "rows";
+        rejected = "the decode kernels: they take at most 64 bf16 rows";
+    }
+    if (tiles && matvec) {
+        uint32_t* bounds = static_cast<uint32_t*>(area);
+        e = launch_segment_bounds(st, off, bounds, (int)experts);
+        seg = bounds;
+    }
+    if (e != hipSuccess) {
+    } else if (decode) {
         e = launch_int4_grouped_decode(d, st, x->data, !f32, p, off, out->data, (int)experts,
                                        (int)T, (int)K, (int)N, matvec, &status, tickets,
                                        static_cast<float*>(area));
         if (e == hipSuccess && status != ACCEL_OK) return status;
+    } else if (tiles_f32) {
+        e = launch_int4_grouped_f32x3(st, static_cast<const float*>(x->data), p, seg,
+                                      static_cast<float*>(out->data), (int)experts, (int)T,
+                                      (int)K, (int)N);
+        if (e == hipSuccess && matvec)
+            e = launch_zero_tail_f32(st, seg, static_cast<float*>(out->data), (int)experts,
+                                     (int)T, (int)N);
     } else if (f32) {
         e = launch_int4_grouped_f32(st, static_cast<const float*>(x->data), p, off,
                                     static_cast<float*>(out->data), (int)experts, (int)T,
                                     (int)K, (int)N, matvec);
     } else {
-        e = launch_int4_grouped_bf16(d, st, static_cast<const uint16_t*>(x->data), p, off,
+        e = launch_int4_grouped_bf16(d, st, static_cast<const uint16_t*>(x->data), p, seg,
                                      static_cast<uint16_t*>(out->data), (int)experts, (int)T,
                                      (int)K, (int)N, matvec);
         if (e == hipSuccess && matvec)
-            e = launch_zero_tail_bf16(st, off, static_cast<uint16_t*>(out->data),
+            e = launch_zero_tail_bf16(st, seg, static_cast<uint16_t*>(out->data),
                                       (int)experts, (int)T, (int)N);
     }
+    keep_selection(d, op, rec, reason, rejected);
     return classify(d, e, "grouped int4 launch");
 }
 

@@ -59,6 +59,7 @@ DECODE_MFMA_KERNEL = "int4_decode_mfma_kernel<2, 8, float>"
 SPLITK_BF16_KERNEL = "int4_gemm_bf16_splitk_kernel<2>"
 SPLITK_F32_KERNEL = "int4_gemm_f32x3_kernel (split K, M=64)"
 GROUPED_KERNEL = "int4_grouped_bf16_kernel"
+GROUPED_F32_KERNEL = "int4_grouped_decode_mfma_kernel<2, 8, float>"
 G32_KERNEL = "int4_g32_matvec_kernel"
 # the decode MoE is two launches: the padding rows, then each expert's rows in
 # blocks of up to 16 on the matrix cores
@@ -84,6 +85,9 @@ def parse():
     ap.add_argument("--configs", action="store_true",
                     help="also time BASELINE configs 2, 4 and 5 (slower)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--only", default="",
+                    help="comma-separated extra lines to time (e.g. prefill_m2048_bf16); "
+                         "the headline always runs")
     ap.add_argument("--eager", action="store_true",
                     help="time plain stream launches, not graph replays (profiler runs)")
     return ap.parse_args()
@@ -340,19 +344,24 @@ def bench_gemm(dev, stream, name, steps=40, warmup=4):
                 gbs=bytes_per / (ms * 1e-3) / 1e9, copies=copies, bytes=bytes_per)
 
 
-def bench_moe(dev, stream, steps=20):
-    """Config 4: Int4GroupedMatMul over 1024 routed bf16 rows, 8 experts.  The
+def bench_moe(dev, stream, steps=20, bf16=True):
+    """Config 4: Int4GroupedMatMul over 1024 routed bf16 rows, 8 experts (with
+    bf16=False, the same rows in f32, the reference API's grouped dtype).  The
     experts' weights (250 MB) rotate over three copies (750 MB), so with the
     cache flushed before the timed replay every call reads them from HBM."""
-    from accel_amd import BF16, U32, workloads
+    from accel_amd import BF16, F32, U32, workloads
     progress("config 4: routing and quantizing eight experts")
     m = workloads.moe_fast()
     R = int(m.counts.sum())
     copies = 3
     ws = [dev.upload_int4(m.packed, m.scales, m.zeros, m.E * m.K * m.N) for _ in range(copies)]
-    xb = dev.upload(workloads.bf16_bits(m.x), BF16)
+    if bf16:
+        xb = dev.upload(workloads.bf16_bits(m.x), BF16)
+        ob = dev.alloc((R, m.N), BF16)
+    else:
+        xb = dev.upload(np.ascontiguousarray(m.x, np.float32))
+        ob = dev.alloc((R, m.N), F32)
     cb = dev.upload(m.counts, U32)
-    ob = dev.alloc((R, m.N), BF16)
     for w in ws:
         dev.Int4GroupedMatMul(xb, w, m.E, cb, ob, stream=stream)
     dev.sync(stream)
@@ -363,21 +372,26 @@ def bench_moe(dev, stream, steps=20):
     t.close()
     flops = 2.0 * R * m.K * m.N
     wbytes = m.packed.nbytes + m.scales.nbytes + m.zeros.nbytes
-    nbytes = wbytes + R * m.K * 2 + R * m.N * 2
+    esz = 2 if bf16 else 4
+    nbytes = wbytes + R * m.K * esz + R * m.N * esz
     for b in (xb, cb, ob):
         b.free()
     for w in ws:
         w.free()
     tflops = flops / (ms * 1e-3) / 1e12
-    return dict(workload=f"Int4GroupedMatMul: {R} routed bf16 rows (512 tokens, top-2 of 8 "
-                         f"experts, seed 3), K={m.K}, N={m.N}, bf16 out; expert weights "
-                         f"rotated over {copies} copies",
+    dt = "bf16" if bf16 else "f32"
+    kernel = GROUPED_KERNEL if bf16 else GROUPED_F32_KERNEL
+    return dict(workload=f"Int4GroupedMatMul: {R} routed {dt} rows (512 tokens, top-2 of 8 "
+                         f"experts, seed 3), K={m.K}, N={m.N}, {dt} out; expert weights "
+                         f"rotated over {copies} copies"
+                         + ("" if bf16 else "; each expert's rows in blocks of up to 16 on "
+                            "the matrix-core decode kernel (x*512s in three bf16 terms)"),
                 us=round(ms * 1e3, 2), rows=R, experts=m.E,
                 counts=[int(c) for c in m.counts],
                 roofline={"bound": "mfma", "achieved": round(tflops, 1),
                           "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                           "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
-                          "traffic": traffic_of(GROUPED_KERNEL), "kernel": GROUPED_KERNEL,
+                          "traffic": traffic_of(kernel), "kernel": kernel,
                           "flops_per_launch": int(flops), "bytes_per_launch": int(nbytes),
                           "hbm_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)})
 
@@ -1079,6 +1093,11 @@ def main():
             "us_per_launch": round(r["ms"] * 1e3, 4),
         },
     }
+    only = {k for k in args.only.split(",") if k}
+
+    def want(*keys):
+        return not only or any(k in only for k in keys)
+
     if not args.no_extra:
         extra = {}
         gref = r["gbs_ref"]
@@ -1092,14 +1111,17 @@ def main():
                          "traffic": traffic_of(GEMV_REF_KERNEL), "kernel": GEMV_REF_KERNEL,
                          "bytes_per_launch": r["bytes"]}}
         extra["gemv_m1_bind_ms"] = round(r["bind_ms"], 3)
-        progress("config 1 in BASELINE's literal format (G=32 along K, f32 scale)")
-        extra["gemv_m1_g32_literal"] = bench_gemv_g32(dev, stream)
-        progress("config 3: prefill M=2048 bf16")
-        p = bench_gemm(dev, stream, "prefill_m2048")
-        extra["prefill_m2048_bf16"] = gemm_line(
-            p, "Int4MatMul M=2048 K=4096 N=4096, bf16 x/out, fp32 accumulate (BASELINE "
-               "config 3, the metric's M=2048 leg)", GEMM_KERNEL, "mfma",
-            2 * 2048 * 4096 * 4096, p["bytes"])
+        if want("gemv_m1_g32_literal"):
+            progress("config 1 in BASELINE's literal format (G=32 along K, f32 scale)")
+            extra["gemv_m1_g32_literal"] = bench_gemv_g32(dev, stream)
+        if want("prefill_m2048_bf16"):
+            progress("config 3: prefill M=2048 bf16")
+            p = bench_gemm(dev, stream, "prefill_m2048")
+            extra["prefill_m2048_bf16"] = gemm_line(
+                p, "Int4MatMul M=2048 K=4096 N=4096, bf16 x/out, fp32 accumulate (BASELINE "
+                   "config 3, the metric's M=2048 leg)", GEMM_KERNEL, "mfma",
+                2 * 2048 * 4096 * 4096, p["bytes"])
+    if not args.no_extra and want("prefill_m2048_f32"):
         progress("config 3 in f32: prefill M=2048 in the reference API's dtype")
         pf = bench_gemm(dev, stream, "prefill_m2048_f32", steps=20, warmup=2)
         lf = gemm_line(
@@ -1111,9 +1133,12 @@ def main():
         lf["roofline"]["note"] = ("achieved counts the product's own flops; the three-term "
                                   "split issues three times as many on the matrix cores")
         extra["prefill_m2048_f32"] = lf
-        progress("short prefill: M=64 bf16 and f32 (split K)")
+    if not args.no_extra:
         for key, name, kern in (("prefill_m64_bf16", "prefill_m64", SPLITK_BF16_KERNEL),
                                 ("prefill_m64_f32", "prefill_m64_f32", SPLITK_F32_KERNEL)):
+            if not want(key):
+                continue
+            progress(f"short prefill: {key} (split K)")
             q = bench_gemm(dev, stream, name, steps=100, warmup=10)
             dt = "bf16" if name == "prefill_m64" else "f32"
             extra[key] = gemm_line(
@@ -1121,23 +1146,33 @@ def main():
                    "tiles split K across the CUs (f32 sums per slice, one reduction pass)",
                 kern, "hbm", 2 * 64 * 4096 * 4096, q["bytes"])
             extra[key]["tflops"] = round(q["tflops"], 1)
-        progress("config 2: decode M=16 K=4096 N=14336")
-        d = bench_gemm(dev, stream, "decode_m16", steps=200, warmup=10)
-        extra["decode_m16_f32"] = gemm_line(
-            d, "Int4MatMul M=16 K=4096 N=14336, f32 x/out (BASELINE config 2, Llama-3-8B "
-               "MLP up-projection at decode batch 16)", DECODE_MFMA_KERNEL, "hbm",
-            2 * 16 * 4096 * 14336, d["bytes"])
-        progress("config 4: MoE grouped product")
-        extra["moe_grouped_bf16"] = bench_moe(dev, stream)
-        extra["moe_decode_f32"] = bench_moe_decode(dev, stream)
+        if want("decode_m16_f32"):
+            progress("config 2: decode M=16 K=4096 N=14336")
+            d = bench_gemm(dev, stream, "decode_m16", steps=200, warmup=10)
+            extra["decode_m16_f32"] = gemm_line(
+                d, "Int4MatMul M=16 K=4096 N=14336, f32 x/out (BASELINE config 2, Llama-3-8B "
+                   "MLP up-projection at decode batch 16)", DECODE_MFMA_KERNEL, "hbm",
+                2 * 16 * 4096 * 14336, d["bytes"])
+        if want("moe_grouped_bf16"):
+            progress("config 4: MoE grouped product")
+            extra["moe_grouped_bf16"] = bench_moe(dev, stream)
+        if want("moe_grouped_f32"):
+            progress("config 4's shape in f32 rows (the reference API's grouped dtype)")
+            extra["moe_grouped_f32"] = bench_moe(dev, stream, steps=10, bf16=False)
+        if want("moe_decode_f32"):
+            extra["moe_decode_f32"] = bench_moe_decode(dev, stream)
         for b in (1, 8):
-            progress(f"config 5: layer chain at batch {b}")
-            extra[f"layer_chain_b{b}"] = bench_layer_chain(dev, stream, b)
-        progress("config 5 at batch 1 on the reference planes")
-        extra["layer_chain_b1_reference_planes"] = bench_layer_chain(dev, stream, 1,
-                                                                     prepared=False)
-        progress("launch floors of the decode shape")
-        extra["floors"] = bench_floors(dev, stream)
+            if want(f"layer_chain_b{b}"):
+                progress(f"config 5: layer chain at batch {b}")
+                extra[f"layer_chain_b{b}"] = bench_layer_chain(dev, stream, b)
+        if want("layer_chain_b1_reference_planes"):
+            progress("config 5 at batch 1 on the reference planes")
+            extra["layer_chain_b1_reference_planes"] = bench_layer_chain(dev, stream, 1,
+                                                                         prepared=False)
+        if want("floors"):
+            progress("launch floors of the decode shape")
+            extra["floors"] = bench_floors(dev, stream)
+    if not args.no_extra and want("published_decode_2048"):
         progress("the reference's published workload (2048 x 2048, one wait a step)")
         pub = bench_published(dev, stream)
         extra["published_decode_2048"] = pub
@@ -1147,6 +1182,7 @@ def main():
             f"({PUBLISHED_US:.0f} us a step, {PUBLISHED_SRC}) over this build's time for the "
             "same workload and protocol (extra.published_decode_2048); BASELINE.md publishes "
             "no figure for config 1 itself")
+    if not args.no_extra:
         if args.configs:
             progress("--configs: widened rows")
             extra["layer_chain_b1_unmerged"] = bench_layer_chain(dev, stream, 1, merged=False)

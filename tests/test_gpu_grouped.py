@@ -174,7 +174,8 @@ def run_int4_grouped(dev, form, x, p, s, z, counts, E, T, K, N, bf16):
                                               # T < 2E: every row on the VALU kernel
                                               (8, 256, 256, [3, 0, 0, 0, 0, 0, 0, 1], 1),
                                               # f32 past 64 rows: the decode kernels up
-                                              # to 1024 rows, one lane per element past
+                                              # to 1024 rows, the f32 matrix-core tiles
+                                              # past (K % 64 == 0)
                                               (4, 512, 1024, [300, 0, 41, 260], 2),
                                               (2, 64, 128, [600, 500], 0)])
 def test_int4_grouped_matches_the_oracle(dev, bf16, form, E, K, N, counts, pad):
@@ -215,22 +216,35 @@ def test_int4_grouped_matvec_wrapped_offsets(dev):
         assert rel_l2(got[t], want[t]) <= 1e-5, t
 
 
-def test_config4_moe_full_size(dev):
-    """Config 4 at full size (1024 routed rows, 8 experts of [4096, 14336]):
-    every row through two per-expert f64 checksums of the output columns, the
-    plain column sum and one weighted by the row's position in its segment
-    (which a dropped, duplicated or misplaced row changes), plus the first and
-    last row of every expert and 64 seeded rows against the oracle row for
-    row."""
+@pytest.mark.parametrize("bf16", [True, False])
+def test_config4_moe_full_size(dev, bf16):
+    """Config 4 at full size (1024 routed rows, 8 experts of [4096, 14336]),
+    with bf16 rows (the config's dtype) and with f32 rows (the reference
+    API's grouped dtype, on the f32 matrix-core tiles): every row through two
+    per-expert f64 checksums of the output columns, the plain column sum and
+    one weighted by the row's position in its segment (which a dropped,
+    duplicated or misplaced row changes), plus the first and last row of every
+    expert and 64 seeded rows against the oracle row for row.  Tolerances:
+    the path's, 2e-2 for bf16 and 1e-5 for f32."""
     m = workloads.moe()
     R = int(m.counts.sum())
     assert R == 1024
+    tol = 2e-2 if bf16 else 1e-5
     w = dev.upload_int4(m.packed, m.scales, m.zeros, m.E * m.K * m.N)
-    xb = dev.upload(workloads.bf16_bits(m.x), BF16)
+    if bf16:
+        xb = dev.upload(workloads.bf16_bits(m.x), BF16)
+        ob = dev.alloc((R, m.N), BF16)
+    else:
+        xb = dev.upload(np.ascontiguousarray(m.x, np.float32))
+        ob = dev.alloc((R, m.N), F32)
     cb = dev.upload(m.counts, U32)
-    ob = dev.alloc((R, m.N), BF16)
     dev.Int4GroupedMatMul(xb, w, m.E, cb, ob)
-    got = workloads.bf16_to_f32(ob.numpy()).astype(np.float64)
+    sel = dev.last_selection()
+    assert sel.op == "Int4GroupedMatMul"
+    assert any(k.startswith("int4_grouped_bf16_kernel" if bf16 else "int4_grouped_decode")
+               for k in sel.launches), sel
+    got = ob.numpy()
+    got = (workloads.bf16_to_f32(got) if bf16 else got).astype(np.float64)
     off = oracle.segment_offsets(m.counts)
     rng = np.random.Generator(np.random.PCG64(44))
     sampled = set(rng.choice(R, 64, replace=False).tolist())
@@ -248,15 +262,65 @@ def test_config4_moe_full_size(dev):
         for weights in (np.ones_like(pos), pos):
             want = (weights * xs).sum(axis=0) @ wdq
             have = (weights * got[lo:hi]).sum(axis=0)
-            assert rel_l2(have, want) <= 2e-2, (e, rel_l2(have, want))
+            assert rel_l2(have, want) <= tol, (e, rel_l2(have, want))
         rows = sorted({lo, hi - 1} | {r for r in sampled if lo <= r < hi})
         want = oracle.quant_matmul_int4(np.ascontiguousarray(m.x[rows]), pe, se, ze,
                                         len(rows), m.K, m.N, threads=16)
-        assert rel_l2(got[rows], oracle.round_bf16(want)) <= 2e-2
+        if bf16:
+            want = oracle.round_bf16(want)
+        assert rel_l2(got[rows], want) <= tol
         del wdq
     for b in (xb, cb, ob):
         b.free()
     w.free()
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_int4_grouped_matvec_wrapped_offsets_on_the_tiles(dev, bf16):
+    """Wrapped offsets at the tiles' sizes (f32 past 1024 rows, bf16 past 64):
+    counts [2^32 - 1, 700, 400] give off = [0, 2^32 - 1, 699, 1099], and
+    e(t) = #{r : off[r+1] <= t} (internal/kernels/grouped.go:66-77) puts rows
+    0-698 on expert 0, 699-1098 on expert 1 and every row from 1099 on
+    expert 2 (no padding): the tiles walk the offsets sorted, not as given."""
+    E, K, N, counts, pad = 3, 256, 256, [0xFFFFFFFF, 700, 400], 21
+    x, p, s, z, off, T = int4_case(E, K, N, counts, pad, seed=12, bf16=bf16)
+    assert T == 1120 and list(off) == [0, 0xFFFFFFFF, 699, 1099]
+    got = run_int4_grouped(dev, "Int4GroupedMatVec", x, p, s, z, counts, E, T, K, N, bf16)
+    want = oracle.int4_grouped_matvec(x, p, s, z, off, E, T, K, N, threads=8,
+                                      out=np.full(T * N, 7.0, np.float32))
+    if bf16:
+        want = oracle.round_bf16(want)
+    tol = 2e-2 if bf16 else 1e-5
+    assert np.all(np.abs(want).sum(axis=1) > 0)   # every row belongs to an expert
+    for lo, hi in ((0, 699), (699, 1099), (1099, T)):
+        assert rel_l2(got[lo:hi], want[lo:hi]) <= tol, (lo, hi)
+
+
+@pytest.mark.parametrize("form", ["Int4GroupedMatVec", "Int4GroupedMatMul"])
+@pytest.mark.parametrize("E,K,N,counts", [(4, 512, 384, [100, 0, 900, 30]),
+                                          (3, 1024, 256, [600, 500, 1]),
+                                          # K % 64 != 0: one lane per element
+                                          (2, 32, 128, [600, 500])])
+def test_int4_grouped_f32_tiles_match_the_oracle(dev, form, E, K, N, counts):
+    """f32 rows past 1024 on the matrix-core tiles: blocks of 128 rows with a
+    short last block, an empty expert, a one-row expert, padding rows; and a
+    K the tiles cannot take (one lane per element)."""
+    x, p, s, z, off, T = int4_case(E, K, N, counts, 5, seed=K + N, bf16=False)
+    assert T > 1024
+    got = run_int4_grouped(dev, form, x, p, s, z, counts, E, T, K, N, False)
+    init = np.full(T * N, 7.0, np.float32)
+    ref = oracle.int4_grouped_matvec if form == "Int4GroupedMatVec" else \
+        oracle.int4_grouped_matmul
+    want = ref(x, p, s, z, off, E, T, K, N, threads=8, out=init)
+    covered = int(off[E])
+    assert rel_l2(got[:covered], want[:covered]) <= 1e-5
+    for e in range(E):
+        if off[e + 1] > off[e]:
+            assert rel_l2(got[off[e]:off[e + 1]], want[off[e]:off[e + 1]]) <= 1e-5, e
+    if form == "Int4GroupedMatVec":
+        assert np.all(got[covered:] == 0)
+    else:
+        assert np.all(got[covered:] == 7.0)
 
 
 @pytest.mark.parametrize("form", ["Int4GroupedMatVec", "Int4GroupedMatMul"])
