@@ -59,12 +59,37 @@ DECODE_MFMA_KERNEL = "int4_decode_mfma_kernel<2, 8, float>"
 SPLITK_BF16_KERNEL = "int4_gemm_bf16_splitk_kernel<2>"
 SPLITK_F32_KERNEL = "int4_gemm_f32x3_kernel (split K, M=64)"
 GROUPED_KERNEL = "int4_grouped_bf16_kernel"
-GROUPED_F32_KERNEL = "int4_grouped_decode_mfma_kernel<2, 8, float>"
 G32_KERNEL = "int4_g32_matvec_kernel"
-# the decode MoE is two launches: the padding rows, then each expert's rows in
-# blocks of up to 16 on the matrix cores
-GROUPED_DECODE_KERNELS = ("int4_grouped_decode_kernel<512, 32, true, float>",
-                          "int4_grouped_decode_mfma_kernel<2, 8, float>")
+REDUCE_KERNEL = "int4_gemm_reduce_kernel"
+# Keys of the PMC summary (profiles/traffic.json) for products of several
+# launches: a key is the kernel's name, with the launch's role where one
+# kernel serves two.  The short prefills are the split-K kernel and the
+# reduction pass.
+SPLITK_BF16_LAUNCHES = (SPLITK_BF16_KERNEL, f"{REDUCE_KERNEL} (after {SPLITK_BF16_KERNEL})")
+SPLITK_F32_LAUNCHES = (SPLITK_F32_KERNEL, f"{REDUCE_KERNEL} (after int4_gemm_f32x3_kernel, M=64)")
+# The grouped decode products are two launches: the VALU decode kernel (the
+# padding rows, and every row should the offsets have wrapped), then each
+# expert's rows in blocks of up to 16 on the matrix cores.
+_GD = "int4_grouped_decode_kernel<512, 32, true, float>"
+_GDM = "int4_grouped_decode_mfma_kernel<2, 8, float>"
+GROUPED_F32_LAUNCHES = (f"{_GD} (1024 rows)", f"{_GDM} (1024 rows)")
+GROUPED_DECODE_LAUNCHES = (f"{_GD} (16 rows)", f"{_GDM} (16 rows)")
+# config 5's five launches a step, by variant
+_PS = "int4_panel_matvec_kernel<4, false, true, true, true>"
+_MF1 = "int4_decode_mfma_kernel<1, 8, float>"
+CHAIN_LAUNCHES = {
+    "prepared_b1": (f"{_PS} (q/k/v set, batch 1)", GEMV_KERNEL, f"{_PS} (gate/up set, batch 1)",
+                    "swiglu_kernel (batch 1)",
+                    "int4_panel_matvec_kernel<7, true, true, true, false> (down, batch 1)"),
+    "planes_b1": ("int4_decode_set_kernel<1, 256, 32, false> (q/k/v set, batch 1)",
+                  GEMV_REF_KERNEL,
+                  "int4_decode_set_kernel<1, 512, 32, false> (gate/up set, batch 1)",
+                  "swiglu_kernel (batch 1)", f"{GEMV_REF_KERNEL} (down, batch 1)"),
+    "planes_b8": ("int4_decode_mfma_set_kernel<1, 8> (q/k/v set, batch 8)",
+                  f"{_MF1} (o, batch 8)",
+                  "int4_decode_mfma_set_kernel<2, 8> (gate/up set, batch 8)",
+                  "swiglu_kernel (batch 8)", f"{_MF1} (down, batch 8)"),
+}
 FLUSH_BYTES = 1 << 30          # device read that evicts the Infinity Cache
 EAGER_MAX = 64                 # timed regions of at most this many calls run as plain launches
 PUBLISHED_US = 760.0           # Int4MatVec [2048] x [2048,2048] on an M2, one plan a step
@@ -380,7 +405,7 @@ def bench_moe(dev, stream, steps=20, bf16=True):
         w.free()
     tflops = flops / (ms * 1e-3) / 1e12
     dt = "bf16" if bf16 else "f32"
-    kernel = GROUPED_KERNEL if bf16 else GROUPED_F32_KERNEL
+    kernel = GROUPED_KERNEL if bf16 else " + ".join(GROUPED_F32_LAUNCHES)
     return dict(workload=f"Int4GroupedMatMul: {R} routed {dt} rows (512 tokens, top-2 of 8 "
                          f"experts, seed 3), K={m.K}, N={m.N}, {dt} out; expert weights "
                          f"rotated over {copies} copies"
@@ -391,7 +416,8 @@ def bench_moe(dev, stream, steps=20, bf16=True):
                 roofline={"bound": "mfma", "achieved": round(tflops, 1),
                           "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                           "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
-                          "traffic": traffic_of(kernel), "kernel": kernel,
+                          "traffic": traffic_sum((kernel,) if bf16 else GROUPED_F32_LAUNCHES),
+                          "kernel": kernel,
                           "flops_per_launch": int(flops), "bytes_per_launch": int(nbytes),
                           "hbm_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)})
 
@@ -435,8 +461,8 @@ def bench_moe_decode(dev, stream, tokens=8, steps=40):
                 counts=[int(c) for c in m.counts],
                 roofline={"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                           "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                          "traffic": traffic_sum(GROUPED_DECODE_KERNELS),
-                          "kernel": " + ".join(GROUPED_DECODE_KERNELS),
+                          "traffic": traffic_sum(GROUPED_DECODE_LAUNCHES),
+                          "kernel": " + ".join(GROUPED_DECODE_LAUNCHES),
                           "bytes_per_launch": int(nbytes)})
 
 
@@ -542,6 +568,8 @@ def bench_layer_chain(dev, stream, batch, steps=100, merged=True, sets=5, prepar
         kernels = ("int4_decode_mfma_set_kernel + int4_decode_mfma_kernel (matrix-core decode) "
                    "+ swiglu_kernel")
     launches = (4 if merged else 7) + 1
+    variant = "prepared_b1" if prepared else "planes_b1" if batch == 1 else "planes_b8"
+    traffic = traffic_sum(CHAIN_LAUNCHES[variant]) if merged and batch in (1, 8) else None
     res = dict(workload=f"config 5: seven Llama-3-8B layer products as one decode step at "
                         f"batch {batch}, down fed SwiGLU(gate, up) computed on the device "
                         f"(q/k/v and gate/up as sets: {launches} launches), f32 x, "
@@ -552,7 +580,7 @@ def bench_layer_chain(dev, stream, batch, steps=100, merged=True, sets=5, prepar
                weight_bytes=total_bytes,
                roofline={"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                         "traffic": None, "kernel": kernels,
+                         "traffic": traffic, "kernel": kernels,
                          "bytes_per_step": int(total_bytes + act_bytes)})
     if bind_ms is not None:
         res["bind_ms_per_layer"] = round(bind_ms, 3)
@@ -1025,15 +1053,18 @@ def bench_floors(dev, stream, steps=640):
     return res
 
 
-def gemm_line(p, workload, kernel, bound, flops, bytes_per):
+def gemm_line(p, workload, kernel, bound, flops, bytes_per, launches=None):
+    """A product's bench line; `launches` names its launches in the PMC
+    summary when it is more than the one kernel."""
+    traffic = traffic_sum(launches or (kernel,))
     if bound == "mfma":
         rl = {"bound": "mfma", "achieved": round(p["tflops"], 1), "peak": BF16_PEAK_TFLOPS,
               "unit": "TFLOP/s", "frac": round(p["tflops"] / BF16_PEAK_TFLOPS, 4),
-              "traffic": traffic_of(kernel), "kernel": kernel, "flops_per_launch": int(flops)}
+              "traffic": traffic, "kernel": kernel, "flops_per_launch": int(flops)}
     else:
         rl = {"bound": "hbm", "achieved": round(p["gbs"], 1), "peak": HBM_PEAK_GBS,
               "unit": "GB/s", "frac": round(p["gbs"] / HBM_PEAK_GBS, 4),
-              "traffic": traffic_of(kernel), "kernel": kernel, "bytes_per_launch": int(bytes_per)}
+              "traffic": traffic, "kernel": kernel, "bytes_per_launch": int(bytes_per)}
     return {"workload": workload, "us": round(p["us"], 2), "roofline": rl}
 
 
@@ -1042,7 +1073,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (this build "
-              "runs on a single MI355X; DESIGN.md describes how the path would shard)",
+              "runs on a single MI355X)",
               file=sys.stderr)
         sys.exit(2)
     EAGER = args.eager
@@ -1134,8 +1165,8 @@ def main():
                                   "split issues three times as many on the matrix cores")
         extra["prefill_m2048_f32"] = lf
     if not args.no_extra:
-        for key, name, kern in (("prefill_m64_bf16", "prefill_m64", SPLITK_BF16_KERNEL),
-                                ("prefill_m64_f32", "prefill_m64_f32", SPLITK_F32_KERNEL)):
+        for key, name, launches in (("prefill_m64_bf16", "prefill_m64", SPLITK_BF16_LAUNCHES),
+                                    ("prefill_m64_f32", "prefill_m64_f32", SPLITK_F32_LAUNCHES)):
             if not want(key):
                 continue
             progress(f"short prefill: {key} (split K)")
@@ -1144,7 +1175,7 @@ def main():
             extra[key] = gemm_line(
                 q, f"Int4MatMul M=64 K=4096 N=4096, {dt} x/out: a short prefill, whose 32 "
                    "tiles split K across the CUs (f32 sums per slice, one reduction pass)",
-                kern, "hbm", 2 * 64 * 4096 * 4096, q["bytes"])
+                " + ".join(launches), "hbm", 2 * 64 * 4096 * 4096, q["bytes"], launches)
             extra[key]["tflops"] = round(q["tflops"], 1)
         if want("decode_m16_f32"):
             progress("config 2: decode M=16 K=4096 N=14336")
