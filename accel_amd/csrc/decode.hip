@@ -1684,6 +1684,15 @@ __device__ __forceinline__ bool grouped_offsets_sorted(const uint32_t* off, int 
 }
 
 // XT: f32 or bf16 bits; the result is written in the same type.
+//
+// Workgroup b takes row t = b % T, and, when the rows are this launch's
+// alone, column tile (b / T) % tiles and K slice b / (T tiles).  When the
+// matrix-core launch takes the rows (mfma_blocks), this launch is left the
+// padding rows, and every row should the offsets have wrapped: then one
+// workgroup a row walks the row's column tiles with K whole (the host plans
+// one slice), so that the workgroups finding no row are T, not T x tiles
+// (1024 f32 rows of N = 14336, all of them the matrix cores': 28 672 such
+// workgroups took 106 us).
 template <int TILE, int CPL, bool PIPE, typename XT = float>
 __global__ __launch_bounds__(kDecThreads) void int4_grouped_decode_kernel(
     const XT* __restrict__ x, const uint32_t* __restrict__ codes,
@@ -1696,14 +1705,15 @@ __global__ __launch_bounds__(kDecThreads) void int4_grouped_decode_kernel(
     int b = blockIdx.x;
     if ((grid & 7) == 0) b = (b & 7) * (grid >> 3) + (b >> 3);
     const int t = b % T;
-    const int tile = (b / T) % tiles;
-    const int slice = b / (T * tiles);
+    const int tile0 = mfma_blocks ? 0 : (b / T) % tiles;
+    const int tile_end = mfma_blocks ? tiles : tile0 + 1;
+    const int slice = mfma_blocks ? 0 : b / (T * tiles);
     const int e = grouped_expert_of(off, E, (uint32_t)t);
     if (e >= E) {
         // past every segment: the matvec form writes zeros, once per column tile
         if (write_padding && slice == 0)
-            for (int c = threadIdx.x; c < TILE; c += kDecThreads) {
-                const size_t o = (size_t)t * N + tile * TILE + c;
+            for (int c = tile0 * TILE + threadIdx.x; c < tile_end * TILE; c += kDecThreads) {
+                const size_t o = (size_t)t * N + c;
                 if constexpr (sizeof(XT) == 2)
                     static_cast<uint16_t*>(out)[o] = 0;
                 else
@@ -1734,13 +1744,16 @@ __global__ __launch_bounds__(kDecThreads) void int4_grouped_decode_kernel(
     void* o = static_cast<char*>(out) + (size_t)t * N * sizeof(XT);
     Epilogue ep;
     ep.bf16 = sizeof(XT) == 2;
-    uint32_t* tk = tickets + ((size_t)t * tiles + tile) * ticket_stride;
-    if (pair)
-        decode_tile<2, TILE, CPL / 2, PIPE, XT>(x + (size_t)t * K, c, s, z, o, p, tk, K, N, tile,
-                                                slice, rows_per_slice, slices, ep);
-    else
-        decode_tile<1, TILE, CPL, PIPE, XT>(x + (size_t)t * K, c, s, z, o, p, tk, K, N, tile,
-                                            slice, rows_per_slice, slices, ep);
+    // (decode_tile ends at a barrier, so its LDS is free for the next tile)
+    for (int tile = tile0; tile < tile_end; tile++) {
+        uint32_t* tk = tickets + ((size_t)t * tiles + tile) * ticket_stride;
+        if (pair)
+            decode_tile<2, TILE, CPL / 2, PIPE, XT>(x + (size_t)t * K, c, s, z, o, p, tk, K, N,
+                                                    tile, slice, rows_per_slice, slices, ep);
+        else
+            decode_tile<1, TILE, CPL, PIPE, XT>(x + (size_t)t * K, c, s, z, o, p, tk, K, N,
+                                                tile, slice, rows_per_slice, slices, ep);
+    }
 }
 
 // The matrix-core blocks of a grouped decode product: workgroup b takes
@@ -1929,17 +1942,28 @@ hipError_t launch_grouped_decode_tile(Device* d, hipStream_t st, const XT* x, In
     }
     // the split-K sums live in the caller's area, past the offsets
     float* partial = slices > 1 ? area : nullptr;
-    const dim3 grid((unsigned)(pairs * slices));
+    // with the matrix-core launch taking the rows: one workgroup a row, which
+    // walks the column tiles with K whole
+    if (mfma_blocks && slices != 1) {
+        *status = fail(ACCEL_E_INVALID, "grouped decode product: %d K slices planned for the "
+                                        "padding launch", slices);
+        return hipSuccess;
+    }
+    const dim3 grid((unsigned)(mfma_blocks ? (long long)T : pairs * slices));
+    const std::string note =
+        mfma_blocks ? " [" + std::to_string(T) + " rows, each walking " + std::to_string(tiles) +
+                          " tiles: the padding rows]"
+                    : grid_note(tiles, slices);
     if (per_slice > 1)
         ACCEL_LAUNCH(tname("int4_grouped_decode_kernel", TILE, CPL, true, type_name<XT>()) +
-                         grid_note(tiles, slices),
+                         note,
                      (int4_grouped_decode_kernel<TILE, CPL, true, XT>), grid,
                            dim3(kDecThreads), 0, st, x, w.codes, w.scales, w.zeros, off, out,
                            partial, tickets, stride, E, T, K, N, rows, slices, write_padding,
                            mfma_blocks);
     else
         ACCEL_LAUNCH(tname("int4_grouped_decode_kernel", TILE, CPL, false, type_name<XT>()) +
-                         grid_note(tiles, slices),
+                         note,
                      (int4_grouped_decode_kernel<TILE, CPL, false, XT>), grid,
                            dim3(kDecThreads), 0, st, x, w.codes, w.scales, w.zeros, off, out,
                            partial, tickets, stride, E, T, K, N, rows, slices, write_padding,

@@ -170,6 +170,8 @@ def run_int4_grouped(dev, form, x, p, s, z, counts, E, T, K, N, bf16):
                                               # 5 and 3 rows over split K
                                               (3, 256, 512, [17, 18, 19], 1),
                                               (2, 2048, 384, [16, 35], 2),
+                                              # padding rows past 512-column tiles
+                                              (2, 1024, 2048, [9, 7], 3),
                                               (2, 4096, 2048, [5, 3], 0),
                                               # T < 2E: every row on the VALU kernel
                                               (8, 256, 256, [3, 0, 0, 0, 0, 0, 0, 1], 1),
@@ -197,14 +199,17 @@ def test_int4_grouped_matches_the_oracle(dev, bf16, form, E, K, N, counts, pad):
         assert np.all(got[covered:] == 7.0)
 
 
-def test_int4_grouped_matvec_wrapped_offsets(dev):
+@pytest.mark.parametrize("N", [256, 2048])
+def test_int4_grouped_matvec_wrapped_offsets(dev, N):
     """Counts whose running sum wraps u32 (segmentOffsets keeps the wrap,
     tensor/segment.go:40-50): off = [0, 2^32 - 1, 2, 4] is not sorted, and the
     row -> expert rule e(t) = #{r : off[r+1] <= t} (internal/kernels/
     grouped.go:66-77) puts rows 0-1, 2-3 and 4-5 on experts 0, 1 and 2.  The
     decode path pairs rows of one expert only under sorted offsets; here every
-    row has to be computed on its own."""
-    E, K, N, counts, pad = 3, 512, 256, [0xFFFFFFFF, 3, 2], 2
+    row has to be computed on its own, by the VALU launch (the matrix-core
+    launch takes sorted offsets only), whose workgroups each walk a row's
+    column tiles: one tile at N = 256, four at N = 2048."""
+    E, K, counts, pad = 3, 512, [0xFFFFFFFF, 3, 2], 2
     x, p, s, z, off, T = int4_case(E, K, N, counts, pad, seed=11, bf16=False)
     assert T == 6 and list(off) == [0, 0xFFFFFFFF, 2, 4]
     got = run_int4_grouped(dev, "Int4GroupedMatVec", x, p, s, z, counts, E, T, K, N, False)
