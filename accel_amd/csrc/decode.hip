@@ -1605,34 +1605,6 @@ hipError_t launch_int4_decode_bf16_rows(Device* d, hipStream_t st, const uint16_
     return launch_decode_mfma<uint16_t>(d, st, a, w, out, M, K, N, status, ep);
 }
 
-// 17..48 f32 rows as 16-row decode launches (the last with the rest): each
-// reads the weights once more, but the f32 matrix-core tiles, 128 rows tall,
-// run mostly empty rows at these counts.  Measured (us, 16-row launches /
-// f32 tiles): K x N = 4096 x 14336, M = 17, 32, 48, 64: 29.0 / 60.1,
-// 35.2 / 61.0, 50.8 / 62.0, 66.9 / 62.9; 14336 x 4096: 30.2 / 54.9,
-// 34.9 / 56.6, 51.0 / 58.0, 65.1 / 59.1; 4096 x 4096: 16.5 / 24.0,
-// 21.6 / 25.3, 32.1 / 26.0; 4096 x 1024: 14.8 / 16.5, 18.3 / 16.9,
-// 27.0 / 18.1.  So two launches where K N >= 2^23, three where K N >= 2^25.
-bool int4_decode_rows_pay(int M, int K, int N) {
-    const int launches = (M + 15) / 16;
-    const uint64_t kn = (uint64_t)K * (uint64_t)N;
-    return M > 16 && ((launches == 2 && kn >= (1ull << 23)) ||
-                      (launches == 3 && kn >= (1ull << 25)));
-}
-
-hipError_t launch_int4_decode_f32_rows(Device* d, hipStream_t st, const float* a, Int4Planes w,
-                                       void* out, int M, int K, int N, int* status,
-                                       Epilogue ep) {
-    *status = ACCEL_OK;
-    const size_t esz = ep.bf16 ? 2 : 4;
-    hipError_t e = hipSuccess;
-    for (int r0 = 0; r0 < M && e == hipSuccess && *status == ACCEL_OK; r0 += 16)
-        e = launch_int4_decode_f32(d, st, a + (size_t)r0 * K, w,
-                                   static_cast<char*>(out) + (size_t)r0 * N * esz,
-                                   std::min(16, M - r0), K, N, status, ep);
-    return e;
-}
-
 namespace {
 
 // ---- ragged int4 GEMV: the decode form of the grouped product -------------

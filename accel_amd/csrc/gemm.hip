@@ -767,8 +767,10 @@ __device__ __forceinline__ void xsplit3(float v0, float v1, uint32_t& hi, uint32
 // past m_end are clamped copies, never stored), columns [n0, n0 + 128), the
 // stages [kt0, kt0 + ktiles) of K.  With `my_part` the f32 sums, row
 // corrections included, go to my_part ([M, N] of the slice) and the caller's
-// reduction applies the epilogue; else they go to `out` through `ep`.
-__device__ __forceinline__ void gemm_tile_f32x3(XLds& lds, const float* __restrict__ a,
+// reduction applies the epilogue; else they go to `out` through `ep`.  MT:
+// the 32-row m-tiles that hold rows (a short band or block runs only those).
+template <int MT>
+__device__ __forceinline__ void gemm_tile_f32x3_t(XLds& lds, const float* __restrict__ a,
                                                 const uint32_t* __restrict__ codes,
                                                 const uint16_t* __restrict__ scales,
                                                 const uint16_t* __restrict__ zeros,
@@ -789,10 +791,10 @@ __device__ __forceinline__ void gemm_tile_f32x3(XLds& lds, const float* __restri
     // + 7 of a stage: two 16-byte loads each.
     const int x_row = tid >> 3;
     const int x_c8 = tid & 7;
-    const float* x_src[4];
-    int x_dst[4];
+    const float* x_src[MT];
+    int x_dst[MT];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < MT; i++) {
         const int r = x_row + 32 * i;
         x_src[i] = a + (size_t)min(m0 + r, m_end - 1) * K + 8 * x_c8;
         x_dst[i] = a_off(r, x_c8);
@@ -809,13 +811,13 @@ __device__ __forceinline__ void gemm_tile_f32x3(XLds& lds, const float* __restri
     const uint16_t* z_src = zeros + (size_t)f_row * groups_per_row + f_g;
     const int my_bc = 32 * ch + c32;
 
-    struct XRegs { f32x4 x[4][2]; };
+    struct XRegs { f32x4 x[MT][2]; };
     struct CRegs2 { uint32_t b[4]; };
     struct SZ { uint16_t s, z; };
     auto load_x = [&](XRegs& g, int kt) {
         const int k0 = (kt0 + min(kt, ktiles - 1)) * BK;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < MT; i++) {
             g.x[i][0] = *reinterpret_cast<const f32x4*>(x_src[i] + k0);
             g.x[i][1] = *reinterpret_cast<const f32x4*>(x_src[i] + k0 + 4);
         }
@@ -839,7 +841,9 @@ __device__ __forceinline__ void gemm_tile_f32x3(XLds& lds, const float* __restri
         f.y = (sv == 0.0f) ? zv : -(zv * sv);
         lds.fold[fb][f_dst] = f;
     };
-    float corr[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float corr[MT];
+#pragma unroll
+    for (int i = 0; i < MT; i++) corr[i] = 0.0f;
     // The three terms of m-tile i's chunk, from its activations and the
     // stage's fold (fv: the eight k of this lane), into LDS buffer `buf`;
     // `real` is false for the stage past the last, staged (from clamped
@@ -871,10 +875,10 @@ __device__ __forceinline__ void gemm_tile_f32x3(XLds& lds, const float* __restri
         }
     };
 
-    // One substep's operands: the three terms' A fragments of the four
+    // One substep's operands: the three terms' A fragments of the MT
     // m-tiles, one code byte of eight rows.
     struct XSub {
-        bf16x8 af[kXTerms][4];
+        bf16x8 af[kXTerms][MT];
         uint32_t tw[2];
     };
     auto read_sub = [&](XSub& r, int buf, int ks) {
@@ -884,7 +888,7 @@ __device__ __forceinline__ void gemm_tile_f32x3(XLds& lds, const float* __restri
 #pragma unroll
         for (int tt = 0; tt < kXTerms; tt++)
 #pragma unroll
-            for (int t = 0; t < 4; t++)
+            for (int t = 0; t < MT; t++)
                 r.af[tt][t] = *reinterpret_cast<const bf16x8*>(
                     S.a[tt] + a_off(t * 32 + c32, ks * 2 + kg));
     };
@@ -910,9 +914,9 @@ __device__ __forceinline__ void gemm_tile_f32x3(XLds& lds, const float* __restri
         }
     };
 
-    f32x16 acc[4][2];
+    f32x16 acc[MT][2];
 #pragma unroll
-    for (int t = 0; t < 4; t++)
+    for (int t = 0; t < MT; t++)
 #pragma unroll
         for (int j = 0; j < 2; j++)
 #pragma unroll
@@ -942,7 +946,7 @@ __device__ __forceinline__ void gemm_tile_f32x3(XLds& lds, const float* __restri
         f32x2 fv[8];
         read_fold(fv, 0);
 #pragma unroll
-        for (int i = 0; i < 4; i++) stage_x(gx[0].x[i], fv, i, 0, true);
+        for (int i = 0; i < MT; i++) stage_x(gx[0].x[i], fv, i, 0, true);
         *reinterpret_cast<u32x4*>(&lds.st[0].b[b_dst]) =
             transpose4(gb[0].b[0], gb[0].b[1], gb[0].b[2], gb[0].b[3]);
     }
@@ -958,7 +962,7 @@ __device__ __forceinline__ void gemm_tile_f32x3(XLds& lds, const float* __restri
 #pragma unroll
         for (int tt = 0; tt < kXTerms; tt++)
 #pragma unroll
-            for (int t = 0; t < 4; t++)
+            for (int t = 0; t < MT; t++)
 #pragma unroll
                 for (int j = 0; j < 2; j++)
                     acc[t][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(r.af[tt][t], bfr[j],
@@ -980,7 +984,7 @@ __device__ __forceinline__ void gemm_tile_f32x3(XLds& lds, const float* __restri
             read_sub(sub[1], buf, 2 + kp);
             mfma_all(sub[0], bq[0]);
 #pragma unroll
-            for (int i = 0; i < 4; i++) stage_x(gx[set ^ 1].x[i], fv, i, buf ^ 1, kt + 1 < ktiles);
+            for (int i = 0; i < MT; i++) stage_x(gx[set ^ 1].x[i], fv, i, buf ^ 1, kt + 1 < ktiles);
             *reinterpret_cast<u32x4*>(&lds.st[buf ^ 1].b[b_dst]) =
                 transpose4(gb[set ^ 1].b[0], gb[set ^ 1].b[1], gb[set ^ 1].b[2], gb[set ^ 1].b[3]);
             load_x(gx[set ^ 1], kt + 3);
@@ -1007,7 +1011,7 @@ __device__ __forceinline__ void gemm_tile_f32x3(XLds& lds, const float* __restri
     // Row corrections: the eight lanes of a row (x_c8) add theirs; LDS holds
     // one value per tile row.
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < MT; i++) {
         float c = corr[i];
         c += __shfl_xor(c, 1, 64);
         c += __shfl_xor(c, 2, 64);
@@ -1017,12 +1021,13 @@ __device__ __forceinline__ void gemm_tile_f32x3(XLds& lds, const float* __restri
     __syncthreads();
     if (x_c8 == 0) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) lds.corr[x_row + 32 * i] = corr[i];
+        for (int i = 0; i < MT; i++) lds.corr[x_row + 32 * i] = corr[i];
     }
-    // The two parities of a column half split the four m-tiles: parity 0
-    // finishes m-tiles 0 and 1, parity 1 m-tiles 2 and 3, each handing the
-    // other its partial sums of the rest through LDS (the sum of the two
-    // parities' f32 values, the same whichever wave adds them).
+    // The two parities of a column half split the m-tiles: parity 0 finishes
+    // [0, MT0), parity 1 [MT0, MT), each handing the other its partial sums
+    // of the rest through LDS (the sum of the two parities' f32 values, the
+    // same whichever wave adds them).
+    constexpr int MT0 = (MT + 1) / 2;
     const int col = n0 + 64 * ch + 2 * c32;
     float bj[2] = {0.0f, 0.0f};
     if (ep.bias) {
@@ -1032,7 +1037,7 @@ __device__ __forceinline__ void gemm_tile_f32x3(XLds& lds, const float* __restri
     auto give = [&](auto KP) {
         constexpr int p = decltype(KP)::value;
 #pragma unroll
-        for (int t = p == 0 ? 2 : 0; t < (p == 0 ? 4 : 2); t++)
+        for (int t = p == 0 ? MT0 : 0; t < (p == 0 ? MT : MT0); t++)
 #pragma unroll
             for (int j = 0; j < 2; j++)
 #pragma unroll
@@ -1045,7 +1050,7 @@ __device__ __forceinline__ void gemm_tile_f32x3(XLds& lds, const float* __restri
     auto take_store = [&](auto KP) {
         constexpr int p = decltype(KP)::value;
 #pragma unroll
-        for (int t = p == 0 ? 0 : 2; t < (p == 0 ? 2 : 4); t++) {
+        for (int t = p == 0 ? 0 : MT0; t < (p == 0 ? MT0 : MT); t++) {
 #pragma unroll
             for (int j = 0; j < 2; j++)
 #pragma unroll
@@ -1080,6 +1085,39 @@ __device__ __forceinline__ void gemm_tile_f32x3(XLds& lds, const float* __restri
     if (kp == 0) give(P0{}); else give(P1{});
     __syncthreads();
     if (kp == 0) take_store(P0{}); else take_store(P1{});
+}
+
+// The tile of rows [m0, min(m0 + 128, m_end)) with the m-tiles it has rows
+// for (uniform across the workgroup).  Measured (us, all four m-tiles / only
+// those with rows): M = 64, K = N = 4096 (split K) 26.8 / 20.3; at 17..48
+// rows the short bands also beat 16-row matrix-core decode launches, which
+// these shapes took before (4096 x 4096 at 32 rows 21.3 / 15.7, 14336 x 4096
+// at 48 rows 49.0 / 39.3).
+__device__ __forceinline__ void gemm_tile_f32x3(XLds& lds, const float* __restrict__ a,
+                                                const uint32_t* __restrict__ codes,
+                                                const uint16_t* __restrict__ scales,
+                                                const uint16_t* __restrict__ zeros,
+                                                void* __restrict__ out, int m0, int m_end,
+                                                int n0, int K, int N, const Epilogue& ep,
+                                                float* my_part, int kt0, int ktiles) {
+    switch ((min(m_end - m0, XBM) + 31) / 32) {
+        case 1:
+            gemm_tile_f32x3_t<1>(lds, a, codes, scales, zeros, out, m0, m_end, n0, K, N, ep,
+                                 my_part, kt0, ktiles);
+            break;
+        case 2:
+            gemm_tile_f32x3_t<2>(lds, a, codes, scales, zeros, out, m0, m_end, n0, K, N, ep,
+                                 my_part, kt0, ktiles);
+            break;
+        case 3:
+            gemm_tile_f32x3_t<3>(lds, a, codes, scales, zeros, out, m0, m_end, n0, K, N, ep,
+                                 my_part, kt0, ktiles);
+            break;
+        default:
+            gemm_tile_f32x3_t<4>(lds, a, codes, scales, zeros, out, m0, m_end, n0, K, N, ep,
+                                 my_part, kt0, ktiles);
+            break;
+    }
 }
 
 // With `part`, split K: workgroup (tile, slice) runs slice `slice` of the

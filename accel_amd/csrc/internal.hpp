@@ -196,13 +196,6 @@ bool int4_decode_bf16_rows_supported(int M, int K, int N, const void* a, const v
 hipError_t launch_int4_decode_bf16_rows(Device* d, hipStream_t st, const uint16_t* a,
                                         Int4Planes w, uint16_t* out, int M, int K, int N,
                                         int* status, const float* bias);
-// 17..48 rows of f32 activations as consecutive 16-row decode products,
-// where that beats the f32 matrix-core tiles (int4_decode_rows_pay); the same
-// shape limits as launch_int4_decode_f32 at 16 rows.
-bool int4_decode_rows_pay(int M, int K, int N);
-hipError_t launch_int4_decode_f32_rows(Device* d, hipStream_t st, const float* a,
-                                       Int4Planes w, void* out, int M, int K, int N,
-                                       int* status, Epilogue ep = Epilogue{});
 // Any shape, f32 activations: one thread per output element (small or ragged
 // shapes).
 hipError_t launch_int4_generic_f32(hipStream_t st, const float* a, Int4Planes w,

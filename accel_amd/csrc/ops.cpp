@@ -136,7 +136,6 @@ int check_out(const char* op, const accel_tensor_t* out, int32_t dtype, int64_t 
 enum class Int4Route {
     kNone,          // an empty product: nothing to launch
     kDecodeF32,     // M <= 16 f32 rows: the decode kernels
-    kDecodeF32Rows, // 17..48 f32 rows as 16-row decode products
     kGemmF32x3,     // M > 16 f32 rows on the matrix cores, three-term split
     kGemmF32,       // M > 16 f32 rows, fp32 VALU tiles
     kGenericF32,    // one lane per output element
@@ -192,22 +191,16 @@ Int4Choice choose_int4(int32_t dtype, const void* a, const void* codes, int M, i
                    "they take N a multiple of 128 and 16-byte aligned codes");
         else
             reject("the decode kernels", "they take at most 16 rows a launch");
-        if (int4_decode_rows_pay(M, K, N) && K % 32 == 0 &&
-            int4_decode_f32_supported(16, K, N, codes) && aligned16(a)) {
-            c.route = Int4Route::kDecodeF32Rows;
-            c.reason = "17..48 f32 rows of a large matrix: consecutive 16-row matrix-core "
-                       "decode products beat a band of the f32 matrix-core tiles here";
-            return c;
-        }
-        if (M <= 48 && M > 16)
-            reject("16-row decode products",
-                   "they pay only for 17..32 rows with K*N >= 2^23 or 33..48 with K*N >= "
-                   "2^25, K % 32 == 0 and 16-byte aligned rows");
         if (M > 16 && int4_gemm_f32x3_supported(K, N) && aligned16(a)) {
             c.route = Int4Route::kGemmF32x3;
             c.reason = "more than 16 f32 rows: the bf16 matrix-core tiles to f32 accuracy "
-                       "(x*512s in three bf16 terms against the exact codes); K split when "
-                       "the tiles leave CUs idle";
+                       "(x*512s in three bf16 terms against the exact codes), a short band "
+                       "running only the 32-row m-tiles it has rows for; K split when the "
+                       "tiles leave CUs idle";
+            if (M <= 48)
+                reject("16-row matrix-core decode products",
+                       "the tiles' short bands beat them from 17 rows (4096 x 4096 at 32 "
+                       "rows: 15.7 against 21.3 us)");
             return c;
         }
         if (M > 16)
@@ -271,8 +264,6 @@ hipError_t launch_int4_route(Device* d, hipStream_t st, Int4Route r, const void*
         case Int4Route::kNone: return hipSuccess;
         case Int4Route::kDecodeF32:
             return launch_int4_decode_f32(d, st, af, p, out, M, K, N, status, ep);
-        case Int4Route::kDecodeF32Rows:
-            return launch_int4_decode_f32_rows(d, st, af, p, out, M, K, N, status, ep);
         case Int4Route::kGemmF32x3:
             return launch_int4_gemm_f32x3(d, st, af, p, out, M, K, N, ep, status);
         case Int4Route::kGemmF32: return launch_int4_gemm_f32(d, st, af, p, out, M, K, N, ep);

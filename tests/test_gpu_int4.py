@@ -105,8 +105,8 @@ SHAPES_F32 = [
     (3, 200, 640), (6, 100, 1024), (12, 72, 512), (2, 4100, 1024), (1, 4096, 640),
     # two rows on the matrix-core decode kernel: one- and two-group tiles
     (2, 4096, 14336), (2, 1024, 640),
-    # 17..48 rows as 16-row decode launches (K N >= 2^23 for two, 2^25 for
-    # three): a last launch of one row (the VALU kernel), of two, of eight
+    # 17..48 rows: the f32 matrix-core tiles running only the m-tiles a short
+    # band has rows for (one, one and two of four), K split
     (17, 1024, 8192), (18, 2048, 4096), (40, 8192, 4096),
     # K long enough that a workgroup loops over several batches of rows (256-
     # and 128-column tiles), and the layer chain's down projection

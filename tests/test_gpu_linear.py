@@ -52,7 +52,7 @@ def _free(*bufs):
     (16, 1024, 768, False),
     (12, 200, 256, False),     # K % 32 != 0: VALU decode, eight rows then four
     (40, 256, 384, False),     # f32 tiled
-    (20, 2048, 4096, False),   # 16-row decode launches: sixteen rows, then four
+    (20, 2048, 4096, False),   # the f32 tiles, one m-tile of rows, K split
     (3, 40, 21, False),        # per-element kernel
 ])
 def test_f32_activations_equal_the_product_plus_bias(dev, M, K, N, vector):

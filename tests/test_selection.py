@@ -47,9 +47,9 @@ F32_ROUTES = {
     (1, 4096, 640): [f"{DEC1}<1, 128, 32, false, float>"],
     (2, 4096, 14336): [f"{MF}<2, 8, float>"],
     (2, 1024, 640): [f"{MF}<1, 8, float>"],
-    (17, 1024, 8192): [f"{MF}<1, 8, float>", f"{DEC1}<1, 512, 32, false, float>"],
-    (18, 2048, 4096): [f"{MF}<1, 8, float>"] * 2,
-    (40, 8192, 4096): [f"{MF}<1, 8, float>"] * 3,
+    (17, 1024, 8192): ["int4_gemm_f32x3_kernel", "int4_gemm_reduce_kernel"],
+    (18, 2048, 4096): ["int4_gemm_f32x3_kernel", "int4_gemm_reduce_kernel"],
+    (40, 8192, 4096): ["int4_gemm_f32x3_kernel", "int4_gemm_reduce_kernel"],
     (1, 16640, 256): [f"{DEC1}<1, 256, 32, true, float>"],
     (2, 33000, 128): [f"{DEC1}<2, 128, 32, true, float>"],
     (1, 14336, 4096): [f"{DEC1}<1, 256, 32, false, float>"],
