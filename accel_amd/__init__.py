@@ -174,6 +174,8 @@ SIGNATURES = {
     "accel_int4_prepared_bytes": ([_vp, _P(ctypes.c_uint64)], _i),
     "accel_int4_matvec_prepared": ([_i, _vp, _P(Tensor), _vp, _P(Tensor)], _i),
     "accel_int4_matvec_prepared_set": ([_i, _vp, _P(Tensor), _P(_vp), _P(Tensor), _i], _i),
+    "accel_int4_matmul_prepared": ([_i, _vp, _P(Tensor), _vp, _P(Tensor)], _i),
+    "accel_int4_matmul_prepared_set": ([_i, _vp, _P(Tensor), _P(_vp), _P(Tensor), _i], _i),
     "accel_int4_matvec_set": ([_i, _vp, _P(Tensor), _P(Int4Desc), _P(Tensor), _i], _i),
     "accel_int4_matmul_set": ([_i, _vp, _P(Tensor), _P(Int4Desc), _P(Tensor), _i], _i),
     "accel_segment_offsets": ([_i, _vp, _P(Tensor), _P(Tensor)], _i),
@@ -605,6 +607,22 @@ class Device:
         outt = (Tensor * max(n, 1))(*[o.tensor() for o in outs])
         ta = a.tensor()
         _check(_lib.accel_int4_matvec_prepared_set(self.index, stream, ctypes.byref(ta), hs,
+                                                   outt, n))
+
+    def Int4MatMulPrepared(self, a: Buffer, w: PreparedInt4, out: Buffer, stream=None) -> None:
+        """Int4MatMul of a ([M, K] f32) and a prepared weight into out ([M, N])."""
+        ta, to = a.tensor(), out.tensor()
+        _check(_lib.accel_int4_matmul_prepared(self.index, stream, ctypes.byref(ta), w.handle,
+                                               ctypes.byref(to)))
+
+    def Int4MatMulPreparedSet(self, a: Buffer, ws, outs, stream=None) -> None:
+        """Int4MatMulPrepared of each of ws (1..4 prepared weights sharing the
+        input rows a) into outs, in one launch a pass of eight rows."""
+        n = len(ws)
+        hs = (ctypes.c_void_p * max(n, 1))(*[w.handle for w in ws])
+        outt = (Tensor * max(n, 1))(*[o.tensor() for o in outs])
+        ta = a.tensor()
+        _check(_lib.accel_int4_matmul_prepared_set(self.index, stream, ctypes.byref(ta), hs,
                                                    outt, n))
 
     def Int4MatVecNoAlloc(self, a: Buffer, w: Int4Weights, out: Buffer, stream=None) -> None:

@@ -307,6 +307,13 @@ hipError_t launch_int4_panel_prepare(hipStream_t st, Int4Planes w, void* dst, in
 // a f32 [K] -> out[i] [N[i]] (f32, or bf16 with ep.bf16) over `count` (1..4)
 // prepared matrices of K rows, in one launch.
 constexpr int kMaxPreparedSet = 4;
+// M rows of a ([M, K], K even, rows 8-byte aligned) against count (1..4)
+// prepared matrices of K rows, out[i] [M, N[i]], in passes of up to eight
+// rows.
+bool int4_panel_rows_supported(int M, int K, const float* a);
+hipError_t launch_int4_panel_rows(hipStream_t st, const float* a, int M,
+                                  const void* const* prepared, void* const* out, const int* N,
+                                  int count, int K, Epilogue ep);
 hipError_t launch_int4_panel_matvec(hipStream_t st, const float* a, const void* const* prepared,
                                     void* const* out, const int* N, int count, int K,
                                     Epilogue ep);

@@ -1413,6 +1413,105 @@ ACCEL_API int accel_int4_matvec_prepared_set(int dev, void* stream, const accel_
     return finish(d, e, status, "Int4MatVecPreparedSet launch");
 }
 
+namespace {
+
+const char* kRowsReason =
+    "2..8 f32 rows of prepared weights: one workgroup a 16-column panel over all of K, each "
+    "lane the panel's columns for every row, no K split and no hand-off (passes of eight "
+    "rows past eight)";
+const char* kRowsRejected =
+    "the matrix-core decode kernel on the reference planes: its time is set by load latency, "
+    "its K split and the hand-off, about the same from two rows to sixteen";
+
+// Int4MatMul's checks of a ([M, K] f32) and out ([M, N_i] f32) against count
+// prepared weights, then the product: one row as Int4MatVecPrepared, more in
+// passes of up to eight rows on the rows kernel.
+int run_prepared_rows(const char* op, int dev, void* stream, const accel_tensor_t* a,
+                      const accel_int4_prepared_t* const* w, accel_tensor_t* out, int count) {
+    char buf[320];
+    if (count < 1 || count > kMaxPreparedSet || !w || !out) {
+        snprintf(buf, sizeof buf, "%d matrices; a set holds one to %d", count, kMaxPreparedSet);
+        return refuse(op, buf);
+    }
+    if (!valid_tensor(a) || !a->data) return refuse(op, "the activations are missing");
+    if (a->dtype != ACCEL_F32 || a->rank != 2) {
+        snprintf(buf, sizeof buf, "activations are %s %s; this product takes f32 [M, K]",
+                 dtype_name(a->dtype), shape_str(a).c_str());
+        return refuse(op, buf);
+    }
+    const int64_t M = a->shape[0], K = a->shape[1];
+    const void* data[kMaxPreparedSet];
+    void* o[kMaxPreparedSet];
+    int N[kMaxPreparedSet];
+    for (int i = 0; i < count; i++) {
+        if (!w[i] || w[i]->magic != kPreparedMagic) {
+            snprintf(buf, sizeof buf, "prepared weight %d is missing", i);
+            return refuse(op, buf);
+        }
+        if (w[i]->dev != dev) {
+            snprintf(buf, sizeof buf, "weight %d was prepared on device %d", i, w[i]->dev);
+            return refuse(op, buf);
+        }
+        if (K != w[i]->K) {
+            snprintf(buf, sizeof buf, "activations are [%lld, %lld] and matrix %d is [%lld, %lld]",
+                     (long long)M, (long long)K, i, (long long)w[i]->K, (long long)w[i]->N);
+            return refuse(op, buf);
+        }
+        const int rc = check_out(op, &out[i], ACCEL_F32, M, w[i]->N, false);
+        if (rc != ACCEL_OK) return rc;
+        data[i] = w[i]->data;
+        o[i] = out[i].data;
+        N[i] = (int)w[i]->N;
+    }
+    if (M > INT32_MAX) return refuse(op, "the product is larger than this backend's extents");
+    const float* af = static_cast<const float*>(a->data);
+    if (M > 1 && !int4_panel_rows_supported((int)M, (int)K, af)) {
+        snprintf(buf, sizeof buf,
+                 "[%lld, %lld] activations: the rows kernel takes K even and 8-byte aligned "
+                 "rows (one row of any K: Int4MatVecPrepared)",
+                 (long long)M, (long long)K);
+        return refuse(op, buf);
+    }
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    if (M == 0) return ACCEL_OK;
+    int status = begin_submission(d);
+    if (status != ACCEL_OK) return status;
+    LaunchRecord rec(false);
+    hipError_t e;
+    if (M == 1) {
+        e = launch_int4_panel_matvec((hipStream_t)stream, af, data, o, N, count, (int)K,
+                                     Epilogue{});
+        keep_selection(d, op, rec,
+                       "one row of prepared weights: Int4MatVecPrepared's kernel, one "
+                       "workgroup a 16-column K-major panel over all of K",
+                       kRowsRejected);
+    } else {
+        e = launch_int4_panel_rows((hipStream_t)stream, af, (int)M, data, o, N, count, (int)K,
+                                   Epilogue{});
+        keep_selection(d, op, rec, kRowsReason, kRowsRejected);
+    }
+    return finish(d, e, status, "Int4MatMulPrepared launch");
+}
+
+}  // namespace
+
+// Int4MatMul over a prepared weight: a f32 [M, K] -> out f32 [M, N].
+ACCEL_API int accel_int4_matmul_prepared(int dev, void* stream, const accel_tensor_t* a,
+                                         const accel_int4_prepared_t* w, accel_tensor_t* out) {
+    clear_error();
+    return run_prepared_rows("Int4MatMulPrepared", dev, stream, a, &w, out, 1);
+}
+
+// The same over up to four prepared weights that share a; each out[i] is
+// exactly accel_int4_matmul_prepared(a, w[i]).
+ACCEL_API int accel_int4_matmul_prepared_set(int dev, void* stream, const accel_tensor_t* a,
+                                             const accel_int4_prepared_t* const* w,
+                                             accel_tensor_t* out, int count) {
+    clear_error();
+    return run_prepared_rows("Int4MatMulPreparedSet", dev, stream, a, w, out, count);
+}
+
 // ---- the selection report ------------------------------------------------
 
 namespace {
@@ -1481,6 +1580,30 @@ ACCEL_API int accel_int4_select(int dev, const char* op, int32_t dtype, int64_t 
                        "the reference-format decode kernel: a column tile of those planes reads "
                        "a narrow strip of every row, so K is split across workgroups and the "
                        "slices meet in a hand-off");
+        return ACCEL_OK;
+    }
+    if (name == "Int4MatMulPrepared") {
+        if (dtype != ACCEL_F32 || M < 1)
+            return fail(ACCEL_E_INVALID, "accel_int4_select: Int4MatMulPrepared takes f32 "
+                                         "rows");
+        if (!int4_panel_supported(K, N))
+            return fail(ACCEL_E_INVALID, "accel_int4_select: [%lld, %lld] cannot be prepared "
+                        "(N a multiple of 128)", (long long)K, (long long)N);
+        const int n = (int)N;
+        const void* data = fake;
+        void* o = out;
+        if (M == 1) {
+            (void)launch_int4_panel_matvec(nullptr, static_cast<const float*>(a), &data, &o, &n,
+                                           1, (int)K, Epilogue{});
+        } else {
+            if (!int4_panel_rows_supported((int)M, (int)K, static_cast<const float*>(a)))
+                return fail(ACCEL_E_INVALID, "accel_int4_select: the rows kernel takes K even "
+                                             "and 8-byte aligned rows");
+            (void)launch_int4_panel_rows(nullptr, static_cast<const float*>(a), (int)M, &data,
+                                         &o, &n, 1, (int)K, Epilogue{});
+        }
+        fill_selection(sel, name, rec.joined(), M == 1 ? "one row of prepared weights: "
+                       "Int4MatVecPrepared's kernel" : kRowsReason, kRowsRejected);
         return ACCEL_OK;
     }
     if (name == "Int4MatVecNoAlloc") {

@@ -218,6 +218,151 @@ __global__ __launch_bounds__(kPanelThreads) void int4_panel_matvec_kernel(
     }
 }
 
+// ---- a few rows: 2..8 rows a launch ------------------------------------------
+//
+// The matrix-core decode kernel (decode.hip) takes about as long at two rows
+// as at sixteen (4096 x 14336: 16.5 against 18.7 us): it is set by its load
+// latency, its K split and the split's hand-off, not by its arithmetic.  On
+// prepared weights the same rows run here with no K split: one workgroup a
+// panel over all of K, as the one-row kernel, each lane holding the 16
+// columns of its panel for each of the MR rows (16 MR accumulators).  Per row
+// pair of the panel a lane unpacks the codes once and folds each row's scale
+// and zero once, (512 s, s == 0 ? z : -z s), shared by the MR rows, whose
+// activations it reads as one 8-byte load each; then per row m
+//     acc[m][j] += (x[m] 512 s) (q_j 2^-9),   bsum[m] += x[m] add
+// (the one-row kernel's arithmetic).  Rows past M (MR rounded up) read row
+// M - 1 and are not stored.  A set of up to four matrices runs as one grid,
+// as for one row.  Measured (us, this kernel / the matrix-core decode on the
+// reference planes) at 2, 4 and 8 rows: 4096 x 4096 5.3 / 10.4, 7.1 / 11.2,
+// 10.6 / 9.6; 4096 x 14336 11.9 / 16.4, 18.4 / 16.7, 37.2 / 16.9; 14336 x
+// 4096 11.0 / 16.1, 16.3 / 16.6, 24.2 / 17.6.  It wins at two rows and loses
+// at eight: a 16-column panel re-reads every row's activations, which at
+// eight rows are four times the code bytes a workgroup loads, in eight times
+// the load instructions, and the address unit sets the time.
+template <int MR, int PPL>
+struct RowsChunk {
+    u32x4 q[PPL];
+    u32x2 sz[PPL];
+    f32x2 x[PPL][MR];
+};
+
+template <int MR, int PPL, bool FULL>
+__device__ __forceinline__ void rows_fetch(RowsChunk<MR, PPL>& c, const float* __restrict__ a,
+                                           const u32x4* __restrict__ qp,
+                                           const u32x2* __restrict__ szp, int pair0, int pairs,
+                                           int K, int M) {
+#pragma unroll
+    for (int i = 0; i < PPL; i++) {
+        const uint32_t j = FULL ? (uint32_t)(pair0 + i * kPanelThreads)
+                                : (uint32_t)min(pair0 + i * kPanelThreads, pairs - 1);
+        c.q[i] = __builtin_nontemporal_load(at_offset(qp, j * 16u));
+        c.sz[i] = *at_offset(szp, j * 8u);
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+            const float* row = a + (size_t)min(m, M - 1) * K;
+            c.x[i][m] = *at_offset(reinterpret_cast<const f32x2*>(row), j * 8u);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+template <int MR, int PPL, bool FULL>
+__device__ __forceinline__ void rows_compute(float (&acc)[MR][kPanelCols], float (&bsum)[MR],
+                                             const RowsChunk<MR, PPL>& c, int pair0, int K) {
+#pragma unroll
+    for (int i = 0; i < PPL; i++) {
+        const int row = 2 * (pair0 + i * kPanelThreads);
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const uint32_t szw = h ? c.sz[i].y : c.sz[i].x;
+            const bool valid = FULL || row + h < K;
+            const float s = half_bits_to_float((uint16_t)(szw & 0xffffu));
+            const float z = half_bits_to_float((uint16_t)(szw >> 16));
+            const float mul = valid ? s * 512.0f : 0.0f;
+            const float add = valid ? (s == 0.0f ? z : -(z * s)) : 0.0f;
+            float f[kPanelCols];
+            unpack_word(h ? c.q[i].z : c.q[i].x, f);
+            unpack_word(h ? c.q[i].w : c.q[i].y, f + 8);
+#pragma unroll
+            for (int m = 0; m < MR; m++) {
+                const float x = h ? c.x[i][m].y : c.x[i][m].x;
+                const float cm = x * mul;
+                bsum[m] = __builtin_fmaf(x, add, bsum[m]);
+#pragma unroll
+                for (int jj = 0; jj < kPanelCols; jj++)
+                    acc[m][jj] = __builtin_fmaf(cm, f[jj], acc[m][jj]);
+            }
+        }
+    }
+}
+
+// out_i[m, 16 q .. 16 q + 15] = a[m, :] . panel q of matrix i, m < M <= MR,
+// for the global panel p of this workgroup.  K even, rows 8-byte aligned.
+// FULL: K a multiple of the chunk (512 PPL row pairs).
+template <int MR, int PPL, bool FULL, bool SET>
+__global__ __launch_bounds__(kPanelThreads) void int4_panel_rows_kernel(
+    const float* __restrict__ a, PanelSet set, int panels, int M, int K, Epilogue ep) {
+    const int p = panel_of(blockIdx.x, panels);
+    const PanelPick pk =
+        SET ? pick_panel(set, p) : PanelPick{set.codes[0], set.sz[0], set.out[0], 0};
+    const int q = p - pk.first;
+    const int pairs = K >> 1;
+    const u32x4* qp = pk.codes + (size_t)q * pairs;
+    const u32x2* szp = pk.sz + (size_t)(q >> 3) * pairs;
+    const int tid = threadIdx.x;
+    float acc[MR][kPanelCols];
+    float bsum[MR];
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+        bsum[m] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kPanelCols; j++) acc[m][j] = 0.0f;
+    }
+    constexpr int kChunkPairs = kPanelThreads * PPL;
+    const int chunks = (pairs + kChunkPairs - 1) / kChunkPairs;
+    for (int ci = 0; ci < chunks; ci++) {
+        const int pair0 = tid + ci * kChunkPairs;
+        RowsChunk<MR, PPL> c;
+        rows_fetch<MR, PPL, FULL>(c, a, qp, szp, pair0, pairs, K, M);
+        rows_compute<MR, PPL, FULL>(acc, bsum, c, pair0, K);
+    }
+
+    // per row, the one-row kernel's reduction: lane swaps, then the eight
+    // waves through LDS
+    __shared__ float red[kPanelThreads / 64][MR][kPanelCols];
+    const int l = tid & 63;
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+        float v[kPanelCols];
+#pragma unroll
+        for (int j = 0; j < kPanelCols; j++) v[j] = acc[m][j] + bsum[m];
+        transpose_reduce<kPanelCols, 32, 4>(v, l);
+        v[0] += xor_partner<2>(v[0], l);
+        v[0] += xor_partner<1>(v[0], l);
+        if ((l & 3) == 0) red[tid >> 6][m][reduced_offset<kPanelCols, 32, 4>(l)] = v[0];
+    }
+    __syncthreads();
+    if (tid < MR * kPanelCols) {
+        const int m = tid / kPanelCols, c = tid % kPanelCols;
+        if (m < M) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kPanelThreads / 64; w++) sum += red[w][m][c];
+            // this matrix's width from its panels: [first, next first) of the set
+            int n = panels;
+            if (SET) {
+#pragma unroll
+                for (int j = 1; j <= kMaxPanelSet; j++)
+                    if (j <= set.count && set.panel0[j] > pk.first && set.panel0[j] < n)
+                        n = set.panel0[j];
+            }
+            const int N = (n - pk.first) * kPanelCols;
+            const int col = q * kPanelCols + c;
+            store_out(pk.out, (size_t)m * N + col, col, sum, ep);
+        }
+    }
+}
+
 // ---- the bind-time copy ------------------------------------------------------
 
 // codes: a 64-row x 64-panel tile through LDS, so the reads run along the
@@ -333,6 +478,59 @@ hipError_t launch_int4_panel_matvec(hipStream_t st, const float* a, const void* 
 #undef PANEL_PIPE
 #undef PANEL_LAUNCH
     return launch_status();
+}
+
+// count (1..4) prepared matrices of K rows against M rows of a ([M, K]),
+// out[i] [M, N[i]]: passes of up to eight rows, each one launch.
+bool int4_panel_rows_supported(int M, int K, const float* a) {
+    return M >= 1 && K % 2 == 0 && (reinterpret_cast<uintptr_t>(a) & 7) == 0;
+}
+
+hipError_t launch_int4_panel_rows(hipStream_t st, const float* a, int M,
+                                  const void* const* prepared, void* const* out, const int* N,
+                                  int count, int K, Epilogue ep) {
+    constexpr int PPL = 2;
+    const size_t esz = ep.bf16 ? 2 : 4;
+    const bool full = K % (2 * kPanelThreads * PPL) == 0;
+    for (int r0 = 0; r0 < M; r0 += 8) {
+        const int rows = std::min(8, M - r0);
+        PanelSet set{};
+        set.count = count;
+        int panels = 0;
+        for (int i = 0; i < count; i++) {
+            size_t sz_off = 0;
+            int4_panel_bytes(K, N[i], &sz_off);
+            const char* base = static_cast<const char*>(prepared[i]);
+            set.codes[i] = reinterpret_cast<const u32x4*>(base);
+            set.sz[i] = reinterpret_cast<const u32x2*>(base + sz_off);
+            set.out[i] = static_cast<char*>(out[i]) + (size_t)r0 * N[i] * esz;
+            set.panel0[i] = panels;
+            panels += N[i] / kPanelCols;
+        }
+        set.panel0[count] = panels;
+        const float* ar = a + (size_t)r0 * K;
+        const dim3 grid(panels), block(kPanelThreads);
+#define ROWS_LAUNCH(R, F, S)                                                              \
+    ACCEL_LAUNCH(tname("int4_panel_rows_kernel", R, PPL, F, S) + grid_note(panels, 1),   \
+                 (int4_panel_rows_kernel<R, PPL, F, S>), grid, block, 0, st, ar, set,    \
+                 panels, rows, K, ep)
+#define ROWS_PICK(R)                                                                      \
+    do {                                                                                  \
+        if (count > 1) {                                                                  \
+            if (full) ROWS_LAUNCH(R, true, true); else ROWS_LAUNCH(R, false, true);       \
+        } else {                                                                          \
+            if (full) ROWS_LAUNCH(R, true, false); else ROWS_LAUNCH(R, false, false);     \
+        }                                                                                 \
+    } while (0)
+        if (rows <= 2) ROWS_PICK(2);
+        else if (rows <= 4) ROWS_PICK(4);
+        else ROWS_PICK(8);
+#undef ROWS_PICK
+#undef ROWS_LAUNCH
+        const hipError_t e = launch_status();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 }  // namespace accel

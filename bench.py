@@ -486,7 +486,8 @@ def bench_layer_chain(dev, stream, batch, steps=100, merged=True, sets=5, prepar
     that joins them.  merged: q, k, v and gate, up each as one set (the same
     results bit for bit).  prepared (default: at batch 1): every matrix bound
     once into the panel layout (outside the timed region) and the products
-    run as Int4MatVecPrepared[Set].  The layer's 115.9 MB of weights rotate
+    run as Int4MatVecPrepared[Set] (Int4MatMulPrepared[Set] past one row,
+    slower than the matrix-core decode at eight rows).  The layer's 115.9 MB of weights rotate
     over `sets` copies (580 MB), so with the cache flushed before the timed
     replay each step reads its weights from HBM."""
     from accel_amd import F32, workloads
@@ -521,7 +522,10 @@ def bench_layer_chain(dev, stream, batch, steps=100, merged=True, sets=5, prepar
 
     def op(a, w, o):
         if prepared:
-            dev.Int4MatVecPrepared(a, w, o, stream)
+            if batch > 1:
+                dev.Int4MatMulPrepared(a, w, o, stream)
+            else:
+                dev.Int4MatVecPrepared(a, w, o, stream)
         elif batch > 1:
             dev.Int4MatMul(a, w, o, stream)
         else:
@@ -529,7 +533,8 @@ def bench_layer_chain(dev, stream, batch, steps=100, merged=True, sets=5, prepar
 
     def ops(a, ws, names):
         if merged:
-            fn = (dev.Int4MatVecPreparedSet if prepared else
+            fn = ((dev.Int4MatMulPreparedSet if batch > 1 else dev.Int4MatVecPreparedSet)
+                  if prepared else
                   dev.Int4MatVecSet if batch == 1 else dev.Int4MatMulSet)
             fn(a, [ws[n] for n in names], [bufs[n] for n in names], stream)
         else:
@@ -561,15 +566,18 @@ def bench_layer_chain(dev, stream, batch, steps=100, merged=True, sets=5, prepar
         4096 + 1024 + 1024 + 4096 + 14336 + 14336 + 4096) + 12 * batch * 14336
     gbs = (total_bytes + act_bytes) / (ms * 1e-3) / 1e9
     if prepared:
-        kernels = "int4_panel_matvec_kernel (prepared weights) + swiglu_kernel"
+        kernels = ("int4_panel_rows_kernel" if batch > 1 else "int4_panel_matvec_kernel") + \
+            " (prepared weights) + swiglu_kernel"
     elif batch == 1:
         kernels = "int4_decode_set_kernel + int4_decode_f32_kernel (VALU decode) + swiglu_kernel"
     else:
         kernels = ("int4_decode_mfma_set_kernel + int4_decode_mfma_kernel (matrix-core decode) "
                    "+ swiglu_kernel")
     launches = (4 if merged else 7) + 1
-    variant = "prepared_b1" if prepared else "planes_b1" if batch == 1 else "planes_b8"
-    traffic = traffic_sum(CHAIN_LAUNCHES[variant]) if merged and batch in (1, 8) else None
+    variant = ("prepared_b1" if batch == 1 else None) if prepared else (
+        "planes_b1" if batch == 1 else "planes_b8")
+    traffic = (traffic_sum(CHAIN_LAUNCHES[variant])
+               if merged and batch in (1, 8) and variant else None)
     res = dict(workload=f"config 5: seven Llama-3-8B layer products as one decode step at "
                         f"batch {batch}, down fed SwiGLU(gate, up) computed on the device "
                         f"(q/k/v and gate/up as sets: {launches} launches), f32 x, "

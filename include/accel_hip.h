@@ -414,6 +414,27 @@ int accel_int4_matvec_prepared_set(int dev, void* stream, const accel_tensor_t* 
                                    const accel_int4_prepared_t* const* w, accel_tensor_t* out,
                                    int count);
 
+/* tensor.Int4MatMul (tensor/int4.go:168-212) over a prepared weight: a f32
+ * [M, K] -> out f32 [M, N], within f32 rounding of accel_int4_matmul (the
+ * sums are added in another order).  One row is accel_int4_matvec_prepared
+ * bit for bit; 2..8 rows are one launch of the rows kernel (every row against
+ * each panel, no K split), more rows passes of eight.  Past one row, K must be
+ * even and a's rows 8-byte aligned.  Allocates nothing.  Faster than
+ * accel_int4_matmul on the planes at two rows (4096 x 14336: 11.9 against
+ * 16.4 us), about even at four, slower at eight (37.2 against 16.9): a panel
+ * re-reads every row's activations. */
+int accel_int4_matmul_prepared(int dev, void* stream, const accel_tensor_t* a,
+                               const accel_int4_prepared_t* w, accel_tensor_t* out);
+
+/* The same over `count` (1..4) prepared weights of K rows that share a
+ * [M, K], out[i] f32 [M, N_i], in one launch a pass; each out[i] is exactly
+ * accel_int4_matmul_prepared(a, w[i]).  No reference counterpart as one
+ * call: the plan-level merge of Int4MatMul dispatches that read the same
+ * activations (a decode step's q, k, v and gate, up at batch M). */
+int accel_int4_matmul_prepared_set(int dev, void* stream, const accel_tensor_t* a,
+                                   const accel_int4_prepared_t* const* w, accel_tensor_t* out,
+                                   int count);
+
 /* Which kernel an operator became, and why: KernelSelection{Op, Kernel,
  * Reason, Rejected} (tensor/compile.go:36-42), as Plan.Selections reports it
  * (tensor/plan.go:36-41), for the int4 products.  kernel lists the launches
@@ -437,7 +458,8 @@ typedef struct accel_selection {
  * addresses matter only for their alignment; NULL a or w: 256-byte aligned).
  * dev < 0 plans for an MI355X as this library models it (256 CUs), so the
  * question can be asked on a host without a GPU.  op is "Int4MatVec",
- * "Int4MatMul", "Int4Linear", "Int4MatVecPrepared" or "Int4MatVecNoAlloc"
+ * "Int4MatMul", "Int4Linear", "Int4MatVecPrepared", "Int4MatMulPrepared" or
+ * "Int4MatVecNoAlloc"
  * (NULL: Int4MatVec for
  * M = 1, else Int4MatMul); flags are ACCEL_SELECT_*.  For Int4MatVecNoAlloc
  * it returns that entry point's refusal (ACCEL_E_INVALID) for a shape whose

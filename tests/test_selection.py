@@ -182,3 +182,30 @@ def test_noalloc_answers_before_a_capture():
 def test_empty_products_launch_nothing():
     sel = A.select(0, 4096, 4096)
     assert sel.launches == [] and "empty" in sel.reason
+
+
+PR = "int4_panel_rows_kernel"
+
+
+@pytest.mark.parametrize("M,K,names", [
+    (1, 4096, ["int4_panel_matvec_kernel<4, false, true, true, false>"]),
+    (2, 4096, [f"{PR}<2, 2, true, false>"]),
+    (3, 4096, [f"{PR}<4, 2, true, false>"]),
+    (8, 14336, [f"{PR}<8, 2, true, false>"]),
+    (8, 1002, [f"{PR}<8, 2, false, false>"]),
+    (17, 4096, [f"{PR}<8, 2, true, false>"] * 2 + [f"{PR}<2, 2, true, false>"]),
+])
+def test_prepared_rows_routes(M, K, names):
+    """Int4MatMulPrepared: one row on the one-row panel kernel, 2..8 rows in
+    one launch of the rows kernel (rows rounded up to 2, 4 or 8), more in
+    passes of eight."""
+    sel = A.select(M, K, 4096, A.F32, a=ALIGNED, op="Int4MatMulPrepared")
+    assert _names(sel) == names, sel
+    assert sel.op == "Int4MatMulPrepared" and sel.reason and sel.rejected
+
+
+def test_prepared_rows_need_even_k_and_aligned_rows():
+    with pytest.raises(A.Refused, match="K even"):
+        A.select(2, 1001, 4096, A.F32, a=ALIGNED, op="Int4MatMulPrepared")
+    with pytest.raises(A.Refused, match="K even"):
+        A.select(2, 4096, 4096, A.F32, a=ALIGNED + 4, op="Int4MatMulPrepared")
