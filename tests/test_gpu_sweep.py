@@ -131,3 +131,47 @@ def test_random_grouped_shapes_match_the_oracle(dev, seed):
         err = rel_l2(got.ravel(), np.asarray(want).ravel())
         assert err <= tolerance(bf16), (seed, done, form, E, K, N, counts, T, bf16, err)
         done += 1
+
+
+PREP_M = [1, 1, 2, 3, 4, 5, 7, 8, 9, 16]
+PREP_K = [1, 2, 7, 64, 130, 1000, 2048, 2050, 4096, 6144]
+PREP_N = [128, 256, 384, 1024, 1152, 2048, 8192]
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_random_prepared_shapes_match_the_oracle(dev, seed):
+    """Prepared weights (accel_int4_prepare) at random shapes: one row through
+    Int4MatVecPrepared at any K, rows through Int4MatMulPrepared (K even),
+    across the chunk boundaries (K a whole chunk or not, past one chunk) and
+    the two panel placements (panel counts that are and are not multiples of
+    64), against the oracle at the f32 tolerance."""
+    rng = np.random.Generator(np.random.PCG64(3000 + seed))
+    done = 0
+    while done < 12:
+        M = int(rng.choice(PREP_M))
+        K = int(rng.choice(PREP_K))
+        N = int(rng.choice(PREP_N))
+        if M > 1 and K % 2:
+            continue
+        if M * K * N > MAX_MACS:
+            continue
+        form = "Int4MatVecPrepared" if M == 1 and bool(rng.integers(2)) else "Int4MatMulPrepared"
+        print(f"prepared sweep seed={seed} case={done}: {form} M={M} K={K} N={N}", flush=True)
+        x = rng.standard_normal((M, K)).astype(np.float32)
+        p, s, z = workloads.fast_int4(K, N, rng)
+        wd = dev.upload_int4(p, s, z, K * N)
+        pw = dev.prepare_int4(wd, K, N)
+        vec = form == "Int4MatVecPrepared"
+        xb = dev.upload(x.reshape(K) if vec else x)
+        ob = dev.alloc((N,) if vec else (M, N), F32)
+        try:
+            getattr(dev, form)(xb, pw, ob)
+            got = ob.numpy()
+        finally:
+            for b in (xb, ob, wd):
+                b.free()
+            pw.free()
+        want = oracle.quant_matmul_int4(x, p, s, z, M, K, N, threads=8)
+        err = rel_l2(got.reshape(want.shape), want)
+        assert err <= 1e-5, (seed, done, form, M, K, N, err)
+        done += 1
