@@ -637,10 +637,9 @@ __global__ __launch_bounds__(256) void int4_gemm_reduce_kernel(const float* __re
 // e's rows are [off[e], min(off[e+1], T)) (groupedtiled.go:87-91), and a
 // block runs as many 32-row m-tiles as it has rows.  The launch is sized for
 // the most blocks the offsets can make; every workgroup counts the real
-// ones and deals the list to the XCDs in contiguous eighths (the dispatcher
-// deals workgroup b to XCD b % 8), so that the column tiles of one row
-// block -- which share its activation rows -- meet in one L2.  The
-// placement affects speed only.  Surplus workgroups exit.
+// ones and finds its (block, column tile) by the XCD placement below (the
+// dispatcher deals workgroup b to XCD b % 8).  The placement affects speed
+// only.  Surplus workgroups exit.
 __global__ __launch_bounds__(kThreads, 1) void int4_grouped_bf16_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
@@ -659,14 +658,30 @@ __global__ __launch_bounds__(kThreads, 1) void int4_grouped_bf16_kernel(
         uint32_t f, l;
         blocks_all += (rows_of(e, f, l) + BM - 1) / BM;
     }
+    // Each XCD (workgroups are dealt to the eight round robin) takes an eighth
+    // of every block's column tiles, block after block: the blocks' differing
+    // m-tile counts are spread evenly over the XCDs, and the few blocks an XCD
+    // works on at once keep their activation rows in its L2.  (One block's
+    // tiles to one XCD left the XCDs with 5-m-tile experts ~10 us behind the
+    // others: config 4 221 -> 216-217 us.)  Column counts that are not a
+    // multiple of eight tiles: contiguous eighths of the whole list.
     const int work = blocks_all * tiles_n;
-    const int per_xcd = (work + 7) / 8;
-    const int slot = blockIdx.x >> 3;
-    if (slot >= per_xcd) return;
-    const int li = (blockIdx.x & 7) * per_xcd + slot;
-    if (li >= work) return;
-    int idx = li / tiles_n;
-    const int n0 = (li % tiles_n) * BN;
+    int idx, n0;
+    if ((tiles_n & 7) == 0) {
+        const int cpx = tiles_n >> 3;
+        const int slot = blockIdx.x >> 3;
+        if (slot >= blocks_all * cpx) return;
+        idx = slot / cpx;
+        n0 = ((blockIdx.x & 7) * cpx + slot % cpx) * BN;
+    } else {
+        const int per_xcd = (work + 7) / 8;
+        const int slot = blockIdx.x >> 3;
+        if (slot >= per_xcd) return;
+        const int li = (blockIdx.x & 7) * per_xcd + slot;
+        if (li >= work) return;
+        idx = li / tiles_n;
+        n0 = (li % tiles_n) * BN;
+    }
     int e = 0, m0 = 0, m_end = 0;
     bool found = false;
     for (; e < E; e++) {
