@@ -170,6 +170,8 @@ SIGNATURES = {
                            _P(SelectionDesc)], _i),
     "accel_hip_last_selection": ([_i, _P(SelectionDesc)], _i),
     "accel_int4_prepare": ([_i, _vp, _P(Int4Desc), ctypes.c_int64, ctypes.c_int64, _P(_vp)], _i),
+    "accel_int4_prepare_tiles": ([_i, _vp, _P(Int4Desc), ctypes.c_int64, ctypes.c_int64,
+                                  _P(_vp)], _i),
     "accel_int4_prepared_free": ([_i, _vp], _i),
     "accel_int4_prepared_bytes": ([_vp, _P(ctypes.c_uint64)], _i),
     "accel_int4_matvec_prepared": ([_i, _vp, _P(Tensor), _vp, _P(Tensor)], _i),
@@ -585,13 +587,16 @@ class Device:
         _check(_lib.accel_int4_matvec(self.index, stream, ctypes.byref(ta), ctypes.byref(tw),
                                       ctypes.byref(to)))
 
-    def prepare_int4(self, w: "Int4Weights", K: int, N: int, stream=None) -> PreparedInt4:
-        """Binds w for one-row products (accel_int4_prepare): a panel copy of
-        its planes, made on the device and waited for."""
+    def prepare_int4(self, w: "Int4Weights", K: int, N: int, stream=None,
+                     tiles: bool = False) -> PreparedInt4:
+        """Binds w once, on the device, waited for: a panel copy of its planes
+        for one- and few-row products (accel_int4_prepare), or with tiles=True
+        the codes and a side copy of the scales and zeros for the matrix-core
+        decode (accel_int4_prepare_tiles)."""
         h = ctypes.c_void_p()
         tw = w.desc()
-        _check(_lib.accel_int4_prepare(self.index, stream, ctypes.byref(tw), int(K), int(N),
-                                       ctypes.byref(h)))
+        fn = _lib.accel_int4_prepare_tiles if tiles else _lib.accel_int4_prepare
+        _check(fn(self.index, stream, ctypes.byref(tw), int(K), int(N), ctypes.byref(h)))
         return PreparedInt4(self, h.value, int(K), int(N))
 
     def Int4MatVecPrepared(self, a: Buffer, w: PreparedInt4, out: Buffer, stream=None) -> None:

@@ -307,6 +307,17 @@ hipError_t launch_int4_panel_prepare(hipStream_t st, Int4Planes w, void* dst, in
 // a f32 [K] -> out[i] [N[i]] (f32, or bf16 with ep.bf16) over `count` (1..4)
 // prepared matrices of K rows, in one launch.
 constexpr int kMaxPreparedSet = 4;
+// Prepared weights for the matrix-core decode: the codes in the reference
+// order and a side copy of the scales and zeros, one contiguous block per
+// (group, 32-row step).  K % 32 == 0 and N % 128 == 0.
+bool int4_side_supported(int64_t K, int64_t N);
+size_t int4_side_bytes(int K, int N);
+hipError_t launch_int4_side_prepare(hipStream_t st, Int4Planes w, uint16_t* side, int K, int N);
+bool int4_decode_side_rows_supported(int M, const float* a);
+hipError_t launch_int4_decode_side(Device* d, hipStream_t st, const float* a,
+                                   const uint32_t* const* codes, const uint16_t* const* side,
+                                   float* const* out, const int* N, int count, int M, int K,
+                                   int* status);
 // M rows of a ([M, K], K even, rows 8-byte aligned) against count (1..4)
 // prepared matrices of K rows, out[i] [M, N[i]], in passes of up to eight
 // rows.

@@ -1239,7 +1239,11 @@ struct accel_int4_prepared {
     int64_t K, N;
     void* data;
     size_t bytes;
+    int layout;        // kPanelLayout or kTilesLayout
+    size_t side_off;   // tiles: the side copy's offset in data
 };
+static constexpr int kPanelLayout = 0;   // accel_int4_prepare: K-major panels
+static constexpr int kTilesLayout = 1;   // accel_int4_prepare_tiles: codes + side copy
 static constexpr uint32_t kPreparedMagic = 0x34544e49u;   // "INT4"
 
 ACCEL_API int accel_int4_prepare(int dev, void* stream, const accel_int4_t* w, int64_t K,
@@ -1280,8 +1284,59 @@ ACCEL_API int accel_int4_prepare(int dev, void* stream, const accel_int4_t* w, i
         (void)hipFree(data);
         return classify(d, e, "prepared weight copy");
     }
-    auto* p = new accel_int4_prepared{kPreparedMagic, dev, K, N, data, bytes};
+    auto* p = new accel_int4_prepared{kPreparedMagic, dev, K, N, data, bytes, kPanelLayout, 0};
     *out = p;
+    return ACCEL_OK;
+}
+
+// The matrix-core decode's prepared form: the code plane copied as it is and
+// a side copy of the scales and zeros, one contiguous block per (group,
+// 32-row step) (int4_side_prepare_kernel).
+ACCEL_API int accel_int4_prepare_tiles(int dev, void* stream, const accel_int4_t* w,
+                                       int64_t K, int64_t N, accel_int4_prepared_t** out) {
+    clear_error();
+    const char* op = "Int4PrepareTiles";
+    if (!out) return refuse(op, "no handle to return the prepared weight in");
+    *out = nullptr;
+    std::string why = check_int4(w, "the weight matrix");
+    if (!why.empty()) return refuse(op, why);
+    char buf[320];
+    if (K < 1 || N < 1 || w->weights != K * N) {
+        snprintf(buf, sizeof buf, "[%lld, %lld] is %lld weights and the matrix holds %lld",
+                 (long long)K, (long long)N, (long long)(K * N), (long long)w->weights);
+        return refuse(op, buf);
+    }
+    if (!int4_side_supported(K, N)) {
+        snprintf(buf, sizeof buf,
+                 "[%lld, %lld]: the matrix-core decode takes K a multiple of 32, N a multiple "
+                 "of 128 and N below 2^27",
+                 (long long)K, (long long)N);
+        return refuse(op, buf);
+    }
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    int status = begin_submission(d);
+    if (status != ACCEL_OK) return status;
+    const size_t code_bytes = (size_t)K * N / 2;
+    const size_t side_off = (code_bytes + 255) / 256 * 256;
+    const size_t bytes = side_off + int4_side_bytes((int)K, (int)N);
+    void* data = nullptr;
+    hipError_t e = hipMalloc(&data, bytes);
+    if (e != hipSuccess) return classify(d, e, "prepared weight allocation");
+    hipStream_t st = (hipStream_t)stream;
+    e = hipMemcpyAsync(data, w->codes, code_bytes, hipMemcpyDeviceToDevice, st);
+    if (e == hipSuccess)
+        e = launch_int4_side_prepare(st, planes(w),
+                                     reinterpret_cast<uint16_t*>(static_cast<char*>(data) +
+                                                                 side_off),
+                                     (int)K, (int)N);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess) {
+        (void)hipFree(data);
+        return classify(d, e, "prepared weight copy");
+    }
+    *out = new accel_int4_prepared{kPreparedMagic, dev, K, N, data, bytes, kTilesLayout,
+                                   side_off};
     return ACCEL_OK;
 }
 
@@ -1306,6 +1361,48 @@ ACCEL_API int accel_int4_prepared_bytes(const accel_int4_prepared_t* p, uint64_t
     *bytes = p->bytes;
     return ACCEL_OK;
 }
+
+namespace {
+
+const char* kTilesReason =
+    "weights prepared for the matrix cores: the matrix-core decode kernel (x*512s in three "
+    "bf16 terms against the exact codes), each 32-row step's scales and zeros one contiguous "
+    "block of the side copy";
+const char* kTilesRejected =
+    "the same kernel on the reference planes: a step's scales and zeros are a piece of each "
+    "of its 32 rows of the two planes";
+
+// M rows of a (f32, 16-byte aligned) against count tiles-prepared weights,
+// passes of up to 16 rows; outputs [M, N_i] f32.
+int run_prepared_tiles(const char* op, Device* d, int dev, void* stream, const float* af,
+                       int64_t M, const accel_int4_prepared_t* const* w, void* const* o,
+                       int count, int status) {
+    (void)dev;
+    const uint32_t* codes[kMaxPreparedSet];
+    const uint16_t* side[kMaxPreparedSet];
+    int N[kMaxPreparedSet];
+    for (int i = 0; i < count; i++) {
+        codes[i] = static_cast<const uint32_t*>(w[i]->data);
+        side[i] = reinterpret_cast<const uint16_t*>(static_cast<const char*>(w[i]->data) +
+                                                    w[i]->side_off);
+        N[i] = (int)w[i]->N;
+    }
+    const int K = (int)w[0]->K;
+    LaunchRecord rec(false);
+    hipError_t e = hipSuccess;
+    for (int64_t r0 = 0; r0 < M && e == hipSuccess && status == ACCEL_OK; r0 += 16) {
+        const int rows = (int)std::min<int64_t>(16, M - r0);
+        float* outs[kMaxPreparedSet];
+        for (int i = 0; i < count; i++)
+            outs[i] = static_cast<float*>(o[i]) + (size_t)r0 * N[i];
+        e = launch_int4_decode_side(d, (hipStream_t)stream, af + (size_t)r0 * K, codes, side,
+                                    outs, N, count, rows, K, &status);
+    }
+    keep_selection(d, op, rec, kTilesReason, kTilesRejected);
+    return finish(d, e, status, "prepared matrix-core launch");
+}
+
+}  // namespace
 
 // Int4MatVec over a prepared weight: Int4MatVec's checks on a and out, the
 // product from the panel layout (one launch, no workspace).
@@ -1335,10 +1432,19 @@ ACCEL_API int accel_int4_matvec_prepared(int dev, void* stream, const accel_tens
     }
     int rc = check_out(op, out, ACCEL_F32, 1, w->N, true);
     if (rc != ACCEL_OK) return rc;
+    if (w->layout == kTilesLayout &&
+        !int4_decode_side_rows_supported(1, static_cast<const float*>(a->data)))
+        return refuse(op, "weights prepared for the matrix cores take 16-byte aligned "
+                          "activations");
     Device* d = device(dev);
     if (!d) return ACCEL_E_NO_DEVICE;
     int status = begin_submission(d);
     if (status != ACCEL_OK) return status;
+    if (w->layout == kTilesLayout) {
+        void* o1 = out->data;
+        return run_prepared_tiles(op, d, dev, stream, static_cast<const float*>(a->data), 1, &w,
+                                  &o1, 1, status);
+    }
     LaunchRecord rec(false);
     const void* data = w->data;
     void* o = out->data;
@@ -1393,14 +1499,24 @@ ACCEL_API int accel_int4_matvec_prepared_set(int dev, void* stream, const accel_
         }
         const int rc = check_out(op, &out[i], ACCEL_F32, 1, w[i]->N, true);
         if (rc != ACCEL_OK) return rc;
+        if (w[i]->layout != w[0]->layout)
+            return refuse(op, "the weights of a set are prepared the same way (all "
+                              "accel_int4_prepare or all accel_int4_prepare_tiles)");
         data[i] = w[i]->data;
         o[i] = out[i].data;
         N[i] = (int)w[i]->N;
     }
+    if (w[0]->layout == kTilesLayout &&
+        !int4_decode_side_rows_supported(1, static_cast<const float*>(a->data)))
+        return refuse(op, "weights prepared for the matrix cores take 16-byte aligned "
+                          "activations");
     Device* d = device(dev);
     if (!d) return ACCEL_E_NO_DEVICE;
     int status = begin_submission(d);
     if (status != ACCEL_OK) return status;
+    if (w[0]->layout == kTilesLayout)
+        return run_prepared_tiles(op, d, dev, stream, static_cast<const float*>(a->data), 1, w,
+                                  o, count, status);
     LaunchRecord rec(false);
     const hipError_t e = launch_int4_panel_matvec((hipStream_t)stream,
                                                   static_cast<const float*>(a->data), data, o, N,
@@ -1459,12 +1575,26 @@ int run_prepared_rows(const char* op, int dev, void* stream, const accel_tensor_
         }
         const int rc = check_out(op, &out[i], ACCEL_F32, M, w[i]->N, false);
         if (rc != ACCEL_OK) return rc;
+        if (w[i]->layout != w[0]->layout)
+            return refuse(op, "the weights of a set are prepared the same way (all "
+                              "accel_int4_prepare or all accel_int4_prepare_tiles)");
         data[i] = w[i]->data;
         o[i] = out[i].data;
         N[i] = (int)w[i]->N;
     }
     if (M > INT32_MAX) return refuse(op, "the product is larger than this backend's extents");
     const float* af = static_cast<const float*>(a->data);
+    if (w[0]->layout == kTilesLayout) {
+        if (M > 0 && !int4_decode_side_rows_supported(1, af))
+            return refuse(op, "weights prepared for the matrix cores take 16-byte aligned "
+                              "activations");
+        Device* dt = device(dev);
+        if (!dt) return ACCEL_E_NO_DEVICE;
+        if (M == 0) return ACCEL_OK;
+        int st2 = begin_submission(dt);
+        if (st2 != ACCEL_OK) return st2;
+        return run_prepared_tiles(op, dt, dev, stream, af, M, w, o, count, st2);
+    }
     if (M > 1 && !int4_panel_rows_supported((int)M, (int)K, af)) {
         snprintf(buf, sizeof buf,
                  "[%lld, %lld] activations: the rows kernel takes K even and 8-byte aligned "
@@ -1580,6 +1710,30 @@ ACCEL_API int accel_int4_select(int dev, const char* op, int32_t dtype, int64_t 
                        "the reference-format decode kernel: a column tile of those planes reads "
                        "a narrow strip of every row, so K is split across workgroups and the "
                        "slices meet in a hand-off");
+        return ACCEL_OK;
+    }
+    if (name == "Int4MatMulPreparedTiles") {
+        if (dtype != ACCEL_F32 || M < 1)
+            return fail(ACCEL_E_INVALID, "accel_int4_select: Int4MatMulPreparedTiles takes f32 "
+                                         "rows");
+        if (!int4_side_supported(K, N))
+            return fail(ACCEL_E_INVALID, "accel_int4_select: [%lld, %lld] cannot be prepared "
+                        "for the matrix cores (K a multiple of 32, N of 128)", (long long)K,
+                        (long long)N);
+        if (!int4_decode_side_rows_supported(1, static_cast<const float*>(a)))
+            return fail(ACCEL_E_INVALID, "accel_int4_select: weights prepared for the matrix "
+                                         "cores take 16-byte aligned activations");
+        const uint32_t* c = static_cast<const uint32_t*>(fake);
+        const uint16_t* sd = static_cast<const uint16_t*>(fake);
+        const int n = (int)N;
+        for (int64_t r0 = 0; r0 < M && status == ACCEL_OK; r0 += 16) {
+            float* o = static_cast<float*>(out);
+            (void)launch_int4_decode_side(d, nullptr, static_cast<const float*>(a), &c, &sd, &o,
+                                          &n, 1, (int)std::min<int64_t>(16, M - r0), (int)K,
+                                          &status);
+        }
+        if (status != ACCEL_OK) return status;
+        fill_selection(sel, name, rec.joined(), kTilesReason, kTilesRejected);
         return ACCEL_OK;
     }
     if (name == "Int4MatMulPrepared") {

@@ -56,6 +56,7 @@ GEMV_REF_KERNEL = "int4_decode_f32_kernel<1, 256, 32, false, float>"
 GEMM_KERNEL = "int4_gemm_bf16_kernel<8, false>"
 GEMM_F32_KERNEL = "int4_gemm_f32x3_kernel"
 DECODE_MFMA_KERNEL = "int4_decode_mfma_kernel<2, 8, float>"
+DECODE_SIDE_KERNEL = "int4_decode_mfma_side_kernel<2, 8>"
 SPLITK_BF16_KERNEL = "int4_gemm_bf16_splitk_kernel<2>"
 SPLITK_F32_KERNEL = "int4_gemm_f32x3_kernel (split K, M=64)"
 GROUPED_KERNEL = "int4_grouped_bf16_kernel"
@@ -85,6 +86,11 @@ CHAIN_LAUNCHES = {
                   GEMV_REF_KERNEL,
                   "int4_decode_set_kernel<1, 512, 32, false> (gate/up set, batch 1)",
                   "swiglu_kernel (batch 1)", f"{GEMV_REF_KERNEL} (down, batch 1)"),
+    "prepared_b8": ("int4_decode_mfma_side_set_kernel<1, 8> (q/k/v set, batch 8)",
+                    "int4_decode_mfma_side_kernel<1, 8> (o, batch 8)",
+                    "int4_decode_mfma_side_set_kernel<2, 8> (gate/up set, batch 8)",
+                    "swiglu_kernel (batch 8)",
+                    "int4_decode_mfma_side_kernel<1, 8> (down, batch 8)"),
     "planes_b8": ("int4_decode_mfma_set_kernel<1, 8> (q/k/v set, batch 8)",
                   f"{_MF1} (o, batch 8)",
                   "int4_decode_mfma_set_kernel<2, 8> (gate/up set, batch 8)",
@@ -356,17 +362,27 @@ def bench_gemv_g32(dev, stream, steps=640, warmup=64):
                           "bytes_per_launch": int(nbytes)})
 
 
-def bench_gemm(dev, stream, name, steps=40, warmup=4):
+def bench_gemm(dev, stream, name, steps=40, warmup=4, tiles=False):
+    """Int4MatMul of a named config over rotated weights; with tiles, each
+    weight bound once for the matrix-core decode (accel_int4_prepare_tiles,
+    outside the timed region) and the calls Int4MatMulPrepared."""
     from accel_amd import workloads
     L = workloads.linear(**workloads.CONFIGS[name])
-    ms, _, copies = time_product(dev, stream, L,
-                                 lambda a, w, o, s: dev.Int4MatMul(a, w, o, s), steps, warmup,
-                                 bf16=L.bf16)
+    bind_ms = None
+    if tiles:
+        ms, _, copies, bind_ms = time_product(
+            dev, stream, L, lambda a, w, o, s: dev.Int4MatMulPrepared(a, w, o, s), steps,
+            warmup, prepare=lambda w: dev.prepare_int4(w, L.K, L.N, stream, tiles=True))
+    else:
+        ms, _, copies = time_product(dev, stream, L,
+                                     lambda a, w, o, s: dev.Int4MatMul(a, w, o, s), steps,
+                                     warmup, bf16=L.bf16)
     flops = 2.0 * L.M * L.N * L.K
     act = 2 if L.bf16 else 4
     bytes_per = workloads.algorithmic_bytes(L.M, L.K, L.N, act, act)
     return dict(ms=ms, us=ms * 1e3, tflops=flops / (ms * 1e-3) / 1e12,
-                gbs=bytes_per / (ms * 1e-3) / 1e9, copies=copies, bytes=bytes_per)
+                gbs=bytes_per / (ms * 1e-3) / 1e9, copies=copies, bytes=bytes_per,
+                bind_ms=bind_ms)
 
 
 def bench_moe(dev, stream, steps=20, bf16=True):
@@ -484,15 +500,16 @@ def bench_layer_chain(dev, stream, batch, steps=100, merged=True, sets=5, prepar
     up), the gate/up pair through tensor.SwiGLU (silu(gate) * up) on the
     device, so the step is seven products and the one elementwise operation
     that joins them.  merged: q, k, v and gate, up each as one set (the same
-    results bit for bit).  prepared (default: at batch 1): every matrix bound
-    once into the panel layout (outside the timed region) and the products
-    run as Int4MatVecPrepared[Set] (Int4MatMulPrepared[Set] past one row,
-    slower than the matrix-core decode at eight rows).  The layer's 115.9 MB of weights rotate
+    results bit for bit).  prepared (the default): every matrix bound once
+    (outside the timed region) -- at batch 1 into the panel layout, at batch 8
+    as codes plus side copies of the scales and zeros for the matrix-core
+    decode -- and the products run as Int4MatVecPrepared[Set] or
+    Int4MatMulPrepared[Set].  The layer's 115.9 MB of weights rotate
     over `sets` copies (580 MB), so with the cache flushed before the timed
     replay each step reads its weights from HBM."""
     from accel_amd import F32, workloads
     if prepared is None:
-        prepared = batch == 1
+        prepared = batch in (1, 8)
     shapes = workloads.LAYER_SHAPES  # name -> (K, N)
     rng = np.random.Generator(np.random.PCG64(4))
     x = rng.standard_normal((batch, 4096)).astype(np.float32)
@@ -510,7 +527,9 @@ def bench_layer_chain(dev, stream, batch, steps=100, merged=True, sets=5, prepar
         ws = {name: dev.upload_int4(*planes[name], K * N) for name, (K, N) in shapes.items()}
         if prepared:
             t0 = time.perf_counter()
-            pws = {name: dev.prepare_int4(ws[name], K, N, stream)
+            # one row: the panel layout; eight: codes and side copies for
+            # the matrix-core decode
+            pws = {name: dev.prepare_int4(ws[name], K, N, stream, tiles=batch > 1)
                    for name, (K, N) in shapes.items()}
             bind_ms = bind_ms or (time.perf_counter() - t0) * 1e3
             for w in ws.values():
@@ -566,15 +585,17 @@ def bench_layer_chain(dev, stream, batch, steps=100, merged=True, sets=5, prepar
         4096 + 1024 + 1024 + 4096 + 14336 + 14336 + 4096) + 12 * batch * 14336
     gbs = (total_bytes + act_bytes) / (ms * 1e-3) / 1e9
     if prepared:
-        kernels = ("int4_panel_rows_kernel" if batch > 1 else "int4_panel_matvec_kernel") + \
-            " (prepared weights) + swiglu_kernel"
+        kernels = ("int4_decode_mfma_side_set_kernel + int4_decode_mfma_side_kernel "
+                   "(matrix-core decode, scales and zeros from the side copies)"
+                   if batch > 1 else "int4_panel_matvec_kernel (prepared weights)") + \
+            " + swiglu_kernel"
     elif batch == 1:
         kernels = "int4_decode_set_kernel + int4_decode_f32_kernel (VALU decode) + swiglu_kernel"
     else:
         kernels = ("int4_decode_mfma_set_kernel + int4_decode_mfma_kernel (matrix-core decode) "
                    "+ swiglu_kernel")
     launches = (4 if merged else 7) + 1
-    variant = ("prepared_b1" if batch == 1 else None) if prepared else (
+    variant = ("prepared_b1" if batch == 1 else "prepared_b8") if prepared else (
         "planes_b1" if batch == 1 else "planes_b8")
     traffic = (traffic_sum(CHAIN_LAUNCHES[variant])
                if merged and batch in (1, 8) and variant else None)
@@ -1201,11 +1222,20 @@ def main():
             extra[key]["tflops"] = round(q["tflops"], 1)
         if want("decode_m16_f32"):
             progress("config 2: decode M=16 K=4096 N=14336")
-            d = bench_gemm(dev, stream, "decode_m16", steps=200, warmup=10)
+            d = bench_gemm(dev, stream, "decode_m16", steps=200, warmup=10, tiles=True)
             extra["decode_m16_f32"] = gemm_line(
                 d, "Int4MatMul M=16 K=4096 N=14336, f32 x/out (BASELINE config 2, Llama-3-8B "
-                   "MLP up-projection at decode batch 16)", DECODE_MFMA_KERNEL, "hbm",
+                   "MLP up-projection at decode batch 16), the weight bound once for the "
+                   "matrix-core decode (accel_int4_prepare_tiles: the codes as they are and a "
+                   "side copy of the scales and zeros, outside the timed region), then "
+                   "Int4MatMulPrepared", DECODE_SIDE_KERNEL, "hbm",
                 2 * 16 * 4096 * 14336, d["bytes"])
+            extra["decode_m16_f32"]["bind_ms"] = round(d["bind_ms"], 3)
+        if want("decode_m16_f32_reference_planes"):
+            d = bench_gemm(dev, stream, "decode_m16", steps=200, warmup=10)
+            extra["decode_m16_f32_reference_planes"] = gemm_line(
+                d, "config 2 on the reference planes as handed over (Int4MatMul, no bind "
+                   "step)", DECODE_MFMA_KERNEL, "hbm", 2 * 16 * 4096 * 14336, d["bytes"])
         if want("moe_grouped_bf16"):
             progress("config 4: MoE grouped product")
             extra["moe_grouped_bf16"] = bench_moe(dev, stream)
@@ -1218,10 +1248,11 @@ def main():
             if want(f"layer_chain_b{b}"):
                 progress(f"config 5: layer chain at batch {b}")
                 extra[f"layer_chain_b{b}"] = bench_layer_chain(dev, stream, b)
-        if want("layer_chain_b1_reference_planes"):
-            progress("config 5 at batch 1 on the reference planes")
-            extra["layer_chain_b1_reference_planes"] = bench_layer_chain(dev, stream, 1,
-                                                                         prepared=False)
+        for b in (1, 8):
+            if want(f"layer_chain_b{b}_reference_planes"):
+                progress(f"config 5 at batch {b} on the reference planes")
+                extra[f"layer_chain_b{b}_reference_planes"] = bench_layer_chain(
+                    dev, stream, b, prepared=False)
         if want("floors"):
             progress("launch floors of the decode shape")
             extra["floors"] = bench_floors(dev, stream)

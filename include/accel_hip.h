@@ -394,6 +394,17 @@ typedef struct accel_int4_prepared accel_int4_prepared_t;
  * Int4 weight operand of a QuantMatVecInt4 node. */
 int accel_int4_prepare(int dev, void* stream, const accel_int4_t* w, int64_t K, int64_t N,
                        accel_int4_prepared_t** out);
+/* The same for the matrix-core decode (2..16 rows, and one): the code plane
+ * copied as it is and a side copy of the scales and zeros, one contiguous
+ * block per (128-column group, 32-row step), so a step's scales and zeros are
+ * one load, not a piece of each of its 32 rows of the planes.  K % 32 == 0,
+ * N % 128 == 0.  The same bytes as the planes.  A weight prepared this way
+ * serves accel_int4_matmul_prepared[_set] (passes of 16 rows past 16) and
+ * accel_int4_matvec_prepared[_set] through the matrix-core decode kernel,
+ * which then takes 16-byte aligned activations; past one row its results
+ * are accel_int4_matmul's on the planes bit for bit. */
+int accel_int4_prepare_tiles(int dev, void* stream, const accel_int4_t* w, int64_t K,
+                             int64_t N, accel_int4_prepared_t** out);
 int accel_int4_prepared_free(int dev, accel_int4_prepared_t* w);
 /* Device bytes the prepared copy holds. */
 int accel_int4_prepared_bytes(const accel_int4_prepared_t* w, uint64_t* bytes);
@@ -458,8 +469,8 @@ typedef struct accel_selection {
  * addresses matter only for their alignment; NULL a or w: 256-byte aligned).
  * dev < 0 plans for an MI355X as this library models it (256 CUs), so the
  * question can be asked on a host without a GPU.  op is "Int4MatVec",
- * "Int4MatMul", "Int4Linear", "Int4MatVecPrepared", "Int4MatMulPrepared" or
- * "Int4MatVecNoAlloc"
+ * "Int4MatMul", "Int4Linear", "Int4MatVecPrepared", "Int4MatMulPrepared",
+ * "Int4MatMulPreparedTiles" or "Int4MatVecNoAlloc"
  * (NULL: Int4MatVec for
  * M = 1, else Int4MatMul); flags are ACCEL_SELECT_*.  For Int4MatVecNoAlloc
  * it returns that entry point's refusal (ACCEL_E_INVALID) for a shape whose
