@@ -172,6 +172,8 @@ SIGNATURES = {
     "accel_int4_prepare": ([_i, _vp, _P(Int4Desc), ctypes.c_int64, ctypes.c_int64, _P(_vp)], _i),
     "accel_int4_prepare_tiles": ([_i, _vp, _P(Int4Desc), ctypes.c_int64, ctypes.c_int64,
                                   _P(_vp)], _i),
+    "accel_int4_prepare_grouped": ([_i, _vp, _P(Int4Desc), ctypes.c_int64, ctypes.c_int64,
+                                    ctypes.c_int64, _P(_vp)], _i),
     "accel_int4_prepared_free": ([_i, _vp], _i),
     "accel_int4_prepared_bytes": ([_vp, _P(ctypes.c_uint64)], _i),
     "accel_int4_matvec_prepared": ([_i, _vp, _P(Tensor), _vp, _P(Tensor)], _i),
@@ -187,6 +189,10 @@ SIGNATURES = {
                                    _P(Tensor), _P(Tensor)], _i),
     "accel_int4_grouped_matmul": ([_i, _vp, _P(Tensor), _P(Int4Desc), ctypes.c_int64,
                                    _P(Tensor), _P(Tensor)], _i),
+    "accel_int4_grouped_matvec_prepared": ([_i, _vp, _P(Tensor), _vp, _P(Tensor), _P(Tensor)],
+                                           _i),
+    "accel_int4_grouped_matmul_prepared": ([_i, _vp, _P(Tensor), _vp, _P(Tensor), _P(Tensor)],
+                                           _i),
     "accel_swiglu": ([_i, _vp, _P(Tensor), _P(Tensor), _P(Tensor)], _i),
     "accel_rmsnorm": ([_i, _vp, _P(Tensor), _P(Tensor), ctypes.c_float, _P(Tensor)], _i),
     "accel_matvec_f32_f16": ([_i, _vp, _P(Tensor), _P(Tensor), _P(Tensor)], _i),
@@ -599,6 +605,17 @@ class Device:
         _check(fn(self.index, stream, ctypes.byref(tw), int(K), int(N), ctypes.byref(h)))
         return PreparedInt4(self, h.value, int(K), int(N))
 
+    def prepare_int4_grouped(self, w: "Int4Weights", experts: int, K: int, N: int,
+                             stream=None) -> PreparedInt4:
+        """Binds `experts` stacked [K, N] int4 matrices once, on the device,
+        waited for: the planes and each expert's side copy of its scales and
+        zeros for the matrix-core decode (accel_int4_prepare_grouped)."""
+        h = ctypes.c_void_p()
+        tw = w.desc()
+        _check(_lib.accel_int4_prepare_grouped(self.index, stream, ctypes.byref(tw),
+                                               int(experts), int(K), int(N), ctypes.byref(h)))
+        return PreparedInt4(self, h.value, int(K), int(N))
+
     def Int4MatVecPrepared(self, a: Buffer, w: PreparedInt4, out: Buffer, stream=None) -> None:
         ta, to = a.tensor(), out.tensor()
         _check(_lib.accel_int4_matvec_prepared(self.index, stream, ctypes.byref(ta), w.handle,
@@ -747,6 +764,22 @@ class Device:
         _check(_lib.accel_int4_grouped_matmul(self.index, stream, ctypes.byref(tx),
                                               ctypes.byref(tw), experts, ctypes.byref(tc),
                                               ctypes.byref(to)))
+
+    def Int4GroupedMatVecPrepared(self, x: Buffer, w: PreparedInt4, counts: Buffer, out: Buffer,
+                                  stream=None) -> None:
+        """Int4GroupedMatVec over experts bound by prepare_int4_grouped."""
+        tx, tc, to = x.tensor(), counts.tensor(), out.tensor()
+        _check(_lib.accel_int4_grouped_matvec_prepared(self.index, stream, ctypes.byref(tx),
+                                                       w.handle, ctypes.byref(tc),
+                                                       ctypes.byref(to)))
+
+    def Int4GroupedMatMulPrepared(self, x: Buffer, w: PreparedInt4, counts: Buffer, out: Buffer,
+                                  stream=None) -> None:
+        """Int4GroupedMatMul over experts bound by prepare_int4_grouped."""
+        tx, tc, to = x.tensor(), counts.tensor(), out.tensor()
+        _check(_lib.accel_int4_grouped_matmul_prepared(self.index, stream, ctypes.byref(tx),
+                                                       w.handle, ctypes.byref(tc),
+                                                       ctypes.byref(to)))
 
     def SwiGLU(self, gate: Buffer, value: Buffer, out: Buffer, stream=None) -> None:
         """tensor.SwiGLU (tensor/elementwise.go:161-188)."""

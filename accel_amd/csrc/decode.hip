@@ -1896,14 +1896,14 @@ __global__ __launch_bounds__(kDecThreads) void int4_grouped_decode_kernel(
 // blocks never share them; block u's tickets are the tile pairs past the
 // earlier blocks'.  (A persistent form, each workgroup looping over the
 // blocks, spilled registers and ran 3% slower.)
-template <int G, int NW, typename XT = float>
-__global__ __launch_bounds__(64 * NW) void int4_grouped_decode_mfma_kernel(
+template <int G, int NW, typename XT, bool SIDE>
+__device__ __forceinline__ void grouped_decode_mfma_body(
     const XT* __restrict__ x, const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
-    const uint32_t* __restrict__ off, void* __restrict__ out, float* partial,
-    uint32_t* tickets, int ticket_stride, int E, int T, int K, int N, int rows_per_slice,
-    int slices, uint32_t* fault, int wait_limit) {
-    using Tl = MfTile<G, NW>;
+    const uint16_t* __restrict__ side, const uint32_t* __restrict__ off,
+    void* __restrict__ out, float* partial, uint32_t* tickets, int ticket_stride, int E, int T,
+    int K, int N, int rows_per_slice, int slices, uint32_t* fault, int wait_limit) {
+    using Tl = MfTile<G, NW, SIDE>;
     __shared__ int blk_e, blk_row0, blk_rows;
     const int tiles = N / Tl::kCols;
     const int per_block = tiles * slices;
@@ -1961,14 +1961,42 @@ __global__ __launch_bounds__(64 * NW) void int4_grouped_decode_mfma_kernel(
     const size_t per = (size_t)K * N;
     Epilogue ep;
     ep.bf16 = sizeof(XT) == 2;
-    decode_mfma_tile<G, NW, XT>(x + (size_t)row0 * K, codes + (size_t)e * (per >> 3),
-                            scales + (size_t)e * (per >> 7), zeros + (size_t)e * (per >> 7),
+    decode_mfma_tile<G, NW, XT, SIDE>(x + (size_t)row0 * K, codes + (size_t)e * (per >> 3),
+                            SIDE ? nullptr : scales + (size_t)e * (per >> 7),
+                            SIDE ? nullptr : zeros + (size_t)e * (per >> 7),
                             static_cast<char*>(out) + (size_t)row0 * N * sizeof(XT),
                             partial ? partial + (size_t)slices * row0 * N : nullptr,
                             tickets ? tickets + ((size_t)u * tiles + tile) * ticket_stride
                                     : nullptr,
                             blk_rows, K, N, tile, slice, rows_per_slice, slices, ep,
-                            fault, wait_limit);
+                            fault, wait_limit,
+                            SIDE ? side + (size_t)e * ((size_t)(N >> 7) * (K >> 5) * 64)
+                                 : nullptr);
+}
+
+template <int G, int NW, typename XT = float>
+__global__ __launch_bounds__(64 * NW) void int4_grouped_decode_mfma_kernel(
+    const XT* __restrict__ x, const uint32_t* __restrict__ codes,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
+    const uint32_t* __restrict__ off, void* __restrict__ out, float* partial,
+    uint32_t* tickets, int ticket_stride, int E, int T, int K, int N, int rows_per_slice,
+    int slices, uint32_t* fault, int wait_limit) {
+    grouped_decode_mfma_body<G, NW, XT, false>(x, codes, scales, zeros, nullptr, off, out,
+                                              partial, tickets, ticket_stride, E, T, K, N,
+                                              rows_per_slice, slices, fault, wait_limit);
+}
+
+// The same over prepared experts: each expert's scales and zeros from its
+// side copy (see MfTile).
+template <int G, int NW, typename XT = float>
+__global__ __launch_bounds__(64 * NW) void int4_grouped_decode_mfma_side_kernel(
+    const XT* __restrict__ x, const uint32_t* __restrict__ codes,
+    const uint16_t* __restrict__ side, const uint32_t* __restrict__ off,
+    void* __restrict__ out, float* partial, uint32_t* tickets, int ticket_stride, int E, int T,
+    int K, int N, int rows_per_slice, int slices, uint32_t* fault, int wait_limit) {
+    grouped_decode_mfma_body<G, NW, XT, true>(x, codes, nullptr, nullptr, side, off, out,
+                                             partial, tickets, ticket_stride, E, T, K, N,
+                                             rows_per_slice, slices, fault, wait_limit);
 }
 
 // K slices of a grouped decode launch: enough workgroups for two per CU
@@ -2025,10 +2053,12 @@ GroupedMfma grouped_mfma(const Device* d, const void* x, Int4Planes w, int E, in
         return g;
     // an expert's scale and zero planes start 4-byte aligned when the base does
     // and K * N / 128 is even
+    // (side copies have no such condition)
     const size_t per = (size_t)K * N;
-    const bool planes_4b = ((reinterpret_cast<uintptr_t>(w.scales) |
-                             reinterpret_cast<uintptr_t>(w.zeros)) & 3) == 0 &&
-                           ((per >> 7) & 1) == 0;
+    const bool planes_4b = w.side != nullptr ||
+                           (((reinterpret_cast<uintptr_t>(w.scales) |
+                              reinterpret_cast<uintptr_t>(w.zeros)) & 3) == 0 &&
+                            ((per >> 7) & 1) == 0);
     g.plan = plan_decode_mfma(d, kMfBlockRows, K, N, planes_4b);
     // The plan above fills the CUs from one block.  The rows make at least
     // ceil(T / 16) blocks; once those blocks' column tiles alone fill the
@@ -2107,12 +2137,20 @@ hipError_t launch_grouped_mfma(Device* d, hipStream_t st, const XT* x, Int4Plane
     const int tiles = N / (128 * G);
     const bool split = g.plan.slices > 1;
     const dim3 grid((unsigned)(g.blocks * tiles * g.plan.slices));
-    ACCEL_LAUNCH(tname("int4_grouped_decode_mfma_kernel", G, 8, type_name<XT>()) +
-                     grid_note(tiles, g.plan.slices),
-                 (int4_grouped_decode_mfma_kernel<G, 8, XT>), grid, dim3(64 * 8), 0, st, x,
-                       w.codes, w.scales, w.zeros, off, out, split ? area : nullptr,
-                       split ? tickets : nullptr, g.stride, E, T, K, N, g.plan.rows,
-                       g.plan.slices, d->fault_dev, d->wait_limit);
+    if (w.side)
+        ACCEL_LAUNCH(tname("int4_grouped_decode_mfma_side_kernel", G, 8, type_name<XT>()) +
+                         grid_note(tiles, g.plan.slices),
+                     (int4_grouped_decode_mfma_side_kernel<G, 8, XT>), grid, dim3(64 * 8), 0,
+                     st, x, w.codes, w.side, off, out, split ? area : nullptr,
+                     split ? tickets : nullptr, g.stride, E, T, K, N, g.plan.rows,
+                     g.plan.slices, d->fault_dev, d->wait_limit);
+    else
+        ACCEL_LAUNCH(tname("int4_grouped_decode_mfma_kernel", G, 8, type_name<XT>()) +
+                         grid_note(tiles, g.plan.slices),
+                     (int4_grouped_decode_mfma_kernel<G, 8, XT>), grid, dim3(64 * 8), 0, st, x,
+                     w.codes, w.scales, w.zeros, off, out, split ? area : nullptr,
+                     split ? tickets : nullptr, g.stride, E, T, K, N, g.plan.rows,
+                     g.plan.slices, d->fault_dev, d->wait_limit);
     return launch_status();
 }
 

@@ -157,6 +157,9 @@ struct Int4Planes {
     const uint32_t* codes;
     const uint16_t* scales;
     const uint16_t* zeros;
+    // prepared grouped weights: each expert's side copy of its scales and
+    // zeros for the matrix-core decode (int4_side_bytes(K, N) apart), or null
+    const uint16_t* side = nullptr;
 };
 
 // What the last store of a product does: add bias[col] (f32, one value per

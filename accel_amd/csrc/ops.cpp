@@ -814,7 +814,7 @@ int run_grouped_f32(const char* op, int dev, void* stream, const accel_tensor_t*
 
 int run_grouped_int4(const char* op, int dev, void* stream, const accel_tensor_t* x,
                      const accel_int4_t* w, int64_t experts, const accel_tensor_t* counts,
-                     accel_tensor_t* out, bool matvec) {
+                     accel_tensor_t* out, bool matvec, const uint16_t* side = nullptr) {
     clear_error();
     char buf[512];
     std::string why = check_int4(w, "the expert weights");
@@ -885,12 +885,14 @@ int run_grouped_int4(const char* op, int dev, void* stream, const accel_tensor_t
                         int4_grouped_decode_supported((int)T, (int)K, (int)N, w->codes, !f32) &&
                         (uint64_t)experts * (uint64_t)K * (uint64_t)N < (1ull << 40);
     const bool tiles = tiles_f32 || (!decode && !f32);
+    // prepared experts: the matrix-core decode reads their side copies
+    Int4Planes p = planes(w);
+    p.side = side;
     // the tiles walk segments: the matvec form's rows follow e(t), whose
     // bounds are the offsets sorted (segment_bounds), in the area
     const size_t bounds_bytes = ((size_t)(experts + 1) * sizeof(uint32_t) + 255) / 256 * 256;
     const size_t area_bytes =
-        decode ? int4_grouped_decode_area(d, x->data, planes(w), (int)experts, (int)T, (int)K,
-                                          (int)N)
+        decode ? int4_grouped_decode_area(d, x->data, p, (int)experts, (int)T, (int)K, (int)N)
                : (tiles && matvec ? bounds_bytes : 0);
     void* area = nullptr;
     uint32_t* off = offsets_in_workspace(d, st, static_cast<const uint32_t*>(counts->data),
@@ -898,12 +900,19 @@ int run_grouped_int4(const char* op, int dev, void* stream, const accel_tensor_t
     if (!off) return status;
     uint32_t* tickets = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(off) -
                                                     kWorkspaceCounterBytes);
-    const Int4Planes p = planes(w);
     hipError_t e = hipSuccess;
     const uint32_t* seg = off;
     LaunchRecord rec(false);
     std::string reason, rejected;
-    if (decode) {
+    if (decode && side) {
+        reason = "few routed rows of prepared experts: each expert's rows in blocks of up to "
+                 "16 on the matrix-core decode kernel, each 32-row step's scales and zeros "
+                 "one contiguous block of the expert's side copy (the VALU decode kernel for "
+                 "the rest, on the planes)";
+        rejected = "the grouped tiles: a 128- or 256-row block for a few rows would be "
+                   "mostly empty; the reference planes: a step's scales and zeros are a piece "
+                   "of each of its 32 rows of the two planes";
+    } else if (decode) {
         reason = "few routed rows: each expert's rows in blocks of up to 16 on the "
                  "matrix-core decode kernel (and the VALU decode kernel for the rest), the "
                  "weights read once a block";
@@ -1239,11 +1248,14 @@ struct accel_int4_prepared {
     int64_t K, N;
     void* data;
     size_t bytes;
-    int layout;        // kPanelLayout or kTilesLayout
-    size_t side_off;   // tiles: the side copy's offset in data
+    int layout;        // kPanelLayout, kTilesLayout or kGroupedLayout
+    size_t side_off;   // tiles, grouped: the side copy's offset in data
+    int64_t experts = 0;                   // grouped: the expert count
+    size_t scales_off = 0, zeros_off = 0;  // grouped: the planes' offsets in data
 };
 static constexpr int kPanelLayout = 0;   // accel_int4_prepare: K-major panels
 static constexpr int kTilesLayout = 1;   // accel_int4_prepare_tiles: codes + side copy
+static constexpr int kGroupedLayout = 2;  // accel_int4_prepare_grouped: planes + side copies
 static constexpr uint32_t kPreparedMagic = 0x34544e49u;   // "INT4"
 
 ACCEL_API int accel_int4_prepare(int dev, void* stream, const accel_int4_t* w, int64_t K,
@@ -1340,6 +1352,82 @@ ACCEL_API int accel_int4_prepare_tiles(int dev, void* stream, const accel_int4_t
     return ACCEL_OK;
 }
 
+// Grouped experts prepared for the matrix-core decode: the three planes
+// copied as they are (the routes that read planes) and each expert's side
+// copy of its scales and zeros (int4_side_prepare_kernel), end to end.
+ACCEL_API int accel_int4_prepare_grouped(int dev, void* stream, const accel_int4_t* w,
+                                         int64_t experts, int64_t K, int64_t N,
+                                         accel_int4_prepared_t** out) {
+    clear_error();
+    const char* op = "Int4PrepareGrouped";
+    if (!out) return refuse(op, "no handle to return the prepared weight in");
+    *out = nullptr;
+    std::string why = check_int4(w, "the expert weights");
+    if (!why.empty()) return refuse(op, why);
+    char buf[320];
+    if (experts < 1 || K < 1 || N < 1 || w->weights / experts != K * N ||
+        w->weights % experts != 0) {
+        snprintf(buf, sizeof buf,
+                 "%lld experts of [%lld, %lld] are %lld weights and the matrix holds %lld",
+                 (long long)experts, (long long)K, (long long)N, (long long)(experts * K * N),
+                 (long long)w->weights);
+        return refuse(op, buf);
+    }
+    if (!int4_side_supported(K, N) || experts > INT32_MAX ||
+        (uint64_t)w->weights >= (1ull << 40)) {
+        snprintf(buf, sizeof buf,
+                 "%lld experts of [%lld, %lld]: the matrix-core decode takes K a multiple of "
+                 "32, N a multiple of 128, N below 2^27 and under 2^40 weights",
+                 (long long)experts, (long long)K, (long long)N);
+        return refuse(op, buf);
+    }
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    int status = begin_submission(d);
+    if (status != ACCEL_OK) return status;
+    auto up = [](size_t b) { return (b + 255) / 256 * 256; };
+    const size_t per = (size_t)K * N;
+    const size_t code_bytes = (size_t)w->weights / 2;
+    const size_t plane_bytes = (size_t)w->weights / 128 * 2;
+    const size_t side_per = int4_side_bytes((int)K, (int)N);
+    const size_t scales_off = up(code_bytes);
+    const size_t zeros_off = scales_off + up(plane_bytes);
+    const size_t side_off = zeros_off + up(plane_bytes);
+    const size_t bytes = side_off + side_per * (size_t)experts;
+    void* data = nullptr;
+    hipError_t e = hipMalloc(&data, bytes);
+    if (e != hipSuccess) return classify(d, e, "prepared weight allocation");
+    hipStream_t st = (hipStream_t)stream;
+    char* base = static_cast<char*>(data);
+    e = hipMemcpyAsync(base, w->codes, code_bytes, hipMemcpyDeviceToDevice, st);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(base + scales_off, w->scales, plane_bytes, hipMemcpyDeviceToDevice,
+                           st);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(base + zeros_off, w->zeros, plane_bytes, hipMemcpyDeviceToDevice,
+                           st);
+    for (int64_t i = 0; i < experts && e == hipSuccess; i++) {
+        const Int4Planes pi{w->codes + i * (per >> 3), w->scales + i * (per >> 7),
+                            w->zeros + i * (per >> 7)};
+        e = launch_int4_side_prepare(st, pi,
+                                     reinterpret_cast<uint16_t*>(base + side_off +
+                                                                 side_per * (size_t)i),
+                                     (int)K, (int)N);
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess) {
+        (void)hipFree(data);
+        return classify(d, e, "prepared weight copy");
+    }
+    auto* p = new accel_int4_prepared{kPreparedMagic, dev, K, N, data, bytes, kGroupedLayout,
+                                      side_off};
+    p->experts = experts;
+    p->scales_off = scales_off;
+    p->zeros_off = zeros_off;
+    *out = p;
+    return ACCEL_OK;
+}
+
 ACCEL_API int accel_int4_prepared_free(int dev, accel_int4_prepared_t* p) {
     clear_error();
     if (!p) return ACCEL_OK;
@@ -1360,6 +1448,53 @@ ACCEL_API int accel_int4_prepared_bytes(const accel_int4_prepared_t* p, uint64_t
         return fail(ACCEL_E_INVALID, "accel_int4_prepared_bytes: not a prepared weight");
     *bytes = p->bytes;
     return ACCEL_OK;
+}
+
+namespace {
+
+// Int4GroupedMatVec / Int4GroupedMatMul over experts prepared with
+// accel_int4_prepare_grouped: the same checks, routes and results, the
+// matrix-core decode reading the side copies.
+int run_grouped_prepared(const char* op, int dev, void* stream, const accel_tensor_t* x,
+                         const accel_int4_prepared_t* w, const accel_tensor_t* counts,
+                         accel_tensor_t* out, bool matvec) {
+    clear_error();
+    if (!w || w->magic != kPreparedMagic) return refuse(op, "the prepared weight is missing");
+    if (w->layout != kGroupedLayout)
+        return refuse(op, "the weight was prepared as one matrix; grouped products take "
+                          "experts prepared with accel_int4_prepare_grouped");
+    if (w->dev != dev) {
+        char b[128];
+        snprintf(b, sizeof b, "the weight was prepared on device %d", w->dev);
+        return refuse(op, b);
+    }
+    const char* base = static_cast<const char*>(w->data);
+    const int64_t n = w->experts * w->K * w->N;
+    accel_int4_t q{reinterpret_cast<const uint32_t*>(base), n / 8,
+                   reinterpret_cast<const uint16_t*>(base + w->scales_off), n / 128,
+                   reinterpret_cast<const uint16_t*>(base + w->zeros_off), n / 128, n};
+    return run_grouped_int4(op, dev, stream, x, &q, w->experts, counts, out, matvec,
+                            reinterpret_cast<const uint16_t*>(base + w->side_off));
+}
+
+}  // namespace
+
+ACCEL_API int accel_int4_grouped_matvec_prepared(int dev, void* stream,
+                                                 const accel_tensor_t* x,
+                                                 const accel_int4_prepared_t* w,
+                                                 const accel_tensor_t* counts,
+                                                 accel_tensor_t* out) {
+    return run_grouped_prepared("Int4GroupedMatVecPrepared", dev, stream, x, w, counts, out,
+                                true);
+}
+
+ACCEL_API int accel_int4_grouped_matmul_prepared(int dev, void* stream,
+                                                 const accel_tensor_t* x,
+                                                 const accel_int4_prepared_t* w,
+                                                 const accel_tensor_t* counts,
+                                                 accel_tensor_t* out) {
+    return run_grouped_prepared("Int4GroupedMatMulPrepared", dev, stream, x, w, counts, out,
+                                false);
 }
 
 namespace {
@@ -1411,6 +1546,10 @@ ACCEL_API int accel_int4_matvec_prepared(int dev, void* stream, const accel_tens
     clear_error();
     const char* op = "Int4MatVecPrepared";
     if (!w || w->magic != kPreparedMagic) return refuse(op, "the prepared weight is missing");
+    if (w->layout == kGroupedLayout)
+        return refuse(op, "the weight was prepared as grouped experts (accel_int4_prepare_grouped); "
+                          "its products are Int4GroupedMatVecPrepared and "
+                          "Int4GroupedMatMulPrepared");
     if (w->dev != dev) {
         char b[128];
         snprintf(b, sizeof b, "the weight was prepared on device %d", w->dev);
@@ -1492,6 +1631,10 @@ ACCEL_API int accel_int4_matvec_prepared_set(int dev, void* stream, const accel_
             snprintf(buf, sizeof buf, "weight %d was prepared on device %d", i, w[i]->dev);
             return refuse(op, buf);
         }
+        if (w[i]->layout == kGroupedLayout)
+            return refuse(op, "the weight was prepared as grouped experts (accel_int4_prepare_grouped); "
+                              "its products are Int4GroupedMatVecPrepared and "
+                              "Int4GroupedMatMulPrepared");
         if (a->shape[0] != w[i]->K) {
             snprintf(buf, sizeof buf, "activations are %lld long and matrix %d is [%lld, %lld]",
                      (long long)a->shape[0], i, (long long)w[i]->K, (long long)w[i]->N);
@@ -1568,6 +1711,10 @@ int run_prepared_rows(const char* op, int dev, void* stream, const accel_tensor_
             snprintf(buf, sizeof buf, "weight %d was prepared on device %d", i, w[i]->dev);
             return refuse(op, buf);
         }
+        if (w[i]->layout == kGroupedLayout)
+            return refuse(op, "the weight was prepared as grouped experts (accel_int4_prepare_grouped); "
+                              "its products are Int4GroupedMatVecPrepared and "
+                              "Int4GroupedMatMulPrepared");
         if (K != w[i]->K) {
             snprintf(buf, sizeof buf, "activations are [%lld, %lld] and matrix %d is [%lld, %lld]",
                      (long long)M, (long long)K, i, (long long)w[i]->K, (long long)w[i]->N);

@@ -73,8 +73,12 @@ SPLITK_F32_LAUNCHES = (SPLITK_F32_KERNEL, f"{REDUCE_KERNEL} (after int4_gemm_f32
 # expert's rows in blocks of up to 16 on the matrix cores.
 _GD = "int4_grouped_decode_kernel<512, 32, true, float>"
 _GDM = "int4_grouped_decode_mfma_kernel<2, 8, float>"
-GROUPED_F32_LAUNCHES = (f"{_GD} (1024 rows)", f"{_GDM} (1024 rows)")
-GROUPED_DECODE_LAUNCHES = (f"{_GD} (16 rows)", f"{_GDM} (16 rows)")
+_GDS = "int4_grouped_decode_mfma_side_kernel<2, 8, float>"
+GROUPED_F32_LAUNCHES = (f"{_GD} (1024 rows)", f"{_GDS} (1024 rows)")
+GROUPED_DECODE_LAUNCHES = (f"{_GD} (16 rows)", f"{_GDS} (16 rows)")
+# the same products on the reference planes
+GROUPED_F32_PLANES_LAUNCHES = (f"{_GD} (1024 rows)", f"{_GDM} (1024 rows)")
+GROUPED_DECODE_PLANES_LAUNCHES = (f"{_GD} (16 rows)", f"{_GDM} (16 rows)")
 # config 5's five launches a step, by variant
 _PS = "int4_panel_matvec_kernel<4, false, true, true, true>"
 _MF1 = "int4_decode_mfma_kernel<1, 8, float>"
@@ -385,11 +389,43 @@ def bench_gemm(dev, stream, name, steps=40, warmup=4, tiles=False):
                 bind_ms=bind_ms)
 
 
-def bench_moe(dev, stream, steps=20, bf16=True):
+def _grouped_timings(dev, stream, steps, call, ws, pws):
+    """Median time of a grouped call over the rotating copies: on the
+    prepared experts (pws) and on the planes (ws), or on the planes alone."""
+    out = {}
+    for prep in ((True, False) if pws else (False,)):
+        copies = pws if prep else ws
+        for i in range(len(copies)):
+            call(copies[i], prep)
+        dev.sync(stream)
+        t = Timed(dev, stream, lambda i: call(copies[i % len(copies)], prep), steps)
+        out[prep] = median_replay(t) / steps
+        t.close()
+    return out
+
+
+def _prepare_grouped(dev, ws, m):
+    """Each copy of the experts bound once (accel_int4_prepare_grouped);
+    returns the copies and the host time of one bind in ms."""
+    pws, bind_ms = [], None
+    for w in ws:
+        t0 = time.perf_counter()
+        pws.append(dev.prepare_int4_grouped(w, m.E, m.K, m.N))
+        bind_ms = bind_ms or (time.perf_counter() - t0) * 1e3
+    return pws, bind_ms
+
+
+def bench_moe(dev, stream, steps=20, bf16=True, prepared=None):
     """Config 4: Int4GroupedMatMul over 1024 routed bf16 rows, 8 experts (with
     bf16=False, the same rows in f32, the reference API's grouped dtype).  The
     experts' weights (250 MB) rotate over three copies (750 MB), so with the
-    cache flushed before the timed replay every call reads them from HBM."""
+    cache flushed before the timed replay every call reads them from HBM.
+    prepared (the default for f32 rows): the experts bound once (outside the
+    timed region) with their scales and zeros side-copied for the
+    matrix-core decode, Int4GroupedMatMulPrepared timed, and the same call on
+    the planes timed beside it."""
+    if prepared is None:
+        prepared = not bf16
     from accel_amd import BF16, F32, U32, workloads
     progress("config 4: routing and quantizing eight experts")
     m = workloads.moe_fast()
@@ -403,14 +439,18 @@ def bench_moe(dev, stream, steps=20, bf16=True):
         xb = dev.upload(np.ascontiguousarray(m.x, np.float32))
         ob = dev.alloc((R, m.N), F32)
     cb = dev.upload(m.counts, U32)
-    for w in ws:
-        dev.Int4GroupedMatMul(xb, w, m.E, cb, ob, stream=stream)
-    dev.sync(stream)
-    t = Timed(dev, stream,
-              lambda i: dev.Int4GroupedMatMul(xb, ws[i % copies], m.E, cb, ob, stream=stream),
-              steps)
-    ms = median_replay(t) / steps
-    t.close()
+    pws, bind_ms = _prepare_grouped(dev, ws, m) if prepared else (None, None)
+
+    def call(w, prep):
+        if prep:
+            dev.Int4GroupedMatMulPrepared(xb, w, cb, ob, stream=stream)
+        else:
+            dev.Int4GroupedMatMul(xb, w, m.E, cb, ob, stream=stream)
+
+    times = _grouped_timings(dev, stream, steps, call, ws, pws)
+    ms = times[prepared]
+    for w in pws or ():
+        w.free()
     flops = 2.0 * R * m.K * m.N
     wbytes = m.packed.nbytes + m.scales.nbytes + m.zeros.nbytes
     esz = 2 if bf16 else 4
@@ -421,29 +461,39 @@ def bench_moe(dev, stream, steps=20, bf16=True):
         w.free()
     tflops = flops / (ms * 1e-3) / 1e12
     dt = "bf16" if bf16 else "f32"
-    kernel = GROUPED_KERNEL if bf16 else " + ".join(GROUPED_F32_LAUNCHES)
-    return dict(workload=f"Int4GroupedMatMul: {R} routed {dt} rows (512 tokens, top-2 of 8 "
+    launches = (GROUPED_F32_LAUNCHES if prepared else GROUPED_F32_PLANES_LAUNCHES)
+    kernel = GROUPED_KERNEL if bf16 else " + ".join(launches)
+    extra = {}
+    if prepared:
+        extra = dict(us_reference_planes=round(times[False] * 1e3, 2), bind_ms=round(bind_ms, 1))
+    op = "Int4GroupedMatMulPrepared" if prepared else "Int4GroupedMatMul"
+    return dict(workload=f"{op}: {R} routed {dt} rows (512 tokens, top-2 of 8 "
                          f"experts, seed 3), K={m.K}, N={m.N}, {dt} out; expert weights "
                          f"rotated over {copies} copies"
                          + ("" if bf16 else "; each expert's rows in blocks of up to 16 on "
-                            "the matrix-core decode kernel (x*512s in three bf16 terms)"),
-                us=round(ms * 1e3, 2), rows=R, experts=m.E,
+                            "the matrix-core decode kernel (x*512s in three bf16 terms)")
+                         + ("; experts bound once (accel_int4_prepare_grouped: the planes and "
+                            "a side copy of each expert's scales and zeros), the same call on "
+                            "the planes in us_reference_planes" if prepared else ""),
+                us=round(ms * 1e3, 2), rows=R, experts=m.E, **extra,
                 counts=[int(c) for c in m.counts],
                 roofline={"bound": "mfma", "achieved": round(tflops, 1),
                           "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                           "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
-                          "traffic": traffic_sum((kernel,) if bf16 else GROUPED_F32_LAUNCHES),
+                          "traffic": traffic_sum((kernel,) if bf16 else launches),
                           "kernel": kernel,
                           "flops_per_launch": int(flops), "bytes_per_launch": int(nbytes),
                           "hbm_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)})
 
 
-def bench_moe_decode(dev, stream, tokens=8, steps=40):
+def bench_moe_decode(dev, stream, tokens=8, steps=40, prepared=True):
     """Decode MoE: `tokens` tokens routed top-2 over config 4's eight experts
     (K=4096, N=14336) as f32 rows, Int4GroupedMatVec -- decode products of
     each expert's routed rows against its matrix (blocks of up to 16 rows on
     the matrix cores).  Three copies of the experts
-    (750 MB) rotate and the cache is flushed before the timed replay."""
+    (750 MB) rotate and the cache is flushed before the timed replay.
+    prepared: the experts bound once (outside the timed region),
+    Int4GroupedMatVecPrepared timed and the call on the planes beside it."""
     from accel_amd import F32, U32, workloads
     progress(f"decode MoE: {tokens} tokens, top-2 of 8 experts")
     m = workloads.moe_fast(tokens=tokens)
@@ -453,14 +503,18 @@ def bench_moe_decode(dev, stream, tokens=8, steps=40):
     xb = dev.upload(m.x)
     cb = dev.upload(m.counts, U32)
     ob = dev.alloc((R, m.N), F32)
-    for w in ws:
-        dev.Int4GroupedMatVec(xb, w, m.E, cb, ob, stream=stream)
-    dev.sync(stream)
-    t = Timed(dev, stream,
-              lambda i: dev.Int4GroupedMatVec(xb, ws[i % copies], m.E, cb, ob, stream=stream),
-              steps)
-    ms = median_replay(t) / steps
-    t.close()
+    pws, bind_ms = _prepare_grouped(dev, ws, m) if prepared else (None, None)
+
+    def call(w, prep):
+        if prep:
+            dev.Int4GroupedMatVecPrepared(xb, w, cb, ob, stream=stream)
+        else:
+            dev.Int4GroupedMatVec(xb, w, m.E, cb, ob, stream=stream)
+
+    times = _grouped_timings(dev, stream, steps, call, ws, pws)
+    ms = times[prepared]
+    for w in pws or ():
+        w.free()
     active = int((m.counts > 0).sum())
     per_expert = (m.packed.nbytes + m.scales.nbytes + m.zeros.nbytes) // m.E
     nbytes = active * per_expert + R * m.K * 4 + R * m.N * 4
@@ -469,16 +523,23 @@ def bench_moe_decode(dev, stream, tokens=8, steps=40):
     for w in ws:
         w.free()
     gbs = nbytes / (ms * 1e-3) / 1e9
-    return dict(workload=f"Int4GroupedMatVec, decode MoE: {tokens} tokens routed top-2 over 8 "
+    launches = GROUPED_DECODE_LAUNCHES if prepared else GROUPED_DECODE_PLANES_LAUNCHES
+    extra = {}
+    if prepared:
+        extra = dict(us_reference_planes=round(times[False] * 1e3, 2), bind_ms=round(bind_ms, 1))
+    op = "Int4GroupedMatVecPrepared" if prepared else "Int4GroupedMatVec"
+    return dict(workload=f"{op}, decode MoE: {tokens} tokens routed top-2 over 8 "
                          f"experts ({R} f32 rows, seed 3's routing), K={m.K}, N={m.N}, f32 out; "
                          f"the {active} active experts' weights read once; experts rotated over "
-                         f"{copies} copies",
-                us=round(ms * 1e3, 2), rows=R, active_experts=active,
+                         f"{copies} copies"
+                         + ("; experts bound once (accel_int4_prepare_grouped), the same call "
+                            "on the planes in us_reference_planes" if prepared else ""),
+                us=round(ms * 1e3, 2), rows=R, active_experts=active, **extra,
                 counts=[int(c) for c in m.counts],
                 roofline={"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                           "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                          "traffic": traffic_sum(GROUPED_DECODE_LAUNCHES),
-                          "kernel": " + ".join(GROUPED_DECODE_LAUNCHES),
+                          "traffic": traffic_sum(launches),
+                          "kernel": " + ".join(launches),
                           "bytes_per_launch": int(nbytes)})
 
 

@@ -519,6 +519,30 @@ int accel_int4_grouped_matmul(int dev, void* stream, const accel_tensor_t* x,
                               const accel_int4_t* w, int64_t experts,
                               const accel_tensor_t* counts, accel_tensor_t* out);
 
+/* The grouped int4 weight bound once for routed decode rows: the three
+ * planes copied as they are and, after them, each expert's side copy of its
+ * scales and zeros (the layout of accel_int4_prepare_tiles, one expert after
+ * another), so a matrix-core decode step reads its scales and zeros as one
+ * load.  `experts` stacked [K,N]; K % 32 == 0, N % 128 == 0, N < 2^27.  The
+ * copy holds the planes' bytes twice over the scales and zeros (about 1.06x
+ * the planes).  No reference counterpart as one call: what a backend's
+ * GraphCompiler.Compile (internal/driver/plan.go:398-400) would do for the
+ * Int4 weight operand of a grouped node.  Freed with
+ * accel_int4_prepared_free; the single-matrix prepared operators refuse it. */
+int accel_int4_prepare_grouped(int dev, void* stream, const accel_int4_t* w, int64_t experts,
+                               int64_t K, int64_t N, accel_int4_prepared_t** out);
+
+/* accel_int4_grouped_matvec / accel_int4_grouped_matmul over experts
+ * prepared by accel_int4_prepare_grouped: the same operands otherwise, the
+ * same checks and routes, and the same results bit for bit; routed rows on
+ * the matrix-core decode read the side copies. */
+int accel_int4_grouped_matvec_prepared(int dev, void* stream, const accel_tensor_t* x,
+                                       const accel_int4_prepared_t* w,
+                                       const accel_tensor_t* counts, accel_tensor_t* out);
+int accel_int4_grouped_matmul_prepared(int dev, void* stream, const accel_tensor_t* x,
+                                       const accel_int4_prepared_t* w,
+                                       const accel_tensor_t* counts, accel_tensor_t* out);
+
 /* ---- decode-step neighbours of the int4 products ---------------------- */
 
 /* tensor.SwiGLU (tensor/elementwise.go:161-188; kernel

@@ -438,3 +438,28 @@ def test_prepared_matvec_refuses_a_missing_weight():
                                                    ctypes.byref(t))
     assert rc == accel_amd.E_INVALID
     assert "prepared weight is missing" in accel_amd.last_error()
+
+
+@pytest.mark.parametrize("E,K,N,why", [
+    (2, 16, 4096, "K a multiple of 32"),
+    (1, 2048, 64, "N a multiple of 128"),
+    (3, 256, 256, "3 experts of [256, 256] are 196608 weights and the matrix holds 131072"),
+])
+def test_prepare_grouped_refuses_what_the_side_copies_cannot_hold(E, K, N, why):
+    h = ctypes.c_void_p()
+    d = _fake_int4(256, 512)
+    rc = accel_amd.lib().accel_int4_prepare_grouped(0, None, ctypes.byref(d), E, K, N,
+                                                    ctypes.byref(h))
+    assert rc == accel_amd.E_INVALID
+    assert why in accel_amd.last_error()
+    assert h.value is None
+
+
+@pytest.mark.parametrize("fn", ["accel_int4_grouped_matvec_prepared",
+                                "accel_int4_grouped_matmul_prepared"])
+def test_grouped_prepared_refuses_a_missing_weight(fn):
+    t = accel_amd.Tensor()
+    rc = getattr(accel_amd.lib(), fn)(0, None, ctypes.byref(t), None, ctypes.byref(t),
+                                      ctypes.byref(t))
+    assert rc == accel_amd.E_INVALID
+    assert "prepared weight is missing" in accel_amd.last_error()
