@@ -415,17 +415,15 @@ def _prepare_grouped(dev, ws, m):
     return pws, bind_ms
 
 
-def bench_moe(dev, stream, steps=20, bf16=True, prepared=None):
+def bench_moe(dev, stream, steps=20, bf16=True, prepared=False):
     """Config 4: Int4GroupedMatMul over 1024 routed bf16 rows, 8 experts (with
     bf16=False, the same rows in f32, the reference API's grouped dtype).  The
     experts' weights (250 MB) rotate over three copies (750 MB), so with the
     cache flushed before the timed replay every call reads them from HBM.
-    prepared (the default for f32 rows): the experts bound once (outside the
-    timed region) with their scales and zeros side-copied for the
-    matrix-core decode, Int4GroupedMatMulPrepared timed, and the same call on
-    the planes timed beside it."""
-    if prepared is None:
-        prepared = not bf16
+    With f32 rows the same call on experts bound once (outside the timed
+    region, scales and zeros side-copied for the matrix-core decode) is timed
+    beside it, as us_prepared; prepared=True makes that the line's figure."""
+    both = prepared or not bf16
     from accel_amd import BF16, F32, U32, workloads
     progress("config 4: routing and quantizing eight experts")
     m = workloads.moe_fast()
@@ -439,7 +437,7 @@ def bench_moe(dev, stream, steps=20, bf16=True, prepared=None):
         xb = dev.upload(np.ascontiguousarray(m.x, np.float32))
         ob = dev.alloc((R, m.N), F32)
     cb = dev.upload(m.counts, U32)
-    pws, bind_ms = _prepare_grouped(dev, ws, m) if prepared else (None, None)
+    pws, bind_ms = _prepare_grouped(dev, ws, m) if both else (None, None)
 
     def call(w, prep):
         if prep:
@@ -466,6 +464,8 @@ def bench_moe(dev, stream, steps=20, bf16=True, prepared=None):
     extra = {}
     if prepared:
         extra = dict(us_reference_planes=round(times[False] * 1e3, 2), bind_ms=round(bind_ms, 1))
+    elif both:
+        extra = dict(us_prepared=round(times[True] * 1e3, 2), bind_ms=round(bind_ms, 1))
     op = "Int4GroupedMatMulPrepared" if prepared else "Int4GroupedMatMul"
     return dict(workload=f"{op}: {R} routed {dt} rows (512 tokens, top-2 of 8 "
                          f"experts, seed 3), K={m.K}, N={m.N}, {dt} out; expert weights "
@@ -474,7 +474,9 @@ def bench_moe(dev, stream, steps=20, bf16=True, prepared=None):
                             "the matrix-core decode kernel (x*512s in three bf16 terms)")
                          + ("; experts bound once (accel_int4_prepare_grouped: the planes and "
                             "a side copy of each expert's scales and zeros), the same call on "
-                            "the planes in us_reference_planes" if prepared else ""),
+                            "the planes in us_reference_planes" if prepared else "")
+                         + ("; the same call on experts bound once (accel_int4_prepare_grouped) "
+                            "in us_prepared" if both and not prepared else ""),
                 us=round(ms * 1e3, 2), rows=R, experts=m.E, **extra,
                 counts=[int(c) for c in m.counts],
                 roofline={"bound": "mfma", "achieved": round(tflops, 1),
