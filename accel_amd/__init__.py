@@ -178,6 +178,7 @@ SIGNATURES = {
     "accel_int4_prepared_bytes": ([_vp, _P(ctypes.c_uint64)], _i),
     "accel_int4_matvec_prepared": ([_i, _vp, _P(Tensor), _vp, _P(Tensor)], _i),
     "accel_int4_matvec_prepared_set": ([_i, _vp, _P(Tensor), _P(_vp), _P(Tensor), _i], _i),
+    "accel_int4_matvec_prepared_swiglu": ([_i, _vp, _P(Tensor), _vp, _vp, _P(Tensor)], _i),
     "accel_int4_matmul_prepared": ([_i, _vp, _P(Tensor), _vp, _P(Tensor)], _i),
     "accel_int4_matmul_prepared_set": ([_i, _vp, _P(Tensor), _P(_vp), _P(Tensor), _i], _i),
     "accel_int4_matvec_set": ([_i, _vp, _P(Tensor), _P(Int4Desc), _P(Tensor), _i], _i),
@@ -630,6 +631,14 @@ class Device:
         ta = a.tensor()
         _check(_lib.accel_int4_matvec_prepared_set(self.index, stream, ctypes.byref(ta), hs,
                                                    outt, n))
+
+    def Int4MatVecPreparedSwiGLU(self, a: Buffer, gate: PreparedInt4, up: PreparedInt4,
+                                 out: Buffer, stream=None) -> None:
+        """out = SwiGLU(a . gate, a . up) for two panel-prepared weights, one
+        launch (Int4MatVecPreparedSet of {gate, up} then SwiGLU, bit for bit)."""
+        ta, to = a.tensor(), out.tensor()
+        _check(_lib.accel_int4_matvec_prepared_swiglu(self.index, stream, ctypes.byref(ta),
+                                                      gate.handle, up.handle, ctypes.byref(to)))
 
     def Int4MatMulPrepared(self, a: Buffer, w: PreparedInt4, out: Buffer, stream=None) -> None:
         """Int4MatMul of a ([M, K] f32) and a prepared weight into out ([M, N])."""

@@ -331,6 +331,10 @@ hipError_t launch_int4_panel_rows(hipStream_t st, const float* a, int M,
 hipError_t launch_int4_panel_matvec(hipStream_t st, const float* a, const void* const* prepared,
                                     void* const* out, const int* N, int count, int K,
                                     Epilogue ep);
+// out [N] = SwiGLU(a . gate, a . up) (internal/kernels/elementwise.go:85-91)
+// for two prepared [K, N] matrices, one launch.
+hipError_t launch_int4_panel_swiglu(hipStream_t st, const float* a, const void* gate,
+                                    const void* up, float* out, int N, int K);
 
 // Decode-step neighbours: MatVecF32F16 (f32 a [K], f16 w [K,N] -> f32 [N]),
 // SwiGLU over n elements, RMSNorm over `rows` rows of `width`.

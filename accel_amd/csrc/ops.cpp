@@ -1672,6 +1672,66 @@ ACCEL_API int accel_int4_matvec_prepared_set(int dev, void* stream, const accel_
     return finish(d, e, status, "Int4MatVecPreparedSet launch");
 }
 
+// SwiGLU(a . gate, a . up) over two weights prepared into the panel layout:
+// Int4MatVecPreparedSet of {gate, up} followed by SwiGLU, in one launch and
+// with the same result bit for bit.
+ACCEL_API int accel_int4_matvec_prepared_swiglu(int dev, void* stream, const accel_tensor_t* a,
+                                                const accel_int4_prepared_t* gate,
+                                                const accel_int4_prepared_t* up,
+                                                accel_tensor_t* out) {
+    clear_error();
+    const char* op = "Int4MatVecPreparedSwiGLU";
+    char buf[320];
+    const accel_int4_prepared_t* w[2] = {gate, up};
+    const char* names[2] = {"gate", "up"};
+    for (int i = 0; i < 2; i++) {
+        if (!w[i] || w[i]->magic != kPreparedMagic) {
+            snprintf(buf, sizeof buf, "the prepared %s weight is missing", names[i]);
+            return refuse(op, buf);
+        }
+        if (w[i]->dev != dev) {
+            snprintf(buf, sizeof buf, "the %s weight was prepared on device %d", names[i],
+                     w[i]->dev);
+            return refuse(op, buf);
+        }
+        if (w[i]->layout != kPanelLayout) {
+            snprintf(buf, sizeof buf,
+                     "the %s weight was not prepared with accel_int4_prepare; this product "
+                     "reads the panel layout",
+                     names[i]);
+            return refuse(op, buf);
+        }
+    }
+    if (gate->K != up->K || gate->N != up->N) {
+        snprintf(buf, sizeof buf, "gate is [%lld, %lld] and up is [%lld, %lld]; they share a shape",
+                 (long long)gate->K, (long long)gate->N, (long long)up->K, (long long)up->N);
+        return refuse(op, buf);
+    }
+    if (!valid_tensor(a) || !a->data) return refuse(op, "the activations are missing");
+    if (a->dtype != ACCEL_F32 || a->rank != 1 || a->shape[0] != gate->K) {
+        snprintf(buf, sizeof buf, "activations are %s %s and the matrices are [%lld, %lld]",
+                 dtype_name(a->dtype), shape_str(a).c_str(), (long long)gate->K,
+                 (long long)gate->N);
+        return refuse(op, buf);
+    }
+    int rc = check_out(op, out, ACCEL_F32, 1, gate->N, true);
+    if (rc != ACCEL_OK) return rc;
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    int status = begin_submission(d);
+    if (status != ACCEL_OK) return status;
+    LaunchRecord rec(false);
+    const hipError_t e = launch_int4_panel_swiglu(
+        (hipStream_t)stream, static_cast<const float*>(a->data), gate->data, up->data,
+        static_cast<float*>(out->data), (int)gate->N, (int)gate->K);
+    keep_selection(d, op, rec,
+                   "two prepared weights of one shape read by SwiGLU: one workgroup a "
+                   "16-column panel of both, SwiGLU of the two sums written, nothing else",
+                   "Int4MatVecPreparedSet and SwiGLU: the two results make a round trip "
+                   "through memory and the elementwise product is a launch of its own");
+    return finish(d, e, status, "Int4MatVecPreparedSwiGLU launch");
+}
+
 namespace {
 
 const char* kRowsReason =

@@ -218,6 +218,67 @@ __global__ __launch_bounds__(kPanelThreads) void int4_panel_matvec_kernel(
     }
 }
 
+// SwiGLU(a . gate, a . up) for two prepared matrices of one shape (a decode
+// step's gate and up projections): a workgroup of twice the lanes computes
+// panel p of both, the first half of its waves gate's and the second up's,
+// each half with int4_panel_matvec_kernel's loads, sums and reduction (so
+// the two 16-value results are that kernel's bit for bit), and writes
+// out[16 p + j] = swiglu1(gate_j, up_j), the SwiGLU kernel's function of the
+// two.  The two 14336-wide results never leave the workgroup, and the
+// elementwise launch between the gate/up products and the down projection
+// is gone.  (One half-size workgroup doing both panels took 84 registers a
+// lane against 59 and ran slower than the two launches it replaces.)
+template <int PPL, bool PIPE, bool X2, bool FULL>
+__global__ __launch_bounds__(2 * kPanelThreads) void int4_panel_swiglu_kernel(
+    const float* __restrict__ a, PanelSet set, int panels, int K, int K2) {
+    const int p = panel_of(blockIdx.x, panels);
+    const int pairs = K2 >> 1;
+    const int m = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kPanelThreads);
+    const int tid = threadIdx.x % kPanelThreads;
+    const u32x4* qp = (m ? set.codes[1] : set.codes[0]) + (size_t)p * pairs;
+    const u32x2* szp = (m ? set.sz[1] : set.sz[0]) + (size_t)(p >> 3) * pairs;
+    float acc[kPanelCols];
+#pragma unroll
+    for (int j = 0; j < kPanelCols; j++) acc[j] = 0.0f;
+    float bsum = 0.0f;
+
+    constexpr int kChunkPairs = kPanelThreads * PPL;
+    PanelChunk<PPL> c;
+    panel_fetch<PPL, X2, FULL>(c, a, qp, szp, tid, pairs, K);
+    if constexpr (PIPE) {
+        const int chunks = (pairs + kChunkPairs - 1) / kChunkPairs;
+        for (int ci = 0; ci < chunks; ci++) {
+            const int pair0 = tid + ci * kChunkPairs;
+            PanelChunk<PPL> n;
+            const bool more = ci + 1 < chunks;
+            if (more) panel_fetch<PPL, X2, FULL>(n, a, qp, szp, pair0 + kChunkPairs, pairs, K);
+            panel_compute<PPL, FULL>(acc, bsum, c, pair0, K);
+            if (more) c = n;
+        }
+    } else {
+        panel_compute<PPL, FULL>(acc, bsum, c, tid, K);
+    }
+
+    __shared__ float red[2][kPanelThreads / 64][kPanelCols];
+    const int l = tid & 63;
+    float v[kPanelCols];
+#pragma unroll
+    for (int j = 0; j < kPanelCols; j++) v[j] = acc[j] + bsum;
+    transpose_reduce<kPanelCols, 32, 4>(v, l);
+    v[0] += xor_partner<2>(v[0], l);
+    v[0] += xor_partner<1>(v[0], l);
+    if ((l & 3) == 0) red[m][tid >> 6][reduced_offset<kPanelCols, 32, 4>(l)] = v[0];
+    __syncthreads();
+    if (threadIdx.x < kPanelCols) {
+        float g = 0.0f, u = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kPanelThreads / 64; w++) g += red[0][w][threadIdx.x];
+#pragma unroll
+        for (int w = 0; w < kPanelThreads / 64; w++) u += red[1][w][threadIdx.x];
+        static_cast<float*>(set.out[0])[p * kPanelCols + threadIdx.x] = swiglu1(g, u);
+    }
+}
+
 // ---- a few rows: 2..8 rows a launch ------------------------------------------
 //
 // The matrix-core decode kernel (decode.hip) takes about as long at two rows
@@ -477,6 +538,46 @@ hipError_t launch_int4_panel_matvec(hipStream_t st, const float* a, const void* 
     }
 #undef PANEL_PIPE
 #undef PANEL_LAUNCH
+    return launch_status();
+}
+
+// out [N] = SwiGLU(a . gate, a . up), gate and up prepared [K, N] matrices.
+hipError_t launch_int4_panel_swiglu(hipStream_t st, const float* a, const void* gate,
+                                    const void* up, float* out, int N, int K) {
+    const int K2 = (K + 1) / 2 * 2;
+    PanelSet set{};
+    set.count = 2;
+    size_t sz_off = 0;
+    int4_panel_bytes(K, N, &sz_off);
+    const void* mats[2] = {gate, up};
+    for (int i = 0; i < 2; i++) {
+        const char* base = static_cast<const char*>(mats[i]);
+        set.codes[i] = reinterpret_cast<const u32x4*>(base);
+        set.sz[i] = reinterpret_cast<const u32x2*>(base + sz_off);
+    }
+    set.out[0] = out;
+    const int panels = N / kPanelCols;
+    const bool x2 = K % 2 == 0 && (reinterpret_cast<uintptr_t>(a) & 7) == 0;
+    const bool ppl7 = x2 && K % (2 * kPanelThreads * 4) != 0 && K % (2 * kPanelThreads * 7) == 0;
+    const int chunk_rows = 2 * kPanelThreads * (ppl7 ? 7 : 4);
+    const bool pipe = K2 > chunk_rows;
+    const bool full = K % chunk_rows == 0;
+    const dim3 grid(panels), block(2 * kPanelThreads);
+#define SWIGLU_LAUNCH(L, P, X, F)                                                          \
+    ACCEL_LAUNCH(tname("int4_panel_swiglu_kernel", L, P, X, F) + grid_note(panels, 1),    \
+                 (int4_panel_swiglu_kernel<L, P, X, F>), grid, block, 0, st, a, set, panels, \
+                 K, K2)
+#define SWIGLU_PIPE(P)                                                                     \
+    do {                                                                                   \
+        if (ppl7) SWIGLU_LAUNCH(7, P, true, true);                                        \
+        else if (full && x2) SWIGLU_LAUNCH(4, P, true, true);                             \
+        else if (x2) SWIGLU_LAUNCH(4, P, true, false);                                    \
+        else SWIGLU_LAUNCH(4, P, false, false);                                           \
+    } while (0)
+    if (pipe) SWIGLU_PIPE(true);
+    else SWIGLU_PIPE(false);
+#undef SWIGLU_PIPE
+#undef SWIGLU_LAUNCH
     return launch_status();
 }
 

@@ -1,6 +1,7 @@
 // Device helpers shared by the decode-shape kernels (int4, f16 and int8
-// matvecs): the split-K hand-off, the cross-lane row-phase reduction and the
-// f16 widening.  Included into one anonymous namespace per translation unit.
+// matvecs): the split-K hand-off, the cross-lane row-phase reduction, the
+// f16 widening and the reference's SwiGLU of one element.  Included into one
+// anonymous namespace per translation unit.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -17,6 +18,17 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 constexpr int kDecThreads = 512;        // lanes per workgroup of the VALU kernel
 constexpr int kBatch = 4;               // rows per lane per fetch batch
 constexpr int kMaxSlices = 64;          // K slices of a VALU decode launch, at most
+
+// SwiGLU of one element (internal/kernels/elementwise.go:85-91):
+// a / (1 + Exp(-a)) * b, Exp the f64 exponential rounded once to f32
+// (kmath/kmath.go:55), every other operation rounded to f32 on its own.
+__device__ __forceinline__ float swiglu1(float x, float b) {
+#pragma clang fp contract(off)
+    const float e = (float)exp(-(double)x);
+    const float d = 1.0f + e;
+    const float q = x / d;
+    return q * b;
+}
 
 __device__ __forceinline__ float half_bits_to_float(uint16_t h) {
     _Float16 v;

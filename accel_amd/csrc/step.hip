@@ -20,19 +20,13 @@
 #include <hip/hip_runtime.h>
 
 #include "internal.hpp"
+#include "splitk.hpp"
 
 namespace accel {
 namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ float swiglu1(float x, float b) {
-#pragma clang fp contract(off)
-    const float e = (float)exp(-(double)x);
-    const float d = 1.0f + e;
-    const float q = x / d;
-    return q * b;
-}
 
 __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ a,
                                                      const float* __restrict__ b,

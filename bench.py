@@ -83,8 +83,8 @@ GROUPED_DECODE_PLANES_LAUNCHES = (f"{_GD} (16 rows)", f"{_GDM} (16 rows)")
 _PS = "int4_panel_matvec_kernel<4, false, true, true, true>"
 _MF1 = "int4_decode_mfma_kernel<1, 8, float>"
 CHAIN_LAUNCHES = {
-    "prepared_b1": (f"{_PS} (q/k/v set, batch 1)", GEMV_KERNEL, f"{_PS} (gate/up set, batch 1)",
-                    "swiglu_kernel (batch 1)",
+    "prepared_b1": (f"{_PS} (q/k/v set, batch 1)", GEMV_KERNEL,
+                    "int4_panel_swiglu_kernel<4, false, true, true> (gate/up, batch 1)",
                     "int4_panel_matvec_kernel<7, true, true, true, false> (down, batch 1)"),
     "planes_b1": ("int4_decode_set_kernel<1, 256, 32, false> (q/k/v set, batch 1)",
                   GEMV_REF_KERNEL,
@@ -557,7 +557,8 @@ def layer_planes(rng):
     return _LAYER_PLANES
 
 
-def bench_layer_chain(dev, stream, batch, steps=100, merged=True, sets=5, prepared=None):
+def bench_layer_chain(dev, stream, batch, steps=100, merged=True, sets=5, prepared=None,
+                      fused=None):
     """Config 5: one Llama-3-8B-shaped decoder layer's seven int4 products
     as a decode step: q,k,v <- x; o <- q; gate,up <- o; down <- SwiGLU(gate,
     up), the gate/up pair through tensor.SwiGLU (silu(gate) * up) on the
@@ -567,12 +568,17 @@ def bench_layer_chain(dev, stream, batch, steps=100, merged=True, sets=5, prepar
     (outside the timed region) -- at batch 1 into the panel layout, at batch 8
     as codes plus side copies of the scales and zeros for the matrix-core
     decode -- and the products run as Int4MatVecPrepared[Set] or
-    Int4MatMulPrepared[Set].  The layer's 115.9 MB of weights rotate
-    over `sets` copies (580 MB), so with the cache flushed before the timed
-    replay each step reads its weights from HBM."""
+    Int4MatMulPrepared[Set].  fused (the default on prepared weights at batch
+    1): gate, up and SwiGLU as one launch, Int4MatVecPreparedSwiGLU (the same
+    result bit for bit), with the step's time unfused reported beside it.
+    The layer's 115.9 MB of weights rotate over `sets` copies (580 MB), so
+    with the cache flushed before the timed replay each step reads its
+    weights from HBM."""
     from accel_amd import F32, workloads
     if prepared is None:
         prepared = batch in (1, 8)
+    if fused is None:
+        fused = prepared and merged and batch == 1
     shapes = workloads.LAYER_SHAPES  # name -> (K, N)
     rng = np.random.Generator(np.random.PCG64(4))
     x = rng.standard_normal((batch, 4096)).astype(np.float32)
@@ -623,20 +629,28 @@ def bench_layer_chain(dev, stream, batch, steps=100, merged=True, sets=5, prepar
             for n in names:
                 op(a, ws[n], bufs[n])
 
-    def step(i):
+    def step_with(i, fuse):
         ws = wsets[i % sets]
         ops(xin, ws, ("q", "k", "v"))
         op(bufs["q"], ws["o"], bufs["o"])
-        ops(bufs["o"], ws, ("gate", "up"))
-        dev.SwiGLU(bufs["gate"], bufs["up"], act, stream)
+        if fuse:
+            dev.Int4MatVecPreparedSwiGLU(bufs["o"], ws["gate"], ws["up"], act, stream)
+        else:
+            ops(bufs["o"], ws, ("gate", "up"))
+            dev.SwiGLU(bufs["gate"], bufs["up"], act, stream)
         op(act, ws["down"], bufs["down"])
 
-    for i in range(sets):
-        step(i)
-    dev.sync(stream)
-    t = Timed(dev, stream, step, steps)
-    ms = median_replay(t) / steps
-    t.close()
+    def timed(fuse):
+        for i in range(sets):
+            step_with(i, fuse)
+        dev.sync(stream)
+        t = Timed(dev, stream, lambda i: step_with(i, fuse), steps)
+        r = median_replay(t) / steps
+        t.close()
+        return r
+
+    ms = timed(fused)
+    ms_unfused = timed(False) if fused else None
     for ws in wsets:
         for w in ws.values():
             w.free()
@@ -646,8 +660,15 @@ def bench_layer_chain(dev, stream, batch, steps=100, merged=True, sets=5, prepar
     # two reads and one write of the 14336-wide rows
     act_bytes = 4 * batch * (4096 + 4096 + 4096 + 14336) + 4 * batch * (
         4096 + 1024 + 1024 + 4096 + 14336 + 14336 + 4096) + 12 * batch * 14336
+    if fused:
+        # gate and up stay in the workgroup: only SwiGLU's result is written
+        act_bytes = 4 * batch * (4096 + 4096 + 4096 + 14336) + 4 * batch * (
+            4096 + 1024 + 1024 + 4096 + 14336 + 4096)
     gbs = (total_bytes + act_bytes) / (ms * 1e-3) / 1e9
-    if prepared:
+    if prepared and fused:
+        kernels = ("int4_panel_matvec_kernel (prepared weights) + int4_panel_swiglu_kernel "
+                   "(gate, up and SwiGLU)")
+    elif prepared:
         kernels = ("int4_decode_mfma_side_set_kernel + int4_decode_mfma_side_kernel "
                    "(matrix-core decode, scales and zeros from the side copies)"
                    if batch > 1 else "int4_panel_matvec_kernel (prepared weights)") + \
@@ -657,15 +678,19 @@ def bench_layer_chain(dev, stream, batch, steps=100, merged=True, sets=5, prepar
     else:
         kernels = ("int4_decode_mfma_set_kernel + int4_decode_mfma_kernel (matrix-core decode) "
                    "+ swiglu_kernel")
-    launches = (4 if merged else 7) + 1
+    launches = (4 if merged else 7) + (0 if fused else 1)
     variant = ("prepared_b1" if batch == 1 else "prepared_b8") if prepared else (
         "planes_b1" if batch == 1 else "planes_b8")
     traffic = (traffic_sum(CHAIN_LAUNCHES[variant])
                if merged and batch in (1, 8) and variant else None)
     res = dict(workload=f"config 5: seven Llama-3-8B layer products as one decode step at "
                         f"batch {batch}, down fed SwiGLU(gate, up) computed on the device "
-                        f"(q/k/v and gate/up as sets: {launches} launches), f32 x, "
-                        + ("weights bound once into the panel layout, " if prepared else
+                        + (f"(q/k/v as a set, gate/up and SwiGLU as one launch: {launches} "
+                           f"launches), f32 x, " if fused else
+                           f"(q/k/v and gate/up as sets: {launches} launches), f32 x, ")
+                        + (("weights bound once into the panel layout, " if batch == 1 else
+                            "weights bound once as codes plus side copies of the scales and "
+                            "zeros (matrix-core decode), ") if prepared else
                            "reference planes, ")
                         + f"rotated over {sets} sets",
                us_per_step=round(ms * 1e3, 2), batch=batch, launches=launches,
@@ -676,6 +701,8 @@ def bench_layer_chain(dev, stream, batch, steps=100, merged=True, sets=5, prepar
                          "bytes_per_step": int(total_bytes + act_bytes)})
     if bind_ms is not None:
         res["bind_ms_per_layer"] = round(bind_ms, 3)
+    if ms_unfused is not None:
+        res["us_per_step_unfused"] = round(ms_unfused * 1e3, 2)
     return res
 
 

@@ -425,6 +425,18 @@ int accel_int4_matvec_prepared_set(int dev, void* stream, const accel_tensor_t* 
                                    const accel_int4_prepared_t* const* w, accel_tensor_t* out,
                                    int count);
 
+/* SwiGLU of two one-row products that share a [K] (a decode step's gate and
+ * up projections), out f32 [N] = SwiGLU(a . gate, a . up) with tensor.SwiGLU
+ * (tensor/elementwise.go:161-188; kernel internal/kernels/elementwise.go:
+ * 85-91), gate and up [K, N] prepared by accel_int4_prepare.  Equal bit for
+ * bit to accel_int4_matvec_prepared_set(a, {gate, up}) followed by
+ * accel_swiglu, in one launch: the two products' results never reach memory.
+ * No reference counterpart as one call: the plan-level fusion of the two
+ * QuantMatVecInt4 dispatches with the SwiGLU dispatch that reads them. */
+int accel_int4_matvec_prepared_swiglu(int dev, void* stream, const accel_tensor_t* a,
+                                      const accel_int4_prepared_t* gate,
+                                      const accel_int4_prepared_t* up, accel_tensor_t* out);
+
 /* tensor.Int4MatMul (tensor/int4.go:168-212) over a prepared weight: a f32
  * [M, K] -> out f32 [M, N], within f32 rounding of accel_int4_matmul (the
  * sums are added in another order).  One row is accel_int4_matvec_prepared

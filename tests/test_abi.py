@@ -463,3 +463,11 @@ def test_grouped_prepared_refuses_a_missing_weight(fn):
                                       ctypes.byref(t))
     assert rc == accel_amd.E_INVALID
     assert "prepared weight is missing" in accel_amd.last_error()
+
+
+def test_prepared_swiglu_refuses_a_missing_weight():
+    t = accel_amd.Tensor()
+    rc = accel_amd.lib().accel_int4_matvec_prepared_swiglu(0, None, ctypes.byref(t), None, None,
+                                                          ctypes.byref(t))
+    assert rc == accel_amd.E_INVALID
+    assert "prepared gate weight is missing" in accel_amd.last_error()

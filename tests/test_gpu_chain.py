@@ -107,3 +107,47 @@ def test_decode_step_chain_matches_the_oracle(dev, batch):
         b.free()
     for w in ws.values():
         w.free()
+
+
+def test_prepared_fused_step_at_batch_1(dev):
+    """The step as bench.py times config 5 at batch 1: every weight prepared
+    into the panel layout, q/k/v as a prepared set, and gate, up and SwiGLU
+    as one launch (Int4MatVecPreparedSwiGLU).  Each product against the
+    oracle on the device's own inputs, SwiGLU's output against the oracle's
+    SwiGLU of the oracle's gate and up products (the f32 tolerance carried
+    through), and the step's output against the whole step in the oracle."""
+    x, g1, g2, planes = _inputs(1)
+    shapes = workloads.LAYER_SHAPES
+    ws = {n: dev.upload_int4(*planes[n], K * N) for n, (K, N) in shapes.items()}
+    pws = {n: dev.prepare_int4(ws[n], K, N) for n, (K, N) in shapes.items()}
+    out = {n: dev.alloc((N,), F32) for n, (K, N) in shapes.items()}
+    xin, gb1, gb2 = dev.upload(x[0]), dev.upload(g1), dev.upload(g2)
+    h1, h2, act = dev.alloc((4096,), F32), dev.alloc((4096,), F32), dev.alloc((14336,), F32)
+    dev.RMSNorm(xin, gb1, EPS, h1)
+    dev.Int4MatVecPreparedSet(h1, [pws[n] for n in ("q", "k", "v")],
+                              [out[n] for n in ("q", "k", "v")])
+    dev.Int4MatVecPrepared(out["q"], pws["o"], out["o"])
+    dev.RMSNorm(out["o"], gb2, EPS, h2)
+    dev.Int4MatVecPreparedSwiGLU(h2, pws["gate"], pws["up"], act)
+    dev.Int4MatVecPrepared(act, pws["down"], out["down"])
+    dev.sync()
+    d = {n: out[n].numpy()[None] for n in ("q", "k", "v", "o", "down")}
+    dh1, dh2, dact = h1.numpy()[None], h2.numpy()[None], act.numpy()[None]
+    for n in ("q", "k", "v"):
+        assert rel_l2(d[n], _product(dh1, planes, n)) <= F32_TOL, n
+    assert rel_l2(d["o"], _product(d["q"], planes, "o")) <= F32_TOL
+    want_act = oracle.swiglu(_product(dh2, planes, "gate").ravel(),
+                             _product(dh2, planes, "up").ravel())[None]
+    assert rel_l2(dact, want_act) <= F32_TOL
+    assert rel_l2(d["down"], _product(dact, planes, "down")) <= F32_TOL
+    o_h1 = oracle.rmsnorm(x, g1, EPS)
+    o_o = _product(_product(o_h1, planes, "q"), planes, "o")
+    o_h2 = oracle.rmsnorm(o_o, g2, EPS)
+    o_act = oracle.swiglu(_product(o_h2, planes, "gate").ravel(),
+                          _product(o_h2, planes, "up").ravel())[None]
+    o_down = _product(o_act, planes, "down")
+    assert rel_l2(d["down"], o_down) <= F32_TOL, rel_l2(d["down"], o_down)
+    for b in list(out.values()) + [xin, gb1, gb2, h1, h2, act]:
+        b.free()
+    for w in list(pws.values()) + list(ws.values()):
+        w.free()
