@@ -494,8 +494,9 @@ int accel_int4_select(int dev, const char* op, int32_t dtype, int64_t M, int64_t
                       accel_selection_t* sel);
 
 /* The selection the last int4 product on device dev made (Int4MatVec,
- * Int4MatMul, Int4Linear, the sets and Int4MatVecNoAlloc), as launched;
- * ACCEL_E_INVALID before the first. */
+ * Int4MatMul, Int4Linear, the sets, the prepared products, the grouped
+ * products and Int4MatVecNoAlloc), as launched; ACCEL_E_INVALID before the
+ * first. */
 int accel_hip_last_selection(int dev, accel_selection_t* sel);
 
 /* The SegmentOffsets node (tensor/segment.go:31-50;
