@@ -174,6 +174,8 @@ SIGNATURES = {
                                   _P(_vp)], _i),
     "accel_int4_prepare_grouped": ([_i, _vp, _P(Int4Desc), ctypes.c_int64, ctypes.c_int64,
                                     ctypes.c_int64, _P(_vp)], _i),
+    "accel_int4_prepare_grouped_panels": ([_i, _vp, _P(Int4Desc), ctypes.c_int64,
+                                           ctypes.c_int64, ctypes.c_int64, _P(_vp)], _i),
     "accel_int4_prepared_free": ([_i, _vp], _i),
     "accel_int4_prepared_bytes": ([_vp, _P(ctypes.c_uint64)], _i),
     "accel_int4_matvec_prepared": ([_i, _vp, _P(Tensor), _vp, _P(Tensor)], _i),
@@ -607,14 +609,18 @@ class Device:
         return PreparedInt4(self, h.value, int(K), int(N))
 
     def prepare_int4_grouped(self, w: "Int4Weights", experts: int, K: int, N: int,
-                             stream=None) -> PreparedInt4:
+                             stream=None, panels: bool = False) -> PreparedInt4:
         """Binds `experts` stacked [K, N] int4 matrices once, on the device,
         waited for: the planes and each expert's side copy of its scales and
-        zeros for the matrix-core decode (accel_int4_prepare_grouped)."""
+        zeros for the matrix-core decode (accel_int4_prepare_grouped), or with
+        panels=True each expert's panel-layout copy for few routed rows
+        (accel_int4_prepare_grouped_panels)."""
         h = ctypes.c_void_p()
         tw = w.desc()
-        _check(_lib.accel_int4_prepare_grouped(self.index, stream, ctypes.byref(tw),
-                                               int(experts), int(K), int(N), ctypes.byref(h)))
+        fn = (_lib.accel_int4_prepare_grouped_panels if panels
+              else _lib.accel_int4_prepare_grouped)
+        _check(fn(self.index, stream, ctypes.byref(tw), int(experts), int(K), int(N),
+                  ctypes.byref(h)))
         return PreparedInt4(self, h.value, int(K), int(N))
 
     def Int4MatVecPrepared(self, a: Buffer, w: PreparedInt4, out: Buffer, stream=None) -> None:

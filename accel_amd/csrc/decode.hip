@@ -2173,8 +2173,27 @@ static int grouped_decode_tile(const Device* d, int T, int N) {
     return N % 256 == 0 ? 256 : 128;
 }
 
+// Experts prepared into the panel layout take f32 rows on the panel kernel
+// where the matrix-core blocks are not launched (fewer than two rows an
+// expert on average) and there are three rows or more; K even and the rows
+// 8-byte aligned.  Measured on config 4's experts (K = 4096, N = 14336,
+// top-2 of 8; panels / matrix-core blocks or VALU on the planes, us): 1
+// token (2 rows) 32.2 / 28.1, 2 tokens 43.7 / 50.5, 4 tokens 55.9 / 96.0,
+// 8 tokens 83.9 / 81.5 (side copies), 16 tokens 147.4 / 99.3.
+bool grouped_panel_route(const void* x, Int4Planes w, bool bf16, int E, int T, int K) {
+    return w.panels && !bf16 && T >= 3 && T <= kGroupedDecodeRows && (long long)T < 2LL * E &&
+           K % 2 == 0 && (reinterpret_cast<uintptr_t>(x) & 7) == 0;
+}
+
 size_t int4_grouped_decode_area(const Device* d, const void* x, Int4Planes w, int E, int T,
                                 int K, int N) {
+    if (grouped_panel_route(x, w, false, E, T, K)) {
+        // the VALU launch alone uses the area: the padding rows at one slice
+        const int tw = N % 512 == 0 ? 512 : grouped_decode_tile(d, T, N);
+        if (tw == 512) return GroupedDecodeShape<512>(d, T, K, N, true).area_bytes(T, N);
+        if (tw == 256) return GroupedDecodeShape<256>(d, T, K, N, true).area_bytes(T, N);
+        return GroupedDecodeShape<128>(d, T, K, N, true).area_bytes(T, N);
+    }
     const GroupedMfma g = grouped_mfma(d, x, w, E, T, K, N);
     const int tw = g.on && N % 512 == 0 ? 512 : grouped_decode_tile(d, T, N);
     size_t bytes;
@@ -2196,6 +2215,28 @@ hipError_t launch_grouped_decode_t(Device* d, hipStream_t st, const XT* x, Int4P
                                       int N, bool write_padding, int* status,
                                       uint32_t* tickets, float* area) {
     *status = ACCEL_OK;
+    if constexpr (sizeof(XT) == 4) {
+        if (grouped_panel_route(x, w, false, E, T, K)) {
+            // the padding rows (and every row should the offsets have
+            // wrapped) on the VALU kernel, the experts' rows on the panels;
+            // as beside the matrix-core blocks, the widest tile
+            const int tw = N % 512 == 0 ? 512 : grouped_decode_tile(d, T, N);
+            hipError_t e;
+            if (tw == 512)
+                e = launch_grouped_decode_tile<512, XT>(d, st, x, w, off, out, E, T, K, N,
+                                                        write_padding, status, tickets, area, true);
+            else if (tw == 256)
+                e = launch_grouped_decode_tile<256, XT>(d, st, x, w, off, out, E, T, K, N,
+                                                        write_padding, status, tickets, area, true);
+            else
+                e = launch_grouped_decode_tile<128, XT>(d, st, x, w, off, out, E, T, K, N,
+                                                        write_padding, status, tickets, area, true);
+            if (e != hipSuccess || *status != ACCEL_OK) return e;
+            return launch_int4_grouped_panel_rows(st, reinterpret_cast<const float*>(x), w.panels,
+                                                  w.panel_stride, off, static_cast<float*>(out),
+                                                  E, T, K, N);
+        }
+    }
     const GroupedMfma g = grouped_mfma(d, x, w, E, T, K, N);
     // with the rows on the matrix cores, the widest tile (fewest workgroups)
     const int tw = g.on && N % 512 == 0 ? 512 : grouped_decode_tile(d, T, N);

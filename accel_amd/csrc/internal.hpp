@@ -160,6 +160,10 @@ struct Int4Planes {
     // prepared grouped weights: each expert's side copy of its scales and
     // zeros for the matrix-core decode (int4_side_bytes(K, N) apart), or null
     const uint16_t* side = nullptr;
+    // or each expert's panel-layout copy (int4_panel_bytes(K, N) rounded up
+    // to 256 bytes apart) for the few-rows panel kernel, or null
+    const void* panels = nullptr;
+    size_t panel_stride = 0;
 };
 
 // What the last store of a product does: add bias[col] (f32, one value per
@@ -335,6 +339,15 @@ hipError_t launch_int4_panel_matvec(hipStream_t st, const float* a, const void* 
 // for two prepared [K, N] matrices, one launch.
 hipError_t launch_int4_panel_swiglu(hipStream_t st, const float* a, const void* gate,
                                     const void* up, float* out, int N, int K);
+// The ragged GEMV on experts prepared into the panel layout, stride bytes
+// apart: x f32 [T, K], K even, x 8-byte aligned, sorted offsets.
+hipError_t launch_int4_grouped_panel_rows(hipStream_t st, const float* x, const void* panels_base,
+                                          size_t stride, const uint32_t* off, float* out, int E,
+                                          int T, int K, int N);
+// Whether the grouped decode product takes the panel kernel for these rows
+// (w.panels set, f32 rows, 3 <= T < 2E and T <= 64, K even, x 8-byte
+// aligned).
+bool grouped_panel_route(const void* x, Int4Planes w, bool bf16, int E, int T, int K);
 
 // Decode-step neighbours: MatVecF32F16 (f32 a [K], f16 w [K,N] -> f32 [N]),
 // SwiGLU over n elements, RMSNorm over `rows` rows of `width`.

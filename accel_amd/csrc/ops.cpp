@@ -814,7 +814,8 @@ int run_grouped_f32(const char* op, int dev, void* stream, const accel_tensor_t*
 
 int run_grouped_int4(const char* op, int dev, void* stream, const accel_tensor_t* x,
                      const accel_int4_t* w, int64_t experts, const accel_tensor_t* counts,
-                     accel_tensor_t* out, bool matvec, const uint16_t* side = nullptr) {
+                     accel_tensor_t* out, bool matvec, const uint16_t* side = nullptr,
+                     const void* panels = nullptr, size_t panel_stride = 0) {
     clear_error();
     char buf[512];
     std::string why = check_int4(w, "the expert weights");
@@ -888,6 +889,8 @@ int run_grouped_int4(const char* op, int dev, void* stream, const accel_tensor_t
     // prepared experts: the matrix-core decode reads their side copies
     Int4Planes p = planes(w);
     p.side = side;
+    p.panels = panels;
+    p.panel_stride = panel_stride;
     // the tiles walk segments: the matvec form's rows follow e(t), whose
     // bounds are the offsets sorted (segment_bounds), in the area
     const size_t bounds_bytes = ((size_t)(experts + 1) * sizeof(uint32_t) + 255) / 256 * 256;
@@ -904,7 +907,15 @@ int run_grouped_int4(const char* op, int dev, void* stream, const accel_tensor_t
     const uint32_t* seg = off;
     LaunchRecord rec(false);
     std::string reason, rejected;
-    if (decode && side) {
+    if (decode && grouped_panel_route(x->data, p, !f32, (int)experts, (int)T, (int)K)) {
+        reason = "few routed f32 rows of experts prepared into the panel layout: workgroup "
+                 "(expert, 16-column panel) runs the expert's rows over all of K in passes of "
+                 "up to four, no K split and no hand-off (the VALU decode kernel for the "
+                 "padding rows, on the planes)";
+        rejected = "the matrix-core blocks: their time is set by load latency, the K split "
+                   "and its hand-off at one to four rows an expert; the grouped tiles: a "
+                   "128- or 256-row block for a few rows would be mostly empty";
+    } else if (decode && side) {
         reason = "few routed rows of prepared experts: each expert's rows in blocks of up to "
                  "16 on the matrix-core decode kernel, each 32-row step's scales and zeros "
                  "one contiguous block of the expert's side copy (the VALU decode kernel for "
@@ -1252,11 +1263,17 @@ struct accel_int4_prepared {
     size_t side_off;   // tiles, grouped: the side copy's offset in data
     int64_t experts = 0;                   // grouped: the expert count
     size_t scales_off = 0, zeros_off = 0;  // grouped: the planes' offsets in data
+    size_t panel_stride = 0;               // grouped panels: bytes per expert's copy
 };
 static constexpr int kPanelLayout = 0;   // accel_int4_prepare: K-major panels
 static constexpr int kTilesLayout = 1;   // accel_int4_prepare_tiles: codes + side copy
 static constexpr int kGroupedLayout = 2;  // accel_int4_prepare_grouped: planes + side copies
+static constexpr int kGroupedPanelLayout = 3;  // accel_int4_prepare_grouped_panels: planes +
+                                               // each expert's panel copy
 static constexpr uint32_t kPreparedMagic = 0x34544e49u;   // "INT4"
+static bool is_grouped(const accel_int4_prepared_t* w) {
+    return w->layout == kGroupedLayout || w->layout == kGroupedPanelLayout;
+}
 
 ACCEL_API int accel_int4_prepare(int dev, void* stream, const accel_int4_t* w, int64_t K,
                                  int64_t N, accel_int4_prepared_t** out) {
@@ -1428,6 +1445,81 @@ ACCEL_API int accel_int4_prepare_grouped(int dev, void* stream, const accel_int4
     return ACCEL_OK;
 }
 
+// Grouped experts prepared for few routed rows: the three planes copied as
+// they are and, after them, each expert's copy in the panel layout
+// (int4_panel_prepare_*_kernel), 256-byte aligned.
+ACCEL_API int accel_int4_prepare_grouped_panels(int dev, void* stream, const accel_int4_t* w,
+                                                int64_t experts, int64_t K, int64_t N,
+                                                accel_int4_prepared_t** out) {
+    clear_error();
+    const char* op = "Int4PrepareGroupedPanels";
+    if (!out) return refuse(op, "no handle to return the prepared weight in");
+    *out = nullptr;
+    std::string why = check_int4(w, "the expert weights");
+    if (!why.empty()) return refuse(op, why);
+    char buf[320];
+    if (experts < 1 || K < 1 || N < 1 || w->weights % experts != 0 ||
+        w->weights / experts != K * N) {
+        snprintf(buf, sizeof buf,
+                 "%lld experts of [%lld, %lld] are %lld weights and the matrix holds %lld",
+                 (long long)experts, (long long)K, (long long)N, (long long)(experts * K * N),
+                 (long long)w->weights);
+        return refuse(op, buf);
+    }
+    if (!int4_panel_supported(K, N) || experts > INT32_MAX ||
+        (uint64_t)w->weights >= (1ull << 40) || (reinterpret_cast<uintptr_t>(w->codes) & 7) != 0) {
+        snprintf(buf, sizeof buf,
+                 "%lld experts of [%lld, %lld]: the panel layout takes N a multiple of 128, K "
+                 "and N below 2^30, under 2^40 weights and 8-byte aligned codes",
+                 (long long)experts, (long long)K, (long long)N);
+        return refuse(op, buf);
+    }
+    Device* d = device(dev);
+    if (!d) return ACCEL_E_NO_DEVICE;
+    int status = begin_submission(d);
+    if (status != ACCEL_OK) return status;
+    auto up = [](size_t b) { return (b + 255) / 256 * 256; };
+    const size_t per = (size_t)K * N;
+    const size_t code_bytes = (size_t)w->weights / 2;
+    const size_t plane_bytes = (size_t)w->weights / 128 * 2;
+    const size_t stride = up(int4_panel_bytes((int)K, (int)N, nullptr));
+    const size_t scales_off = up(code_bytes);
+    const size_t zeros_off = scales_off + up(plane_bytes);
+    const size_t panels_off = zeros_off + up(plane_bytes);
+    const size_t bytes = panels_off + stride * (size_t)experts;
+    void* data = nullptr;
+    hipError_t e = hipMalloc(&data, bytes);
+    if (e != hipSuccess) return classify(d, e, "prepared weight allocation");
+    hipStream_t st = (hipStream_t)stream;
+    char* base = static_cast<char*>(data);
+    e = hipMemcpyAsync(base, w->codes, code_bytes, hipMemcpyDeviceToDevice, st);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(base + scales_off, w->scales, plane_bytes, hipMemcpyDeviceToDevice,
+                           st);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(base + zeros_off, w->zeros, plane_bytes, hipMemcpyDeviceToDevice,
+                           st);
+    for (int64_t i = 0; i < experts && e == hipSuccess; i++) {
+        const Int4Planes pi{w->codes + i * (per >> 3), w->scales + i * (per >> 7),
+                            w->zeros + i * (per >> 7)};
+        e = launch_int4_panel_prepare(st, pi, base + panels_off + stride * (size_t)i, (int)K,
+                                      (int)N);
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess) {
+        (void)hipFree(data);
+        return classify(d, e, "prepared weight copy");
+    }
+    auto* p = new accel_int4_prepared{kPreparedMagic, dev, K, N, data, bytes,
+                                      kGroupedPanelLayout, panels_off};
+    p->experts = experts;
+    p->scales_off = scales_off;
+    p->zeros_off = zeros_off;
+    p->panel_stride = stride;
+    *out = p;
+    return ACCEL_OK;
+}
+
 ACCEL_API int accel_int4_prepared_free(int dev, accel_int4_prepared_t* p) {
     clear_error();
     if (!p) return ACCEL_OK;
@@ -1460,9 +1552,9 @@ int run_grouped_prepared(const char* op, int dev, void* stream, const accel_tens
                          accel_tensor_t* out, bool matvec) {
     clear_error();
     if (!w || w->magic != kPreparedMagic) return refuse(op, "the prepared weight is missing");
-    if (w->layout != kGroupedLayout)
+    if (!is_grouped(w))
         return refuse(op, "the weight was prepared as one matrix; grouped products take "
-                          "experts prepared with accel_int4_prepare_grouped");
+                          "experts prepared with accel_int4_prepare_grouped[_panels]");
     if (w->dev != dev) {
         char b[128];
         snprintf(b, sizeof b, "the weight was prepared on device %d", w->dev);
@@ -1473,6 +1565,9 @@ int run_grouped_prepared(const char* op, int dev, void* stream, const accel_tens
     accel_int4_t q{reinterpret_cast<const uint32_t*>(base), n / 8,
                    reinterpret_cast<const uint16_t*>(base + w->scales_off), n / 128,
                    reinterpret_cast<const uint16_t*>(base + w->zeros_off), n / 128, n};
+    if (w->layout == kGroupedPanelLayout)
+        return run_grouped_int4(op, dev, stream, x, &q, w->experts, counts, out, matvec, nullptr,
+                                base + w->side_off, w->panel_stride);
     return run_grouped_int4(op, dev, stream, x, &q, w->experts, counts, out, matvec,
                             reinterpret_cast<const uint16_t*>(base + w->side_off));
 }
@@ -1546,7 +1641,7 @@ ACCEL_API int accel_int4_matvec_prepared(int dev, void* stream, const accel_tens
     clear_error();
     const char* op = "Int4MatVecPrepared";
     if (!w || w->magic != kPreparedMagic) return refuse(op, "the prepared weight is missing");
-    if (w->layout == kGroupedLayout)
+    if (is_grouped(w))
         return refuse(op, "the weight was prepared as grouped experts (accel_int4_prepare_grouped); "
                           "its products are Int4GroupedMatVecPrepared and "
                           "Int4GroupedMatMulPrepared");
@@ -1631,7 +1726,7 @@ ACCEL_API int accel_int4_matvec_prepared_set(int dev, void* stream, const accel_
             snprintf(buf, sizeof buf, "weight %d was prepared on device %d", i, w[i]->dev);
             return refuse(op, buf);
         }
-        if (w[i]->layout == kGroupedLayout)
+        if (is_grouped(w[i]))
             return refuse(op, "the weight was prepared as grouped experts (accel_int4_prepare_grouped); "
                               "its products are Int4GroupedMatVecPrepared and "
                               "Int4GroupedMatMulPrepared");
@@ -1771,7 +1866,7 @@ int run_prepared_rows(const char* op, int dev, void* stream, const accel_tensor_
             snprintf(buf, sizeof buf, "weight %d was prepared on device %d", i, w[i]->dev);
             return refuse(op, buf);
         }
-        if (w[i]->layout == kGroupedLayout)
+        if (is_grouped(w[i]))
             return refuse(op, "the weight was prepared as grouped experts (accel_int4_prepare_grouped); "
                               "its products are Int4GroupedMatVecPrepared and "
                               "Int4GroupedMatMulPrepared");

@@ -357,19 +357,18 @@ __device__ __forceinline__ void rows_compute(float (&acc)[MR][kPanelCols], float
     }
 }
 
-// out_i[m, 16 q .. 16 q + 15] = a[m, :] . panel q of matrix i, m < M <= MR,
-// for the global panel p of this workgroup.  K even, rows 8-byte aligned.
-// FULL: K a multiple of the chunk (512 PPL row pairs).
-template <int MR, int PPL, bool FULL, bool SET>
-__global__ __launch_bounds__(kPanelThreads) void int4_panel_rows_kernel(
-    const float* __restrict__ a, PanelSet set, int panels, int M, int K, Epilogue ep) {
-    const int p = panel_of(blockIdx.x, panels);
-    const PanelPick pk =
-        SET ? pick_panel(set, p) : PanelPick{set.codes[0], set.sz[0], set.out[0], 0};
-    const int q = p - pk.first;
+// out[m, 16 q + c] (row stride N) = a[m, :] . panel (qp, szp), m < M <= MR,
+// c < 16, through ep: the product of one panel and M rows, every lane
+// holding the panel's 16 columns for each row, then the one-row kernel's
+// reduction per row (lane swaps, then the eight waves through LDS).  Ends at
+// a barrier, so a caller may run it again at once.  K even, rows 8-byte
+// aligned; FULL: K a multiple of the chunk (512 PPL row pairs).
+template <int MR, int PPL, bool FULL>
+__device__ __forceinline__ void panel_rows_tile(const float* __restrict__ a,
+                                                const u32x4* __restrict__ qp,
+                                                const u32x2* __restrict__ szp, void* out, int M,
+                                                int K, int N, int q, const Epilogue& ep) {
     const int pairs = K >> 1;
-    const u32x4* qp = pk.codes + (size_t)q * pairs;
-    const u32x2* szp = pk.sz + (size_t)(q >> 3) * pairs;
     const int tid = threadIdx.x;
     float acc[MR][kPanelCols];
     float bsum[MR];
@@ -388,8 +387,6 @@ __global__ __launch_bounds__(kPanelThreads) void int4_panel_rows_kernel(
         rows_compute<MR, PPL, FULL>(acc, bsum, c, pair0, K);
     }
 
-    // per row, the one-row kernel's reduction: lane swaps, then the eight
-    // waves through LDS
     __shared__ float red[kPanelThreads / 64][MR][kPanelCols];
     const int l = tid & 63;
 #pragma unroll
@@ -409,18 +406,80 @@ __global__ __launch_bounds__(kPanelThreads) void int4_panel_rows_kernel(
             float sum = 0.0f;
 #pragma unroll
             for (int w = 0; w < kPanelThreads / 64; w++) sum += red[w][m][c];
-            // this matrix's width from its panels: [first, next first) of the set
-            int n = panels;
-            if (SET) {
-#pragma unroll
-                for (int j = 1; j <= kMaxPanelSet; j++)
-                    if (j <= set.count && set.panel0[j] > pk.first && set.panel0[j] < n)
-                        n = set.panel0[j];
-            }
-            const int N = (n - pk.first) * kPanelCols;
             const int col = q * kPanelCols + c;
-            store_out(pk.out, (size_t)m * N + col, col, sum, ep);
+            store_out(out, (size_t)m * N + col, col, sum, ep);
         }
+    }
+    __syncthreads();
+}
+
+// out_i[m, 16 q .. 16 q + 15] = a[m, :] . panel q of matrix i, m < M <= MR,
+// for the global panel p of this workgroup.  K even, rows 8-byte aligned.
+// FULL: K a multiple of the chunk (512 PPL row pairs).
+template <int MR, int PPL, bool FULL, bool SET>
+__global__ __launch_bounds__(kPanelThreads) void int4_panel_rows_kernel(
+    const float* __restrict__ a, PanelSet set, int panels, int M, int K, Epilogue ep) {
+    const int p = panel_of(blockIdx.x, panels);
+    const PanelPick pk =
+        SET ? pick_panel(set, p) : PanelPick{set.codes[0], set.sz[0], set.out[0], 0};
+    const int q = p - pk.first;
+    const int pairs = K >> 1;
+    // this matrix's width from its panels: [first, next first) of the set
+    int n = panels;
+    if (SET) {
+#pragma unroll
+        for (int j = 1; j <= kMaxPanelSet; j++)
+            if (j <= set.count && set.panel0[j] > pk.first && set.panel0[j] < n)
+                n = set.panel0[j];
+    }
+    panel_rows_tile<MR, PPL, FULL>(a, pk.codes + (size_t)q * pairs,
+                                   pk.sz + (size_t)(q >> 3) * pairs, pk.out, M, K,
+                                   (n - pk.first) * kPanelCols, q, ep);
+}
+
+// The ragged GEMV (decode MoE) on experts prepared into the panel layout,
+// one expert's copy `stride` bytes after the last (codes, then the sz words
+// at sz_off): workgroup (expert e, panel p) runs the rows of e,
+// [off[e], min(off[e+1], T)), against its panel p in passes of up to four
+// rows (panel_rows_tile, each pass one, two or four rows wide), K whole and
+// no hand-off.  Sorted offsets only: when they have wrapped, every
+// workgroup returns and the VALU decode launch takes every row; it also
+// writes the rows past the last segment.
+template <int PPL, bool FULL>
+__global__ __launch_bounds__(kPanelThreads) void int4_grouped_panel_rows_kernel(
+    const float* __restrict__ x, const char* __restrict__ panels_base, size_t stride,
+    size_t sz_off, const uint32_t* __restrict__ off, float* __restrict__ out, int E, int T,
+    int K, int N) {
+    const int panels = N / kPanelCols;
+    const int e = blockIdx.x / panels;
+    const int q = panel_of(blockIdx.x % panels, panels);
+    __shared__ int s_first, s_count;
+    if (threadIdx.x == 0) {
+        bool sorted = true;
+        for (int r = 0; r < E; r++) sorted = sorted && off[r] <= off[r + 1];
+        const uint32_t first = min(off[e], (uint32_t)T);
+        const uint32_t last = min(off[e + 1], (uint32_t)T);
+        s_first = (int)first;
+        s_count = sorted && last > first ? (int)(last - first) : 0;
+    }
+    __syncthreads();
+    const int first = s_first, count = s_count;
+    if (count == 0) return;
+    const int pairs = K >> 1;
+    const char* base = panels_base + (size_t)e * stride;
+    const u32x4* qp = reinterpret_cast<const u32x4*>(base) + (size_t)q * pairs;
+    const u32x2* szp = reinterpret_cast<const u32x2*>(base + sz_off) + (size_t)(q >> 3) * pairs;
+    const Epilogue ep{};
+    for (int r0 = 0; r0 < count; r0 += 4) {
+        const int rows = min(4, count - r0);
+        const float* a = x + (size_t)(first + r0) * K;
+        float* o = out + (size_t)(first + r0) * N;
+        if (rows == 1)
+            panel_rows_tile<1, PPL, FULL>(a, qp, szp, o, 1, K, N, q, ep);
+        else if (rows == 2)
+            panel_rows_tile<2, PPL, FULL>(a, qp, szp, o, 2, K, N, q, ep);
+        else
+            panel_rows_tile<4, PPL, FULL>(a, qp, szp, o, rows, K, N, q, ep);
     }
 }
 
@@ -578,6 +637,30 @@ hipError_t launch_int4_panel_swiglu(hipStream_t st, const float* a, const void* 
     else SWIGLU_PIPE(false);
 #undef SWIGLU_PIPE
 #undef SWIGLU_LAUNCH
+    return launch_status();
+}
+
+// The ragged GEMV on panel-prepared experts (int4_grouped_panel_rows_kernel):
+// x f32 [T, K] (K even, 8-byte aligned), E experts of [K, N] `stride` bytes
+// apart from panels_base, sorted offsets off[E + 1]; out f32 [T, N] for the
+// experts' rows (the rest is the VALU launch's).
+hipError_t launch_int4_grouped_panel_rows(hipStream_t st, const float* x, const void* panels_base,
+                                          size_t stride, const uint32_t* off, float* out, int E,
+                                          int T, int K, int N) {
+    constexpr int PPL = 2;
+    size_t sz_off = 0;
+    int4_panel_bytes(K, N, &sz_off);
+    const bool full = K % (2 * kPanelThreads * PPL) == 0;
+    const long long wgs = (long long)E * (N / kPanelCols);
+    if (wgs > INT32_MAX) return hipErrorInvalidConfiguration;
+    const char* base = static_cast<const char*>(panels_base);
+#define GPR_LAUNCH(F)                                                                        \
+    ACCEL_LAUNCH(tname("int4_grouped_panel_rows_kernel", PPL, F) + grid_note(wgs, 1),         \
+                 (int4_grouped_panel_rows_kernel<PPL, F>), dim3((unsigned)wgs),              \
+                 dim3(kPanelThreads), 0, st, x, base, stride, sz_off, off, out, E, T, K, N)
+    if (full) GPR_LAUNCH(true);
+    else GPR_LAUNCH(false);
+#undef GPR_LAUNCH
     return launch_status();
 }
 

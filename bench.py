@@ -79,6 +79,9 @@ GROUPED_DECODE_LAUNCHES = (f"{_GD} (16 rows)", f"{_GDS} (16 rows)")
 # the same products on the reference planes
 GROUPED_F32_PLANES_LAUNCHES = (f"{_GD} (1024 rows)", f"{_GDM} (1024 rows)")
 GROUPED_DECODE_PLANES_LAUNCHES = (f"{_GD} (16 rows)", f"{_GDM} (16 rows)")
+# the decode MoE's rows on experts bound into the panel layout
+GROUPED_DECODE_PANEL_LAUNCHES = (f"{_GD} (8 rows)",
+                                 "int4_grouped_panel_rows_kernel<2, true> (8 rows)")
 # config 5's five launches a step, by variant
 _PS = "int4_panel_matvec_kernel<4, false, true, true, true>"
 _MF1 = "int4_decode_mfma_kernel<1, 8, float>"
@@ -389,28 +392,28 @@ def bench_gemm(dev, stream, name, steps=40, warmup=4, tiles=False):
                 bind_ms=bind_ms)
 
 
-def _grouped_timings(dev, stream, steps, call, ws, pws):
-    """Median time of a grouped call over the rotating copies: on the
-    prepared experts (pws) and on the planes (ws), or on the planes alone."""
+def _grouped_timings(dev, stream, steps, call, forms):
+    """Median time of a grouped call over the rotating copies of each form
+    of the experts (forms: key -> copies; call(copy, key))."""
     out = {}
-    for prep in ((True, False) if pws else (False,)):
-        copies = pws if prep else ws
+    for key, copies in forms.items():
         for i in range(len(copies)):
-            call(copies[i], prep)
+            call(copies[i], key)
         dev.sync(stream)
-        t = Timed(dev, stream, lambda i: call(copies[i % len(copies)], prep), steps)
-        out[prep] = median_replay(t) / steps
+        t = Timed(dev, stream, lambda i: call(copies[i % len(copies)], key), steps)
+        out[key] = median_replay(t) / steps
         t.close()
     return out
 
 
-def _prepare_grouped(dev, ws, m):
-    """Each copy of the experts bound once (accel_int4_prepare_grouped);
-    returns the copies and the host time of one bind in ms."""
+def _prepare_grouped(dev, ws, m, panels=False):
+    """Each copy of the experts bound once (accel_int4_prepare_grouped, or
+    with panels accel_int4_prepare_grouped_panels); returns the copies and
+    the host time of one bind in ms."""
     pws, bind_ms = [], None
     for w in ws:
         t0 = time.perf_counter()
-        pws.append(dev.prepare_int4_grouped(w, m.E, m.K, m.N))
+        pws.append(dev.prepare_int4_grouped(w, m.E, m.K, m.N, panels=panels))
         bind_ms = bind_ms or (time.perf_counter() - t0) * 1e3
     return pws, bind_ms
 
@@ -445,7 +448,8 @@ def bench_moe(dev, stream, steps=20, bf16=True, prepared=False):
         else:
             dev.Int4GroupedMatMul(xb, w, m.E, cb, ob, stream=stream)
 
-    times = _grouped_timings(dev, stream, steps, call, ws, pws)
+    times = _grouped_timings(dev, stream, steps, call,
+                             {True: pws, False: ws} if both else {False: ws})
     ms = times[prepared]
     for w in pws or ():
         w.free()
@@ -488,14 +492,17 @@ def bench_moe(dev, stream, steps=20, bf16=True, prepared=False):
                           "hbm_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)})
 
 
-def bench_moe_decode(dev, stream, tokens=8, steps=40, prepared=True):
+def bench_moe_decode(dev, stream, tokens=8, steps=40, form="side"):
     """Decode MoE: `tokens` tokens routed top-2 over config 4's eight experts
     (K=4096, N=14336) as f32 rows, Int4GroupedMatVec -- decode products of
     each expert's routed rows against its matrix (blocks of up to 16 rows on
     the matrix cores).  Three copies of the experts
     (750 MB) rotate and the cache is flushed before the timed replay.
-    prepared: the experts bound once (outside the timed region),
-    Int4GroupedMatVecPrepared timed and the call on the planes beside it."""
+    The experts are bound once (outside the timed region) in both prepared
+    forms, and the call is timed on each and on the planes: `form` ("panels":
+    accel_int4_prepare_grouped_panels, the few-rows panel kernel; "side":
+    accel_int4_prepare_grouped, the matrix-core blocks on side copies;
+    "planes") is the line's figure, the others are reported beside it."""
     from accel_amd import F32, U32, workloads
     progress(f"decode MoE: {tokens} tokens, top-2 of 8 experts")
     m = workloads.moe_fast(tokens=tokens)
@@ -505,18 +512,22 @@ def bench_moe_decode(dev, stream, tokens=8, steps=40, prepared=True):
     xb = dev.upload(m.x)
     cb = dev.upload(m.counts, U32)
     ob = dev.alloc((R, m.N), F32)
-    pws, bind_ms = _prepare_grouped(dev, ws, m) if prepared else (None, None)
+    forms = {"planes": ws}
+    bind = {}
+    for f in ("panels", "side"):
+        forms[f], bind[f] = _prepare_grouped(dev, ws, m, panels=f == "panels")
 
-    def call(w, prep):
-        if prep:
-            dev.Int4GroupedMatVecPrepared(xb, w, cb, ob, stream=stream)
-        else:
+    def call(w, f):
+        if f == "planes":
             dev.Int4GroupedMatVec(xb, w, m.E, cb, ob, stream=stream)
+        else:
+            dev.Int4GroupedMatVecPrepared(xb, w, cb, ob, stream=stream)
 
-    times = _grouped_timings(dev, stream, steps, call, ws, pws)
-    ms = times[prepared]
-    for w in pws or ():
-        w.free()
+    times = _grouped_timings(dev, stream, steps, call, forms)
+    ms = times[form]
+    for f in ("panels", "side"):
+        for w in forms[f]:
+            w.free()
     active = int((m.counts > 0).sum())
     per_expert = (m.packed.nbytes + m.scales.nbytes + m.zeros.nbytes) // m.E
     nbytes = active * per_expert + R * m.K * 4 + R * m.N * 4
@@ -525,17 +536,25 @@ def bench_moe_decode(dev, stream, tokens=8, steps=40, prepared=True):
     for w in ws:
         w.free()
     gbs = nbytes / (ms * 1e-3) / 1e9
-    launches = GROUPED_DECODE_LAUNCHES if prepared else GROUPED_DECODE_PLANES_LAUNCHES
-    extra = {}
-    if prepared:
-        extra = dict(us_reference_planes=round(times[False] * 1e3, 2), bind_ms=round(bind_ms, 1))
-    op = "Int4GroupedMatVecPrepared" if prepared else "Int4GroupedMatVec"
+    launches = {"panels": GROUPED_DECODE_PANEL_LAUNCHES, "side": GROUPED_DECODE_LAUNCHES,
+                "planes": GROUPED_DECODE_PLANES_LAUNCHES}[form]
+    extra = {f"us_{k}": round(v * 1e3, 2) for k, v in
+             (("panels", times["panels"]), ("side_copies", times["side"]),
+              ("reference_planes", times["planes"]))}
+    extra.update({f"bind_ms_{k}": round(v, 1) for k, v in bind.items()})
+    op = "Int4GroupedMatVec" if form == "planes" else "Int4GroupedMatVecPrepared"
     return dict(workload=f"{op}, decode MoE: {tokens} tokens routed top-2 over 8 "
                          f"experts ({R} f32 rows, seed 3's routing), K={m.K}, N={m.N}, f32 out; "
                          f"the {active} active experts' weights read once; experts rotated over "
                          f"{copies} copies"
-                         + ("; experts bound once (accel_int4_prepare_grouped), the same call "
-                            "on the planes in us_reference_planes" if prepared else ""),
+                         + {"panels": "; experts bound once into the panel layout "
+                                      "(accel_int4_prepare_grouped_panels): the few-rows panel "
+                                      "kernel",
+                            "side": "; experts bound once with side copies of their scales and "
+                                    "zeros (accel_int4_prepare_grouped): the matrix-core blocks",
+                            "planes": ""}[form]
+                         + "; the same call on each form of the experts in us_panels, "
+                           "us_side_copies and us_reference_planes",
                 us=round(ms * 1e3, 2), rows=R, active_experts=active, **extra,
                 counts=[int(c) for c in m.counts],
                 roofline={"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
@@ -1334,6 +1353,9 @@ def main():
             extra["moe_grouped_f32"] = bench_moe(dev, stream, steps=10, bf16=False)
         if want("moe_decode_f32"):
             extra["moe_decode_f32"] = bench_moe_decode(dev, stream)
+        if want("moe_decode_f32_4tok"):
+            extra["moe_decode_f32_4tok"] = bench_moe_decode(dev, stream, tokens=4,
+                                                            form="panels")
         for b in (1, 8):
             if want(f"layer_chain_b{b}"):
                 progress(f"config 5: layer chain at batch {b}")

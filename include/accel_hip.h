@@ -544,11 +544,25 @@ int accel_int4_grouped_matmul(int dev, void* stream, const accel_tensor_t* x,
  * accel_int4_prepared_free; the single-matrix prepared operators refuse it. */
 int accel_int4_prepare_grouped(int dev, void* stream, const accel_int4_t* w, int64_t experts,
                                int64_t K, int64_t N, accel_int4_prepared_t** out);
+/* The same experts bound for the decode MoE's few routed rows: the three
+ * planes copied as they are and, after them, each expert's copy in
+ * accel_int4_prepare's panel layout (2x the planes' bytes).  The grouped
+ * products then take f32 rows, three or more and fewer than two an expert
+ * on average (K even, rows 8-byte aligned), on the few-rows panel kernel: one
+ * workgroup an (expert, 16-column panel), K whole, no hand-off; within the
+ * f32 tolerance of the planes' products (the sums run in another order),
+ * not bit for bit.  Other rows take the planes' routes.  N % 128 == 0,
+ * 8-byte aligned codes.  No reference counterpart as one call (as
+ * accel_int4_prepare_grouped). */
+int accel_int4_prepare_grouped_panels(int dev, void* stream, const accel_int4_t* w,
+                                      int64_t experts, int64_t K, int64_t N,
+                                      accel_int4_prepared_t** out);
 
 /* accel_int4_grouped_matvec / accel_int4_grouped_matmul over experts
- * prepared by accel_int4_prepare_grouped: the same operands otherwise, the
- * same checks and routes, and the same results bit for bit; routed rows on
- * the matrix-core decode read the side copies. */
+ * prepared by accel_int4_prepare_grouped (the same results bit for bit;
+ * routed rows on the matrix-core decode read the side copies) or by
+ * accel_int4_prepare_grouped_panels (few f32 rows on the panel kernel, as
+ * above): the same operands otherwise, and the same checks. */
 int accel_int4_grouped_matvec_prepared(int dev, void* stream, const accel_tensor_t* x,
                                        const accel_int4_prepared_t* w,
                                        const accel_tensor_t* counts, accel_tensor_t* out);

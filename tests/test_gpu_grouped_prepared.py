@@ -183,3 +183,126 @@ def test_prepared_forms_are_not_mixed(dev):
     pw.free()
     one.free()
     w.free()
+
+
+# ---- experts prepared into the panel layout -----------------------------------
+
+PANEL_CASES = [
+    # f32 rows, 3 <= T < 2E: the panel kernel
+    (8, 4096, 1024, [2, 0, 3, 1, 0, 4, 2, 1], 1),
+    (4, 512, 640, [3, 1, 0, 2], 1),
+    (3, 256, 512, [5, 0, 0], 0),          # five rows: passes of four and one
+    (2, 1024, 8192, [2, 1], 0),
+    (4, 2048, 384, [1, 1, 1, 1], 0),      # 24 panels an expert
+    (4, 4096, 256, [7, 0, 0, 0], 0),      # seven rows: four and three
+]
+
+def _run(dev, form, x, w, E, counts, T, N):
+    xb = dev.upload(x)
+    cb = dev.upload(np.asarray(counts, np.uint32), U32)
+    ob = dev.alloc((T, N), F32)
+    ob.write(np.full((T, N), 7.0, np.float32))
+    if isinstance(w, A.PreparedInt4):
+        getattr(dev, form + "Prepared")(xb, w, cb, ob)
+    else:
+        getattr(dev, form)(xb, w, E, cb, ob)
+    got, sel = ob.numpy(), dev.last_selection()
+    for b in (xb, cb, ob):
+        b.free()
+    return got, sel
+
+
+def _want(form, x, p, s, z, off, E, T, K, N):
+    init = np.full(T * N, 7.0, np.float32)
+    if form == "Int4GroupedMatVec":
+        return oracle.int4_grouped_matvec(x, p, s, z, off, E, T, K, N, threads=8, out=init)
+    return oracle.int4_grouped_matmul(x, p, s, z, off, E, T, K, N, threads=8, out=init)
+
+
+@pytest.mark.parametrize("form", ["Int4GroupedMatVec", "Int4GroupedMatMul"])
+@pytest.mark.parametrize("E,K,N,counts,pad", PANEL_CASES)
+def test_panel_experts_match_the_oracle(dev, form, E, K, N, counts, pad):
+    x, p, s, z, off, T = _case(E, K, N, counts, pad, seed=7 * E + K, bf16=False)
+    w = dev.upload_int4(p, s, z, E * K * N)
+    pw = dev.prepare_int4_grouped(w, E, K, N, panels=True)
+    assert pw.nbytes >= 2 * (E * K * N // 2)
+    got, sel = _run(dev, form, x, pw, E, counts, T, N)
+    assert sel.op == form + "Prepared"
+    assert any(k.startswith("int4_grouped_panel_rows_kernel<") for k in sel.launches), sel
+    assert not any("mfma" in k for k in sel.launches), sel
+    want = _want(form, x, p, s, z, off, E, T, K, N)
+    assert rel_l2(got, want) <= 1e-5, rel_l2(got, want)
+    covered = int(off[E])
+    assert np.all(got[covered:] == (0 if form == "Int4GroupedMatVec" else 7.0))
+    # every covered row on its own, so no row is dropped, doubled or misplaced
+    for t in range(covered):
+        assert rel_l2(got[t], want[t]) <= 1e-5, t
+    pw.free()
+    w.free()
+
+
+@pytest.mark.parametrize("E,K,N,counts,pad", [
+    (2, 2048, 384, [16, 35], 2),            # two rows an expert or more: matrix cores
+    (4, 512, 1024, [300, 0, 41, 260], 2),   # past 64 rows
+    (3, 1001, 256, [2, 1, 1], 0),           # K odd: the VALU decode kernel
+    (4, 512, 256, [1, 1, 0, 0], 0),         # two rows: the VALU decode kernel
+])
+def test_panel_experts_other_rows_take_the_planes_routes(dev, E, K, N, counts, pad):
+    x, p, s, z, off, T = _case(E, K, N, counts, pad, seed=E + 3 * K, bf16=False)
+    w = dev.upload_int4(p, s, z, E * K * N)
+    pw = dev.prepare_int4_grouped(w, E, K, N, panels=True)
+    got, gsel = _run(dev, "Int4GroupedMatMul", x, pw, E, counts, T, N)
+    ref, rsel = _run(dev, "Int4GroupedMatMul", x, w, E, counts, T, N)
+    assert not any(k.startswith("int4_grouped_panel_rows_kernel") for k in gsel.launches)
+    assert gsel.launches == rsel.launches
+    assert np.array_equal(got, ref)
+    pw.free()
+    w.free()
+
+
+def test_panel_experts_wrapped_offsets(dev):
+    """off = [0, 2^32 - 1, 2, 4, 4]: not sorted, so the panel launch's
+    workgroups return and the VALU launch takes every row on the planes the
+    prepared copy keeps; e(t) = #{r : off[r+1] <= t} puts rows 0-1, 2-3 and
+    4-5 on experts 0, 1 and 3 (internal/kernels/grouped.go:66-77)."""
+    E, K, N, counts, pad = 4, 512, 256, [0xFFFFFFFF, 3, 2, 0], 2
+    x, p, s, z, off, T = _case(E, K, N, counts, pad, seed=11, bf16=False)
+    w = dev.upload_int4(p, s, z, E * K * N)
+    pw = dev.prepare_int4_grouped(w, E, K, N, panels=True)
+    got, sel = _run(dev, "Int4GroupedMatVec", x, pw, E, counts, T, N)
+    assert any(k.startswith("int4_grouped_panel_rows_kernel<") for k in sel.launches)
+    want = _want("Int4GroupedMatVec", x, p, s, z, off, E, T, K, N)
+    for t in range(T):
+        assert rel_l2(got[t], want[t]) <= 1e-5, t
+    pw.free()
+    w.free()
+
+
+def test_panel_experts_decode_moe_full_size(dev):
+    """The decode MoE at full size (4 tokens top-2 over config 4's experts,
+    8 f32 rows): every row against the oracle row for row, and the same
+    rows on the planes within the f32 tolerance."""
+    m = workloads.moe_fast(tokens=4)
+    R = int(m.counts.sum())
+    w = dev.upload_int4(m.packed, m.scales, m.zeros, m.E * m.K * m.N)
+    pw = dev.prepare_int4_grouped(w, m.E, m.K, m.N, panels=True)
+    x = np.ascontiguousarray(m.x, np.float32)
+    got, sel = _run(dev, "Int4GroupedMatVec", x, pw, m.E, m.counts, R, m.N)
+    assert any(k.startswith("int4_grouped_panel_rows_kernel<") for k in sel.launches)
+    off = oracle.segment_offsets(m.counts)
+    for e in range(m.E):
+        lo, hi = int(off[e]), int(off[e + 1])
+        if lo == hi:
+            continue
+        base = e * m.K * m.N
+        want = oracle.quant_matmul_int4(np.ascontiguousarray(x[lo:hi]),
+                                        m.packed[base // 8:(base + m.K * m.N) // 8],
+                                        m.scales[base // 128:(base + m.K * m.N) // 128],
+                                        m.zeros[base // 128:(base + m.K * m.N) // 128],
+                                        hi - lo, m.K, m.N, threads=16)
+        for r in range(hi - lo):
+            assert rel_l2(got[lo + r], want[r]) <= 1e-5, (e, r)
+    ref, _ = _run(dev, "Int4GroupedMatVec", x, w, m.E, m.counts, R, m.N)
+    assert rel_l2(got, ref) <= 1e-5
+    pw.free()
+    w.free()
