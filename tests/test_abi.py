@@ -471,3 +471,17 @@ def test_prepared_swiglu_refuses_a_missing_weight():
                                                           ctypes.byref(t))
     assert rc == accel_amd.E_INVALID
     assert "prepared gate weight is missing" in accel_amd.last_error()
+
+
+@pytest.mark.parametrize("E,K,N,why", [
+    (1, 2048, 64, "N a multiple of 128"),
+    (3, 256, 256, "3 experts of [256, 256] are 196608 weights and the matrix holds 131072"),
+])
+def test_prepare_grouped_panels_refuses_what_the_panels_cannot_hold(E, K, N, why):
+    h = ctypes.c_void_p()
+    d = _fake_int4(256, 512)
+    rc = accel_amd.lib().accel_int4_prepare_grouped_panels(0, None, ctypes.byref(d), E, K, N,
+                                                           ctypes.byref(h))
+    assert rc == accel_amd.E_INVALID
+    assert why in accel_amd.last_error()
+    assert h.value is None
