@@ -454,13 +454,18 @@ __global__ __launch_bounds__(kPanelThreads) void int4_grouped_panel_rows_kernel(
     const int e = blockIdx.x / panels;
     const int q = panel_of(blockIdx.x % panels, panels);
     __shared__ int s_first, s_count;
-    if (threadIdx.x == 0) {
-        bool sorted = true;
-        for (int r = 0; r < E; r++) sorted = sorted && off[r] <= off[r + 1];
-        const uint32_t first = min(off[e], (uint32_t)T);
-        const uint32_t last = min(off[e + 1], (uint32_t)T);
-        s_first = (int)first;
-        s_count = sorted && last > first ? (int)(last - first) : 0;
+    if (threadIdx.x < 64) {
+        // the offsets' order checked by the first wave, a pair a lane
+        const int lane = threadIdx.x;
+        bool ok = true;
+        for (int r = lane; r < E; r += 64) ok = ok && off[r] <= off[r + 1];
+        const bool sorted = __all(ok);
+        if (lane == 0) {
+            const uint32_t first = min(off[e], (uint32_t)T);
+            const uint32_t last = min(off[e + 1], (uint32_t)T);
+            s_first = (int)first;
+            s_count = sorted && last > first ? (int)(last - first) : 0;
+        }
     }
     __syncthreads();
     const int first = s_first, count = s_count;
