@@ -440,9 +440,10 @@ __global__ __launch_bounds__(kPanelThreads) void int4_panel_rows_kernel(
 // The ragged GEMV (decode MoE) on experts prepared into the panel layout,
 // one expert's copy `stride` bytes after the last (codes, then the sz words
 // at sz_off): workgroup (expert e, panel p) runs the rows of e,
-// [off[e], min(off[e+1], T)), against its panel p in passes of up to four
-// rows (panel_rows_tile, each pass one, two or four rows wide), K whole and
-// no hand-off.  Sorted offsets only: when they have wrapped, every
+// [off[e], min(off[e+1], T)), against its panel p in passes of one or two
+// rows (panel_rows_tile), K whole and no hand-off.  (Passes of up to four
+// rows took more registers, fewer waves, and 55.5 against 53.5 us at 4
+// tokens top-2 of config 4's experts.)  Sorted offsets only: when they have wrapped, every
 // workgroup returns and the VALU decode launch takes every row; it also
 // writes the rows past the last segment.
 template <int PPL, bool FULL>
@@ -475,16 +476,14 @@ __global__ __launch_bounds__(kPanelThreads) void int4_grouped_panel_rows_kernel(
     const u32x4* qp = reinterpret_cast<const u32x4*>(base) + (size_t)q * pairs;
     const u32x2* szp = reinterpret_cast<const u32x2*>(base + sz_off) + (size_t)(q >> 3) * pairs;
     const Epilogue ep{};
-    for (int r0 = 0; r0 < count; r0 += 4) {
-        const int rows = min(4, count - r0);
+    for (int r0 = 0; r0 < count; r0 += 2) {
+        const int rows = min(2, count - r0);
         const float* a = x + (size_t)(first + r0) * K;
         float* o = out + (size_t)(first + r0) * N;
         if (rows == 1)
             panel_rows_tile<1, PPL, FULL>(a, qp, szp, o, 1, K, N, q, ep);
-        else if (rows == 2)
-            panel_rows_tile<2, PPL, FULL>(a, qp, szp, o, 2, K, N, q, ep);
         else
-            panel_rows_tile<4, PPL, FULL>(a, qp, szp, o, rows, K, N, q, ep);
+            panel_rows_tile<2, PPL, FULL>(a, qp, szp, o, 2, K, N, q, ep);
     }
 }
 

@@ -191,10 +191,10 @@ PANEL_CASES = [
     # f32 rows, 3 <= T < 2E: the panel kernel
     (8, 4096, 1024, [2, 0, 3, 1, 0, 4, 2, 1], 1),
     (4, 512, 640, [3, 1, 0, 2], 1),
-    (3, 256, 512, [5, 0, 0], 0),          # five rows: passes of four and one
+    (3, 256, 512, [5, 0, 0], 0),          # five rows: passes of two, two and one
     (2, 1024, 8192, [2, 1], 0),
     (4, 2048, 384, [1, 1, 1, 1], 0),      # 24 panels an expert
-    (4, 4096, 256, [7, 0, 0, 0], 0),      # seven rows: four and three
+    (4, 4096, 256, [7, 0, 0, 0], 0),      # seven rows: three passes of two and one
 ]
 
 def _run(dev, form, x, w, E, counts, T, N):
