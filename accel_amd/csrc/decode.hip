@@ -2177,10 +2177,10 @@ static int grouped_decode_tile(const Device* d, int T, int N) {
 // where the matrix-core blocks are not launched (fewer than two rows an
 // expert on average) and there are three rows or more; K even and the rows
 // 8-byte aligned.  Measured on config 4's experts (K = 4096, N = 14336,
-// top-2 of 8; panels in passes of up to four rows / matrix-core blocks or
-// VALU on the planes, us): 1
-// token (2 rows) 32.2 / 28.1, 2 tokens 43.7 / 50.5, 4 tokens 55.9 / 96.0,
-// 8 tokens 83.9 / 81.5 (side copies), 16 tokens 147.4 / 99.3.
+// top-2 of 8; us, panels in passes of up to four rows / the planes' route,
+// matrix-core blocks or VALU): 1 token (2 rows) 32.2 / 28.1, 2 tokens
+// 43.7 / 50.5, 4 tokens 55.9 / 96.0, 8 tokens 83.9 / 81.5 (side copies),
+// 16 tokens 147.4 / 99.3.
 bool grouped_panel_route(const void* x, Int4Planes w, bool bf16, int E, int T, int K) {
     return w.panels && !bf16 && T >= 3 && T <= kGroupedDecodeRows && (long long)T < 2LL * E &&
            K % 2 == 0 && (reinterpret_cast<uintptr_t>(x) & 7) == 0;
