@@ -2186,9 +2186,11 @@ bool grouped_panel_route(const void* x, Int4Planes w, bool bf16, int E, int T, i
            K % 2 == 0 && (reinterpret_cast<uintptr_t>(x) & 7) == 0;
 }
 
-size_t int4_grouped_decode_area(const Device* d, const void* x, Int4Planes w, int E, int T,
-                                int K, int N) {
-    if (grouped_panel_route(x, w, false, E, T, K)) {
+size_t int4_grouped_decode_area(const Device* d, const void* x, bool bf16, Int4Planes w, int E,
+                                int T, int K, int N) {
+    // the same rule the launch applies (launch_grouped_decode_t): bf16 rows
+    // never take the panels, and then plan their own split-K sums below
+    if (grouped_panel_route(x, w, bf16, E, T, K)) {
         // the VALU launch alone uses the area: the padding rows at one slice
         const int tw = N % 512 == 0 ? 512 : grouped_decode_tile(d, T, N);
         if (tw == 512) return GroupedDecodeShape<512>(d, T, K, N, true).area_bytes(T, N);

@@ -276,11 +276,12 @@ constexpr int kGroupedDecodeRows = 64;
 constexpr int kGroupedDecodeRowsF32 = 1024;
 // The grouped decode launches take the workspace's counters (`tickets`) and an
 // area past the offsets for their split-K sums, of the size
-// int4_grouped_decode_area gives for the same x, w and shape (the workspace is
-// sized once, before the offsets are computed, so it cannot grow and move them).
+// int4_grouped_decode_area gives for the same x, dtype, w and shape (the
+// workspace is sized once, before the offsets are computed, so it cannot grow
+// and move them); both plan with the same routing rules.
 bool int4_grouped_decode_supported(int T, int K, int N, const void* codes, bool bf16);
-size_t int4_grouped_decode_area(const Device* d, const void* x, Int4Planes w, int E, int T,
-                                int K, int N);
+size_t int4_grouped_decode_area(const Device* d, const void* x, bool bf16, Int4Planes w, int E,
+                                int T, int K, int N);
 hipError_t launch_int4_grouped_decode(Device* d, hipStream_t st, const void* x, bool bf16,
                                       Int4Planes w, const uint32_t* off, void* out, int E, int T,
                                       int K, int N, bool write_padding, int* status,

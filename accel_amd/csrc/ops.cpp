@@ -895,7 +895,8 @@ int run_grouped_int4(const char* op, int dev, void* stream, const accel_tensor_t
     // bounds are the offsets sorted (segment_bounds), in the area
     const size_t bounds_bytes = ((size_t)(experts + 1) * sizeof(uint32_t) + 255) / 256 * 256;
     const size_t area_bytes =
-        decode ? int4_grouped_decode_area(d, x->data, p, (int)experts, (int)T, (int)K, (int)N)
+        decode ? int4_grouped_decode_area(d, x->data, !f32, p, (int)experts, (int)T, (int)K,
+                                          (int)N)
                : (tiles && matvec ? bounds_bytes : 0);
     void* area = nullptr;
     uint32_t* off = offsets_in_workspace(d, st, static_cast<const uint32_t*>(counts->data),

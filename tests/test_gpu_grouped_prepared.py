@@ -306,3 +306,26 @@ def test_panel_experts_decode_moe_full_size(dev):
     assert rel_l2(got, ref) <= 1e-5
     pw.free()
     w.free()
+
+
+@pytest.mark.parametrize("form", ["Int4GroupedMatVec", "Int4GroupedMatMul"])
+def test_panel_experts_with_bf16_rows_take_the_planes_route(dev, form):
+    """bf16 rows on experts prepared into the panel layout, 3 <= T < 2E: the
+    panel kernel takes f32 rows only, so these run the VALU decode kernel on
+    the planes with K split, and the workspace area for its split-K sums is
+    planned for that route (a plan for the panel route's one-slice padding
+    launch left the sums no room).  Equal to the planes' product bit for bit
+    and to the oracle at the bf16 tolerance."""
+    E, K, N, counts, pad = 8, 1024, 128, [0, 1, 0, 1, 0, 0, 0, 0], 2
+    x, p, s, z, off, T = _case(E, K, N, counts, pad, seed=9, bf16=True)
+    assert 3 <= T < 2 * E
+    w = dev.upload_int4(p, s, z, E * K * N)
+    pw = dev.prepare_int4_grouped(w, E, K, N, panels=True)
+    (ref, rsel), (got, gsel) = _both(dev, form, x, w, pw, E, counts, T, N, True)
+    assert not any(k.startswith("int4_grouped_panel_rows_kernel") for k in gsel.launches)
+    assert gsel.launches == rsel.launches
+    assert np.array_equal(got, ref)
+    want = oracle.round_bf16(_want(form, x, p, s, z, off, E, T, K, N))
+    assert rel_l2(workloads.bf16_to_f32(got), want) <= 2e-2
+    pw.free()
+    w.free()

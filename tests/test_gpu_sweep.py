@@ -175,3 +175,63 @@ def test_random_prepared_shapes_match_the_oracle(dev, seed):
         err = rel_l2(got.reshape(want.shape), want)
         assert err <= 1e-5, (seed, done, form, M, K, N, err)
         done += 1
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_grouped_prepared_shapes_match_the_oracle(dev, seed):
+    """Experts bound once, in either prepared form, at random shapes and
+    routings: side copies (accel_int4_prepare_grouped; the planes' grouped
+    product bit for bit) and panel copies (accel_int4_prepare_grouped_panels;
+    the panel kernel where 3 <= T < 2E), few rows an expert so that the panel
+    route, the matrix-core blocks and the VALU decode kernel all come up,
+    both forms, against the oracle at the path's tolerance."""
+    rng = np.random.Generator(np.random.PCG64(4000 + seed))
+    done = 0
+    while done < 8:
+        bf16 = rng.random() < 0.25
+        E = int(rng.integers(2, 13))
+        K = int(rng.choice([64, 256, 1024, 2048, 4096]))
+        N = int(rng.choice([128, 256, 384, 1024, 8192]))
+        cap = int(rng.choice([1, 2, 3, 8]))
+        counts = [int(c) if rng.random() > 0.25 else 0 for c in rng.integers(0, cap + 1, E)]
+        off = oracle.segment_offsets(np.array(counts, np.uint32))
+        T = int(off[E]) + int(rng.integers(0, 3))
+        if T == 0 or T * K * N > MAX_MACS or E * K * N > 4 * MAX_MACS:
+            continue
+        panels = bool(rng.integers(2))
+        form = "Int4GroupedMatVec" if rng.integers(2) else "Int4GroupedMatMul"
+        print(f"grouped prepared sweep seed={seed} case={done}: {form} E={E} K={K} N={N} "
+              f"counts={counts} T={T} bf16={bf16} panels={panels}", flush=True)
+        x = rng.standard_normal((T, K)).astype(np.float32)
+        p, s, z = workloads.fast_int4(E * K, N, rng)
+        init = np.full((T, N), 7.0, np.float32)
+        wd = dev.upload_int4(p, s, z, E * K * N)
+        pw = dev.prepare_int4_grouped(wd, E, K, N, panels=panels)
+        xb, xf = upload_x(dev, x, bf16)
+        cb = dev.upload(np.array(counts, np.uint32), U32)
+        outs = []
+        try:
+            for prepared in (True, False):
+                ob = dev.alloc((T, N), BF16 if bf16 else F32)
+                ob.write(workloads.bf16_bits(init) if bf16 else init)
+                if prepared:
+                    getattr(dev, form + "Prepared")(xb, pw, cb, ob)
+                else:
+                    getattr(dev, form)(xb, wd, E, cb, ob)
+                outs.append(read_out(ob, bf16))
+                ob.free()
+        finally:
+            for b in (xb, cb, wd):
+                b.free()
+            pw.free()
+        got, planes = outs
+        ref = oracle.int4_grouped_matvec if form == "Int4GroupedMatVec" else \
+            oracle.int4_grouped_matmul
+        want = ref(xf, p, s, z, off, E, T, K, N, threads=8, out=init.ravel().copy())
+        if bf16:
+            want = oracle.round_bf16(want)
+        err = rel_l2(got.ravel(), np.asarray(want).ravel())
+        assert err <= tolerance(bf16), (seed, done, form, E, K, N, counts, T, bf16, panels, err)
+        if not panels:
+            assert np.array_equal(got, planes), (seed, done)
+        done += 1
