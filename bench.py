@@ -1376,8 +1376,8 @@ def main():
         extra["vs_baseline_basis"] = (
             "vs_baseline is the reference's published figure for its own decode benchmark "
             f"({PUBLISHED_US:.0f} us a step, {PUBLISHED_SRC}) over this build's time for the "
-            "same workload and protocol (extra.published_decode_2048); BASELINE.md publishes "
-            "no figure for config 1 itself")
+            "same workload and protocol (extra.published_decode_2048); no figure is published "
+            "for config 1 itself")
     if not args.no_extra:
         if args.configs:
             progress("--configs: widened rows")
