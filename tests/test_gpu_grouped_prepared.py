@@ -12,7 +12,14 @@ offsets, the f32 and bf16 tiles past the decode route's rows, and the
 decode MoE and config 4's f32 rows at full size.  The small cases are also
 held to the oracle at the path's tolerance (f32 1e-5, bf16 2e-2, rel-L2;
 tensor/int4_test.go:275-354).  A prepared set of experts is refused by the
-single-matrix operators and a single prepared matrix by the grouped ones."""
+single-matrix operators and a single prepared matrix by the grouped ones.
+
+Experts prepared into the panel layout (accel_int4_prepare_grouped_panels)
+take f32 rows with 3 <= T < 2E on the few-rows panel kernel, whose sums run
+in another order: held to the oracle row for row at the f32 tolerance
+(passes of two rows ending in one, padding rows, wrapped offsets, the 4-token
+decode MoE at full size); their other rows, bf16 rows included, take the
+planes' routes and equal the planes' products bit for bit."""
 import numpy as np
 import pytest
 
